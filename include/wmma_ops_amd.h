@@ -1,0 +1,141 @@
+/*
+ * wmma_ops_amd.h -- C-ABI of the MI355X (gfx950 / CDNA4) matrix-core hot path.
+ *
+ * Plain pointers, sizes and an opaque stream handle; no torch or HIP types appear in
+ * any signature.  Every entry point is asynchronous on `stream` (a hipStream_t passed
+ * as void*; NULL means the null stream), never synchronises, never allocates device
+ * memory, and returns a status code (WMMA_OK == 0).  On failure the text of the last
+ * error on the calling thread is available from wmma_last_error().  Arguments are
+ * validated completely before anything touches the GPU, so every validation error is
+ * reachable without a device.
+ *
+ * The reference (glovepost/wmma_ops) exposes its path as pybind functions inside one
+ * PyTorch extension (wmma_gemm.hip:2120-2157).  Each function below names the reference
+ * interface it replaces.  Matrices are row-major; leading dimensions are in elements.
+ */
+#ifndef WMMA_OPS_AMD_H
+#define WMMA_OPS_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WMMA_OPS_AMD_ABI_VERSION 1
+
+/* Status codes. */
+#define WMMA_OK 0
+#define WMMA_ERR_INVALID_ARG 1   /* bad shape, null pointer, bad leading dimension      */
+#define WMMA_ERR_UNSUPPORTED 2   /* valid request this build does not implement         */
+#define WMMA_ERR_MISALIGNED 3    /* pointer or leading dimension breaks 16-byte vectors  */
+#define WMMA_ERR_WORKSPACE 4     /* workspace missing or smaller than *_workspace_size  */
+#define WMMA_ERR_HIP 5           /* launch or runtime error reported by HIP              */
+
+/* GEMM tile configurations.  0..3 are the reference's matmul_tiled menu
+ * (wmma_gemm.hip:1500-1523: 0=64x64, 1=128x64, 2=256x64, 3=128x128); 4 and 5 add the
+ * larger CDNA4 tiles.  WMMA_TILE_AUTO lets the planner choose tile and split-K. */
+#define WMMA_TILE_AUTO (-1)
+#define WMMA_TILE_64x64 0
+#define WMMA_TILE_128x64 1
+#define WMMA_TILE_256x64 2
+#define WMMA_TILE_128x128 3
+#define WMMA_TILE_256x128 4
+#define WMMA_TILE_256x256 5
+#define WMMA_TILE_COUNT 6
+
+/* Kernel families a GEMM plan can select. */
+#define WMMA_KERNEL_TILED 0   /* MFMA tiled kernel (optionally split-K + reduce)        */
+#define WMMA_KERNEL_SKINNY 1  /* M <= 16 streaming kernel, split-K + reduce             */
+
+typedef struct wmma_gemm_plan {
+    int kernel;            /* WMMA_KERNEL_*                                              */
+    int tile_cfg;          /* WMMA_TILE_* actually used (-1 for the skinny kernel)       */
+    int tile_m, tile_n;    /* output tile of one workgroup                               */
+    int split_k;           /* number of K partitions (1 = no split, no workspace)        */
+    int k_per_split;       /* K elements per partition (multiple of 64)                  */
+    int grid;              /* workgroups of the main kernel                              */
+    size_t workspace_bytes;/* fp32 partial sums: split_k * M * N * 4, 0 when split_k==1  */
+} wmma_gemm_plan;
+
+/* Text of the last error reported on this thread ("" if none). */
+const char* wmma_last_error(void);
+
+/* ABI version of the loaded library (WMMA_OPS_AMD_ABI_VERSION). */
+int wmma_abi_version(void);
+
+/* Number of compute units the planner assumes for device `device` (queried from HIP
+ * once per device; 256 for an MI355X).  Returns 256 when no device can be queried. */
+int wmma_device_cu_count(int device);
+
+/* Host-only planner: the kernel, tile, split-K and workspace a GEMM of this shape uses
+ * on a device with `num_cus` compute units.  tile_cfg as for wmma_gemm_f16f32.
+ * Replaces the reference's select_optimal_tile (wmma_tile_selection.hpp:30-66) and
+ * split_k::compute_config (wmma_xor_swizzle.hpp:293-332). */
+int wmma_gemm_plan_make(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* out);
+
+/* Workspace bytes wmma_gemm_f16f32 needs for this shape on the current device. */
+size_t wmma_gemm_workspace_size(int M, int N, int K, int tile_cfg);
+
+/*
+ * C_out[M,N] = alpha * (A[M,K] @ B[K,N]) + beta * C_in[M,N]      (fp16 in, fp32 accumulate
+ * and out).  C_in is read only when beta != 0 and C_in != NULL; C_in may equal C_out
+ * (in-place).  tile_cfg: WMMA_TILE_AUTO or 0..WMMA_TILE_COUNT-1.  workspace: device
+ * memory of at least wmma_gemm_workspace_size(M,N,K,tile_cfg) bytes (may be NULL when
+ * that is 0).
+ * Replaces wmma_matmul (wmma_gemm.hip:1432-1470), wmma_matmul_tiled (:1473-1528),
+ * wmma_matmul_adaptive (:1197-1263), wmma_gemm (:1891-1945), wmma_gemm_inplace
+ * (:1949-1994) and wmma_gemm_adaptive (:1997-2078), and the unreachable split-K wrapper
+ * (wmma_xor_swizzle.hpp:1172-1219).
+ */
+int wmma_gemm_f16f32(const void* A, int64_t lda, const void* B, int64_t ldb,
+                     const float* C_in, int64_t ldc_in, float* C_out, int64_t ldc,
+                     int M, int N, int K, float alpha, float beta, int tile_cfg,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * INT4 weights.  The reference has no INT4 code; the layout is this library's own.
+ * "GPTQ layout": qweight is int32 [K/8, N]; weight q[k][n] (0..15) sits in bits
+ * 4*(k%8) .. 4*(k%8)+3 of qweight[k/8][n].  K % 64 == 0 and N % 32 == 0 are required.
+ * Prepacked layout: int32 [N/32][K/64][64 lanes][4]; lane l of block (nt, kc) holds
+ * column n = 32*nt + l%32 and the four GPTQ words of k-groups 8*kc + 4*(l/32) + 0..3.
+ */
+int wmma_int4_prepack(const int32_t* qweight, int K, int N, int32_t* packed, void* stream);
+/* Inverse of wmma_int4_prepack (prepacked layout back to the GPTQ layout). */
+int wmma_int4_unprepack(const int32_t* packed, int K, int N, int32_t* qweight, void* stream);
+/* Debug unpack: GPTQ-layout qweight -> uint8 q[K][N] (row-major). */
+int wmma_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q, void* stream);
+
+#define WMMA_ZEROS_PACKED 0  /* zeros int32 [K/G, N/8]; z[g][n] in bits 4*(n%8).. of [g][n/8] */
+#define WMMA_ZEROS_U8 1      /* zeros uint8 [K/G, N]                                       */
+
+/* Workspace bytes wmma_w4a16_gemm needs (fp32 split-K partials). */
+size_t wmma_w4a16_workspace_size(int M, int N, int K, int group_size);
+
+/*
+ * Y[M,N] (fp32) = A[M,K] (fp16) @ W[K,N], W[k][n] = fp16((q[k][n] - z[k/G][n]) * s[k/G][n])
+ * (dequantised value rounded once to fp16).  packed: output of wmma_int4_prepack.
+ * scales: fp16 [K/G, N].  zeros: per zeros_format.  G = group_size, G % 32 == 0, K % G == 0.
+ * No reference counterpart (BASELINE-defined W4A16 path).
+ */
+int wmma_w4a16_gemm(const void* A, int64_t lda, const int32_t* packed, const void* scales,
+                    const void* zeros, int zeros_format, int M, int N, int K, int group_size,
+                    float* Y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Flash-attention forward.  Q [B,H,Sq,D], K and V [B,H,Sk,D], O [B,H,Sq,D]; fp16,
+ * contiguous.  O = softmax(scale * Q K^T (+ causal mask: key j <= query i when
+ * Sq == Sk; with Sq != Sk the mask is aligned to the bottom right, key j <= i + Sk - Sq))
+ * V, FP32 online softmax and accumulation.  D in {64, 128}.
+ * Replaces the documented (unbound) flash_attention(Q,K,V,causal=False,scale=-1.0)
+ * (README.md:221-251).  A caller's scale <= 0 is resolved to 1/sqrt(D) before this call.
+ */
+int wmma_flash_attn_fwd(const void* Q, const void* K, const void* V, void* O, int B, int H,
+                        int Sq, int Sk, int D, float scale, int causal, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WMMA_OPS_AMD_H */

@@ -1,0 +1,139 @@
+"""INT4 / W4A16 oracle (CPU, numpy).  Test infrastructure only -- see oracle/__init__.py.
+
+The reference has no INT4 code (no name, layout or test to follow).  The semantics here
+are the task's W4A16 definition and this library's written layout specification
+(include/wmma_ops_amd.h):
+
+  GPTQ qweight  int32 [K/8, N]; q[k][n] = (qweight[k//8][n] >> 4*(k%8)) & 0xF
+  packed zeros  int32 [K/G, N/8]; z[g][n] = (zeros[g][n//8] >> 4*(n%8)) & 0xF
+  prepacked     int32 [N/32][K/64][64][4]; block (nt, kc), lane l, word w holds the
+                GPTQ word of k-group kg = 8*kc + 4*(l//32) + w for column 32*nt + l%32,
+                with its nibbles reordered: nibble p holds k-offset PERM[p]
+  dequant       W[k][n] = fp16((q - z) * s), q - z exact, one rounding to fp16
+  W4A16         Y = A.float() @ W.float()   (fp32 accumulate)
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+PERM = (0, 2, 4, 6, 1, 3, 5, 7)  # nibble position -> k offset inside a prepacked word
+
+
+def pack_gptq(q: np.ndarray) -> np.ndarray:
+    """uint8 q [K, N] (values 0..15) -> int32 qweight [K/8, N]."""
+    q = np.asarray(q, dtype=np.uint32)
+    K, N = q.shape
+    assert K % 8 == 0
+    q = q.reshape(K // 8, 8, N)
+    out = np.zeros((K // 8, N), dtype=np.uint32)
+    for j in range(8):
+        out |= (q[:, j, :] & 0xF) << np.uint32(4 * j)
+    return out.view(np.int32)
+
+
+def unpack_gptq(qweight: np.ndarray) -> np.ndarray:
+    """int32 qweight [K/8, N] -> uint8 q [K, N]."""
+    w = np.asarray(qweight).view(np.uint32)
+    kg, N = w.shape
+    out = np.empty((kg, 8, N), dtype=np.uint8)
+    for j in range(8):
+        out[:, j, :] = (w >> np.uint32(4 * j)) & 0xF
+    return out.reshape(kg * 8, N)
+
+
+def pack_zeros(z: np.ndarray) -> np.ndarray:
+    """uint8 z [K/G, N] -> int32 [K/G, N/8], nibble n%8 of word n//8."""
+    z = np.asarray(z, dtype=np.uint32)
+    ng, N = z.shape
+    assert N % 8 == 0
+    z = z.reshape(ng, N // 8, 8)
+    out = np.zeros((ng, N // 8), dtype=np.uint32)
+    for j in range(8):
+        out |= (z[:, :, j] & 0xF) << np.uint32(4 * j)
+    return out.view(np.int32)
+
+
+def unpack_zeros(zp: np.ndarray) -> np.ndarray:
+    w = np.asarray(zp).view(np.uint32)
+    ng, n8 = w.shape
+    out = np.empty((ng, n8, 8), dtype=np.uint8)
+    for j in range(8):
+        out[:, :, j] = (w >> np.uint32(4 * j)) & 0xF
+    return out.reshape(ng, n8 * 8)
+
+
+def _permute_word_nibbles(w: np.ndarray, inverse: bool = False) -> np.ndarray:
+    w = np.asarray(w, dtype=np.uint32)
+    out = np.zeros_like(w)
+    for p, koff in enumerate(PERM):
+        if not inverse:  # nibble p of the result holds k-offset PERM[p] of the source
+            out |= ((w >> np.uint32(4 * koff)) & 0xF) << np.uint32(4 * p)
+        else:
+            out |= ((w >> np.uint32(4 * p)) & 0xF) << np.uint32(4 * koff)
+    return out
+
+
+def prepack(qweight: np.ndarray) -> np.ndarray:
+    """GPTQ qweight [K/8, N] -> prepacked int32, returned with shape [K/8, N]."""
+    w = np.asarray(qweight).view(np.uint32)
+    kg, N = w.shape
+    K = kg * 8
+    assert K % 64 == 0 and N % 32 == 0
+    KC, NT = K // 64, N // 32
+    # w[kg, n] with kg = 8*kc + 4*h + word, n = 32*nt + c  ->  out[nt, kc, 32*h + c, word]
+    t = w.reshape(KC, 2, 4, NT, 32)            # [kc, h, word, nt, c]
+    t = t.transpose(3, 0, 1, 4, 2)             # [nt, kc, h, c, word]
+    t = _permute_word_nibbles(t)
+    return np.ascontiguousarray(t).reshape(kg, N).view(np.int32)
+
+
+def unprepack(packed: np.ndarray) -> np.ndarray:
+    """Inverse of prepack."""
+    p = np.asarray(packed).view(np.uint32)
+    kg, N = p.shape
+    K = kg * 8
+    KC, NT = K // 64, N // 32
+    t = p.reshape(NT, KC, 2, 32, 4)            # [nt, kc, h, c, word]
+    t = _permute_word_nibbles(t, inverse=True)
+    t = t.transpose(1, 2, 4, 0, 3)             # [kc, h, word, nt, c]
+    return np.ascontiguousarray(t).reshape(kg, N).view(np.int32)
+
+
+def dequant(q: np.ndarray, scales: np.ndarray, zeros_u8: np.ndarray, G: int) -> np.ndarray:
+    """fp16((q - z) * s): the difference is exact in fp16 and numpy's float16 multiply
+    rounds the exact product once."""
+    q = np.asarray(q, dtype=np.int32)
+    K, N = q.shape
+    g = np.arange(K) // G
+    z = np.asarray(zeros_u8, dtype=np.int32)[g, :]
+    s = np.asarray(scales, dtype=np.float16)[g, :]
+    return (q - z).astype(np.float16) * s
+
+
+def dequant_f64_route(q: np.ndarray, scales: np.ndarray, zeros_u8: np.ndarray, G: int) -> np.ndarray:
+    """The same value by an independent route: exact float64 product, one rounding."""
+    q = np.asarray(q, dtype=np.float64)
+    K, _ = q.shape
+    g = np.arange(K) // G
+    z = np.asarray(zeros_u8, dtype=np.float64)[g, :]
+    s = np.asarray(scales, dtype=np.float16).astype(np.float64)[g, :]
+    return ((q - z) * s).astype(np.float16)
+
+
+def w4a16_ref(A: torch.Tensor, q: np.ndarray, scales: np.ndarray, zeros_u8: np.ndarray,
+              G: int) -> torch.Tensor:
+    """Y = A.float() @ W.float(), W = dequant(...), fp32 on the CPU."""
+    W = torch.from_numpy(dequant(q, scales, zeros_u8, G).astype(np.float32))
+    return torch.matmul(A.detach().cpu().float(), W)
+
+
+def make_inputs(M: int, K: int, N: int, G: int, seed: int):
+    """Seeded W4A16 inputs as the task describes them: A ~ N(0,1) fp16; q ~ U{0..15};
+    s ~ U(0.001, 0.02) fp16; z ~ U{0..15}."""
+    g = torch.Generator().manual_seed(seed)
+    A = torch.randn(M, K, generator=g).half()
+    q = torch.randint(0, 16, (K, N), generator=g, dtype=torch.int32).numpy().astype(np.uint8)
+    s = (torch.rand(K // G, N, generator=g) * (0.02 - 0.001) + 0.001).half().numpy()
+    z = torch.randint(0, 16, (K // G, N), generator=g, dtype=torch.int32).numpy().astype(np.uint8)
+    return A, q, s, z

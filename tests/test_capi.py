@@ -1,0 +1,179 @@
+"""C-ABI boundary tests that need no GPU.
+
+* the library loads and exports every function include/wmma_ops_amd.h declares;
+* argument validation returns the documented status codes (nothing reaches the GPU:
+  every case below fails validation before a launch);
+* the host planner's decisions for the BASELINE shapes;
+* the torch extension imports and reproduces the reference's argument errors
+  (wmma_gemm.hip:1433-1446, 1522-1523).
+"""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "wmma_ops_amd.h")
+LIB = os.path.join(ROOT, "wmma_ops_amd", "libwmma_ops_amd.so")
+
+OK, INVALID, UNSUPPORTED, MISALIGNED, WORKSPACE = 0, 1, 2, 3, 4
+
+
+class Plan(ctypes.Structure):
+    _fields_ = [("kernel", ctypes.c_int), ("tile_cfg", ctypes.c_int), ("tile_m", ctypes.c_int),
+                ("tile_n", ctypes.c_int), ("split_k", ctypes.c_int), ("k_per_split", ctypes.c_int),
+                ("grid", ctypes.c_int), ("workspace_bytes", ctypes.c_size_t)]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    L = ctypes.CDLL(LIB)
+    vp, i64, i32, f32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    L.wmma_last_error.restype = ctypes.c_char_p
+    L.wmma_gemm_f16f32.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, f32, f32, i32,
+                                   vp, sz, vp]
+    L.wmma_gemm_plan_make.argtypes = [i32, i32, i32, i32, i32, ctypes.POINTER(Plan)]
+    L.wmma_gemm_workspace_size.restype = sz
+    L.wmma_w4a16_workspace_size.restype = sz
+    L.wmma_int4_prepack.argtypes = [vp, i32, i32, vp, vp]
+    L.wmma_int4_unpack.argtypes = [vp, i32, i32, vp, vp]
+    L.wmma_w4a16_gemm.argtypes = [vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, vp, i64, vp, sz, vp]
+    L.wmma_flash_attn_fwd.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, i32, vp]
+    return L
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*(wmma_[A-Za-z0-9_]+)\s*\(",
+                       text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    for must in ["wmma_gemm_f16f32", "wmma_gemm_workspace_size", "wmma_int4_prepack",
+                 "wmma_int4_unpack", "wmma_w4a16_gemm", "wmma_flash_attn_fwd", "wmma_last_error"]:
+        assert must in names, names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert lib.wmma_abi_version() == 1
+
+
+# ---------------------------------------------------------------- GEMM validation --
+def gemm(lib, A=None, lda=64, B=None, ldb=64, Cin=None, ldcin=64, Cout=None, ldc=64, M=64, N=64,
+         K=64, alpha=1.0, beta=0.0, cfg=-1, ws=None, wsb=0):
+    return lib.wmma_gemm_f16f32(A, lda, B, ldb, Cin, ldcin, Cout, ldc, M, N, K, alpha, beta, cfg,
+                                ws, wsb, None)
+
+
+FAKE = 0x10000  # never dereferenced: every call below fails validation first
+
+
+def test_gemm_validation_codes(lib):
+    assert gemm(lib, M=-1) == INVALID
+    assert b"negative" in lib.wmma_last_error()
+    assert gemm(lib, cfg=6) == INVALID
+    assert b"Invalid tile_config" in lib.wmma_last_error()
+    assert gemm(lib, A=FAKE, B=FAKE, Cout=None) == INVALID          # NULL output
+    assert gemm(lib, A=None, B=FAKE, Cout=FAKE) == INVALID          # NULL A with K > 0
+    assert gemm(lib, A=FAKE, B=FAKE, Cout=FAKE, lda=32) == INVALID  # lda < K
+    assert gemm(lib, A=FAKE, B=FAKE, Cout=FAKE, ldb=32) == INVALID  # ldb < N
+    assert gemm(lib, A=FAKE, B=FAKE, Cout=FAKE, ldc=32) == INVALID  # ldc < N
+    assert gemm(lib, A=FAKE, B=FAKE, Cout=FAKE, Cin=FAKE, beta=1.0, ldcin=8) == INVALID
+    # split-K shape without workspace
+    assert gemm(lib, A=FAKE, B=FAKE, Cout=FAKE, M=1, N=4096, K=4096, lda=4096, ldb=4096, ldc=4096) == WORKSPACE
+    assert b"workspace" in lib.wmma_last_error()
+    need = lib.wmma_gemm_workspace_size(1, 4096, 4096, -1)
+    assert need > 0
+    assert gemm(lib, A=FAKE, B=FAKE, Cout=FAKE, M=1, N=4096, K=4096, lda=4096, ldb=4096, ldc=4096,
+                ws=FAKE, wsb=need - 4) == WORKSPACE
+    # empty output is a no-op success, no pointers needed
+    assert gemm(lib, M=0) == OK
+    assert gemm(lib, N=0) == OK
+
+
+def test_plan_make(lib):
+    p = Plan()
+    assert lib.wmma_gemm_plan_make(4096, 4096, 4096, -1, 256, ctypes.byref(p)) == OK
+    assert (p.kernel, p.tile_m, p.tile_n, p.split_k, p.grid, p.workspace_bytes) == (0, 256, 256, 1, 256, 0)
+    assert lib.wmma_gemm_plan_make(1, 14336, 4096, -1, 256, ctypes.byref(p)) == OK
+    assert p.kernel == 1 and p.split_k >= 2 and p.k_per_split % 64 == 0
+    assert p.workspace_bytes == p.split_k * 1 * 14336 * 4
+    for cfg, (bm, bn) in {0: (64, 64), 1: (128, 64), 2: (256, 64), 3: (128, 128), 4: (256, 128), 5: (256, 256)}.items():
+        assert lib.wmma_gemm_plan_make(1000, 1000, 1000, cfg, 256, ctypes.byref(p)) == OK
+        assert (p.tile_m, p.tile_n, p.split_k) == (bm, bn, 1)
+    assert lib.wmma_gemm_plan_make(10, 10, 10, 9, 256, ctypes.byref(p)) == INVALID
+    assert lib.wmma_gemm_plan_make(10, 10, 10, -1, 256, None) == INVALID
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (16, 11008, 4096), (64, 14336, 4096),
+                                   (128, 4096, 14336), (512, 512, 512), (1024, 1024, 1024),
+                                   (2048, 2048, 2048), (4096, 4096, 2048), (300, 70, 5000)])
+def test_plan_split_covers_k(lib, M, N, K):
+    p = Plan()
+    assert lib.wmma_gemm_plan_make(M, N, K, -1, 256, ctypes.byref(p)) == OK
+    assert p.k_per_split * (p.split_k - 1) < K <= p.k_per_split * p.split_k
+    if p.split_k > 1:
+        assert p.k_per_split % 64 == 0
+        assert p.workspace_bytes == p.split_k * M * N * 4
+    else:
+        assert p.workspace_bytes == 0
+
+
+# ---------------------------------------------------------------- INT4 / flash validation --
+def test_int4_validation_codes(lib):
+    assert lib.wmma_int4_prepack(FAKE, 100, 64, FAKE, None) == UNSUPPORTED   # K % 64
+    assert lib.wmma_int4_prepack(FAKE, 128, 48, FAKE, None) == UNSUPPORTED   # N % 32
+    assert lib.wmma_int4_prepack(None, 128, 64, FAKE, None) == INVALID
+    assert lib.wmma_int4_prepack(FAKE, 128, 64, FAKE + 4, None) == MISALIGNED
+    assert lib.wmma_int4_unpack(FAKE, 12, 64, FAKE, None) == INVALID
+    w = lambda **kw: lib.wmma_w4a16_gemm(kw.get("A", FAKE), kw.get("lda", 4096), FAKE, FAKE, FAKE,
+                                         kw.get("zf", 0), kw.get("M", 1), 4096, 4096, kw.get("G", 128),
+                                         FAKE, 4096, kw.get("ws", None), kw.get("wsb", 0), None)
+    assert w(G=48) == UNSUPPORTED
+    assert w(G=0) == UNSUPPORTED
+    assert w(zf=7) == INVALID
+    assert w(A=FAKE + 2) == MISALIGNED
+    assert w(lda=100) == INVALID
+    assert w(M=0) == OK
+
+
+def test_flash_validation_codes(lib):
+    f = lambda **kw: lib.wmma_flash_attn_fwd(FAKE, FAKE, FAKE, kw.get("O", FAKE), 1, 1, kw.get("S", 128),
+                                             kw.get("S", 128), kw.get("D", 128), kw.get("scale", 0.1), 0, None)
+    assert f(D=96) == UNSUPPORTED
+    assert f(scale=0.0) == INVALID
+    assert f(scale=float("nan")) == INVALID
+    assert f(O=None) == INVALID
+    assert f(O=FAKE + 8) == MISALIGNED
+    assert f(S=0) == OK
+
+
+# ---------------------------------------------------------------- torch layer on CPU --
+def test_torch_extension_reference_errors(wo):
+    A = torch.zeros(4, 8, dtype=torch.float16)
+    B = torch.zeros(8, 4, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="Inputs must be CUDA tensors"):
+        wo.matmul(A, B)
+    with pytest.raises(RuntimeError, match="Inputs must be CUDA tensors"):
+        wo.matmul_tiled(A, B, 1)
+    with pytest.raises(RuntimeError, match="Inputs must be CUDA tensors"):
+        wo.gemm(A, B, alpha=2.0, beta=0.5, C=None)
+    with pytest.raises(RuntimeError, match="Inputs must be CUDA tensors"):
+        wo.flash_attention(torch.zeros(1, 1, 4, 64, dtype=torch.float16),
+                           torch.zeros(1, 1, 4, 64, dtype=torch.float16),
+                           torch.zeros(1, 1, 4, 64, dtype=torch.float16))
+    for name in ["matmul", "matmul_adaptive", "matmul_tiled", "gemm", "gemm_inplace", "gemm_adaptive",
+                 "flash_attention", "prepack_int4", "matmul_int4", "unpack_int4",
+                 "matmul_kunroll", "matmul_hilbert", "matmul_opt", "matmul_pingpong"]:
+        assert callable(getattr(wo, name))
+
+
+def test_torch_plan_binding(wo):
+    assert wo.gemm_plan(4096, 4096, 4096) == [0, 5, 256, 256, 1, 4096, 256, 0]

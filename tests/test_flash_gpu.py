@@ -1,0 +1,70 @@
+"""GPU parity of flash-attention forward against fp32 CPU SDPA (max rel err <= 1e-3)."""
+import math
+
+import pytest
+import torch
+
+from oracle import attention as oatt
+from oracle import gemm as og
+from tests.conftest import report
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def _check(O, ref):
+    assert O.dtype == torch.float16 and tuple(O.shape) == tuple(ref.shape)
+    assert torch.isfinite(O).all()
+    err = og.max_rel_err(O.float(), ref)
+    assert err <= TOL, f"max rel err {err:.3e}"
+    return err
+
+
+# [4, 32, 4096, 128], scale 1/sqrt(128), causal and non-causal.  The CPU
+# reference is evaluated on a sample of (batch, head) pairs at the full sequence length.
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_baseline_config(wo, causal):
+    B, H, S, D = 4, 32, 4096, 128
+    report("flash", B=B, H=H, S=S, D=D, causal=causal)
+    Q, K, V = oatt.make_inputs(B, H, S, D, seed=42 + 4)
+    O = wo.flash_attention(Q.cuda(), K.cuda(), V.cuda(), causal=causal, scale=1.0 / math.sqrt(D))
+    assert torch.isfinite(O).all()
+    assert O.abs().max().item() <= V.abs().max().item() * (1 + 1e-3)
+    for b, h in [(0, 0), (1, 17), (3, 31)]:
+        ref = oatt.sdpa_ref(Q[b:b + 1, h:h + 1], K[b:b + 1, h:h + 1], V[b:b + 1, h:h + 1], causal)
+        _check(O[b:b + 1, h:h + 1], ref)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,H,Sq,Sk,D", [(2, 8, 512, 512, 64), (1, 4, 77, 77, 128), (2, 2, 200, 200, 64),
+                                         (1, 3, 100, 300, 128), (1, 2, 300, 100, 64), (1, 1, 1, 1, 128),
+                                         (1, 2, 129, 129, 128)])
+def test_flash_shapes(wo, causal, B, H, Sq, Sk, D):
+    report("flash_shape", B=B, H=H, Sq=Sq, Sk=Sk, D=D, causal=causal)
+    Q, K, V = oatt.make_inputs(B, H, Sq, D, seed=Sq + Sk + D, Sk=Sk)
+    O = wo.flash_attention(Q.cuda(), K.cuda(), V.cuda(), causal=causal)
+    _check(O, oatt.sdpa_ref(Q, K, V, causal))
+
+
+def test_flash_custom_scale(wo):
+    Q, K, V = oatt.make_inputs(2, 4, 256, 64, seed=3)
+    O = wo.flash_attention(Q.cuda(), K.cuda(), V.cuda(), False, 0.1)
+    _check(O, oatt.sdpa_ref(Q, K, V, False, 0.1))
+
+
+def test_flash_invariants(wo):
+    Q, K, V = oatt.make_inputs(1, 2, 256, 128, seed=5)
+    Vc = V[:, :, :1, :].expand_as(V).contiguous()
+    O = wo.flash_attention(Q.cuda(), K.cuda(), Vc.cuda())
+    assert torch.allclose(O.float().cpu(), Vc.float(), atol=2e-3)
+    Oc = wo.flash_attention(Q.cuda(), K.cuda(), V.cuda(), causal=True)
+    assert torch.allclose(Oc[0, :, 0].float().cpu(), V[0, :, 0].float(), atol=1e-3)
+
+
+def test_flash_errors(wo):
+    x = torch.zeros(1, 1, 8, 96, dtype=torch.half, device="cuda")
+    with pytest.raises(RuntimeError, match="head_dim"):
+        wo.flash_attention(x, x, x)
+    y = torch.zeros(1, 1, 8, 64, dtype=torch.float32, device="cuda")
+    with pytest.raises(RuntimeError, match="float16"):
+        wo.flash_attention(y, y, y)

@@ -1,0 +1,175 @@
+"""GPU parity of the FP16 GEMM family against the CPU oracle (fp32 torch).
+
+Bar: max|Y - Y_ref| / max|Y_ref| <= 1e-3 (the reference's metric and the task's bound,
+test_rocwmma_patch.py:66-74, test_fragment_loading.py:116-120), exact where the data
+makes every partial sum exact.  Inputs are seeded on the CPU (seed 42 + config index)
+and copied to the device, so both sides see identical values.
+"""
+import pytest
+import torch
+
+from oracle import gemm as og
+from tests.conftest import report
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def _inputs(M, N, K, seed, bstd=1.0):
+    g = torch.Generator().manual_seed(seed)
+    A = torch.randn(M, K, generator=g).half()
+    B = (torch.randn(K, N, generator=g) * bstd).half()
+    return A, B
+
+
+def _check(Y, ref, tol=TOL):
+    assert Y.dtype == torch.float32 and tuple(Y.shape) == tuple(ref.shape)
+    assert torch.isfinite(Y).all()
+    err = og.max_rel_err(Y, ref)
+    assert err <= tol, f"max rel err {err:.3e} > {tol}"
+    return err
+
+
+def test_known_answer_fragment(wo):
+    A, B, C = og.kat_fragment()
+    report("kat", M=64, N=64, K=16)
+    for fn in (wo.matmul, wo.matmul_adaptive, wo.matmul_asmOpt):
+        assert torch.equal(fn(A.cuda(), B.cuda()).cpu(), C)
+    for cfg in range(6):
+        assert torch.equal(wo.matmul_tiled(A.cuda(), B.cuda(), cfg).cpu(), C)
+
+
+# configs[0] and configs[1] of the task: square and rectangular shapes
+@pytest.mark.parametrize("M,N,K", [(512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048),
+                                   (4096, 4096, 4096), (4096, 4096, 2048)])
+def test_matmul_baseline_shapes(wo, M, N, K):
+    report("matmul", M=M, N=N, K=K, plan=wo.gemm_plan(M, N, K))
+    A, B = _inputs(M, N, K, 42 + 1)
+    ref = og.gemm_ref(A, B)
+    Ad, Bd = A.cuda(), B.cuda()
+    _check(wo.matmul(Ad, Bd), ref)
+    _check(wo.matmul_adaptive(Ad, Bd), ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(1024, 1024, 1024), (4096, 4096, 4096)])
+def test_gemm_epilogue_out_of_place_and_in_place(wo, M, N, K):
+    # C = 2.0*A*B + 0.5*C with C fp32 N(0,1), out-of-place and in-place.
+    report("gemm_epilogue", M=M, N=N, K=K)
+    A, B = _inputs(M, N, K, 42 + 1)
+    C = torch.randn(M, N, generator=torch.Generator().manual_seed(7))
+    ref = og.gemm_ref(A, B, 2.0, 0.5, C)
+    Ad, Bd, Cd = A.cuda(), B.cuda(), C.cuda()
+    out = wo.gemm(Ad, Bd, alpha=2.0, beta=0.5, C=Cd)
+    _check(out, ref)
+    assert torch.equal(Cd.cpu(), C)                       # out-of-place leaves C alone
+    out2 = wo.gemm_adaptive(Ad, Bd, 2.0, 0.5, Cd)
+    assert torch.equal(out, out2)
+    Ci = Cd.clone()
+    assert wo.gemm_inplace(Ad, Bd, Ci, 2.0, 0.5) is None
+    assert torch.equal(Ci, out)                           # in-place == out-of-place bitwise
+
+
+def test_gemm_beta_rules(wo):
+    A, B = _inputs(256, 192, 320, 5)
+    Ad, Bd = A.cuda(), B.cuda()
+    nan_c = torch.full((256, 192), float("nan"), device="cuda")
+    out = wo.gemm(Ad, Bd, alpha=1.5, beta=0.0, C=nan_c)   # beta == 0 never reads C
+    assert torch.isfinite(out).all()
+    _check(out, og.gemm_ref(A, B, 1.5))
+    out = wo.gemm(Ad, Bd, alpha=1.0, beta=3.0, C=None)    # beta without C is ignored
+    _check(out, og.gemm_ref(A, B))
+    Ci = nan_c.clone()
+    wo.gemm_inplace(Ad, Bd, Ci, 1.0, 0.0)
+    assert torch.isfinite(Ci).all()
+    with pytest.raises(RuntimeError, match="C dimensions must match output"):
+        wo.gemm(Ad, Bd, 1.0, 1.0, torch.zeros(3, 3, device="cuda"))
+    with pytest.raises(RuntimeError, match="C must be float32"):
+        wo.gemm(Ad, Bd, 1.0, 1.0, torch.zeros(256, 192, device="cuda", dtype=torch.float16))
+
+
+# skinny shapes that take the split-K / streaming paths
+SKINNY = [(m, n, 4096) for m in (1, 16, 64, 128) for n in (4096, 11008, 14336)] + \
+         [(m, 4096, 14336) for m in (1, 16, 64, 128)]
+
+
+@pytest.mark.parametrize("M,N,K", SKINNY)
+def test_skinny_split_k(wo, M, N, K):
+    report("skinny", M=M, N=N, K=K, plan=wo.gemm_plan(M, N, K))
+    A, B = _inputs(M, N, K, 42 + 2, bstd=0.02)
+    ref = og.gemm_ref(A, B)
+    _check(wo.matmul(A.cuda(), B.cuda()), ref)
+
+
+def test_skinny_epilogue_in_place(wo):
+    A, B = _inputs(16, 4096, 4096, 11, bstd=0.02)
+    C = torch.randn(16, 4096, generator=torch.Generator().manual_seed(12))
+    ref = og.gemm_ref(A, B, 2.0, 0.5, C)
+    Ci = C.cuda()
+    wo.gemm_inplace(A.cuda(), B.cuda(), Ci, 2.0, 0.5)
+    _check(Ci, ref)
+
+
+@pytest.mark.parametrize("cfg", range(6))
+@pytest.mark.parametrize("M,N,K", [(512, 384, 320), (300, 264, 136), (1, 8, 64), (257, 520, 1000)])
+def test_matmul_tiled_every_config(wo, cfg, M, N, K):
+    report("tiled", cfg=cfg, M=M, N=N, K=K)
+    A, B = _inputs(M, N, K, 100 + cfg)
+    _check(wo.matmul_tiled(A.cuda(), B.cuda(), cfg), og.gemm_ref(A, B))
+
+
+def test_matmul_tiled_invalid_config(wo):
+    A = torch.zeros(64, 64, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="Invalid tile_config"):
+        wo.matmul_tiled(A, A, 7)
+
+
+@pytest.mark.parametrize("M,N,K", [(33, 40, 24), (130, 72, 200), (17, 19, 23), (5, 3, 7),
+                                   (1, 1, 1), (70, 129, 513), (3, 4096, 520), (640, 8, 8)])
+def test_ragged_shapes(wo, M, N, K):
+    # N or K not multiples of 8 take the element-wise load path.
+    report("ragged", M=M, N=N, K=K)
+    A, B = _inputs(M, N, K, M * 1000 + N + K)
+    ref = og.gemm_ref(A, B)
+    _check(wo.matmul(A.cuda(), B.cuda()), ref)
+    C = torch.randn(M, N)
+    _check(wo.gemm(A.cuda(), B.cuda(), 0.5, -2.0, C.cuda()), og.gemm_ref(A, B, 0.5, -2.0, C))
+
+
+def test_empty_and_zero_k(wo):
+    out = wo.matmul(torch.zeros(0, 16, dtype=torch.half, device="cuda"),
+                    torch.zeros(16, 8, dtype=torch.half, device="cuda"))
+    assert out.shape == (0, 8)
+    out = wo.matmul(torch.zeros(4, 0, dtype=torch.half, device="cuda"),
+                    torch.zeros(0, 8, dtype=torch.half, device="cuda"))
+    assert out.shape == (4, 8) and torch.count_nonzero(out) == 0
+    C = torch.randn(4, 8, device="cuda")
+    out = wo.gemm(torch.zeros(4, 0, dtype=torch.half, device="cuda"),
+                  torch.zeros(0, 8, dtype=torch.half, device="cuda"), 1.0, 2.0, C)
+    assert torch.allclose(out, 2.0 * C)
+
+
+def test_noncontiguous_inputs(wo):
+    A, B = _inputs(96, 80, 128, 3)
+    At = A.t().contiguous().cuda().t()   # non-contiguous view of A
+    Bt = B.t().contiguous().cuda().t()
+    assert not At.is_contiguous()
+    _check(wo.matmul(At, Bt), og.gemm_ref(A, B))
+
+
+def test_identity_and_linearity(wo):
+    A, _ = _inputs(256, 256, 256, 9)
+    eye = torch.eye(256, dtype=torch.half)
+    assert torch.equal(wo.matmul(A.cuda(), eye.cuda()).cpu(), A.float())
+    _, B = _inputs(256, 256, 256, 10)
+    y1 = wo.gemm(A.cuda(), B.cuda(), alpha=4.0)
+    y2 = wo.matmul(A.cuda(), B.cuda())
+    assert torch.equal(y1, 4.0 * y2)
+
+
+def test_integer_data_exact(wo):
+    # small integers: every partial sum is exact in fp32, so any tiling or split is exact
+    g = torch.Generator().manual_seed(21)
+    for M, N, K in [(1, 4096, 4096), (16, 4096, 4096), (256, 512, 4096), (2048, 2048, 2048)]:
+        A = torch.randint(-2, 3, (M, K), generator=g).half()
+        B = torch.randint(-2, 3, (K, N), generator=g).half()
+        assert torch.equal(wo.matmul(A.cuda(), B.cuda()).cpu(), og.gemm_ref(A, B)), (M, N, K)

@@ -1,0 +1,231 @@
+"""Pins the CPU oracle before it is trusted as the checker (no GPU needed).
+
+Each oracle function is checked against something other than a retyping of its own
+formula: the reference's known-answer test, float64 brute force, a second independent
+restatement in C, closed-form invariants, and the committed golden fixtures.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oatt
+from oracle import cref
+from oracle import gemm as og
+from oracle import int4 as oi
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+# ------------------------------------------------------------------------------- GEMM --
+def test_kat_fragment_exact():
+    # test_fragment_loading.py:237-256: C[i][k] = (i % 16) * 120 exactly.
+    A, B, C = og.kat_fragment()
+    assert torch.equal(og.gemm_ref(A, B), C)
+    assert C[5, 7].item() == 5 * 120
+    assert np.array_equal(cref.gemm(A.numpy(), B.numpy()), C.numpy())
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (1, 17, 9), (7, 5, 16), (16, 24, 33), (33, 9, 64)])
+def test_gemm_ref_matches_f64_bruteforce(M, N, K):
+    g = torch.Generator().manual_seed(42 + M + N + K)
+    A = torch.randn(M, K, generator=g).half()
+    B = torch.randn(K, N, generator=g).half()
+    C = torch.randn(M, N, generator=g)
+    ref64 = og.gemm_ref_f64(A.numpy(), B.numpy(), 2.0, 0.5, C.numpy())
+    got = og.gemm_ref(A, B, 2.0, 0.5, C).double().numpy()
+    assert np.allclose(got, ref64, rtol=1e-5, atol=1e-5 * max(1.0, np.abs(ref64).max()))
+    got_c = cref.gemm(A.numpy(), B.numpy(), 2.0, 0.5, C.numpy())
+    assert np.allclose(got_c, ref64, rtol=1e-5, atol=1e-5 * max(1.0, np.abs(ref64).max()))
+
+
+def test_gemm_invariants():
+    g = torch.Generator().manual_seed(7)
+    A = torch.randn(48, 32, generator=g).half()
+    B = torch.randn(32, 40, generator=g).half()
+    # identity B returns A exactly
+    assert torch.equal(og.gemm_ref(A, torch.eye(32).half()), A.float())
+    # zero A gives zero
+    assert torch.count_nonzero(og.gemm_ref(torch.zeros_like(A), B)) == 0
+    # a column permutation of B permutes the columns of C
+    perm = torch.randperm(40, generator=g)
+    assert torch.equal(og.gemm_ref(A, B[:, perm]), og.gemm_ref(A, B)[:, perm])
+    # linearity in alpha (power-of-two alpha is exact)
+    assert torch.equal(og.gemm_ref(A, B, alpha=4.0), 4.0 * og.gemm_ref(A, B))
+
+
+def test_gemm_beta_zero_never_reads_c():
+    # wmma_gemm.hip:1914: C is read only if beta != 0 and C was given.
+    A = torch.ones(4, 8).half()
+    B = torch.ones(8, 4).half()
+    C = torch.full((4, 4), float("nan"))
+    out = og.gemm_ref(A, B, alpha=1.0, beta=0.0, C=C)
+    assert torch.isfinite(out).all() and torch.equal(out, torch.full((4, 4), 8.0))
+    out_c = cref.gemm(A.numpy(), B.numpy(), 1.0, 0.0, C.numpy())
+    assert np.isfinite(out_c).all()
+    # beta != 0 without C: beta ignored
+    assert torch.equal(og.gemm_ref(A, B, alpha=2.0, beta=3.0, C=None), torch.full((4, 4), 16.0))
+
+
+@pytest.mark.parametrize("K,split", [(4096, 1), (4096, 4), (4096, 16), (1000, 3), (64, 8), (4097, 32)])
+def test_splitk_partition(K, split):
+    # wmma_xor_swizzle.hpp:327: k_per_split = ceil(K / split); ranges cover [0, K) once.
+    parts = og.splitk_partition(K, split)
+    kps = -(-K // split)
+    assert parts[0][0] == 0 and parts[-1][1] == K
+    for (a0, a1), (b0, b1) in zip(parts, parts[1:]):
+        assert a1 == b0
+    assert all(b - a <= kps for a, b in parts)
+    assert sum(b - a for a, b in parts) == K
+
+
+def test_splitk_sum_equals_full_product():
+    g = torch.Generator().manual_seed(3)
+    A = torch.randint(-3, 4, (16, 256), generator=g).half()  # integer data: sums exact
+    B = torch.randint(-3, 4, (256, 24), generator=g).half()
+    full = og.gemm_ref(A, B)
+    for split in (1, 2, 3, 4, 16):
+        assert torch.equal(og.splitk_gemm_ref(A, B, split), full)
+        assert np.array_equal(cref.gemm(A.numpy(), B.numpy(), split=split), full.numpy())
+
+
+def test_max_rel_err_metric():
+    ref = torch.tensor([[1.0, -4.0], [2.0, 0.0]])
+    y = ref.clone()
+    y[0, 1] = -3.9
+    assert abs(og.max_rel_err(y, ref) - 0.1 / 4.0) < 1e-7
+    assert og.max_rel_err(torch.zeros(2), torch.zeros(2)) == 0.0
+
+
+# ------------------------------------------------------------------------------- INT4 --
+def _rand_q(K, N, seed):
+    return np.random.default_rng(seed).integers(0, 16, (K, N), dtype=np.uint8)
+
+
+def test_pack_unpack_roundtrip_and_bit_positions():
+    q = _rand_q(64, 40, 1)
+    qw = oi.pack_gptq(q)
+    assert qw.dtype == np.int32 and qw.shape == (8, 40)
+    assert np.array_equal(oi.unpack_gptq(qw), q)
+    # k = 8*row + j sits at bits 4j..4j+3 (GPTQ convention)
+    assert ((qw[3, 5].astype(np.int64) & 0xFFFFFFFF) >> (4 * 6)) & 0xF == q[3 * 8 + 6, 5]
+    assert np.array_equal(cref.pack_gptq(q), qw)
+
+
+def test_single_nibble_positions():
+    # one nonzero weight at every k offset: bit position moves as specified
+    for k in range(8):
+        q = np.zeros((8, 1), dtype=np.uint8)
+        q[k, 0] = 0xA
+        assert (int(oi.pack_gptq(q)[0, 0]) & 0xFFFFFFFF) == 0xA << (4 * k)
+
+
+def test_zeros_pack_roundtrip():
+    z = _rand_q(4, 64, 2)
+    zp = oi.pack_zeros(z)
+    assert zp.shape == (4, 8)
+    assert np.array_equal(oi.unpack_zeros(zp), z)
+    assert (int(zp[1, 2]) & 0xFFFFFFFF) >> 12 & 0xF == z[1, 2 * 8 + 3]
+
+
+@pytest.mark.parametrize("K,N", [(64, 32), (128, 64), (256, 96), (512, 128)])
+def test_prepack_bijection_and_c_restatement(K, N):
+    q = _rand_q(K, N, K + N)
+    qw = oi.pack_gptq(q)
+    pk = oi.prepack(qw)
+    assert pk.shape == qw.shape and pk.dtype == np.int32
+    assert np.array_equal(oi.unprepack(pk), qw)
+    assert np.array_equal(cref.prepack(qw), pk)           # independent C restatement
+    # same multiset of nibbles
+    nib = lambda a: np.sort(np.concatenate([(a.view(np.uint32) >> (4 * j)) & 0xF for j in range(8)], axis=None))
+    assert np.array_equal(nib(pk), nib(qw))
+
+
+def test_prepack_layout_spot_values():
+    # block (nt, kc), lane l, word w <- GPTQ word kg = 8*kc + 4*(l//32) + w, column 32*nt + l%32,
+    # nibble p holds k-offset PERM[p].
+    K, N = 128, 64
+    q = _rand_q(K, N, 11)
+    qw = oi.pack_gptq(q)
+    pk = oi.prepack(qw).view(np.uint32).reshape(N // 32, K // 64, 64, 4)
+    for (nt, kc, l, w) in [(0, 0, 0, 0), (1, 1, 63, 3), (0, 1, 33, 2), (1, 0, 17, 1)]:
+        kg = 8 * kc + 4 * (l // 32) + w
+        n = 32 * nt + l % 32
+        word = int(pk[nt, kc, l, w])
+        for p, koff in enumerate(oi.PERM):
+            assert (word >> (4 * p)) & 0xF == q[8 * kg + koff, n]
+
+
+def test_dequant_two_independent_routes():
+    K, N, G = 256, 64, 64
+    q = _rand_q(K, N, 5)
+    z = _rand_q(K // G, N, 6)
+    s = (np.random.default_rng(7).uniform(0.001, 0.02, (K // G, N))).astype(np.float16)
+    a = oi.dequant(q, s, z, G)
+    b = oi.dequant_f64_route(q, s, z, G)
+    c = cref.dequant(q, s, z, G)
+    assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+    assert np.array_equal(a.view(np.uint16), c.view(np.uint16))
+
+
+def test_dequant_special_cases():
+    K, N, G = 64, 32, 32
+    q = _rand_q(K, N, 8)
+    s = np.full((K // G, N), 0.0123, dtype=np.float16)
+    z_eq = q[::G].copy()  # z equal to the first row of each group
+    w = oi.dequant(q, s, z_eq, G)
+    assert np.all(w[::G] == 0)
+    ones = np.ones((K // G, N), dtype=np.float16)
+    w1 = oi.dequant(q, ones, np.zeros((K // G, N), dtype=np.uint8), G)
+    assert np.array_equal(w1.astype(np.int32), q.astype(np.int32))
+
+
+def test_w4a16_ref_against_c():
+    A, q, s, z = oi.make_inputs(3, 128, 64, 64, seed=9)
+    ref = oi.w4a16_ref(A, q, s, z, 64).numpy()
+    W = cref.dequant(q, s, z, 64)
+    got = cref.w4a16(A.numpy(), W)
+    assert np.allclose(got, ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
+
+
+def test_golden_int4_fixture():
+    path = os.path.join(GOLDEN, "int4_k256_n64_g64.npz")
+    d = np.load(path)
+    q, s, z = d["q"], d["scales"], d["zeros_u8"]
+    assert np.array_equal(oi.pack_gptq(q), d["qweight"])
+    assert np.array_equal(oi.prepack(d["qweight"]), d["packed"])
+    assert np.array_equal(oi.pack_zeros(z), d["zeros_packed"])
+    assert np.array_equal(oi.dequant(q, s, z, 64).view(np.uint16), d["w_fp16_bits"])
+    A = torch.from_numpy(d["A"])
+    assert np.allclose(oi.w4a16_ref(A, q, s, z, 64).numpy(), d["Y"], rtol=0, atol=0)
+
+
+# -------------------------------------------------------------------------- attention --
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("Sq,Sk,D", [(8, 8, 16), (13, 13, 32), (5, 9, 16), (9, 5, 16)])
+def test_sdpa_ref_matches_naive_f64(causal, Sq, Sk, D):
+    Q, K, V = oatt.make_inputs(1, 2, Sq, D, seed=Sq * 7 + Sk, Sk=Sk)
+    ref = oatt.attention_naive_f64(Q.numpy(), K.numpy(), V.numpy(), causal)
+    got = oatt.sdpa_ref(Q, K, V, causal).double().numpy()
+    assert np.allclose(got, ref, atol=2e-6)
+
+
+def test_sdpa_invariants():
+    Q, K, V = oatt.make_inputs(1, 1, 16, 16, seed=1)
+    # identical V rows -> every output row equals that row
+    Vc = V[:, :, :1, :].expand_as(V).contiguous()
+    assert torch.allclose(oatt.sdpa_ref(Q, K, Vc), Vc.float(), atol=1e-6)
+    # causal row 0 attends only key 0
+    assert torch.allclose(oatt.sdpa_ref(Q, K, V, causal=True)[0, 0, 0], V[0, 0, 0].float(), atol=1e-6)
+    # scale -> 0 gives the mean of V (uniform weights), prefix means when causal
+    out = torch.nn.functional.scaled_dot_product_attention(Q.float(), K.float(), V.float(), scale=1e-30)
+    assert torch.allclose(out[0, 0, 3], V.float()[0, 0].mean(0), atol=1e-5)
+    outc = torch.nn.functional.scaled_dot_product_attention(Q.float(), K.float(), V.float(),
+                                                            is_causal=True, scale=1e-30)
+    assert torch.allclose(outc[0, 0, 3], V.float()[0, 0, :4].mean(0), atol=1e-5)
+    # permuting keys together with values leaves the non-causal output unchanged
+    perm = torch.randperm(16)
+    assert torch.allclose(oatt.sdpa_ref(Q, K[:, :, perm], V[:, :, perm]), oatt.sdpa_ref(Q, K, V), atol=1e-6)
+    # default scale is 1/sqrt(D)
+    assert oatt.resolve_scale(128, -1.0) == pytest.approx(1 / np.sqrt(128))

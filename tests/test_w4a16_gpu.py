@@ -1,0 +1,106 @@
+"""GPU parity of the INT4 prepack/unpack kernels (bit-exact) and W4A16 dequant-GEMM
+(max rel err <= 1e-3 against the fp32 CPU oracle)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gemm as og
+from oracle import int4 as oi
+from tests.conftest import report
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "int4_k256_n64_g64.npz")
+
+
+def test_golden_fixture_bit_exact(wo):
+    d = np.load(GOLDEN)
+    qw = torch.from_numpy(d["qweight"]).cuda()
+    assert np.array_equal(wo.prepack_int4(qw).cpu().numpy(), d["packed"])
+    assert np.array_equal(wo.unpack_int4(qw).cpu().numpy(), d["q"])
+    assert np.array_equal(wo.unprepack_int4(torch.from_numpy(d["packed"]).cuda()).cpu().numpy(),
+                          d["qweight"])
+    A = torch.from_numpy(d["A"])
+    Y = wo.matmul_int4(A.cuda(), torch.from_numpy(d["packed"]).cuda(),
+                       torch.from_numpy(d["scales"]).cuda(), torch.from_numpy(d["zeros_packed"]).cuda(), 64)
+    assert og.max_rel_err(Y, torch.from_numpy(d["Y"])) <= 1e-3
+
+
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 14336), (64, 32), (192, 96)])
+def test_prepack_unpack_bit_exact(wo, K, N):
+    report("prepack", K=K, N=N)
+    q = np.random.default_rng(K + N).integers(0, 16, (K, N), dtype=np.uint8)
+    qw = oi.pack_gptq(q)
+    qd = torch.from_numpy(qw).cuda()
+    pk = wo.prepack_int4(qd)
+    assert np.array_equal(pk.cpu().numpy(), oi.prepack(qw))
+    assert np.array_equal(wo.unpack_int4(qd).cpu().numpy(), q)
+    assert torch.equal(wo.unprepack_int4(pk), qd)
+
+
+# M in {1,16,128,2048}, K=4096, N in {4096, 14336}, G=128, seed 42 + 3
+@pytest.mark.parametrize("N", [4096, 14336])
+@pytest.mark.parametrize("M", [1, 16, 128, 2048])
+def test_w4a16_baseline(wo, M, N):
+    K, G = 4096, 128
+    report("w4a16", M=M, N=N, K=K, G=G)
+    A, q, s, z = oi.make_inputs(M, K, N, G, seed=42 + 3)
+    ref = oi.w4a16_ref(A, q, s, z, G)
+    pk = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
+    Y = wo.matmul_int4(A.cuda(), pk, torch.from_numpy(s).cuda(),
+                       torch.from_numpy(oi.pack_zeros(z)).cuda(), G)
+    assert torch.isfinite(Y).all()
+    err = og.max_rel_err(Y, ref)
+    assert err <= 1e-3, err
+
+
+@pytest.mark.parametrize("M,K,N,G", [(1, 256, 64, 32), (3, 512, 96, 64), (5, 1024, 128, 256),
+                                     (40, 512, 160, 128), (300, 1024, 96, 1024), (2, 64, 32, 64)])
+def test_w4a16_group_sizes_and_u8_zeros(wo, M, K, N, G):
+    report("w4a16_g", M=M, K=K, N=N, G=G)
+    A, q, s, z = oi.make_inputs(M, K, N, G, seed=M + K + N + G)
+    ref = oi.w4a16_ref(A, q, s, z, G)
+    pk = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
+    Ad, sd = A.cuda(), torch.from_numpy(s).cuda()
+    Yp = wo.matmul_int4(Ad, pk, sd, torch.from_numpy(oi.pack_zeros(z)).cuda(), G)
+    Yu = wo.matmul_int4(Ad, pk, sd, torch.from_numpy(z).cuda(), G)
+    assert og.max_rel_err(Yp, ref) <= 1e-3
+    assert torch.equal(Yp, Yu)
+
+
+def test_w4a16_zero_when_q_equals_z(wo):
+    K, N, G = 256, 64, 128
+    q = np.full((K, N), 9, dtype=np.uint8)
+    z = np.full((K // G, N), 9, dtype=np.uint8)
+    s = np.full((K // G, N), 0.01, dtype=np.float16)
+    A = torch.randn(4, K).half()
+    pk = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
+    Y = wo.matmul_int4(A.cuda(), pk, torch.from_numpy(s).cuda(), torch.from_numpy(z).cuda(), G)
+    assert torch.count_nonzero(Y) == 0
+
+
+def test_w4a16_integer_weights_exact(wo):
+    # s = 1, z = 0 and small integer activations: every sum exact
+    K, N, G = 512, 64, 128
+    q = np.random.default_rng(1).integers(0, 16, (K, N), dtype=np.uint8)
+    A = torch.randint(-2, 3, (16, K)).half()
+    s = np.ones((K // G, N), dtype=np.float16)
+    z = np.zeros((K // G, N), dtype=np.uint8)
+    pk = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
+    for m in (1, 4, 16):
+        Y = wo.matmul_int4(A[:m].cuda(), pk, torch.from_numpy(s).cuda(), torch.from_numpy(z).cuda(), G)
+        assert torch.equal(Y.cpu(), A[:m].float() @ torch.from_numpy(q.astype(np.float32)))
+
+
+def test_w4a16_errors(wo):
+    pk = torch.zeros(8, 64, dtype=torch.int32, device="cuda")
+    A = torch.zeros(1, 64, dtype=torch.half, device="cuda")
+    s = torch.zeros(1, 64, dtype=torch.half, device="cuda")
+    z = torch.zeros(1, 8, dtype=torch.int32, device="cuda")
+    with pytest.raises(RuntimeError, match="scales must be float16"):
+        wo.matmul_int4(A, pk, s.float(), z, 64)
+    with pytest.raises(RuntimeError, match="Inner dimensions must match"):
+        wo.matmul_int4(torch.zeros(1, 32, dtype=torch.half, device="cuda"), pk, s, z, 64)
+    with pytest.raises(RuntimeError, match="must be a multiple of 64"):
+        wo.prepack_int4(torch.zeros(3, 64, dtype=torch.int32, device="cuda"))

@@ -1,0 +1,64 @@
+"""wmma_ops for MI355X (gfx950): hand-written MFMA kernels behind the wmma_ops API.
+
+Drop-in for the reference module ``wmma_ops`` (pybind functions at
+wmma_gemm.hip:2120-2157)::
+
+    import wmma_ops_amd as wmma_ops
+    C = wmma_ops.matmul(A, B)                        # fp16 x fp16 -> fp32
+    C = wmma_ops.gemm(A, B, alpha=2.0, beta=0.5, C=C0)
+    wmma_ops.gemm_inplace(A, B, C, 2.0, 0.5)
+    O = wmma_ops.flash_attention(Q, K, V, causal=True)
+    P = wmma_ops.prepack_int4(qweight); Y = wmma_ops.matmul_int4(A, P, scales, zeros, 128)
+
+Every function runs the HIP kernels in ``libwmma_ops_amd.so`` through the C++ extension
+``_C``; there is no fallback path.  Importing fails loudly when the extension has not been
+built (``python -m wmma_ops_amd.build``).
+"""
+from __future__ import annotations
+
+import os as _os
+
+_PKG = _os.path.dirname(_os.path.abspath(__file__))
+LIBRARY_PATH = _os.path.join(_PKG, "libwmma_ops_amd.so")
+HEADER_PATH = _os.path.join(_os.path.dirname(_PKG), "include", "wmma_ops_amd.h")
+
+try:
+    import torch as _torch  # noqa: F401  (loads libtorch/libc10 before the extension)
+    from . import _C
+except ImportError as _e:  # pragma: no cover - exercised only on an unbuilt tree
+    raise ImportError(
+        "wmma_ops_amd: the native extension is not built; run `python -m wmma_ops_amd.build` "
+        f"(original error: {_e})"
+    ) from _e
+
+matmul = _C.matmul
+matmul_adaptive = _C.matmul_adaptive
+matmul_tiled = _C.matmul_tiled
+gemm = _C.gemm
+gemm_inplace = _C.gemm_inplace
+gemm_adaptive = _C.gemm_adaptive
+flash_attention = _C.flash_attention
+prepack_int4 = _C.prepack_int4
+unprepack_int4 = _C.unprepack_int4
+unpack_int4 = _C.unpack_int4
+matmul_int4 = _C.matmul_int4
+gemm_plan = _C.gemm_plan
+
+# The reference binds 13 more matmul_* names, each a gfx1151 tuning experiment computing
+# the same C = A @ B (wmma_gemm.hip:2122-2137).  They resolve to the planner-driven MFMA
+# GEMM here so code written against the reference keeps importing and running.
+_REFERENCE_VARIANTS = (
+    "matmul_hilbert", "matmul_kunroll", "matmul_native", "matmul_zerocopy", "matmul_quad",
+    "matmul_highOcc", "matmul_noPrefetch", "matmul_asmOpt", "matmul_swizzled",
+    "matmul_xor_optimized", "matmul_coop", "matmul_pingpong", "matmul_opt",
+)
+for _name in _REFERENCE_VARIANTS:
+    globals()[_name] = _C.matmul
+
+TILE_CONFIGS = {0: (64, 64), 1: (128, 64), 2: (256, 64), 3: (128, 128), 4: (256, 128), 5: (256, 256)}
+
+__all__ = [
+    "matmul", "matmul_adaptive", "matmul_tiled", "gemm", "gemm_inplace", "gemm_adaptive",
+    "flash_attention", "prepack_int4", "unprepack_int4", "unpack_int4", "matmul_int4",
+    "gemm_plan", "TILE_CONFIGS", "LIBRARY_PATH", "HEADER_PATH", *_REFERENCE_VARIANTS,
+]

@@ -1,0 +1,122 @@
+"""Build the gfx950 C-ABI library and the PyTorch extension in-tree.
+
+    python -m wmma_ops_amd.build            # or wmma_ops_amd.build.build()
+
+Outputs (inside the package directory, next to this file):
+    libwmma_ops_amd.so                      HIP kernels + C-ABI (include/wmma_ops_amd.h)
+    _C.cpython-*.so                         pybind/torch layer, links the library above
+
+Only hipcc (for *.hip, --offload-arch=gfx950) and the host C++ compiler are used; no
+JIT cache, so the built files travel with the source tree.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+import sysconfig
+from concurrent.futures import ThreadPoolExecutor
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+BUILD = os.path.join(ROOT, "_build")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+ARCH = "gfx950"
+
+LIB_NAME = "libwmma_ops_amd.so"
+EXT_NAME = "_C" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so")
+
+HIP_SOURCES = ["capi.hip", "gemm.hip", "w4a16.hip", "flash_fwd.hip"]
+HOST_SOURCES = ["plan.cpp"]
+
+HIP_FLAGS = [
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    f"--offload-arch={ARCH}",
+    # No packed-FP32 VALU instructions anywhere in this library's device code.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(
+        l for l in res.stdout.splitlines()
+        if "packed-fp32-ops" not in l and "unknown target feature" not in l.lower()
+    )
+    if res.returncode != 0:
+        raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{out}")
+    if verbose and out.strip():
+        print(out)
+
+
+def build_library(verbose: bool = False) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    jobs = []
+    objs = []
+    for src in HIP_SOURCES:
+        obj = os.path.join(BUILD, src + ".o")
+        objs.append(obj)
+        jobs.append([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+    for src in HOST_SOURCES:
+        obj = os.path.join(BUILD, src + ".o")
+        objs.append(obj)
+        jobs.append(["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-c",
+                     os.path.join(CSRC, src), "-o", obj])
+    with ThreadPoolExecutor(max_workers=min(len(jobs), 8)) as ex:
+        list(ex.map(lambda c: _run(c, verbose), jobs))
+    lib = os.path.join(PKG, LIB_NAME)
+    tmp = lib + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
+    os.replace(tmp, lib)
+    return lib
+
+
+def build_extension(verbose: bool = False) -> str:
+    import torch
+    from torch.utils import cpp_extension as ce
+
+    try:
+        incs = ce.include_paths(device_type="cuda")
+        libdirs = ce.library_paths(device_type="cuda")
+    except TypeError:  # older signature
+        incs = ce.include_paths(True)
+        libdirs = ce.library_paths(True)
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    py_inc = sysconfig.get_paths()["include"]
+    out = os.path.join(PKG, EXT_NAME)
+    tmp = out + ".tmp"
+    cmd = [
+        "g++", "-O2", "-std=c++17", "-fPIC", "-shared",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        "-DTORCH_EXTENSION_NAME=_C", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        # HIP runtime headers used by torch's HIP stream API target the AMD platform.
+        "-D__HIP_PLATFORM_AMD__=1",
+        "-Wno-deprecated-declarations",
+        *[f"-I{p}" for p in incs], f"-I{py_inc}",
+        os.path.join(CSRC, "torch_ext.cpp"),
+        *[f"-L{p}" for p in libdirs], f"-L{PKG}",
+        "-lwmma_ops_amd", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip",
+        "-ltorch_python", f"-L{ROCM}/lib", "-lamdhip64",
+        "-Wl,-rpath,$ORIGIN",
+        "-o", tmp,
+    ]
+    _run(cmd, verbose)
+    os.replace(tmp, out)
+    return out
+
+
+def build(verbose: bool = False) -> None:
+    build_library(verbose)
+    build_extension(verbose)
+
+
+if __name__ == "__main__":
+    build(verbose="-v" in sys.argv)
+    print("built", os.path.join(PKG, LIB_NAME), os.path.join(PKG, EXT_NAME))

@@ -1,0 +1,276 @@
+// C-ABI entry points (declared in include/wmma_ops_amd.h).
+//
+// Each entry point validates every argument first -- shapes, pointers, leading
+// dimensions, alignment, workspace -- and only then enqueues kernels on the caller's
+// stream.  Nothing here allocates or synchronises.  Errors are reported as a status
+// code plus a per-thread message (wmma_last_error).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+#include <string>
+
+#include "kernels.hpp"
+#include "plan.hpp"
+
+using namespace wmma_amd;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int ok() {
+    g_last_error.clear();
+    return WMMA_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return ok();
+    return fail(WMMA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr int kMaxDevices = 64;
+int g_cu_count[kMaxDevices];
+std::once_flag g_cu_once[kMaxDevices];
+
+int current_cus() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    return wmma_device_cu_count(dev);
+}
+
+// Largest byte offset a buffer-resource load may use (offsets are 32-bit, and
+// 0x80000000 and above mark masked lanes).
+constexpr int64_t kMaxOffset = 0x7fffffffLL;
+
+}  // namespace
+
+extern "C" {
+
+const char* wmma_last_error(void) { return g_last_error.c_str(); }
+
+int wmma_abi_version(void) { return WMMA_OPS_AMD_ABI_VERSION; }
+
+int wmma_device_cu_count(int device) {
+    if (device < 0 || device >= kMaxDevices) return 256;
+    std::call_once(g_cu_once[device], [device] {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        g_cu_count[device] = n;
+    });
+    return g_cu_count[device];
+}
+
+int wmma_gemm_plan_make(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* out) {
+    if (!out) return fail(WMMA_ERR_INVALID_ARG, "plan output pointer is NULL");
+    if (M < 0 || N < 0 || K < 0) return fail(WMMA_ERR_INVALID_ARG, "negative GEMM dimension");
+    if (tile_cfg < WMMA_TILE_AUTO || tile_cfg >= WMMA_TILE_COUNT)
+        return fail(WMMA_ERR_INVALID_ARG,
+                    "Invalid tile_config: 0=64x64, 1=128x64, 2=256x64, 3=128x128, 4=256x128, "
+                    "5=256x256");
+    int rc = make_plan(M, N, K, tile_cfg, num_cus, out);
+    return rc == WMMA_OK ? ok() : fail(rc, "planner rejected the shape");
+}
+
+size_t wmma_gemm_workspace_size(int M, int N, int K, int tile_cfg) {
+    wmma_gemm_plan p{};
+    if (make_plan(M, N, K, tile_cfg, current_cus(), &p) != WMMA_OK) return 0;
+    return p.workspace_bytes;
+}
+
+int wmma_gemm_f16f32(const void* A, int64_t lda, const void* B, int64_t ldb, const float* C_in,
+                     int64_t ldc_in, float* C_out, int64_t ldc, int M, int N, int K, float alpha,
+                     float beta, int tile_cfg, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+    if (M < 0 || N < 0 || K < 0) return fail(WMMA_ERR_INVALID_ARG, "negative GEMM dimension");
+    if (tile_cfg < WMMA_TILE_AUTO || tile_cfg >= WMMA_TILE_COUNT)
+        return fail(WMMA_ERR_INVALID_ARG,
+                    "Invalid tile_config: 0=64x64, 1=128x64, 2=256x64, 3=128x128, 4=256x128, "
+                    "5=256x256");
+    if (M == 0 || N == 0) return ok();  // empty output
+    if (!C_out) return fail(WMMA_ERR_INVALID_ARG, "C_out is NULL");
+    if (ldc < N) return fail(WMMA_ERR_INVALID_ARG, "ldc (%lld) < N (%d)", (long long)ldc, N);
+    const bool use_c = beta != 0.0f && C_in != nullptr;
+    if (use_c && ldc_in < N)
+        return fail(WMMA_ERR_INVALID_ARG, "ldc_in (%lld) < N (%d)", (long long)ldc_in, N);
+    if (K > 0) {
+        if (!A || !B) return fail(WMMA_ERR_INVALID_ARG, "A or B is NULL");
+        if (lda < K) return fail(WMMA_ERR_INVALID_ARG, "lda (%lld) < K (%d)", (long long)lda, K);
+        if (ldb < N) return fail(WMMA_ERR_INVALID_ARG, "ldb (%lld) < N (%d)", (long long)ldb, N);
+        // 32-bit buffer offsets: one 256-row A tile and one 64-row B stage must fit.
+        if ((256 + 1) * lda * 2 > kMaxOffset || (64 + 1) * ldb * 2 > kMaxOffset ||
+            (int64_t)kSkinnyMaxM * lda * 2 > kMaxOffset)
+            return fail(WMMA_ERR_UNSUPPORTED, "leading dimension too large for 32-bit offsets");
+    }
+    wmma_gemm_plan plan{};
+    int rc = make_plan(M, N, K, tile_cfg, current_cus(), &plan);
+    if (rc != WMMA_OK) return fail(rc, "planner rejected the shape");
+    if (plan.workspace_bytes > 0) {
+        if (!workspace)
+            return fail(WMMA_ERR_WORKSPACE, "split-K needs a workspace of %zu bytes",
+                        plan.workspace_bytes);
+        if (workspace_bytes < plan.workspace_bytes)
+            return fail(WMMA_ERR_WORKSPACE, "workspace too small: %zu < %zu bytes", workspace_bytes,
+                        plan.workspace_bytes);
+        if ((reinterpret_cast<uintptr_t>(workspace) & 3u) != 0)
+            return fail(WMMA_ERR_MISALIGNED, "workspace must be 4-byte aligned");
+    }
+    GemmLaunch g{};
+    g.A = A;
+    g.B = B;
+    g.C_in = use_c ? C_in : nullptr;
+    g.C_out = C_out;
+    g.workspace = workspace;
+    g.lda = lda;
+    g.ldb = ldb;
+    g.ldc_in = ldc_in;
+    g.ldc = ldc;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.alpha = alpha;
+    g.beta = beta;
+    g.vec = K > 0 && (K % 8 == 0) && (N % 8 == 0) && (lda % 8 == 0) && (ldb % 8 == 0) &&
+            aligned16(A) && aligned16(B);
+    g.plan = plan;
+    return hip_status(launch_gemm(g, static_cast<hipStream_t>(stream)), "gemm launch");
+}
+
+// ------------------------------------------------------------------------------ INT4 --
+static int check_int4_shape(int K, int N) {
+    if (K <= 0 || N <= 0) return fail(WMMA_ERR_INVALID_ARG, "K and N must be positive");
+    if (K % 64 != 0) return fail(WMMA_ERR_UNSUPPORTED, "K (%d) must be a multiple of 64", K);
+    if (N % 32 != 0) return fail(WMMA_ERR_UNSUPPORTED, "N (%d) must be a multiple of 32", N);
+    return WMMA_OK;
+}
+
+int wmma_int4_prepack(const int32_t* qweight, int K, int N, int32_t* packed, void* stream) {
+    if (int rc = check_int4_shape(K, N)) return rc;
+    if (!qweight || !packed) return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
+    if (!aligned16(packed)) return fail(WMMA_ERR_MISALIGNED, "packed output must be 16-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(qweight) & 3u) != 0)
+        return fail(WMMA_ERR_MISALIGNED, "qweight must be 4-byte aligned");
+    return hip_status(launch_int4_prepack(qweight, K, N, packed, static_cast<hipStream_t>(stream)),
+                      "int4 prepack launch");
+}
+
+int wmma_int4_unprepack(const int32_t* packed, int K, int N, int32_t* qweight, void* stream) {
+    if (int rc = check_int4_shape(K, N)) return rc;
+    if (!qweight || !packed) return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
+    if (!aligned16(packed)) return fail(WMMA_ERR_MISALIGNED, "packed input must be 16-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(qweight) & 3u) != 0)
+        return fail(WMMA_ERR_MISALIGNED, "qweight must be 4-byte aligned");
+    return hip_status(
+        launch_int4_unprepack(packed, K, N, qweight, static_cast<hipStream_t>(stream)),
+        "int4 unprepack launch");
+}
+
+int wmma_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q, void* stream) {
+    if (K <= 0 || N <= 0 || K % 8 != 0)
+        return fail(WMMA_ERR_INVALID_ARG, "K must be a positive multiple of 8 and N positive");
+    if (!qweight || !q) return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
+    if ((reinterpret_cast<uintptr_t>(qweight) & 3u) != 0)
+        return fail(WMMA_ERR_MISALIGNED, "qweight must be 4-byte aligned");
+    return hip_status(launch_int4_unpack(qweight, K, N, q, static_cast<hipStream_t>(stream)),
+                      "int4 unpack launch");
+}
+
+size_t wmma_w4a16_workspace_size(int M, int N, int K, int group_size) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0 || group_size <= 0) return 0;
+    int split = 1, kps = K;
+    bool mfma = false;
+    w4a16_plan(M, N, K, group_size, current_cus(), &split, &kps, &mfma);
+    return split > 1 ? (size_t)split * M * N * sizeof(float) : 0;
+}
+
+int wmma_w4a16_gemm(const void* A, int64_t lda, const int32_t* packed, const void* scales,
+                    const void* zeros, int zeros_format, int M, int N, int K, int group_size,
+                    float* Y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
+    if (M < 0) return fail(WMMA_ERR_INVALID_ARG, "M must be non-negative");
+    if (int rc = check_int4_shape(K, N)) return rc;
+    if (group_size <= 0 || group_size % 32 != 0 || K % group_size != 0)
+        return fail(WMMA_ERR_UNSUPPORTED,
+                    "group_size (%d) must be a positive multiple of 32 dividing K (%d)", group_size,
+                    K);
+    if (zeros_format != WMMA_ZEROS_PACKED && zeros_format != WMMA_ZEROS_U8)
+        return fail(WMMA_ERR_INVALID_ARG, "unknown zeros format %d", zeros_format);
+    if (M == 0) return ok();
+    if (!A || !packed || !scales || !zeros || !Y) return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
+    if (lda < K || ldy < N) return fail(WMMA_ERR_INVALID_ARG, "leading dimension too small");
+    if (!aligned16(A) || lda % 8 != 0)
+        return fail(WMMA_ERR_MISALIGNED, "A must be 16-byte aligned with lda a multiple of 8");
+    if (!aligned16(packed)) return fail(WMMA_ERR_MISALIGNED, "packed weights must be 16-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(scales) & 1u) != 0)
+        return fail(WMMA_ERR_MISALIGNED, "scales must be 2-byte aligned");
+    if (zeros_format == WMMA_ZEROS_PACKED && (reinterpret_cast<uintptr_t>(zeros) & 3u) != 0)
+        return fail(WMMA_ERR_MISALIGNED, "packed zeros must be 4-byte aligned");
+    if ((int64_t)M * lda * 2 > kMaxOffset)
+        return fail(WMMA_ERR_UNSUPPORTED, "activation matrix too large for 32-bit offsets");
+    W4A16Launch w{};
+    w4a16_plan(M, N, K, group_size, current_cus(), &w.split, &w.k_per_split, &w.mfma);
+    const size_t need = w.split > 1 ? (size_t)w.split * M * N * sizeof(float) : 0;
+    if (need > 0 && (!workspace || workspace_bytes < need))
+        return fail(WMMA_ERR_WORKSPACE, "W4A16 split-K needs a workspace of %zu bytes", need);
+    w.A = A;
+    w.lda = lda;
+    w.packed = packed;
+    w.scales = scales;
+    w.zeros = zeros;
+    w.zeros_format = zeros_format;
+    w.M = M;
+    w.N = N;
+    w.K = K;
+    w.G = group_size;
+    w.Y = Y;
+    w.ldy = ldy;
+    w.workspace = workspace;
+    return hip_status(launch_w4a16(w, static_cast<hipStream_t>(stream)), "w4a16 launch");
+}
+
+// ----------------------------------------------------------------------------- flash --
+int wmma_flash_attn_fwd(const void* Q, const void* K, const void* V, void* O, int B, int H,
+                        int Sq, int Sk, int D, float scale, int causal, void* stream) {
+    if (B < 0 || H < 0 || Sq < 0 || Sk < 0) return fail(WMMA_ERR_INVALID_ARG, "negative dimension");
+    if (D != 64 && D != 128) return fail(WMMA_ERR_UNSUPPORTED, "head_dim %d (supported: 64, 128)", D);
+    if (!(scale > 0.0f) || !std::isfinite(scale))
+        return fail(WMMA_ERR_INVALID_ARG, "scale must be positive and finite");
+    if (B == 0 || H == 0 || Sq == 0) return ok();
+    if (Sk == 0) return fail(WMMA_ERR_INVALID_ARG, "Sk must be positive when Sq > 0");
+    if (!Q || !K || !V || !O) return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
+    if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O))
+        return fail(WMMA_ERR_MISALIGNED, "Q, K, V and O must be 16-byte aligned");
+    if ((int64_t)Sq * D * 2 > kMaxOffset || (int64_t)Sk * D * 2 > kMaxOffset)
+        return fail(WMMA_ERR_UNSUPPORTED, "sequence too long for 32-bit offsets");
+    if ((int64_t)B * H > 2147483647LL) return fail(WMMA_ERR_UNSUPPORTED, "too many heads");
+    FlashLaunch f{};
+    f.Q = Q;
+    f.K = K;
+    f.V = V;
+    f.O = O;
+    f.B = B;
+    f.H = H;
+    f.Sq = Sq;
+    f.Sk = Sk;
+    f.D = D;
+    f.scale = scale;
+    f.causal = causal != 0;
+    return hip_status(launch_flash_fwd(f, static_cast<hipStream_t>(stream)), "flash launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,116 @@
+// Device-side building blocks shared by every gfx950 kernel in this library.
+//
+// Everything here is CDNA4-specific: 64-lane wavefronts, MFMA matrix instructions,
+// buffer-resource loads whose hardware range check supplies zero-fill for masked lanes,
+// and the workgroup-to-XCD placement of a 256-CU, 8-XCD part.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wmma_amd {
+
+typedef _Float16 f16;
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kNumXcd = 8;
+
+// Offset that lies outside every buffer resource built below: a masked lane loads 0.
+constexpr uint32_t kOobOffset = 0x80000000u;
+// num_records for resources whose validity is expressed per lane through kOobOffset.
+constexpr int32_t kRecordsAll = 0x7fffffff;
+// Third descriptor word for gfx9-family raw buffers (byte-addressed, no stride).
+constexpr int32_t kRsrcFlags = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base,
+                                                            int32_t records = kRecordsAll) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, records,
+                                             kRsrcFlags);
+}
+
+// 16-byte load through a buffer resource; offset kOobOffset yields zeros.
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
+}
+__device__ __forceinline__ u32x2 buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0);
+}
+__device__ __forceinline__ uint16_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, byte_off, 0, 0);
+}
+
+// v_mfma_f32_32x32x16_f16: D(32x32 fp32) += A(32x16) * B(16x32).
+// Lane l supplies row l%32 of A and column l%32 of B, eight K values each (the K half is
+// selected by l/32; A and B use the same K assignment, so any consistent permutation of
+// K within a lane is harmless).  D: lane l holds column l%32, element r holds row
+// 8*(r/4) + 4*(l/32) + r%4.
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+// v_mfma_f32_16x16x32_f16: D(16x16) += A(16x32) * B(32x16).  Lane l supplies row l%16
+// of A / column l%16 of B with eight K values (K quarter l/16).  D: lane l holds column
+// l%16, element r holds row 4*(l/16) + r.
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f16x8 as_f16x8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
+__device__ __forceinline__ u32x4 as_u32x4(f16x8 v) { return __builtin_bit_cast(u32x4, v); }
+
+// v_perm_b32 selectors: pack the low (resp. high) 16-bit halves of two words, first
+// argument's half in the high half of the result.
+constexpr uint32_t kPermLo = 0x05040100u;
+constexpr uint32_t kPermHi = 0x07060302u;
+
+// Transpose an 8x8 block of 16-bit values held as 8 rows of 16 bytes: out[c] holds
+// column c (eight values, row 0 lowest).  32 v_perm_b32.
+__device__ __forceinline__ void transpose8x8(const u32x4 in[8], u32x4 out[8]) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const uint32_t sel = (c & 1) ? kPermHi : kPermLo;
+        const int w = c >> 1;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            out[c][d] = __builtin_amdgcn_perm(in[2 * d + 1][w], in[2 * d][w], sel);
+        }
+    }
+}
+
+// LDS chunk swizzle for 128-byte rows of eight 16-byte chunks.  Eight consecutive rows
+// read at one chunk position land on eight distinct chunks (conflict-free 16-byte
+// reads), and rows 8 apart also differ, so the transposing B store (rows 8*i + j) is
+// conflict-free as well.
+__device__ __forceinline__ int swz8(int row) { return (row ^ (row >> 3)) & 7; }
+
+// Workgroups are dispatched to the 8 XCDs round-robin (id % 8).  Re-map the linear id
+// so that each XCD receives a contiguous run of tile ids: the tiles sharing one XCD's
+// 4 MB L2 are then neighbours in the grouped order below.
+__device__ __forceinline__ int xcd_remap(int pid, int total) {
+    if (total % kNumXcd != 0) return pid;
+    const int per = total / kNumXcd;
+    return (pid % kNumXcd) * per + pid / kNumXcd;
+}
+
+// Grouped tile order: walk `group` tile rows at a time, column-major inside the group,
+// so consecutive ids share A rows and B columns.
+__device__ __forceinline__ void grouped_tile(int pid, int tiles_m, int tiles_n, int group,
+                                             int* tm, int* tn) {
+    const int per_group = group * tiles_n;
+    const int g = pid / per_group;
+    const int first_m = g * group;
+    const int gsize = min(tiles_m - first_m, group);
+    const int in = pid - g * per_group;
+    *tm = first_m + in % gsize;
+    *tn = in / gsize;
+}
+
+}  // namespace wmma_amd

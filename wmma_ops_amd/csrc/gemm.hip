@@ -1,0 +1,443 @@
+// FP16 x FP16 -> FP32 GEMM kernels for gfx950 (MI355X).
+//
+//   C_out = alpha * A[M,K] @ B[K,N] + beta * C_in        (A, B row-major fp16; C fp32)
+//
+// Three kernels:
+//  * gemm_tiled_kernel   -- MFMA 32x32x16 tiled GEMM.  One workgroup owns a BMxBN output
+//                           tile; 64-deep K stages are double-buffered in LDS.  A tiles
+//                           are copied as 16-byte row chunks; B tiles are transposed in
+//                           registers (8x8 blocks, v_perm) on their way into LDS so that
+//                           both MFMA operands are read as K-contiguous 16-byte chunks.
+//                           LDS rows are XOR-swizzled (swz8) against bank conflicts.
+//                           Workgroup ids are re-mapped per XCD and walked in grouped
+//                           order so each XCD's L2 sees neighbouring tiles.
+//  * gemm_skinny_kernel  -- M <= 16.  Streams B once from HBM with coalesced 16-byte
+//                           loads, computes C^T = B^T A^T with MFMA 16x16x32 so the wide
+//                           N dimension fills the matrix rows, reduces its four waves'
+//                           K slices in LDS.
+//  * splitk_reduce_kernel-- sums split-K partials in a fixed order and applies the
+//                           alpha/beta epilogue (reading C_in once).
+//
+// Reference semantics followed: the epilogue r = alpha*acc; if (beta != 0 && C_in)
+// r += beta*C_in (wmma_gemm.hip:636-666); in-place when C_in == C_out
+// (wmma_gemm.hip:1988-1991) -- each output element is read and then written by the same
+// thread, and no pointer here is declared __restrict__.  Split-K partitions K into
+// k_per_split ranges (wmma_xor_swizzle.hpp:293-332) and reduces with a separate kernel
+// (wmma_xor_swizzle.hpp:334-353).
+#include "common.hpp"
+#include "kernels.hpp"
+#include "plan.hpp"
+
+namespace wmma_amd {
+
+namespace {
+
+constexpr int BK = kBlockK;  // 64
+
+struct GemmArgs {
+    const f16* A;
+    const f16* B;
+    const float* Cin;
+    float* Cout;
+    float* ws;  // split-K partials [split][M][N] (dense), used when split > 1
+    int64_t lda, ldb, ldcin, ldc;
+    int M, N, K;
+    float alpha, beta;
+    int tiles_m, tiles_n;
+    int k_per_split;
+    int split;
+};
+
+// ------------------------------------------------------------------------------------
+// Tiled MFMA kernel
+// ------------------------------------------------------------------------------------
+template <int BM, int BN, int WM, int WN, bool VEC>
+__global__ void __launch_bounds__(WM * WN * kWave)
+gemm_tiled_kernel(GemmArgs p) {
+    constexpr int NT = WM * WN * kWave;
+    constexpr int TM = BM / WM, TN = BN / WN;  // wave tile
+    constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 MFMA tiles per wave
+    constexpr int A_CH = BM * 8;               // 16-byte chunks of one A stage
+    constexpr int B_CH = BN * 8;               // 16-byte chunks of one B^T stage
+    constexpr int STAGE = A_CH + B_CH;
+    constexpr int A_PER = A_CH / NT;           // A chunks per thread
+    constexpr int B_BLK = BN;                  // 8x8 blocks per B stage: (BK/8)*(BN/8)
+    constexpr int B_PER = (B_BLK + NT - 1) / NT;
+    static_assert(A_CH % NT == 0, "A stage must split evenly over threads");
+    static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32");
+
+    __shared__ u32x4 smem[2 * STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+
+    const int tiles = p.tiles_m * p.tiles_n;
+    int tm, tn;
+    grouped_tile(xcd_remap(blockIdx.x, tiles), p.tiles_m, p.tiles_n, 4, &tm, &tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int kbeg = blockIdx.y * p.k_per_split;
+    const int kend = min(p.K, kbeg + p.k_per_split);
+    const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+
+    const int M = p.M, N = p.N;
+    const int64_t lda = p.lda, ldb = p.ldb;
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
+
+    u32x4 ra[A_PER];
+    u32x4 rb[B_PER][8];
+
+    // Global -> registers for the stage starting at k0.
+    auto gload = [&](int k0) {
+        const __amdgpu_buffer_rsrc_t ra_rs = make_rsrc(p.A + (int64_t)m0 * lda + k0);
+        const __amdgpu_buffer_rsrc_t rb_rs = make_rsrc(p.B + (int64_t)k0 * ldb + n0);
+#pragma unroll
+        for (int i = 0; i < A_PER; ++i) {
+            const int v = tid + i * NT;
+            const int r = v >> 3, c = v & 7;
+            const bool row_ok = m0 + r < M;
+            if constexpr (VEC) {
+                const bool ok = row_ok && (k0 + c * 8 < kend);
+                ra[i] = buf_load16(ra_rs, ok ? (uint32_t)((r * lda + c * 8) * 2) : kOobOffset);
+            } else {
+                u32x4 v4;
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const int k = k0 + c * 8 + e;
+                    uint32_t lo = buf_load2(ra_rs, row_ok && k < kend
+                                                       ? (uint32_t)((r * lda + c * 8 + e) * 2)
+                                                       : kOobOffset);
+                    uint32_t hi = buf_load2(ra_rs, row_ok && k + 1 < kend
+                                                       ? (uint32_t)((r * lda + c * 8 + e + 1) * 2)
+                                                       : kOobOffset);
+                    v4[e >> 1] = lo | (hi << 16);
+                }
+                ra[i] = v4;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < B_PER; ++i) {
+            const int b = tid + i * NT;
+            const int kb = b / (BN / 8), nb = b % (BN / 8);
+            if (B_PER * NT == B_BLK || b < B_BLK) {
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    const int k = k0 + kb * 8 + r;
+                    if constexpr (VEC) {
+                        const bool ok = (k < kend) && (n0 + nb * 8 < N);
+                        rb[i][r] = buf_load16(
+                            rb_rs, ok ? (uint32_t)(((kb * 8 + r) * ldb + nb * 8) * 2) : kOobOffset);
+                    } else {
+                        u32x4 v4;
+#pragma unroll
+                        for (int e = 0; e < 8; e += 2) {
+                            const int n = n0 + nb * 8 + e;
+                            uint32_t lo = buf_load2(
+                                rb_rs, (k < kend && n < N)
+                                           ? (uint32_t)(((kb * 8 + r) * ldb + nb * 8 + e) * 2)
+                                           : kOobOffset);
+                            uint32_t hi = buf_load2(
+                                rb_rs, (k < kend && n + 1 < N)
+                                           ? (uint32_t)(((kb * 8 + r) * ldb + nb * 8 + e + 1) * 2)
+                                           : kOobOffset);
+                            v4[e >> 1] = lo | (hi << 16);
+                        }
+                        rb[i][r] = v4;
+                    }
+                }
+            }
+        }
+    };
+
+    // Registers -> LDS stage `buf`.  A rows keep K contiguous; B is stored transposed
+    // (row = n, K contiguous).
+    auto sstore = [&](int buf) {
+        u32x4* s = smem + buf * STAGE;
+#pragma unroll
+        for (int i = 0; i < A_PER; ++i) {
+            const int v = tid + i * NT;
+            const int r = v >> 3, c = v & 7;
+            s[r * 8 + (c ^ swz8(r))] = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < B_PER; ++i) {
+            const int b = tid + i * NT;
+            const int kb = b / (BN / 8), nb = b % (BN / 8);
+            if (B_PER * NT == B_BLK || b < B_BLK) {
+                u32x4 t[8];
+                transpose8x8(rb[i], t);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int n = nb * 8 + j;
+                    s[A_CH + n * 8 + (kb ^ swz8(n))] = t[j];
+                }
+            }
+        }
+    };
+
+    auto compute = [&](int buf) {
+        const u32x4* s = smem + buf * STAGE;
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            const int ch = ks * 2 + (lane >> 5);
+            f16x8 af[FM], bf[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const int r = wm * TM + i * 32 + (lane & 31);
+                af[i] = as_f16x8(s[r * 8 + (ch ^ swz8(r))]);
+            }
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int n = wn * TN + j * 32 + (lane & 31);
+                bf[j] = as_f16x8(s[A_CH + n * 8 + (ch ^ swz8(n))]);
+            }
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(af[i], bf[j], acc[i][j]);
+        }
+    };
+
+    if (nk > 0) {
+        gload(kbeg);
+        sstore(0);
+    }
+    __syncthreads();
+    for (int it = 0; it < nk; ++it) {
+        const int cur = it & 1;
+        const bool more = it + 1 < nk;
+        if (more) gload(kbeg + (it + 1) * BK);
+        compute(cur);
+        if (more) sstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue.  D layout: lane column lane%32, element r -> row 8*(r/4)+4*(lane/32)+r%4.
+    const bool partial = p.split > 1;
+    float* out = partial ? p.ws + (size_t)blockIdx.y * (size_t)M * (size_t)N : p.Cout;
+    const int64_t ldo = partial ? (int64_t)N : p.ldc;
+    const bool use_c = !partial && p.beta != 0.0f && p.Cin != nullptr;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int col = n0 + wn * TN + j * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm * TM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (row < M && col < N) {
+                    float v = acc[i][j][r];
+                    if (!partial) {
+                        v = p.alpha * v;
+                        if (use_c) v += p.beta * p.Cin[(int64_t)row * p.ldcin + col];
+                    }
+                    out[(int64_t)row * ldo + col] = v;
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------
+// Skinny kernel (M <= 16): C^T[N,M] = B^T[N,K] A^T[K,M] on MFMA 16x16x32.
+// Workgroup: 4 waves, 128 output columns, K range [kbeg,kend) split round-robin over the
+// waves in 32-deep steps.  Lane l loads B rows k0+8*(l/16)+0..7 at columns
+// 8*(l%16)+0..7 (16 lanes read 256 contiguous bytes per row), transposes the 8x8 block
+// in registers, and issues 8 MFMAs: MFMA j covers columns 8*i+j (i = matrix row l%16).
+// ------------------------------------------------------------------------------------
+constexpr int SK_COLS = kSkinnyBlockN;
+constexpr int SK_WAVES = 4;
+
+template <bool VEC>
+__global__ void __launch_bounds__(SK_WAVES * kWave)
+gemm_skinny_kernel(GemmArgs p) {
+    __shared__ float red[SK_WAVES][kSkinnyMaxM][SK_COLS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int q = lane >> 4;   // K quarter
+    const int c16 = lane & 15;
+    const int n0 = blockIdx.x * SK_COLS;
+    const int kbeg = blockIdx.y * p.k_per_split;
+    const int kend = min(p.K, kbeg + p.k_per_split);
+    const int M = p.M, N = p.N;
+
+    f32x4 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = f32x4{};
+
+    const __amdgpu_buffer_rsrc_t a_rs = make_rsrc(p.A);
+    const bool m_ok = c16 < M;
+    const int ncol = n0 + 8 * c16;
+
+    for (int k0 = kbeg + wave * 32; k0 < kend; k0 += SK_WAVES * 32) {
+        const __amdgpu_buffer_rsrc_t b_rs = make_rsrc(p.B + (int64_t)k0 * p.ldb + n0);
+        u32x4 rb[8];
+        u32x4 av;
+        const int ka = k0 + 8 * q;
+        if constexpr (VEC) {
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                const bool ok = (ka + r < kend) && (ncol < N);
+                rb[r] = buf_load16(b_rs, ok ? (uint32_t)(((8 * q + r) * p.ldb + 8 * c16) * 2)
+                                            : kOobOffset);
+            }
+            const bool ok = m_ok && ka < kend;
+            av = buf_load16(a_rs, ok ? (uint32_t)((c16 * p.lda + ka) * 2) : kOobOffset);
+        } else {
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                u32x4 v4;
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const bool k_ok = ka + r < kend;
+                    uint32_t lo = buf_load2(b_rs, (k_ok && ncol + e < N)
+                                                      ? (uint32_t)(((8 * q + r) * p.ldb + 8 * c16 + e) * 2)
+                                                      : kOobOffset);
+                    uint32_t hi = buf_load2(b_rs, (k_ok && ncol + e + 1 < N)
+                                                      ? (uint32_t)(((8 * q + r) * p.ldb + 8 * c16 + e + 1) * 2)
+                                                      : kOobOffset);
+                    v4[e >> 1] = lo | (hi << 16);
+                }
+                rb[r] = v4;
+            }
+            u32x4 v4;
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                uint32_t lo = buf_load2(a_rs, (m_ok && ka + e < kend)
+                                                  ? (uint32_t)((c16 * p.lda + ka + e) * 2)
+                                                  : kOobOffset);
+                uint32_t hi = buf_load2(a_rs, (m_ok && ka + e + 1 < kend)
+                                                  ? (uint32_t)((c16 * p.lda + ka + e + 1) * 2)
+                                                  : kOobOffset);
+                v4[e >> 1] = lo | (hi << 16);
+            }
+            av = v4;
+        }
+        u32x4 bt[8];
+        transpose8x8(rb, bt);
+        const f16x8 a8 = as_f16x8(av);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = mfma16(as_f16x8(bt[j]), a8, acc[j]);
+    }
+
+    // D of MFMA j: lane holds m = lane%16, rows 4*(lane/16)+r -> column 8*(4q+r)+j.
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][c16][8 * (4 * q + r) + j] = acc[j][r];
+    __syncthreads();
+
+    const bool partial = p.split > 1;
+    float* out = partial ? p.ws + (size_t)blockIdx.y * (size_t)M * (size_t)N : p.Cout;
+    const int64_t ldo = partial ? (int64_t)N : p.ldc;
+    const bool use_c = !partial && p.beta != 0.0f && p.Cin != nullptr;
+    for (int idx = tid; idx < kSkinnyMaxM * SK_COLS; idx += SK_WAVES * kWave) {
+        const int m = idx / SK_COLS, n = idx % SK_COLS;
+        if (m < M && n0 + n < N) {
+            float v = red[0][m][n];
+#pragma unroll
+            for (int w = 1; w < SK_WAVES; ++w) v += red[w][m][n];
+            if (!partial) {
+                v = p.alpha * v;
+                if (use_c) v += p.beta * p.Cin[(int64_t)m * p.ldcin + n0 + n];
+            }
+            out[(int64_t)m * ldo + n0 + n] = v;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------
+// Split-K reduction + epilogue: out = alpha * sum_s ws[s] (+ beta * C_in).
+// ------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+splitk_reduce_kernel(const float* ws, int split, const float* Cin, int64_t ldcin, float* Cout,
+                     int64_t ldc, int M, int N, float alpha, float beta) {
+    const int64_t total = (int64_t)M * N;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const bool use_c = beta != 0.0f && Cin != nullptr;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const int64_t row = i / N, col = i % N;
+        float v = ws[i];
+        for (int s = 1; s < split; ++s) v += ws[(int64_t)s * total + i];
+        v = alpha * v;
+        if (use_c) v += beta * Cin[row * ldcin + col];
+        Cout[row * ldc + col] = v;
+    }
+}
+
+template <int CFG, bool VEC>
+void launch_tiled(const GemmArgs& a, hipStream_t stream) {
+    constexpr TileShape t = kTiles[CFG];
+    dim3 grid(a.tiles_m * a.tiles_n, a.split);
+    hipLaunchKernelGGL((gemm_tiled_kernel<t.bm, t.bn, t.wm, t.wn, VEC>), grid,
+                       dim3(t.wm * t.wn * kWave), 0, stream, a);
+}
+
+template <bool VEC>
+void launch_tiled_cfg(int cfg, const GemmArgs& a, hipStream_t stream) {
+    switch (cfg) {
+        case 0: launch_tiled<0, VEC>(a, stream); break;
+        case 1: launch_tiled<1, VEC>(a, stream); break;
+        case 2: launch_tiled<2, VEC>(a, stream); break;
+        case 3: launch_tiled<3, VEC>(a, stream); break;
+        case 4: launch_tiled<4, VEC>(a, stream); break;
+        default: launch_tiled<5, VEC>(a, stream); break;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_gemm(const GemmLaunch& g, hipStream_t stream) {
+    const wmma_gemm_plan& pl = g.plan;
+    GemmArgs a{};
+    a.A = static_cast<const f16*>(g.A);
+    a.B = static_cast<const f16*>(g.B);
+    a.Cin = g.C_in;
+    a.Cout = g.C_out;
+    a.ws = static_cast<float*>(g.workspace);
+    a.lda = g.lda;
+    a.ldb = g.ldb;
+    a.ldcin = g.ldc_in;
+    a.ldc = g.ldc;
+    a.M = g.M;
+    a.N = g.N;
+    a.K = g.K;
+    a.alpha = g.alpha;
+    a.beta = g.beta;
+    a.k_per_split = pl.k_per_split > 0 ? pl.k_per_split : 1;
+    a.split = pl.split_k;
+    a.tiles_m = ceil_div(g.M, pl.tile_m);
+    a.tiles_n = ceil_div(g.N, pl.tile_n);
+
+    if (pl.kernel == WMMA_KERNEL_SKINNY) {
+        dim3 grid(ceil_div(g.N, SK_COLS), pl.split_k);
+        if (g.vec)
+            hipLaunchKernelGGL(gemm_skinny_kernel<true>, grid, dim3(SK_WAVES * kWave), 0, stream, a);
+        else
+            hipLaunchKernelGGL(gemm_skinny_kernel<false>, grid, dim3(SK_WAVES * kWave), 0, stream, a);
+    } else {
+        if (g.vec)
+            launch_tiled_cfg<true>(pl.tile_cfg, a, stream);
+        else
+            launch_tiled_cfg<false>(pl.tile_cfg, a, stream);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || pl.split_k <= 1) return e;
+
+    const int64_t total = (int64_t)g.M * g.N;
+    int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream,
+                       static_cast<const float*>(g.workspace), pl.split_k, g.C_in, g.ldc_in,
+                       g.C_out, g.ldc, g.M, g.N, g.alpha, g.beta);
+    return hipGetLastError();
+}
+
+}  // namespace wmma_amd

@@ -1,0 +1,66 @@
+// Internal launch interface between the C-ABI layer (capi.hip) and the kernel files.
+// Every launcher only enqueues work on `stream`; argument checking happens in capi.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/wmma_ops_amd.h"
+
+namespace wmma_amd {
+
+struct GemmLaunch {
+    const void* A;
+    const void* B;
+    const float* C_in;
+    float* C_out;
+    void* workspace;
+    int64_t lda, ldb, ldc_in, ldc;
+    int M, N, K;
+    float alpha, beta;
+    bool vec;  // 16-byte vector path: K, N, lda, ldb multiples of 8, A and B 16-byte aligned
+    wmma_gemm_plan plan;
+};
+hipError_t launch_gemm(const GemmLaunch& g, hipStream_t stream);
+
+// INT4 weight layout conversions (w4a16.hip).
+hipError_t launch_int4_prepack(const int32_t* qweight, int K, int N, int32_t* packed,
+                               hipStream_t stream);
+hipError_t launch_int4_unprepack(const int32_t* packed, int K, int N, int32_t* qweight,
+                                 hipStream_t stream);
+hipError_t launch_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q,
+                              hipStream_t stream);
+
+struct W4A16Launch {
+    const void* A;
+    int64_t lda;
+    const int32_t* packed;
+    const void* scales;
+    const void* zeros;
+    int zeros_format;
+    int M, N, K, G;
+    float* Y;
+    int64_t ldy;
+    void* workspace;
+    int split;        // K partitions (1: no workspace)
+    int k_per_split;  // multiple of 64 and of G when split > 1
+    bool mfma;        // MFMA path for larger M
+};
+hipError_t launch_w4a16(const W4A16Launch& w, hipStream_t stream);
+// Planner for the W4A16 kernels (host-only).
+void w4a16_plan(int M, int N, int K, int G, int num_cus, int* split, int* k_per_split,
+                bool* mfma);
+
+struct FlashLaunch {
+    const void* Q;
+    const void* K;
+    const void* V;
+    void* O;
+    int B, H, Sq, Sk, D;
+    float scale;
+    bool causal;
+};
+hipError_t launch_flash_fwd(const FlashLaunch& f, hipStream_t stream);
+
+}  // namespace wmma_amd

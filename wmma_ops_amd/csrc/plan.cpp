@@ -1,0 +1,94 @@
+// Host-only GEMM planner.  Chooses the kernel family, tile and split-K partition.
+//
+// The reference picks a tile from gfx1151-tuned thresholds (select_optimal_tile,
+// wmma_tile_selection.hpp:30-66) and has an unreachable split-K config
+// (compute_config, wmma_xor_swizzle.hpp:293-332: target tiles = 4 x CUs, split capped at
+// 32 and at K/256, k_per_split = ceil(K/split)).  Here the choice is made against a
+// 256-CU device: fill the chip with whole waves of workgroups, prefer the tile that
+// reuses the most bytes per LDS byte, and split K only when too few output tiles exist
+// to occupy the CUs.  The result never depends on the plan beyond fp32 summation order.
+#include "plan.hpp"
+
+#include <algorithm>
+
+namespace wmma_amd {
+
+static void finish_split(int M, int N, int K, int tiles, int split, wmma_gemm_plan* p) {
+    // k_per_split is a whole number of 64-deep stages so that every split but the last
+    // is full; the split count is then recomputed so no split is empty.
+    int kps = ceil_div(ceil_div(K, split), kBlockK) * kBlockK;
+    if (kps < kBlockK) kps = kBlockK;
+    split = std::max(1, ceil_div(K, kps));
+    p->split_k = split;
+    p->k_per_split = split > 1 ? kps : std::max(K, 0);
+    p->grid = tiles * split;
+    p->workspace_bytes = split > 1 ? (size_t)split * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+int make_plan(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* out) {
+    if (!out || M < 0 || N < 0 || K < 0) return WMMA_ERR_INVALID_ARG;
+    if (tile_cfg < WMMA_TILE_AUTO || tile_cfg >= WMMA_TILE_COUNT) return WMMA_ERR_INVALID_ARG;
+    if (num_cus <= 0) num_cus = 256;
+    wmma_gemm_plan p{};
+
+    if (tile_cfg != WMMA_TILE_AUTO) {
+        // Explicit tile (matmul_tiled): exactly that tile, no split.
+        const TileShape& t = kTiles[tile_cfg];
+        p.kernel = WMMA_KERNEL_TILED;
+        p.tile_cfg = tile_cfg;
+        p.tile_m = t.bm;
+        p.tile_n = t.bn;
+        int tiles = ceil_div(M, t.bm) * ceil_div(N, t.bn);
+        finish_split(M, N, K, tiles, 1, &p);
+        *out = p;
+        return WMMA_OK;
+    }
+
+    if (M <= kSkinnyMaxM && M > 0 && N > 0 && K > 0) {
+        // Streaming kernel: each workgroup owns kSkinnyBlockN columns and one K range;
+        // split K until the chip holds about two workgroups per CU.
+        p.kernel = WMMA_KERNEL_SKINNY;
+        p.tile_cfg = -1;
+        p.tile_m = kSkinnyMaxM;
+        p.tile_n = kSkinnyBlockN;
+        int tiles = ceil_div(N, kSkinnyBlockN);
+        int want = std::max(1, (2 * num_cus + tiles - 1) / tiles);
+        int split = std::min({want, std::max(1, K / 256), kMaxSplitK});
+        finish_split(M, N, K, tiles, split, &p);
+        *out = p;
+        return WMMA_OK;
+    }
+
+    // Tiled MFMA kernel: rank tiles by estimated time = waves of workgroups x tile area
+    // / tile efficiency.  A wave of workgroups is num_cus of them (one per CU).
+    const int order[] = {WMMA_TILE_256x256, WMMA_TILE_256x128, WMMA_TILE_128x128,
+                         WMMA_TILE_128x64, WMMA_TILE_64x64};
+    int best = WMMA_TILE_64x64;
+    double best_cost = 1e300;
+    for (int cfg : order) {
+        const TileShape& t = kTiles[cfg];
+        int64_t tiles = (int64_t)ceil_div(std::max(M, 1), t.bm) * ceil_div(std::max(N, 1), t.bn);
+        int64_t waves = ceil_div64(tiles, num_cus);
+        double cost = (double)waves * t.bm * t.bn / kTileEff[cfg];
+        if (cost < best_cost * 0.999) {
+            best_cost = cost;
+            best = cfg;
+        }
+    }
+    const TileShape& t = kTiles[best];
+    p.kernel = WMMA_KERNEL_TILED;
+    p.tile_cfg = best;
+    p.tile_m = t.bm;
+    p.tile_n = t.bn;
+    int tiles = ceil_div(M, t.bm) * ceil_div(N, t.bn);
+    int split = 1;
+    if (tiles > 0 && tiles * 2 <= num_cus && K >= 512) {
+        split = std::min({num_cus / tiles, K / 256, kMaxSplitK});
+        split = std::max(split, 1);
+    }
+    finish_split(M, N, K, tiles, split, &p);
+    *out = p;
+    return WMMA_OK;
+}
+
+}  // namespace wmma_amd

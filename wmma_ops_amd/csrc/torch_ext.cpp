@@ -1,0 +1,321 @@
+// PyTorch-ROCm extension: the reference's Python API on top of the C-ABI.
+//
+// Mirrors the pybind module of the reference (wmma_gemm.hip:2120-2157): the same
+// function names, argument meaning, defaults and TORCH_CHECK messages
+// (wmma_gemm.hip:1197-1263, 1432-1528, 1891-2078).  Tensors are validated here, made
+// contiguous, outputs come from the caching allocator, and the work is enqueued on the
+// current HIP stream of A's device through the C-ABI in include/wmma_ops_amd.h.  Unlike
+// the reference a device guard is taken, so the launch goes to the tensors' device.
+//
+// Additions the reference lacks: flash_attention (documented at README.md:221-251 but
+// never bound), the INT4 entry points (prepack_int4, unpack_int4, unprepack_int4,
+// matmul_int4), and the split-K workspace, which is taken from the caching allocator.
+#include <torch/extension.h>
+
+#include <c10/hip/HIPStream.h>
+#include <c10/hip/HIPGuard.h>
+
+#include <cmath>
+#include <string>
+
+#include "../../include/wmma_ops_amd.h"
+
+namespace {
+
+void check_status(int rc, const char* what) {
+    TORCH_CHECK(rc == WMMA_OK, what, " failed (status ", rc, "): ", wmma_last_error());
+}
+
+void* current_stream(const torch::Tensor& t) {
+    return static_cast<void*>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
+}
+
+// Shared checks of A and B (wmma_gemm.hip:1198-1212).
+void check_ab(const torch::Tensor& A, const torch::Tensor& B, bool same_device_check) {
+    TORCH_CHECK(A.is_cuda() && B.is_cuda(), "Inputs must be CUDA tensors");
+    if (same_device_check) TORCH_CHECK(A.device() == B.device(), "Inputs must be on same device");
+    TORCH_CHECK(A.dtype() == torch::kFloat16 && B.dtype() == torch::kFloat16,
+                "Inputs must be float16");
+    TORCH_CHECK(A.dim() == 2 && B.dim() == 2, "Inputs must be 2D");
+    TORCH_CHECK(A.size(1) == B.size(0), "Inner dimensions must match");
+}
+
+void check_aligned(const torch::Tensor& t, const char* msg) {
+    TORCH_CHECK((reinterpret_cast<uintptr_t>(t.data_ptr()) % 16) == 0, msg);
+}
+
+torch::Tensor workspace_for(size_t bytes, const torch::Tensor& like) {
+    if (bytes == 0) return torch::Tensor();
+    return torch::empty({(int64_t)bytes}, torch::dtype(torch::kUInt8).device(like.device()));
+}
+
+// One GEMM through the C-ABI.  C_in may be undefined; C_out preallocated.
+void run_gemm(const torch::Tensor& A, const torch::Tensor& B, const torch::Tensor& C_in,
+              torch::Tensor& C_out, double alpha, double beta, int tile_cfg) {
+    const int M = (int)A.size(0), K = (int)A.size(1), N = (int)B.size(1);
+    TORCH_CHECK(A.size(0) <= INT32_MAX && A.size(1) <= INT32_MAX && B.size(1) <= INT32_MAX,
+                "dimensions exceed int32");
+    const size_t ws_bytes = wmma_gemm_workspace_size(M, N, K, tile_cfg);
+    torch::Tensor ws = workspace_for(ws_bytes, A);
+    const float* cin = C_in.defined() ? C_in.data_ptr<float>() : nullptr;
+    const int64_t ldcin = C_in.defined() ? C_in.stride(0) : N;
+    int rc = wmma_gemm_f16f32(A.data_ptr(), A.stride(0), B.data_ptr(), B.stride(0), cin, ldcin,
+                              C_out.data_ptr<float>(), C_out.stride(0), M, N, K,
+                              static_cast<float>(alpha), static_cast<float>(beta), tile_cfg,
+                              ws.defined() ? ws.data_ptr() : nullptr, ws_bytes, current_stream(A));
+    check_status(rc, "wmma_gemm_f16f32");
+}
+
+torch::Tensor matmul_impl(torch::Tensor A, torch::Tensor B, int tile_cfg, bool same_device) {
+    check_ab(A, B, same_device);
+    const c10::hip::HIPGuard guard(A.device());
+    A = A.contiguous();
+    B = B.contiguous();
+    check_aligned(A, "A must be 16-byte aligned for vectorized loads");
+    check_aligned(B, "B must be 16-byte aligned for vectorized loads");
+    auto C = torch::empty({A.size(0), B.size(1)}, torch::dtype(torch::kFloat32).device(A.device()));
+    run_gemm(A, B, torch::Tensor(), C, 1.0, 0.0, tile_cfg);
+    return C;
+}
+
+// matmul (wmma_gemm.hip:1432-1470).  The tile is chosen by the planner.
+torch::Tensor matmul(torch::Tensor A, torch::Tensor B) {
+    return matmul_impl(A, B, WMMA_TILE_AUTO, true);
+}
+
+// matmul_adaptive (wmma_gemm.hip:1197-1263).
+torch::Tensor matmul_adaptive(torch::Tensor A, torch::Tensor B) {
+    return matmul_impl(A, B, WMMA_TILE_AUTO, true);
+}
+
+// matmul_tiled (wmma_gemm.hip:1473-1528): like the reference, no same-device check.
+torch::Tensor matmul_tiled(torch::Tensor A, torch::Tensor B, int64_t tile_config) {
+    TORCH_CHECK(A.is_cuda() && B.is_cuda(), "Inputs must be CUDA tensors");
+    TORCH_CHECK(A.dtype() == torch::kFloat16 && B.dtype() == torch::kFloat16,
+                "Inputs must be float16");
+    TORCH_CHECK(A.dim() == 2 && B.dim() == 2, "Inputs must be 2D");
+    TORCH_CHECK(A.size(1) == B.size(0), "Inner dimensions must match");
+    TORCH_CHECK(tile_config >= 0 && tile_config < WMMA_TILE_COUNT,
+                "Invalid tile_config: 0=64x64, 1=128x64, 2=256x64, 3=128x128, 4=256x128, "
+                "5=256x256");
+    return matmul_impl(A, B, (int)tile_config, false);
+}
+
+// gemm / gemm_adaptive (wmma_gemm.hip:1891-1945, 1997-2078): C is read only when
+// beta != 0 and C is given; beta != 0 without C is silently ignored, as in the reference.
+torch::Tensor gemm_impl(torch::Tensor A, torch::Tensor B, double alpha, double beta,
+                        c10::optional<torch::Tensor> C_opt) {
+    check_ab(A, B, true);
+    const c10::hip::HIPGuard guard(A.device());
+    A = A.contiguous();
+    B = B.contiguous();
+    check_aligned(A, "A must be 16-byte aligned");
+    check_aligned(B, "B must be 16-byte aligned");
+    const int64_t M = A.size(0), N = B.size(1);
+    torch::Tensor C_in;
+    if (beta != 0.0 && C_opt.has_value() && C_opt->defined()) {
+        C_in = C_opt.value();
+        TORCH_CHECK(C_in.is_cuda(), "C must be a CUDA tensor");
+        TORCH_CHECK(C_in.device() == A.device(), "C must be on same device as A and B");
+        TORCH_CHECK(C_in.dtype() == torch::kFloat32, "C must be float32");
+        TORCH_CHECK(C_in.dim() == 2, "C must be 2D");
+        TORCH_CHECK(C_in.size(0) == M && C_in.size(1) == N, "C dimensions must match output (M×N)");
+        C_in = C_in.contiguous();
+    }
+    auto C_out = torch::empty({M, N}, torch::dtype(torch::kFloat32).device(A.device()));
+    run_gemm(A, B, C_in, C_out, alpha, beta, WMMA_TILE_AUTO);
+    return C_out;
+}
+
+torch::Tensor gemm(torch::Tensor A, torch::Tensor B, double alpha, double beta,
+                   c10::optional<torch::Tensor> C) {
+    return gemm_impl(A, B, alpha, beta, C);
+}
+
+torch::Tensor gemm_adaptive(torch::Tensor A, torch::Tensor B, double alpha, double beta,
+                            c10::optional<torch::Tensor> C) {
+    return gemm_impl(A, B, alpha, beta, C);
+}
+
+// gemm_inplace (wmma_gemm.hip:1949-1994).  The reference silently updates a contiguous
+// copy when C is not contiguous (:1970); here a non-contiguous C is rejected instead, so
+// the caller's tensor is always the one written.
+void gemm_inplace(torch::Tensor A, torch::Tensor B, torch::Tensor C, double alpha, double beta) {
+    TORCH_CHECK(A.is_cuda() && B.is_cuda() && C.is_cuda(), "Inputs must be CUDA tensors");
+    TORCH_CHECK(A.device() == B.device() && A.device() == C.device(),
+                "All tensors must be on same device");
+    TORCH_CHECK(A.dtype() == torch::kFloat16 && B.dtype() == torch::kFloat16,
+                "A and B must be float16");
+    TORCH_CHECK(C.dtype() == torch::kFloat32, "C must be float32");
+    TORCH_CHECK(A.dim() == 2 && B.dim() == 2 && C.dim() == 2, "Inputs must be 2D");
+    TORCH_CHECK(A.size(1) == B.size(0), "Inner dimensions must match");
+    TORCH_CHECK(C.size(0) == A.size(0) && C.size(1) == B.size(1),
+                "C dimensions must match output (M×N)");
+    TORCH_CHECK(C.is_contiguous(), "C must be contiguous for in-place update");
+    const c10::hip::HIPGuard guard(A.device());
+    A = A.contiguous();
+    B = B.contiguous();
+    check_aligned(A, "A must be 16-byte aligned");
+    check_aligned(B, "B must be 16-byte aligned");
+    run_gemm(A, B, C, C, alpha, beta, WMMA_TILE_AUTO);
+}
+
+// flash_attention(Q, K, V, causal=False, scale=-1.0) (README.md:221-251): Q [B,H,Sq,D],
+// K/V [B,H,Sk,D] fp16; scale <= 0 selects 1/sqrt(D).  Returns fp16 [B,H,Sq,D].
+torch::Tensor flash_attention(torch::Tensor Q, torch::Tensor K, torch::Tensor V, bool causal,
+                              double scale) {
+    TORCH_CHECK(Q.is_cuda() && K.is_cuda() && V.is_cuda(), "Inputs must be CUDA tensors");
+    TORCH_CHECK(Q.device() == K.device() && Q.device() == V.device(),
+                "Inputs must be on same device");
+    TORCH_CHECK(Q.dtype() == torch::kFloat16 && K.dtype() == torch::kFloat16 &&
+                    V.dtype() == torch::kFloat16,
+                "Inputs must be float16");
+    TORCH_CHECK(Q.dim() == 4 && K.dim() == 4 && V.dim() == 4, "Inputs must be 4D [B, H, N, D]");
+    TORCH_CHECK(K.sizes() == V.sizes(), "K and V must have the same shape");
+    TORCH_CHECK(Q.size(0) == K.size(0) && Q.size(1) == K.size(1) && Q.size(3) == K.size(3),
+                "Q and K must agree in batch, heads and head_dim");
+    const int64_t D = Q.size(3);
+    TORCH_CHECK(D == 64 || D == 128, "head_dim must be 64 or 128");
+    const c10::hip::HIPGuard guard(Q.device());
+    Q = Q.contiguous();
+    K = K.contiguous();
+    V = V.contiguous();
+    const float sc = scale > 0.0 ? (float)scale : (float)(1.0 / std::sqrt((double)D));
+    auto O = torch::empty_like(Q);
+    int rc = wmma_flash_attn_fwd(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(),
+                                 (int)Q.size(0), (int)Q.size(1), (int)Q.size(2), (int)K.size(2),
+                                 (int)D, sc, causal ? 1 : 0, current_stream(Q));
+    check_status(rc, "wmma_flash_attn_fwd");
+    return O;
+}
+
+void check_qweight(const torch::Tensor& q) {
+    TORCH_CHECK(q.is_cuda(), "qweight must be a CUDA tensor");
+    TORCH_CHECK(q.dtype() == torch::kInt32, "qweight must be int32");
+    TORCH_CHECK(q.dim() == 2, "qweight must be 2D [K/8, N]");
+}
+
+// prepack_int4(qweight[K/8, N] int32, GPTQ order) -> prepacked int32 [N/32, K/64, 64, 4]
+// (returned flattened as [K/8, N] so it has the same element count and dtype).
+torch::Tensor prepack_int4(torch::Tensor qweight) {
+    check_qweight(qweight);
+    const c10::hip::HIPGuard guard(qweight.device());
+    qweight = qweight.contiguous();
+    const int K = (int)qweight.size(0) * 8, N = (int)qweight.size(1);
+    auto out = torch::empty_like(qweight);
+    check_status(wmma_int4_prepack(qweight.data_ptr<int32_t>(), K, N, out.data_ptr<int32_t>(),
+                                   current_stream(qweight)),
+                 "wmma_int4_prepack");
+    return out;
+}
+
+torch::Tensor unprepack_int4(torch::Tensor packed) {
+    check_qweight(packed);
+    const c10::hip::HIPGuard guard(packed.device());
+    packed = packed.contiguous();
+    const int K = (int)packed.size(0) * 8, N = (int)packed.size(1);
+    auto out = torch::empty_like(packed);
+    check_status(wmma_int4_unprepack(packed.data_ptr<int32_t>(), K, N, out.data_ptr<int32_t>(),
+                                     current_stream(packed)),
+                 "wmma_int4_unprepack");
+    return out;
+}
+
+// unpack_int4(qweight[K/8, N]) -> uint8 [K, N] of values 0..15.
+torch::Tensor unpack_int4(torch::Tensor qweight) {
+    check_qweight(qweight);
+    const c10::hip::HIPGuard guard(qweight.device());
+    qweight = qweight.contiguous();
+    const int K = (int)qweight.size(0) * 8, N = (int)qweight.size(1);
+    auto out = torch::empty({K, N}, torch::dtype(torch::kUInt8).device(qweight.device()));
+    check_status(wmma_int4_unpack(qweight.data_ptr<int32_t>(), K, N, out.data_ptr<uint8_t>(),
+                                  current_stream(qweight)),
+                 "wmma_int4_unpack");
+    return out;
+}
+
+// matmul_int4(A[M,K] fp16, packed (from prepack_int4), scales[K/G, N] fp16,
+//             zeros[K/G, N/8] int32 packed or [K/G, N] uint8, group_size=128) -> fp32 [M, N]
+torch::Tensor matmul_int4(torch::Tensor A, torch::Tensor packed, torch::Tensor scales,
+                          torch::Tensor zeros, int64_t group_size) {
+    TORCH_CHECK(A.is_cuda() && packed.is_cuda() && scales.is_cuda() && zeros.is_cuda(),
+                "Inputs must be CUDA tensors");
+    TORCH_CHECK(A.device() == packed.device() && A.device() == scales.device() &&
+                    A.device() == zeros.device(),
+                "Inputs must be on same device");
+    TORCH_CHECK(A.dtype() == torch::kFloat16, "A must be float16");
+    TORCH_CHECK(A.dim() == 2, "A must be 2D");
+    check_qweight(packed);
+    const int64_t K = packed.size(0) * 8, N = packed.size(1);
+    TORCH_CHECK(A.size(1) == K, "Inner dimensions must match");
+    TORCH_CHECK(group_size > 0 && K % group_size == 0, "group_size must divide K");
+    const int64_t ng = K / group_size;
+    TORCH_CHECK(scales.dtype() == torch::kFloat16 && scales.dim() == 2 && scales.size(0) == ng &&
+                    scales.size(1) == N,
+                "scales must be float16 [K/group_size, N]");
+    int zfmt;
+    if (zeros.dtype() == torch::kInt32) {
+        TORCH_CHECK(zeros.dim() == 2 && zeros.size(0) == ng && zeros.size(1) * 8 == N,
+                    "packed zeros must be int32 [K/group_size, N/8]");
+        zfmt = WMMA_ZEROS_PACKED;
+    } else {
+        TORCH_CHECK(zeros.dtype() == torch::kUInt8 && zeros.dim() == 2 && zeros.size(0) == ng &&
+                        zeros.size(1) == N,
+                    "zeros must be int32 [K/group_size, N/8] or uint8 [K/group_size, N]");
+        zfmt = WMMA_ZEROS_U8;
+    }
+    const c10::hip::HIPGuard guard(A.device());
+    A = A.contiguous();
+    packed = packed.contiguous();
+    scales = scales.contiguous();
+    zeros = zeros.contiguous();
+    check_aligned(A, "A must be 16-byte aligned");
+    const int M = (int)A.size(0);
+    auto Y = torch::empty({A.size(0), N}, torch::dtype(torch::kFloat32).device(A.device()));
+    const size_t ws_bytes = wmma_w4a16_workspace_size(M, (int)N, (int)K, (int)group_size);
+    torch::Tensor ws = workspace_for(ws_bytes, A);
+    int rc = wmma_w4a16_gemm(A.data_ptr(), A.stride(0), packed.data_ptr<int32_t>(),
+                             scales.data_ptr(), zeros.data_ptr(), zfmt, M, (int)N, (int)K,
+                             (int)group_size, Y.data_ptr<float>(), Y.stride(0),
+                             ws.defined() ? ws.data_ptr() : nullptr, ws_bytes, current_stream(A));
+    check_status(rc, "wmma_w4a16_gemm");
+    return Y;
+}
+
+// Planner introspection: (kernel, tile_cfg, tile_m, tile_n, split_k, k_per_split, grid,
+// workspace_bytes) for a shape on the current device.
+std::vector<int64_t> gemm_plan(int64_t M, int64_t N, int64_t K, int64_t tile_cfg, int64_t num_cus) {
+    wmma_gemm_plan p{};
+    check_status(wmma_gemm_plan_make((int)M, (int)N, (int)K, (int)tile_cfg, (int)num_cus, &p),
+                 "wmma_gemm_plan_make");
+    return {p.kernel, p.tile_cfg, p.tile_m, p.tile_n, p.split_k, p.k_per_split, p.grid,
+            (int64_t)p.workspace_bytes};
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    m.doc() = "MI355X (gfx950) MFMA implementation of the wmma_ops API";
+    m.def("matmul", &matmul, "MFMA GEMM (FP16->FP32), tile chosen by the planner");
+    m.def("matmul_adaptive", &matmul_adaptive, "MFMA GEMM with automatic tile / split-K choice");
+    m.def("matmul_tiled", &matmul_tiled,
+          "MFMA GEMM with a fixed tile: 0=64x64, 1=128x64, 2=256x64, 3=128x128, 4=256x128, 5=256x256");
+    m.def("gemm", &gemm, "BLAS-style GEMM: C = alpha * A @ B + beta * C", py::arg("A"), py::arg("B"),
+          py::arg("alpha") = 1.0, py::arg("beta") = 0.0, py::arg("C") = py::none());
+    m.def("gemm_inplace", &gemm_inplace, "In-place GEMM: C = alpha * A @ B + beta * C (modifies C)",
+          py::arg("A"), py::arg("B"), py::arg("C"), py::arg("alpha") = 1.0, py::arg("beta") = 0.0);
+    m.def("gemm_adaptive", &gemm_adaptive,
+          "Auto-tuned GEMM: C = alpha * A @ B + beta * C (planner-selected tile)", py::arg("A"),
+          py::arg("B"), py::arg("alpha") = 1.0, py::arg("beta") = 0.0, py::arg("C") = py::none());
+    m.def("flash_attention", &flash_attention, "Flash-attention forward (fp16 in/out, fp32 softmax)",
+          py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("causal") = false,
+          py::arg("scale") = -1.0);
+    m.def("prepack_int4", &prepack_int4, "GPTQ int4 qweight [K/8,N] -> MFMA layout", py::arg("qweight"));
+    m.def("unprepack_int4", &unprepack_int4, "Inverse of prepack_int4", py::arg("packed"));
+    m.def("unpack_int4", &unpack_int4, "GPTQ int4 qweight [K/8,N] -> uint8 [K,N]", py::arg("qweight"));
+    m.def("matmul_int4", &matmul_int4, "W4A16 dequant GEMM: fp16 A @ int4 W -> fp32",
+          py::arg("A"), py::arg("packed"), py::arg("scales"), py::arg("zeros"),
+          py::arg("group_size") = 128);
+    m.def("gemm_plan", &gemm_plan, "Planner decision for a GEMM shape", py::arg("M"), py::arg("N"),
+          py::arg("K"), py::arg("tile_cfg") = -1, py::arg("num_cus") = 256);
+}
