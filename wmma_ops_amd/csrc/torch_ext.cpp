@@ -12,8 +12,10 @@
 // matmul_int4), and the split-K workspace, which is taken from the caching allocator.
 #include <torch/extension.h>
 
-#include <c10/hip/HIPStream.h>
-#include <c10/hip/HIPGuard.h>
+// ROCm torch reports HIP devices as DeviceType::CUDA; its guard and stream helpers for
+// such devices are the "MasqueradingAsCUDA" variants.
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
 #include <cmath>
 #include <string>
@@ -27,7 +29,7 @@ void check_status(int rc, const char* what) {
 }
 
 void* current_stream(const torch::Tensor& t) {
-    return static_cast<void*>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
+    return static_cast<void*>(c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream());
 }
 
 // Shared checks of A and B (wmma_gemm.hip:1198-1212).
@@ -68,7 +70,7 @@ void run_gemm(const torch::Tensor& A, const torch::Tensor& B, const torch::Tenso
 
 torch::Tensor matmul_impl(torch::Tensor A, torch::Tensor B, int tile_cfg, bool same_device) {
     check_ab(A, B, same_device);
-    const c10::hip::HIPGuard guard(A.device());
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(A.device());
     A = A.contiguous();
     B = B.contiguous();
     check_aligned(A, "A must be 16-byte aligned for vectorized loads");
@@ -106,7 +108,7 @@ torch::Tensor matmul_tiled(torch::Tensor A, torch::Tensor B, int64_t tile_config
 torch::Tensor gemm_impl(torch::Tensor A, torch::Tensor B, double alpha, double beta,
                         c10::optional<torch::Tensor> C_opt) {
     check_ab(A, B, true);
-    const c10::hip::HIPGuard guard(A.device());
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(A.device());
     A = A.contiguous();
     B = B.contiguous();
     check_aligned(A, "A must be 16-byte aligned");
@@ -152,7 +154,7 @@ void gemm_inplace(torch::Tensor A, torch::Tensor B, torch::Tensor C, double alph
     TORCH_CHECK(C.size(0) == A.size(0) && C.size(1) == B.size(1),
                 "C dimensions must match output (M×N)");
     TORCH_CHECK(C.is_contiguous(), "C must be contiguous for in-place update");
-    const c10::hip::HIPGuard guard(A.device());
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(A.device());
     A = A.contiguous();
     B = B.contiguous();
     check_aligned(A, "A must be 16-byte aligned");
@@ -176,7 +178,7 @@ torch::Tensor flash_attention(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
                 "Q and K must agree in batch, heads and head_dim");
     const int64_t D = Q.size(3);
     TORCH_CHECK(D == 64 || D == 128, "head_dim must be 64 or 128");
-    const c10::hip::HIPGuard guard(Q.device());
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(Q.device());
     Q = Q.contiguous();
     K = K.contiguous();
     V = V.contiguous();
@@ -199,7 +201,7 @@ void check_qweight(const torch::Tensor& q) {
 // (returned flattened as [K/8, N] so it has the same element count and dtype).
 torch::Tensor prepack_int4(torch::Tensor qweight) {
     check_qweight(qweight);
-    const c10::hip::HIPGuard guard(qweight.device());
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(qweight.device());
     qweight = qweight.contiguous();
     const int K = (int)qweight.size(0) * 8, N = (int)qweight.size(1);
     auto out = torch::empty_like(qweight);
@@ -211,7 +213,7 @@ torch::Tensor prepack_int4(torch::Tensor qweight) {
 
 torch::Tensor unprepack_int4(torch::Tensor packed) {
     check_qweight(packed);
-    const c10::hip::HIPGuard guard(packed.device());
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(packed.device());
     packed = packed.contiguous();
     const int K = (int)packed.size(0) * 8, N = (int)packed.size(1);
     auto out = torch::empty_like(packed);
@@ -224,7 +226,7 @@ torch::Tensor unprepack_int4(torch::Tensor packed) {
 // unpack_int4(qweight[K/8, N]) -> uint8 [K, N] of values 0..15.
 torch::Tensor unpack_int4(torch::Tensor qweight) {
     check_qweight(qweight);
-    const c10::hip::HIPGuard guard(qweight.device());
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(qweight.device());
     qweight = qweight.contiguous();
     const int K = (int)qweight.size(0) * 8, N = (int)qweight.size(1);
     auto out = torch::empty({K, N}, torch::dtype(torch::kUInt8).device(qweight.device()));
@@ -264,7 +266,7 @@ torch::Tensor matmul_int4(torch::Tensor A, torch::Tensor packed, torch::Tensor s
                     "zeros must be int32 [K/group_size, N/8] or uint8 [K/group_size, N]");
         zfmt = WMMA_ZEROS_U8;
     }
-    const c10::hip::HIPGuard guard(A.device());
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(A.device());
     A = A.contiguous();
     packed = packed.contiguous();
     scales = scales.contiguous();
