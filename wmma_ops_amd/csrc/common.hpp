@@ -63,6 +63,36 @@ __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// ---- LDS access (address space 3) -------------------------------------------------------
+#define WMMA_LDS __attribute__((address_space(3)))
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Direct global -> LDS copy of 16 bytes per lane (buffer_load_dwordx4 ... lds).  The LDS
+// destination is `dst` (wave-uniform) + 16 * lane; lanes whose offset lies outside the
+// resource write zeros.  The copy is tracked by vmcnt, not by any VGPR.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off,
+                                          WMMA_LDS void* dst) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, byte_off, 0, 0, 0);
+}
+
+// ds_read_b64_tr_b16.  Inside each group of 16 lanes, the 8-byte rows the lanes address
+// form a 16x4 matrix R (row = source lane); lane i = 4a + b of the group receives
+// R[4j + a][b] for j = 0..3.  So when source lane 4j + a points at row k0 + j, columns
+// c0 + 4a .. c0 + 4a + 3 of a row-major 16-bit tile, lane i receives the column c0 + i,
+// rows k0 .. k0 + 3: a K-contiguous MFMA operand read out of N-contiguous storage.
+__device__ __forceinline__ f16x4 lds_read_tr16(const WMMA_LDS void* p) {
+    return __builtin_bit_cast(
+        f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((WMMA_LDS s16x4*)p));
+}
+
+// s_waitcnt on vmcnt only (expcnt and lgkmcnt left at their maxima).  gfx9 encoding:
+// vmcnt[3:0] in bits 3:0 and vmcnt[5:4] in bits 15:14.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 __device__ __forceinline__ f16x8 as_f16x8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
 __device__ __forceinline__ u32x4 as_u32x4(f16x8 v) { return __builtin_bit_cast(u32x4, v); }
 

@@ -2,15 +2,20 @@
 //
 //   C_out = alpha * A[M,K] @ B[K,N] + beta * C_in        (A, B row-major fp16; C fp32)
 //
-// Three kernels:
-//  * gemm_tiled_kernel   -- MFMA 32x32x16 tiled GEMM.  One workgroup owns a BMxBN output
-//                           tile; 64-deep K stages are double-buffered in LDS.  A tiles
-//                           are copied as 16-byte row chunks; B tiles are transposed in
-//                           registers (8x8 blocks, v_perm) on their way into LDS so that
-//                           both MFMA operands are read as K-contiguous 16-byte chunks.
-//                           LDS rows are XOR-swizzled (swz8) against bank conflicts.
-//                           Workgroup ids are re-mapped per XCD and walked in grouped
-//                           order so each XCD's L2 sees neighbouring tiles.
+// Kernels:
+//  * gemm_mfma_kernel    -- the main path (A, B 16-byte aligned; K, N, lda, ldb multiples
+//                           of 8).  MFMA 32x32x16 on K-stages that travel global -> LDS by
+//                           buffer_load ... lds DMA (no VGPR staging) into an NS-deep LDS
+//                           ring.  A fragments are read with ds_read_b128, B fragments with
+//                           the gfx950 transposing read ds_read_b64_tr_b16 straight out of
+//                           row-major [K][N] storage.  One barrier per stage, placed before
+//                           the stage's last k-step so the next stage's first fragments are
+//                           read while the last MFMAs of this one run.  Workgroup ids are
+//                           re-mapped per XCD and walked in grouped order so each XCD's L2
+//                           sees neighbouring tiles.
+//  * gemm_tiled_kernel   -- generic path for unaligned shapes (any M, N, K): element-wise
+//                           masked loads, B transposed in registers (8x8 blocks, v_perm) on
+//                           its way into a double-buffered LDS stage.
 //  * gemm_skinny_kernel  -- M <= 16.  Streams B once from HBM with coalesced 16-byte
 //                           loads, computes C^T = B^T A^T with MFMA 16x16x32 so the wide
 //                           N dimension fills the matrix rows, reduces its four waves'
@@ -47,6 +52,307 @@ struct GemmArgs {
     int k_per_split;
     int split;
 };
+
+// ------------------------------------------------------------------------------------
+// LDS-DMA MFMA kernel (A and B 16-byte aligned, K and N multiples of 8)
+//
+// One workgroup owns a BMxBN output tile and walks its K range in BK-deep stages held in
+// an NS-deep LDS ring.  Every 16-byte chunk of a stage travels global -> LDS by
+// buffer_load ... lds: no VGPR staging, no transpose instructions.  Lanes of one DMA
+// instruction write 1 KB of LDS contiguously, so the swizzled LDS layout is produced by
+// choosing which global chunk each lane fetches.  Out-of-range chunks (M, N and K tails)
+// come back as zeros from the buffer range check.
+//   A stage: [BM][BK] fp16, rows of KCH 16-byte chunks, chunk c of row r stored at
+//            c ^ swz_a(r).  Fragments: ds_read_b128 (row = lane%32, K half = lane/32).
+//   B stage: [BK][BN] fp16 (row-major as in memory), chunk c of row k stored at
+//            c ^ swz_b(k).  Fragments: two ds_read_b64_tr_b16 per 32x32x16 operand, which
+//            deliver column lane%32 with four consecutive K values each.
+// Both operands therefore present K-contiguous MFMA fragments with the same K order.
+// Wave (wm, wn) owns a TMxTN sub-tile of (TM/32)x(TN/32) 32x32 accumulators.
+// ------------------------------------------------------------------------------------
+template <int KCH>
+__device__ __forceinline__ int swz_a(int r) {
+    // Conflict-free for 16-byte reads of 16 consecutive rows (64 banks) and of 8
+    // consecutive rows (32 banks).
+    if constexpr (KCH == 8)
+        return (r ^ (r >> 3)) & 7;
+    else
+        return ((r >> 1) ^ (r >> 3)) & 3;
+}
+
+template <int BNC>
+__device__ __forceinline__ int swz_b(int k) {
+    // The transposing read touches four consecutive rows k..k+3 at one chunk pair; the
+    // XOR spreads them over distinct banks.
+    if constexpr (BNC >= 16)
+        return 4 * (k & 3);
+    else
+        return 2 * (k & 3);
+}
+
+// Per-lane constants of the LDS-DMA kernel.
+template <int A_DMA, int B_DMA, int FM, int FN>
+struct MfmaLane {
+    uint32_t a_off[A_DMA], b_off[B_DMA];  // DMA source offsets (kOobOffset when masked)
+    int a_k[A_DMA], b_k[B_DMA];           // K offset of each DMA chunk inside a stage
+    int a_addr[FM];                       // byte offset of the lane's A row in a stage
+    int a_sw[FM];                         // swizzle of that row
+    int b_addr[FN];                       // byte offset of the lane's first tr-read
+    int h;                                // lane / 32
+    int dma_a, dma_b;                     // this wave's DMA slice of a stage (uniform)
+};
+
+// Fragment reads of one 16-deep k-step of a stage (A via ds_read_b128, B via two
+// ds_read_b64_tr_b16 per 32x32x16 operand).
+template <int BN, int FM, int FN, class Lane>
+__device__ __forceinline__ void mfma_read(const WMMA_LDS unsigned char* s, const Lane& L, int ks,
+                                          f16x8 (&a)[FM], f16x8 (&b)[FN]) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int c = (2 * ks + L.h) ^ L.a_sw[i];
+        a[i] = as_f16x8(*(const WMMA_LDS u32x4*)(s + L.a_addr[i] + (c << 4)));
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const WMMA_LDS unsigned char* pb = s + L.b_addr[j] + ks * 16 * (BN * 2);
+        const f16x4 lo = lds_read_tr16(pb);
+        const f16x4 hi = lds_read_tr16(pb + 4 * (BN * 2));
+        b[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+}
+
+template <int FM, int FN>
+__device__ __forceinline__ void mfma_block(const f16x8 (&a)[FM], const f16x8 (&b)[FN],
+                                           f32x16 (&acc)[FM][FN]) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+}
+
+// Scheduling hint for one k-step: MF MFMAs interleaved one-for-one with RD LDS reads,
+// optionally preceded by `lead` VMEM (DMA) instructions spread over the first MFMAs.
+template <int MF, int RD, int DMA>
+__device__ __forceinline__ void mfma_sched() {
+    constexpr int X = RD < MF ? RD : MF;
+#pragma unroll
+    for (int x = 0; x < X; ++x) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if (x < DMA) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+    if constexpr (DMA > X) __builtin_amdgcn_sched_group_barrier(0x020, DMA - X, 0);
+    if constexpr (MF > X) __builtin_amdgcn_sched_group_barrier(0x008, MF - X, 0);
+    if constexpr (RD > X) __builtin_amdgcn_sched_group_barrier(0x100, RD - X, 0);
+}
+
+// One main-loop iteration of the LDS-DMA kernel (stage t):
+//   (a) k-steps 0..KS-2 of stage t, each interleaved with the reads of the next k-step;
+//   (b) this wave's DMA of stage t+1 complete (vmcnt), LDS reads drained, barrier: from
+//       here every wave's copy of stage t+1 is visible, and every wave has finished
+//       reading stage t-1;
+//   (c) DMA of stage t+NS-1 into the buffer stage t-1 used;
+//   (d) the last k-step of stage t, interleaved with the first reads of stage t+1.
+// The three buffers are distinct (NS >= 3), so they are passed as __restrict__
+// pointers: that lets the compiler keep the DMA in flight across the reads.  Ordering
+// between a DMA and later reads of the same buffer is the vmcnt wait + barrier of (b).
+template <int BM, int BN, int BK, int WM, int WN, int NS, int A_DMA, int B_DMA, class Lane>
+__device__ __forceinline__ void mfma_iter(const WMMA_LDS unsigned char* __restrict__ cur,
+                                          const WMMA_LDS unsigned char* __restrict__ nxt,
+                                          WMMA_LDS unsigned char* __restrict__ dma_dst,
+                                          const Lane& L, __amdgpu_buffer_rsrc_t ra,
+                                          __amdgpu_buffer_rsrc_t rb, int kleft,
+                                          f16x8 (&af)[2][BM / WM / 32], f16x8 (&bf)[2][BN / WN / 32],
+                                          f32x16 (&acc)[BM / WM / 32][BN / WN / 32]) {
+    constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
+    constexpr int KS = BK / 16;
+    constexpr int PER_STAGE = A_DMA + B_DMA;
+    constexpr int RD = FM + 2 * FN, MF = FM * FN;
+    static_assert(KS % 2 == 0, "fragment double buffer assumes an even k-step count");
+    // (a)
+#pragma unroll
+    for (int ks = 0; ks + 1 < KS; ++ks) {
+        mfma_read<BN>(cur, L, ks + 1, af[(ks + 1) & 1], bf[(ks + 1) & 1]);
+        mfma_block(af[ks & 1], bf[ks & 1], acc);
+        mfma_sched<MF, RD, 0>();
+    }
+    // (b)
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads are done
+    wait_vmcnt<(NS - 3) * PER_STAGE>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    // (c)
+    const bool full = kleft >= BK;
+#pragma unroll
+    for (int i = 0; i < A_DMA; ++i)
+        lds_dma16(ra, (full || L.a_k[i] < kleft) ? L.a_off[i] : kOobOffset,
+                  dma_dst + L.dma_a + i * 1024);
+#pragma unroll
+    for (int i = 0; i < B_DMA; ++i)
+        lds_dma16(rb, (full || L.b_k[i] < kleft) ? L.b_off[i] : kOobOffset,
+                  dma_dst + L.dma_b + i * 1024);
+    // (d)
+    mfma_read<BN>(nxt, L, 0, af[0], bf[0]);
+    mfma_block(af[1], bf[1], acc);
+    mfma_sched<MF, RD, PER_STAGE>();
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int NS>
+__global__ void __launch_bounds__(WM * WN * kWave)
+__attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
+gemm_mfma_kernel(GemmArgs p) {
+    constexpr int NW = WM * WN;
+    constexpr int TM = BM / WM, TN = BN / WN;
+    constexpr int FM = TM / 32, FN = TN / 32;
+    constexpr int KCH = BK / 8, BNC = BN / 8;
+    constexpr int A_BYTES = BM * BK * 2, B_BYTES = BK * BN * 2;
+    constexpr int STAGE = A_BYTES + B_BYTES;
+    constexpr int A_DMA = A_BYTES / (1024 * NW);  // 1 KB DMA instructions per wave
+    constexpr int B_DMA = B_BYTES / (1024 * NW);
+    constexpr int PER_STAGE = A_DMA + B_DMA;      // vmcnt increments per stage
+    static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "DMA split");
+    static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32");
+    static_assert(NS >= 3 && (NS - 2) * PER_STAGE < 64, "vmcnt range");
+
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * STAGE];
+    WMMA_LDS unsigned char* lds = (WMMA_LDS unsigned char*)smem;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+
+    const int tiles = p.tiles_m * p.tiles_n;
+    int tm, tn;
+    grouped_tile(xcd_remap(blockIdx.x, tiles), p.tiles_m, p.tiles_n, 4, &tm, &tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int kbeg = blockIdx.y * p.k_per_split;
+    const int kend = min(p.K, kbeg + p.k_per_split);
+    const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    const int M = p.M, N = p.N;
+    const int64_t lda = p.lda, ldb = p.ldb;
+
+    MfmaLane<A_DMA, B_DMA, FM, FN> L;
+#pragma unroll
+    for (int i = 0; i < A_DMA; ++i) {
+        const int P = 64 * (wave * A_DMA + i) + lane;
+        const int r = P / KCH, c = (P % KCH) ^ swz_a<KCH>(r);
+        L.a_off[i] = m0 + r < M ? (uint32_t)((r * lda + 8 * c) * 2) : kOobOffset;
+        L.a_k[i] = 8 * c;
+    }
+#pragma unroll
+    for (int i = 0; i < B_DMA; ++i) {
+        const int P = 64 * (wave * B_DMA + i) + lane;
+        const int k = P / BNC, c = (P % BNC) ^ swz_b<BNC>(k);
+        L.b_off[i] = n0 + 8 * c < N ? (uint32_t)((k * ldb + 8 * c) * 2) : kOobOffset;
+        L.b_k[i] = k;
+    }
+    L.h = lane >> 5;
+    L.dma_a = wave * (A_DMA * 1024);
+    L.dma_b = A_BYTES + wave * (B_DMA * 1024);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int r = wm * TM + i * 32 + (lane & 31);
+        L.a_addr[i] = r * (BK * 2);
+        L.a_sw[i] = swz_a<KCH>(r);
+    }
+    {
+        // tr-read source lane s = 4*jj + aa of 16-lane group g: row 8*(g/2) + jj (+4 for
+        // the upper half), columns 16*(g%2) + 4*aa .. +3 of the wave's 32-column tile.
+        const int g = lane >> 4, s16 = lane & 15, jj = s16 >> 2, aa = s16 & 3;
+        const int krow = 8 * (g >> 1) + jj;
+        const int sw = swz_b<BNC>(jj);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int n = wn * TN + j * 32 + 16 * (g & 1) + 4 * aa;
+            L.b_addr[j] = A_BYTES + krow * (BN * 2) + (((n >> 3) ^ sw) << 4) + ((n & 7) << 1);
+        }
+    }
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
+
+    const f16* Ablk = p.A + (int64_t)m0 * lda;
+    const f16* Bblk = p.B + n0;
+    auto rsrc_a = [&](int kt) { return make_rsrc(Ablk + kbeg + (int64_t)min(kt, nk - 1) * BK); };
+    auto rsrc_b = [&](int kt) {
+        return make_rsrc(Bblk + (int64_t)(kbeg + (int64_t)min(kt, nk - 1) * BK) * ldb);
+    };
+    auto kleft = [&](int kt) { return kt < nk ? kend - (kbeg + kt * BK) : 0; };
+
+    if (nk > 0) {
+        // Prologue: stages 0 .. NS-2 in flight (stages past the end load zeros), stage 0
+        // landed and visible, the first k-step of stage 0 read.
+#pragma unroll
+        for (int s = 0; s < NS - 1; ++s) {
+            WMMA_LDS unsigned char* dst = lds + s * STAGE;
+            const int kl = kleft(s);
+            const bool full = kl >= BK;
+            const __amdgpu_buffer_rsrc_t ra = rsrc_a(s), rb = rsrc_b(s);
+#pragma unroll
+            for (int i = 0; i < A_DMA; ++i)
+                lds_dma16(ra, (full || L.a_k[i] < kl) ? L.a_off[i] : kOobOffset,
+                          dst + L.dma_a + i * 1024);
+#pragma unroll
+            for (int i = 0; i < B_DMA; ++i)
+                lds_dma16(rb, (full || L.b_k[i] < kl) ? L.b_off[i] : kOobOffset,
+                          dst + L.dma_b + i * 1024);
+        }
+        wait_vmcnt<(NS - 2) * PER_STAGE>();
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        f16x8 af[2][FM], bf[2][FN];
+        mfma_read<BN>(lds, L, 0, af[0], bf[0]);
+
+        for (int t = 0; t < nk; ++t) {
+            const int tf = t + NS - 1;  // stage whose DMA is issued in this iteration
+            mfma_iter<BM, BN, BK, WM, WN, NS, A_DMA, B_DMA>(
+                lds + (t % NS) * STAGE, lds + ((t + 1) % NS) * STAGE, lds + (tf % NS) * STAGE, L,
+                rsrc_a(tf), rsrc_b(tf), kleft(tf), af, bf, acc);
+        }
+        wait_vmcnt<0>();
+    }
+
+    // Epilogue.  D layout: lane column lane%32, element r -> row 8*(r/4)+4*(lane/32)+r%4.
+    const bool partial = p.split > 1;
+    float* out = partial ? p.ws + (size_t)blockIdx.y * (size_t)M * (size_t)N : p.Cout;
+    const int64_t ldo = partial ? (int64_t)N : p.ldc;
+    const float alpha = partial ? 1.0f : p.alpha;
+    const bool use_c = !partial && p.beta != 0.0f && p.Cin != nullptr;
+    const int h = lane >> 5;
+    const int row0 = m0 + wm * TM + 4 * h, col0 = n0 + wn * TN + (lane & 31);
+    const bool full_tile = m0 + BM <= M && n0 + BN <= N;
+    if (full_tile && !use_c) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = row0 + i * 32 + 8 * (r >> 2) + (r & 3);
+                    out[(int64_t)row * ldo + col0 + j * 32] = alpha * acc[i][j][r];
+                }
+    } else {
+        const float beta = p.beta;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int col = col0 + j * 32;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = row0 + i * 32 + 8 * (r >> 2) + (r & 3);
+                    if (row < M && col < N) {
+                        float v = alpha * acc[i][j][r];
+                        if (use_c) v += beta * p.Cin[(int64_t)row * p.ldcin + col];
+                        out[(int64_t)row * ldo + col] = v;
+                    }
+                }
+            }
+    }
+}
 
 // ------------------------------------------------------------------------------------
 // Tiled MFMA kernel
@@ -393,6 +699,34 @@ void launch_tiled_cfg(int cfg, const GemmArgs& a, hipStream_t stream) {
     }
 }
 
+// LDS-DMA kernel: K depth of a stage and LDS ring depth per tile configuration, chosen
+// so that the ring fits the 160 KB of LDS of one CU.
+struct MfmaStages {
+    int bk, ns;
+};
+constexpr MfmaStages kMfmaStages[WMMA_TILE_COUNT] = {
+    {64, 4}, {64, 4}, {64, 3}, {64, 4}, {64, 3}, {32, 4}};
+
+template <int CFG>
+void launch_mfma(const GemmArgs& a, hipStream_t stream) {
+    constexpr TileShape t = kTiles[CFG];
+    constexpr MfmaStages st = kMfmaStages[CFG];
+    dim3 grid(a.tiles_m * a.tiles_n, a.split);
+    hipLaunchKernelGGL((gemm_mfma_kernel<t.bm, t.bn, st.bk, t.wm, t.wn, st.ns>), grid,
+                       dim3(t.wm * t.wn * kWave), 0, stream, a);
+}
+
+void launch_mfma_cfg(int cfg, const GemmArgs& a, hipStream_t stream) {
+    switch (cfg) {
+        case 0: launch_mfma<0>(a, stream); break;
+        case 1: launch_mfma<1>(a, stream); break;
+        case 2: launch_mfma<2>(a, stream); break;
+        case 3: launch_mfma<3>(a, stream); break;
+        case 4: launch_mfma<4>(a, stream); break;
+        default: launch_mfma<5>(a, stream); break;
+    }
+}
+
 }  // namespace
 
 hipError_t launch_gemm(const GemmLaunch& g, hipStream_t stream) {
@@ -425,7 +759,7 @@ hipError_t launch_gemm(const GemmLaunch& g, hipStream_t stream) {
             hipLaunchKernelGGL(gemm_skinny_kernel<false>, grid, dim3(SK_WAVES * kWave), 0, stream, a);
     } else {
         if (g.vec)
-            launch_tiled_cfg<true>(pl.tile_cfg, a, stream);
+            launch_mfma_cfg(pl.tile_cfg, a, stream);
         else
             launch_tiled_cfg<false>(pl.tile_cfg, a, stream);
     }

@@ -23,7 +23,7 @@ constexpr TileShape kTiles[WMMA_TILE_COUNT] = {
     {256, 64, 4, 1},   // 2: wave tile 64x64
     {128, 128, 2, 2},  // 3: wave tile 64x64
     {256, 128, 2, 2},  // 4: wave tile 128x64
-    {256, 256, 2, 2},  // 5: wave tile 128x128
+    {256, 256, 2, 4},  // 5: wave tile 128x64 (8 waves, two per SIMD)
 };
 
 constexpr int kBlockK = 64;        // K depth of one LDS stage (fp16: 128-byte rows)
