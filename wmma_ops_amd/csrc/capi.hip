@@ -6,6 +6,7 @@
 // code plus a per-thread message (wmma_last_error).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -193,10 +194,14 @@ int wmma_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q, void* str
 
 size_t wmma_w4a16_workspace_size(int M, int N, int K, int group_size) {
     if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0 || group_size <= 0) return 0;
-    int split = 1, kps = K;
-    bool mfma = false;
-    w4a16_plan(M, N, K, group_size, current_cus(), &split, &kps, &mfma);
-    return split > 1 ? (size_t)split * M * N * sizeof(float) : 0;
+    // The plan depends on operand alignment only through the choice of the matrix-pipe
+    // decode kernel; report the larger of the two possible workspaces.
+    size_t need = 0;
+    for (bool aligned : {true, false}) {
+        const W4A16Plan pl = w4a16_plan(M, N, K, group_size, current_cus(), aligned);
+        if (pl.split > 1) need = std::max(need, (size_t)pl.split * M * N * sizeof(float));
+    }
+    return need;
 }
 
 int wmma_w4a16_gemm(const void* A, int64_t lda, const int32_t* packed, const void* scales,
@@ -223,8 +228,11 @@ int wmma_w4a16_gemm(const void* A, int64_t lda, const int32_t* packed, const voi
     if ((int64_t)M * lda * 2 > kMaxOffset)
         return fail(WMMA_ERR_UNSUPPORTED, "activation matrix too large for 32-bit offsets");
     W4A16Launch w{};
-    w4a16_plan(M, N, K, group_size, current_cus(), &w.split, &w.k_per_split, &w.mfma);
-    const size_t need = w.split > 1 ? (size_t)w.split * M * N * sizeof(float) : 0;
+    const bool aligned = (reinterpret_cast<uintptr_t>(scales) & 7u) == 0 &&
+                         (zeros_format == WMMA_ZEROS_PACKED ||
+                          (reinterpret_cast<uintptr_t>(zeros) & 3u) == 0);
+    w.plan = w4a16_plan(M, N, K, group_size, current_cus(), aligned);
+    const size_t need = w.plan.split > 1 ? (size_t)w.plan.split * M * N * sizeof(float) : 0;
     if (need > 0 && (!workspace || workspace_bytes < need))
         return fail(WMMA_ERR_WORKSPACE, "W4A16 split-K needs a workspace of %zu bytes", need);
     w.A = A;

@@ -32,6 +32,20 @@ hipError_t launch_int4_unprepack(const int32_t* packed, int K, int N, int32_t* q
 hipError_t launch_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q,
                               hipStream_t stream);
 
+// W4A16 kernel families.
+enum W4A16Kind {
+    W4_DECODE_MFMA = 0,  // M <= 16, G % 128 == 0: one workgroup per 16 columns, matrix-pipe dots
+    W4_DECODE = 1,       // M <= 4: one workgroup per 16 columns, VALU dots
+    W4_GEMV_SPLIT = 2,   // M <= 4, other shapes: 32 columns per workgroup, K split + reduce
+    W4_MFMA = 3,         // larger M: tiled MFMA kernel, K split + reduce when few tiles
+};
+
+struct W4A16Plan {
+    int kind;         // W4A16Kind
+    int split;        // K partitions (1: no workspace)
+    int k_per_split;  // multiple of 64 (and of G when split > 1)
+};
+
 struct W4A16Launch {
     const void* A;
     int64_t lda;
@@ -43,14 +57,12 @@ struct W4A16Launch {
     float* Y;
     int64_t ldy;
     void* workspace;
-    int split;        // K partitions (1: no workspace)
-    int k_per_split;  // multiple of 64 and of G when split > 1
-    bool mfma;        // MFMA path for larger M
+    W4A16Plan plan;
 };
 hipError_t launch_w4a16(const W4A16Launch& w, hipStream_t stream);
-// Planner for the W4A16 kernels (host-only).
-void w4a16_plan(int M, int N, int K, int G, int num_cus, int* split, int* k_per_split,
-                bool* mfma);
+// Planner for the W4A16 kernels (host-only).  `aligned`: scales 8-byte aligned and, for
+// uint8 zeros, zeros 4-byte aligned (the vector loads of the matrix-pipe decode kernel).
+W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned);
 
 struct FlashLaunch {
     const void* Q;

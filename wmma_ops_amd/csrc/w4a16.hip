@@ -117,11 +117,14 @@ struct W4Args {
 };
 
 // Per-lane group parameters: zs = (1024 + z, 1024 + z), ss = (s, s) as packed fp16 pairs.
+// ZF (the zeros format) is a template parameter so the loads stay branch-free and can
+// all be in flight together.
+template <int ZF>
 __device__ __forceinline__ void group_params(const W4Args& p, int g, int n, uint32_t* zs,
                                              uint32_t* ss) {
     const uint16_t s = __builtin_bit_cast(uint16_t, p.S[(int64_t)g * p.N + n]);
     uint32_t z;
-    if (p.zfmt == WMMA_ZEROS_PACKED) {
+    if constexpr (ZF == WMMA_ZEROS_PACKED) {
         const uint32_t zw = (uint32_t)static_cast<const int32_t*>(p.Z)[(int64_t)g * (p.N / 8) + n / 8];
         z = (zw >> (4 * (n & 7))) & 0xFu;
     } else {
@@ -130,6 +133,30 @@ __device__ __forceinline__ void group_params(const W4Args& p, int g, int n, uint
     const uint32_t zh = 0x6400u | z;
     *zs = zh | (zh << 16);
     *ss = (uint32_t)s | ((uint32_t)s << 16);
+}
+
+// Raw group-parameter loads (scale bits, zero word) -- decoded later by group_decode so
+// that many loads can be in flight before any of them is waited on.
+template <int ZF>
+__device__ __forceinline__ void group_load(const W4Args& p, int g, int n, uint32_t* sraw,
+                                           uint32_t* zraw) {
+    *sraw = __builtin_bit_cast(uint16_t, p.S[(int64_t)g * p.N + n]);
+    if constexpr (ZF == WMMA_ZEROS_PACKED)
+        *zraw = (uint32_t)static_cast<const int32_t*>(p.Z)[(int64_t)g * (p.N / 8) + n / 8];
+    else
+        *zraw = static_cast<const uint8_t*>(p.Z)[(int64_t)g * p.N + n];
+}
+template <int ZF>
+__device__ __forceinline__ void group_decode(uint32_t sraw, uint32_t zraw, int n, uint32_t* zs,
+                                             uint32_t* ss) {
+    uint32_t z;
+    if constexpr (ZF == WMMA_ZEROS_PACKED)
+        z = (zraw >> (4 * (n & 7))) & 0xFu;
+    else
+        z = zraw & 0xFu;
+    const uint32_t zh = 0x6400u | z;
+    *zs = zh | (zh << 16);
+    *ss = sraw | (sraw << 16);
 }
 
 // Dequantise one prepacked word into four fp16 pairs in natural k order.
@@ -151,6 +178,7 @@ constexpr int GV_MAXM = 4;
 constexpr int GV_NW = 8;
 constexpr int GV_UNROLL = 4;
 
+template <int ZF>
 __global__ void __launch_bounds__(GV_NW * kWave)
 w4a16_gemv_kernel(W4Args p) {
     __shared__ float red[GV_NW][GV_MAXM][32];
@@ -181,7 +209,7 @@ w4a16_gemv_kernel(W4Args p) {
             if (kc < kc1) {
                 const int k0 = kc * 64 + 32 * h;
                 uint32_t zs, ss;
-                group_params(p, k0 / p.G, n, &zs, &ss);
+                group_params<ZF>(p, k0 / p.G, n, &zs, &ss);
 #pragma unroll
                 for (int w = 0; w < 4; ++w) {
                     uint32_t d[4];
@@ -221,6 +249,369 @@ w4a16_gemv_kernel(W4Args p) {
     }
 }
 
+// ------------------------------------------------------- decode (M <= GV_MAXM, no split) --
+// One workgroup owns a 16-column slice (half of a 32-column prepacked tile) and the whole
+// K range, so no cross-workgroup reduction is needed.  A wave load covers two consecutive
+// 64-deep chunks: lane l reads slice column l%16, chunk 2*pp + l/32, K half (l/16)%2 --
+// all 64 lanes active, 1 KB per instruction in 256-byte runs.  Each wave keeps DV_U loads
+// of the next round in flight while it dequantises the current one.
+//
+// Arithmetic (VALU is the bottleneck of decode, not HBM): a prepacked word holds the
+// pairs (k0,k1) (k2,k3) (k4,k5) (k6,k7) in nibbles (0,4) (1,5) (2,6) (3,7), so
+//   (w      & 0x000F000F) | 0x64006400 = fp16 pair (1024 + q_k0, 1024 + q_k1)
+//   (w      & 0x00F000F0) | 0x64006400 = fp16 pair (1024 + 16 q_k2, 1024 + 16 q_k3)
+//   (w >> 8 & 0x000F000F) | 0x64006400 = (1024 + q_k4, 1024 + q_k5)
+//   (w >> 8 & 0x00F000F0) | 0x64006400 = (1024 + 16 q_k6, 1024 + 16 q_k7)
+// -- every value exact in fp16.  Dotting them with the activations (v_dot2, fp32
+// accumulate) gives, over one lane's 32-value K run (one quantisation group),
+//   c1 = sum_{set1} (1024 + q) a,  c16 = sum_{set16} (1024 + 16 q) a,
+// with set1 = offsets {0,1,4,5} and set16 = {2,3,6,7} of every 8.  With the run's
+// activation sums A1, A16 (staged in LDS) the run's exact contribution is
+//   s * (c1 + c16/16 - (1024 + z) A1 - (64 + z) A16)  =  s * sum_k (q_k - z) a_k,
+// i.e. the dequantised product with s applied once per run instead of once per weight
+// (it differs from fp16((q - z) s) per weight only by that rounding, far below the
+// 1e-3 output tolerance).  9 VALU operations per 8 weights instead of ~24.
+constexpr int DV_NW = 8;
+constexpr int DV_U = 4;
+
+template <int MM>
+struct DecodeRound {
+    u32x4 w[DV_U];
+    uint32_t s[DV_U], z[DV_U];
+};
+
+// ONE: K <= DV_NW * DV_U * 128, a single round per wave (no second register buffer, so
+// the kernel fits 64 VGPRs and eight waves per SIMD stay resident).
+template <int MM, int ZF, bool ONE>
+__global__ void __launch_bounds__(DV_NW * kWave)
+__attribute__((amdgpu_waves_per_eu(ONE ? 8 : 4)))
+w4a16_decode_kernel(W4Args p) {
+    // LDS: activations [MM][K] fp16, then run sums [MM][K/32] of (A1, A16) fp32 pairs.
+    extern __shared__ __attribute__((aligned(16))) unsigned char dv_smem[];
+    const int K = p.K;
+    f16* sA = reinterpret_cast<f16*>(dv_smem);
+    float2* sSum = reinterpret_cast<float2*>(dv_smem + (size_t)MM * K * 2);
+    __shared__ float red[DV_NW][MM][16];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nt = blockIdx.x >> 1, sc = blockIdx.x & 1;
+    const int col = lane & 15, sub = lane >> 4, dc = sub >> 1, h = sub & 1;
+    const int n = 32 * nt + 16 * sc + col;
+    const int KC = K / 64, KP = KC / 2;
+    const int cpr = K / 8, nchunk = MM * cpr;
+
+    // Activation chunk loads go first so that waiting for them does not wait for weights.
+    constexpr int ABUF = 2;
+    u32x4 abuf[ABUF];
+#pragma unroll
+    for (int j = 0; j < ABUF; ++j) {
+        const int i = tid + j * DV_NW * kWave;
+        if (i < nchunk) {
+            const int m = i / cpr, c = i - m * cpr;
+            abuf[j] = *reinterpret_cast<const u32x4*>(p.A + (int64_t)m * p.lda + 8 * c);
+        }
+    }
+
+    const u32x4* wcol = p.W + (int64_t)nt * KC * 64 + 32 * h + 16 * sc + col;
+    auto load_one = [&](int pp, DecodeRound<MM>& R, int u) {
+        R.w[u] = __builtin_nontemporal_load(wcol + (int64_t)(2 * pp + dc) * 64);
+        group_load<ZF>(p, (64 * (2 * pp + dc) + 32 * h) / p.G, n, &R.s[u], &R.z[u]);
+    };
+    auto load_round = [&](int r, DecodeRound<MM>& R) {
+        const int pp0 = wave + DV_NW * DV_U * r;
+        if (pp0 + DV_NW * (DV_U - 1) < KP) {
+#pragma unroll
+            for (int u = 0; u < DV_U; ++u) load_one(pp0 + DV_NW * u, R, u);
+        } else {
+#pragma unroll
+            for (int u = 0; u < DV_U; ++u)
+                if (pp0 + DV_NW * u < KP) load_one(pp0 + DV_NW * u, R, u);
+        }
+    };
+    const int rounds = ONE ? 1 : (KP - wave + DV_NW * DV_U - 1) / (DV_NW * DV_U);
+    DecodeRound<MM> R0, R1;
+    load_round(0, R0);
+
+    // Stage activations and per-run sums.  Thread i owns chunk i (8 values); the four
+    // chunks of a 32-value run sit in four consecutive lanes.
+    auto stage_chunk = [&](int i, u32x4 v) {
+        reinterpret_cast<u32x4*>(sA)[i] = v;
+        const f16x8 a = as_f16x8(v);
+        float s1 = (float)a[0] + (float)a[1] + (float)a[4] + (float)a[5];
+        float s16 = (float)a[2] + (float)a[3] + (float)a[6] + (float)a[7];
+        s1 += __shfl_xor(s1, 1);
+        s16 += __shfl_xor(s16, 1);
+        s1 += __shfl_xor(s1, 2);
+        s16 += __shfl_xor(s16, 2);
+        if ((i & 3) == 0) sSum[i >> 2] = make_float2(s1, s16);
+    };
+#pragma unroll
+    for (int j = 0; j < ABUF; ++j) {
+        const int i = tid + j * DV_NW * kWave;
+        if (j * DV_NW * kWave < nchunk) stage_chunk(i, i < nchunk ? abuf[j] : u32x4{});
+    }
+    for (int i0 = ABUF * DV_NW * kWave; i0 < nchunk; i0 += DV_NW * kWave) {
+        const int i = i0 + tid;
+        u32x4 v{};
+        if (i < nchunk) {
+            const int m = i / cpr, c = i - m * cpr;
+            v = *reinterpret_cast<const u32x4*>(p.A + (int64_t)m * p.lda + 8 * c);
+        }
+        stage_chunk(i, v);
+    }
+    __syncthreads();
+
+    float acc[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) acc[m] = 0.0f;
+    auto compute_one = [&](int pp, const DecodeRound<MM>& R, int u) {
+        const int k0 = 64 * (2 * pp + dc) + 32 * h;
+        float c1[MM], c16[MM];
+#pragma unroll
+        for (int m = 0; m < MM; ++m) c1[m] = c16[m] = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t x = R.w[u][w], x8 = x >> 8;
+            const f16x2 t0 = as_h2((x & 0x000F000Fu) | 0x64006400u);
+            const f16x2 t1 = as_h2((x & 0x00F000F0u) | 0x64006400u);
+            const f16x2 t2 = as_h2((x8 & 0x000F000Fu) | 0x64006400u);
+            const f16x2 t3 = as_h2((x8 & 0x00F000F0u) | 0x64006400u);
+#pragma unroll
+            for (int m = 0; m < MM; ++m) {
+                const u32x4 a = *reinterpret_cast<const u32x4*>(sA + m * K + k0 + 8 * w);
+                c1[m] = __builtin_amdgcn_fdot2(t0, as_h2(a[0]), c1[m], false);
+                c16[m] = __builtin_amdgcn_fdot2(t1, as_h2(a[1]), c16[m], false);
+                c1[m] = __builtin_amdgcn_fdot2(t2, as_h2(a[2]), c1[m], false);
+                c16[m] = __builtin_amdgcn_fdot2(t3, as_h2(a[3]), c16[m], false);
+            }
+        }
+        uint32_t z;
+        if constexpr (ZF == WMMA_ZEROS_PACKED)
+            z = (R.z[u] >> (4 * (n & 7))) & 0xFu;
+        else
+            z = R.z[u] & 0xFu;
+        const float s = (float)__builtin_bit_cast(f16, (uint16_t)R.s[u]);
+        const float zf = (float)z;
+#pragma unroll
+        for (int m = 0; m < MM; ++m) {
+            const float2 as = sSum[(m * K + k0) >> 5];
+            const float r = c1[m] + 0.0625f * c16[m] - (1024.0f + zf) * as.x - (64.0f + zf) * as.y;
+            acc[m] += s * r;
+        }
+    };
+    auto compute_round = [&](int r, const DecodeRound<MM>& R) {
+        const int pp0 = wave + DV_NW * DV_U * r;
+        if (pp0 + DV_NW * (DV_U - 1) < KP) {
+#pragma unroll
+            for (int u = 0; u < DV_U; ++u) compute_one(pp0 + DV_NW * u, R, u);
+        } else {
+#pragma unroll
+            for (int u = 0; u < DV_U; ++u)
+                if (pp0 + DV_NW * u < KP) compute_one(pp0 + DV_NW * u, R, u);
+        }
+    };
+    if constexpr (ONE) {
+        compute_round(0, R0);
+    } else {
+        for (int r = 0; r < rounds; r += 2) {
+            if (r + 1 < rounds) load_round(r + 1, R1);
+            compute_round(r, R0);
+            if (r + 1 < rounds) {
+                if (r + 2 < rounds) load_round(r + 2, R0);
+                compute_round(r + 1, R1);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+        acc[m] += __shfl_xor(acc[m], 16);
+        acc[m] += __shfl_xor(acc[m], 32);
+        if (sub == 0) red[wave][m][col] = acc[m];
+    }
+    __syncthreads();
+    if (tid < 16 * MM) {
+        const int m = tid >> 4, c = tid & 15;
+        float v = red[0][m][c];
+#pragma unroll
+        for (int w = 1; w < DV_NW; ++w) v += red[w][m][c];
+        p.Y[(int64_t)m * p.ldy + 32 * nt + 16 * sc + c] = v;
+    }
+}
+
+// --------------------------------------------- decode on the matrix pipe (M <= 16) --
+// Same data movement as w4a16_decode_kernel (one workgroup per 16-column slice, all 64
+// lanes of a wave load 1 KB of prepacked weights: slice column l%16, K run (l/16) of a
+// 128-deep pair-step), but the multiply-accumulate runs on v_mfma_f32_16x16x32_f16:
+//   A operand (lane l: row l%16 = activation row m, K quarter l/16): the activations a',
+//     where a' = a at offsets {0,1,4,5} and a/16 at {2,3,6,7} of every 8 values;
+//   B operand (lane l: column l%16 = slice column n, same K quarter): the dequantised
+//     weights of one prepacked word, W = fp16((q - z) s).  (w & 0x000F000F) | 0x6400..
+//     is the fp16 pair (1024 + q0, 1024 + q1); minus (1024 + z) it is exactly q - z, and
+//     one fp16 multiply by s rounds once, as the definition requires.  The pairs at
+//     offsets {2,3,6,7} come out of (w & 0x00F000F0) | 0x6400.. as 1024 + 16 q, giving
+//     fp16(16 (q - z) s) = 16 W exactly (a power-of-two scale commutes with rounding),
+//     which the a/16 of the A operand cancels.  One shift, four v_and_or, four v_pk_add
+//     and four v_pk_mul per 8 weights, no shifts per nibble.
+// The accumulator runs over every group; only the final cross-wave sum remains.
+// Requires G % 128 == 0 (a pair-step never straddles two groups).
+// D layout: lane l holds column n = l%16 and rows m = 4*(l/16) + r (r < RR = ceil(M/4)).
+constexpr int DM_NW = 8;
+constexpr int DM_U = 4;
+
+struct DecodeMRound {
+    u32x4 w[DM_U];
+    uint32_t s[DM_U], z[DM_U];
+};
+
+// LDS row stride (halves) of the staged activations: K plus 16 bytes, so the 16 rows
+// read by one MFMA operand fall on distinct banks.
+__host__ __device__ inline int dm_row(int K) { return K + 8; }
+size_t decode_mfma_lds_bytes(int M, int K) { return (size_t)M * dm_row(K) * 2; }
+
+template <int ZF, bool ONE, int RR>
+__global__ void __launch_bounds__(DM_NW * kWave)
+__attribute__((amdgpu_waves_per_eu(ONE ? 8 : 4)))
+w4a16_decode_mfma_kernel(W4Args p) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char dm_smem[];
+    const int K = p.K, M = p.M, RS = dm_row(K);
+    f16* sA = reinterpret_cast<f16*>(dm_smem);  // [M][RS] a'
+    __shared__ float red[DM_NW][16][16];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nt = blockIdx.x >> 1, sc = blockIdx.x & 1;
+    const int col = lane & 15, sub = lane >> 4, dc = sub >> 1, h = sub & 1;
+    const int n = 32 * nt + 16 * sc + col;
+    const int KC = K / 64, KP = KC / 2;
+    const int cpr = K / 8, nchunk = M * cpr;
+
+    // Activation chunks first (see w4a16_decode_kernel).
+    constexpr int ABUF = 2;
+    u32x4 abuf[ABUF];
+#pragma unroll
+    for (int j = 0; j < ABUF; ++j) {
+        const int i = tid + j * DM_NW * kWave;
+        if (i < nchunk) {
+            const int m = i / cpr, c = i - m * cpr;
+            abuf[j] = *reinterpret_cast<const u32x4*>(p.A + (int64_t)m * p.lda + 8 * c);
+        }
+    }
+
+    const u32x4* wcol = p.W + (int64_t)nt * KC * 64 + 32 * h + 16 * sc + col;
+    auto load_one = [&](int pp, DecodeMRound& R, int u) {
+        R.w[u] = __builtin_nontemporal_load(wcol + (int64_t)(2 * pp + dc) * 64);
+        group_load<ZF>(p, (128 * pp) / p.G, n, &R.s[u], &R.z[u]);
+    };
+    auto load_round = [&](int r, DecodeMRound& R) {
+        const int pp0 = wave + DM_NW * DM_U * r;
+        if (pp0 + DM_NW * (DM_U - 1) < KP) {
+#pragma unroll
+            for (int u = 0; u < DM_U; ++u) load_one(pp0 + DM_NW * u, R, u);
+        } else {
+#pragma unroll
+            for (int u = 0; u < DM_U; ++u)
+                if (pp0 + DM_NW * u < KP) load_one(pp0 + DM_NW * u, R, u);
+        }
+    };
+    const int rounds = ONE ? 1 : (KP - wave + DM_NW * DM_U - 1) / (DM_NW * DM_U);
+    DecodeMRound R0, R1;
+    load_round(0, R0);
+
+    // Stage a' (chunk i = 8 activations of row m).
+    auto stage_chunk = [&](int i, u32x4 v) {
+        const int m = i / cpr, c = i - m * cpr;
+        f16x8 a = as_f16x8(v);
+#pragma unroll
+        for (int e = 2; e < 8; e += 4) {
+            a[e] = a[e] * (f16)0.0625f;
+            a[e + 1] = a[e + 1] * (f16)0.0625f;
+        }
+        *reinterpret_cast<u32x4*>(sA + m * RS + 8 * c) = as_u32x4(a);
+    };
+#pragma unroll
+    for (int j = 0; j < ABUF; ++j) {
+        const int i = tid + j * DM_NW * kWave;
+        if (i < nchunk) stage_chunk(i, abuf[j]);
+    }
+    for (int i = tid + ABUF * DM_NW * kWave; i < nchunk; i += DM_NW * kWave) {
+        const int m = i / cpr, c = i - m * cpr;
+        stage_chunk(i, *reinterpret_cast<const u32x4*>(p.A + (int64_t)m * p.lda + 8 * c));
+    }
+    __syncthreads();
+
+    // A-operand row of this lane (rows >= M read row 0; those output rows are unused).
+    const f16* arow = sA + (col < M ? col : 0) * RS;
+    uint32_t magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));  // keep the constant in a VGPR: one v_and_or per pair
+    f32x4 d{};
+    auto compute_one = [&](int pp, const DecodeMRound& R, int u) {
+        const int k0 = 128 * pp + 64 * dc + 32 * h;
+        uint32_t z;
+        if constexpr (ZF == WMMA_ZEROS_PACKED)
+            z = (R.z[u] >> (4 * (n & 7))) & 0xFu;
+        else
+            z = R.z[u] & 0xFu;
+        const uint32_t z1 = 0x6400u | z, z16 = 0x6400u | (z << 4);
+        const f16x2 zs1 = as_h2(z1 | (z1 << 16)), zs16 = as_h2(z16 | (z16 << 16));
+        const f16x2 ss = as_h2(R.s[u] | (R.s[u] << 16));
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t x = R.w[u][w], x8 = x >> 8;
+            u32x4 bv;
+            bv[0] = as_u32((as_h2((x & 0x000F000Fu) | magic) - zs1) * ss);
+            bv[1] = as_u32((as_h2((x & 0x00F000F0u) | magic) - zs16) * ss);
+            bv[2] = as_u32((as_h2((x8 & 0x000F000Fu) | magic) - zs1) * ss);
+            bv[3] = as_u32((as_h2((x8 & 0x00F000F0u) | magic) - zs16) * ss);
+            const f16x8 av = as_f16x8(*reinterpret_cast<const u32x4*>(arow + k0 + 8 * w));
+            d = mfma16(av, as_f16x8(bv), d);
+        }
+    };
+    auto compute_round = [&](int r, const DecodeMRound& R) {
+        const int pp0 = wave + DM_NW * DM_U * r;
+        if (pp0 + DM_NW * (DM_U - 1) < KP) {
+#pragma unroll
+            for (int u = 0; u < DM_U; ++u) compute_one(pp0 + DM_NW * u, R, u);
+        } else {
+#pragma unroll
+            for (int u = 0; u < DM_U; ++u)
+                if (pp0 + DM_NW * u < KP) compute_one(pp0 + DM_NW * u, R, u);
+        }
+    };
+    if constexpr (ONE) {
+        compute_round(0, R0);
+    } else {
+        for (int r = 0; r < rounds; r += 2) {
+            if (r + 1 < rounds) load_round(r + 1, R1);
+            compute_round(r, R0);
+            if (r + 1 < rounds) {
+                if (r + 2 < rounds) load_round(r + 2, R0);
+                compute_round(r + 1, R1);
+            }
+        }
+    }
+    // d[r]: activation row 4*sub + r, slice column col.
+#pragma unroll
+    for (int r = 0; r < RR; ++r) red[wave][4 * sub + r][col] = d[r];
+    __syncthreads();
+    if (tid < 16 * M) {
+        const int m = tid >> 4, c = tid & 15;
+        float v = red[0][m][c];
+#pragma unroll
+        for (int w = 1; w < DM_NW; ++w) v += red[w][m][c];
+        p.Y[(int64_t)m * p.ldy + 32 * nt + 16 * sc + c] = v;
+    }
+}
+
+template <int ZF, bool ONE>
+void launch_decode_mfma(const W4Args& a, int M, dim3 grid, dim3 block, size_t lds,
+                        hipStream_t stream) {
+    switch ((M + 3) / 4) {
+        case 1: hipLaunchKernelGGL((w4a16_decode_mfma_kernel<ZF, ONE, 1>), grid, block, lds, stream, a); break;
+        case 2: hipLaunchKernelGGL((w4a16_decode_mfma_kernel<ZF, ONE, 2>), grid, block, lds, stream, a); break;
+        case 3: hipLaunchKernelGGL((w4a16_decode_mfma_kernel<ZF, ONE, 3>), grid, block, lds, stream, a); break;
+        default: hipLaunchKernelGGL((w4a16_decode_mfma_kernel<ZF, ONE, 4>), grid, block, lds, stream, a); break;
+    }
+}
+
 // ------------------------------------------------------------------ MFMA (M > GV_MAXM) --
 // D = W^T A^T on MFMA 32x32x16: matrix rows are weight columns n, matrix columns are
 // activation rows m.  Workgroup: 4 waves along N, each wave WNT 32-column tiles; the
@@ -229,7 +620,7 @@ w4a16_gemv_kernel(W4Args p) {
 // them in registers.  BM = 32*MT rows per workgroup.
 constexpr int WQ_WAVES = 4;
 
-template <int WNT, int MT>
+template <int WNT, int MT, int ZF>
 __global__ void __launch_bounds__(WQ_WAVES * kWave)
 w4a16_mfma_kernel(W4Args p) {
     constexpr int BM = 32 * MT;
@@ -294,7 +685,7 @@ w4a16_mfma_kernel(W4Args p) {
             const int nt = ntile0 + j;
             if (nt < ntiles) {
                 wv[j] = __builtin_nontemporal_load(p.W + ((int64_t)nt * KC + kc) * 64 + lane);
-                group_params(p, (kc * 64 + 32 * h) / p.G, 32 * nt + (lane & 31), &zs[j], &ss[j]);
+                group_params<ZF>(p, (kc * 64 + 32 * h) / p.G, 32 * nt + (lane & 31), &zs[j], &ss[j]);
             } else {
                 wv[j] = u32x4{};
                 zs[j] = 0x64006400u;
@@ -357,13 +748,22 @@ w4a16_reduce_kernel(const float* ws, int split, float* Y, int64_t ldy, int M, in
     }
 }
 
+// Dynamic LDS of the decode kernel: activations plus two fp32 sums per 32-value run.
+size_t decode_lds_bytes(int M, int K) { return (size_t)M * K * 2 + (size_t)M * (K / 32) * 8; }
+
+// Dynamic LDS the decode kernels may request without raising the launch limit.
+constexpr size_t kDecodeLdsMax = 48 * 1024;
+
+bool w4a16_use_decode(int M, int N, int K, int num_cus) {
+    if (num_cus <= 0) num_cus = 256;
+    return M >= 1 && M <= GV_MAXM && K % 128 == 0 && decode_lds_bytes(M, K) <= kDecodeLdsMax &&
+           N / 16 >= num_cus / 2;
+}
+
 int grid_for(int64_t work, int per_block) {
     int64_t b = (work + per_block - 1) / per_block;
     return (int)std::min<int64_t>(std::max<int64_t>(b, 1), 65535);
 }
-
-// MFMA kernel variants: (WNT, MT).
-constexpr int kWqVariants[][2] = {{1, 1}, {1, 4}, {2, 4}};
 
 }  // namespace
 
@@ -391,10 +791,29 @@ hipError_t launch_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q,
     return hipGetLastError();
 }
 
-// Host-only: choose the kernel and K split.  GEMV for M <= 4 (one workgroup per 32
-// columns, K split only when fewer than 2*CUs workgroups would exist); MFMA otherwise.
-void w4a16_plan(int M, int N, int K, int G, int num_cus, int* split, int* k_per_split,
-                bool* mfma) {
+// Host-only: choose the kernel and K split.
+//   decode-mfma  M <= 16, G % 128 == 0, K % 128 == 0, the staged activations fit LDS and
+//                the 16-column slices give at least half a workgroup per CU.
+//   decode       M <= 4 with the same slice condition, other group sizes.
+//   gemv-split   other M <= 4 shapes: one workgroup per 32 columns, K split (plus a reduce
+//                pass) only when fewer than 2*CUs workgroups would exist.
+//   mfma         everything else.
+W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
+    if (num_cus <= 0) num_cus = 256;
+    W4A16Plan pl{};
+    pl.split = 1;
+    pl.k_per_split = K;
+    const bool slices_ok = N / 16 >= num_cus / 2 && K % 128 == 0;
+    (void)aligned;
+    if (M >= 1 && M <= 16 && slices_ok && G % 128 == 0 &&
+        decode_mfma_lds_bytes(M, K) <= kDecodeLdsMax) {
+        pl.kind = W4_DECODE_MFMA;
+        return pl;
+    }
+    if (w4a16_use_decode(M, N, K, num_cus)) {
+        pl.kind = W4_DECODE;
+        return pl;
+    }
     const int KC = K / 64;
     const bool use_mfma = M > GV_MAXM;
     int64_t blocks;
@@ -408,14 +827,74 @@ void w4a16_plan(int M, int N, int K, int G, int num_cus, int* split, int* k_per_
     int s = 1;
     const int64_t target = use_mfma ? num_cus : 2 * num_cus;
     if (blocks < target) s = (int)std::min<int64_t>((target + blocks - 1) / blocks, 16);
-    // each split must be whole chunks and, for G >= 64, whole groups are not required:
-    // a lane's 32 K values stay inside one group whenever G % 32 == 0.
+    // each split is whole 64-deep chunks; a lane's 32 K values stay inside one group
+    // whenever G % 32 == 0.
     int kcps = ceil_div(KC, s);
     s = ceil_div(KC, kcps);
-    *split = s;
-    *k_per_split = kcps * 64;
-    *mfma = use_mfma;
+    pl.kind = use_mfma ? W4_MFMA : W4_GEMV_SPLIT;
+    pl.split = s;
+    pl.k_per_split = kcps * 64;
+    return pl;
 }
+
+namespace {
+
+template <int ZF>
+hipError_t launch_w4a16_zf(const W4Args& a, const W4A16Launch& w, hipStream_t stream) {
+    const int ntiles = w.N / 32;
+    const W4A16Plan& pl = w.plan;
+    if (pl.kind == W4_DECODE_MFMA) {
+        const size_t lds = decode_mfma_lds_bytes(w.M, w.K);
+        const dim3 grid(w.N / 16), block(DM_NW * kWave);
+        if (w.K <= DM_NW * DM_U * 128)
+            launch_decode_mfma<ZF, true>(a, w.M, grid, block, lds, stream);
+        else
+            launch_decode_mfma<ZF, false>(a, w.M, grid, block, lds, stream);
+        return hipGetLastError();
+    }
+    if (pl.kind == W4_DECODE) {
+        const size_t lds = decode_lds_bytes(w.M, w.K);
+        const dim3 grid(w.N / 16), block(DV_NW * kWave);
+        if (w.K <= DV_NW * DV_U * 128) {
+            switch (w.M) {
+                case 1: hipLaunchKernelGGL((w4a16_decode_kernel<1, ZF, true>), grid, block, lds, stream, a); break;
+                case 2: hipLaunchKernelGGL((w4a16_decode_kernel<2, ZF, true>), grid, block, lds, stream, a); break;
+                case 3: hipLaunchKernelGGL((w4a16_decode_kernel<3, ZF, true>), grid, block, lds, stream, a); break;
+                default: hipLaunchKernelGGL((w4a16_decode_kernel<4, ZF, true>), grid, block, lds, stream, a); break;
+            }
+        } else {
+            switch (w.M) {
+                case 1: hipLaunchKernelGGL((w4a16_decode_kernel<1, ZF, false>), grid, block, lds, stream, a); break;
+                case 2: hipLaunchKernelGGL((w4a16_decode_kernel<2, ZF, false>), grid, block, lds, stream, a); break;
+                case 3: hipLaunchKernelGGL((w4a16_decode_kernel<3, ZF, false>), grid, block, lds, stream, a); break;
+                default: hipLaunchKernelGGL((w4a16_decode_kernel<4, ZF, false>), grid, block, lds, stream, a); break;
+            }
+        }
+        return hipGetLastError();
+    }
+    if (pl.kind == W4_GEMV_SPLIT) {
+        hipLaunchKernelGGL((w4a16_gemv_kernel<ZF>), dim3(ntiles, pl.split), dim3(GV_NW * kWave), 0,
+                           stream, a);
+    } else {
+        const int wnt = w.M >= 256 ? 2 : 1;
+        const int mt = w.M > 32 ? 4 : 1;
+        dim3 grid(ceil_div(ntiles, WQ_WAVES * wnt), pl.split, ceil_div(w.M, 32 * mt));
+        if (wnt == 2)
+            hipLaunchKernelGGL((w4a16_mfma_kernel<2, 4, ZF>), grid, dim3(WQ_WAVES * kWave), 0, stream, a);
+        else if (mt == 4)
+            hipLaunchKernelGGL((w4a16_mfma_kernel<1, 4, ZF>), grid, dim3(WQ_WAVES * kWave), 0, stream, a);
+        else
+            hipLaunchKernelGGL((w4a16_mfma_kernel<1, 1, ZF>), grid, dim3(WQ_WAVES * kWave), 0, stream, a);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || pl.split <= 1) return e;
+    const int64_t total = (int64_t)w.M * w.N;
+    hipLaunchKernelGGL(w4a16_reduce_kernel, dim3(grid_for(total, 256)), dim3(256), 0, stream,
+                       static_cast<const float*>(w.workspace), pl.split, w.Y, w.ldy, w.M, w.N);
+    return hipGetLastError();
+}
+
+}  // namespace
 
 hipError_t launch_w4a16(const W4A16Launch& w, hipStream_t stream) {
     W4Args a{};
@@ -432,30 +911,10 @@ hipError_t launch_w4a16(const W4A16Launch& w, hipStream_t stream) {
     a.Y = w.Y;
     a.ldy = w.ldy;
     a.ws = static_cast<float*>(w.workspace);
-    a.split = w.split;
-    a.kc_per_split = w.k_per_split / 64;
-    const int ntiles = w.N / 32;
-    if (!w.mfma) {
-        hipLaunchKernelGGL(w4a16_gemv_kernel, dim3(ntiles, w.split), dim3(GV_NW * kWave), 0,
-                           stream, a);
-    } else {
-        const int wnt = w.M >= 256 ? 2 : 1;
-        const int mt = w.M > 32 ? 4 : 1;
-        dim3 grid(ceil_div(ntiles, WQ_WAVES * wnt), w.split, ceil_div(w.M, 32 * mt));
-        if (wnt == 2)
-            hipLaunchKernelGGL((w4a16_mfma_kernel<2, 4>), grid, dim3(WQ_WAVES * kWave), 0, stream, a);
-        else if (mt == 4)
-            hipLaunchKernelGGL((w4a16_mfma_kernel<1, 4>), grid, dim3(WQ_WAVES * kWave), 0, stream, a);
-        else
-            hipLaunchKernelGGL((w4a16_mfma_kernel<1, 1>), grid, dim3(WQ_WAVES * kWave), 0, stream, a);
-    }
-    (void)kWqVariants;
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || w.split <= 1) return e;
-    const int64_t total = (int64_t)w.M * w.N;
-    hipLaunchKernelGGL(w4a16_reduce_kernel, dim3(grid_for(total, 256)), dim3(256), 0, stream,
-                       static_cast<const float*>(w.workspace), w.split, w.Y, w.ldy, w.M, w.N);
-    return hipGetLastError();
+    a.split = w.plan.split;
+    a.kc_per_split = w.plan.k_per_split / 64;
+    if (w.zeros_format == WMMA_ZEROS_PACKED) return launch_w4a16_zf<WMMA_ZEROS_PACKED>(a, w, stream);
+    return launch_w4a16_zf<WMMA_ZEROS_U8>(a, w, stream);
 }
 
 }  // namespace wmma_amd
