@@ -1,19 +1,32 @@
 #!/usr/bin/env python3
-"""Headline benchmark of the wmma_ops MI355X hot path.
+"""Benchmarks of the wmma_ops MI355X hot path.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-w4a16]
+    python bench.py --workload NAME      # one JSON line per case of one config family
+    python bench.py --suite              # every config family (one JSON line per case)
 
-Metric: "FP16 GEMM TFLOPS (% MFMA peak) @4096^3; W4A16 M=1 HBM GB/s".
+Default run (the driver's contract): ONE JSON line for the headline metric of
+BASELINE.json, "FP16 GEMM TFLOPS (% MFMA peak) @4096^3; W4A16 M=1 HBM GB/s".
 A step is one wmma_ops_amd.matmul of the 4096^3 FP16 GEMM: A[4096,4096] and
-B[4096,4096] fp16 ~ N(0,1) (seed 43), fp32 output, inputs resident in HBM.  W warmup
+B[4096,4096] fp16 ~ N(0,1) (seed 42 + 1), fp32 output, inputs resident in HBM.  W warmup
 steps, then K timed steps between two synchronisations; `value` = 2*M*N*K / time.
-The W4A16 M=1 decode figures (configs[3], K=4096, N in {4096, 14336}, G=128) ride along
-in the same JSON line: weights rotate over > 512 MB so the 256 MB MALL cannot hold them,
-and launches are replayed from a HIP graph so the figure is kernel time, not host
-dispatch.  The CPU baseline (rank 0, N=1) is the oracle's fp32 torch.matmul on the host
-cores over a bounded sample of the same 4096^3 workload.
+`roofline.achieved` divides the same FLOPs by the kernel's mean duration measured with
+HIP events on the stream the kernel is launched on (the current stream).  The W4A16 M=1
+decode figures (configs[3], K=4096, N in {4096, 14336}, G=128) ride along in the same
+line; the CPU baseline (N=1 only) is the oracle's fp32 torch.matmul on the host cores
+over a bounded sample of the same 4096^3 workload.
 
-Prints ONE JSON line.  One GPU only: --gpus N with N > 1 exits with a message.
+Workload families (--workload):
+  gemm       configs[0..1]: M=N=K in {512,1024,2048,4096} and 4096x4096x2048
+  epilogue   configs[1]: C = 2.0*A@B + 0.5*C, out-of-place and in-place, 1024^3/4096^3
+  skinny     configs[2]: M in {1,16,64,128} x N in {4096,11008,14336}, K=4096; K=14336,N=4096
+  w4a16      configs[3]: M in {1,16,128,2048} x N in {4096,14336}, K=4096, G=128
+  flash      configs[4]: [4,32,4096,128], causal and non-causal
+  copy       a plain 256 MiB device copy (calibrates the rocprofv3 byte counters)
+HBM-bound cases rotate their inputs over more than 512 MB (twice the 256 MB MALL) so the
+bytes really come from HBM; microsecond-scale kernels are replayed from a HIP graph.
+
+One GPU only: --gpus N with N > 1 exits with a message.
 """
 from __future__ import annotations
 
@@ -31,8 +44,10 @@ if ROOT not in sys.path:
 
 PEAK_FP16_FLOPS = 2.5e15   # MI355X dense FP16 MFMA (published)
 PEAK_HBM_BPS = 8.0e12      # MI355X HBM3E (published)
+ROTATE_BYTES = 600e6       # > 2 x 256 MB MALL
 M = N = K = 4096
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_f16f32_4096_traffic.json")
+METRIC = "FP16 GEMM TFLOPS (% MFMA peak) @4096^3; W4A16 M=1 HBM GB/s"
 
 
 def parse():
@@ -43,12 +58,15 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-w4a16", action="store_true", help="skip the W4A16 decode figures")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--workload", choices=sorted(FAMILIES), help="one config family")
+    ap.add_argument("--suite", action="store_true", help="every config family")
     return ap.parse_args()
 
 
+# ---------------------------------------------------------------------------- timing --
 def time_events(fn, reps):
-    """Mean duration (ms) of fn() measured with one event pair per launch on the current
-    stream (the stream the C-ABI launches on)."""
+    """Mean duration (ms) of fn() from one event pair per call on the current stream
+    (the stream the C-ABI launches on)."""
     import torch
 
     pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -61,6 +79,223 @@ def time_events(fn, reps):
     return statistics.mean(s.elapsed_time(e) for s, e in pairs)
 
 
+def time_batches(fn, calls, batches=5):
+    """Median over `batches` of (event-timed batch of `calls` back-to-back calls)/calls,
+    in ms.  fn(i) runs call i (so inputs can rotate)."""
+    import torch
+
+    for i in range(min(calls, 3)):
+        fn(i)
+    torch.cuda.synchronize()
+    out = []
+    for _ in range(batches):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for i in range(calls):
+            fn(i)
+        e.record()
+        torch.cuda.synchronize()
+        out.append(s.elapsed_time(e) / calls)
+    return statistics.median(out)
+
+
+def time_graph(fn, copies, batches=5):
+    """Per-call time (ms) of `copies` calls fn(0..copies-1) captured in one HIP graph and
+    replayed `batches` times (median); returns (ms, outputs of the captured calls)."""
+    import torch
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for i in range(min(copies, 3)):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    outs = []
+    with torch.cuda.graph(graph):
+        for i in range(copies):
+            outs.append(fn(i))
+    graph.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(batches):
+        s0, e0 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        graph.replay()
+        e0.record()
+        torch.cuda.synchronize()
+        ts.append(s0.elapsed_time(e0) / copies)
+    return statistics.median(ts), outs
+
+
+def line(**kw):
+    print(json.dumps(kw), flush=True)
+
+
+def copies_for(nbytes):
+    return max(2, math.ceil(ROTATE_BYTES / max(nbytes, 1)))
+
+
+# ------------------------------------------------------------------------ families --
+def fam_gemm(wo):
+    import torch
+
+    from oracle import gemm as og
+
+    for (m, n, k) in [(512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048),
+                      (4096, 4096, 4096), (4096, 4096, 2048)]:
+        g = torch.Generator().manual_seed(42 + (0 if m == 512 else 1))
+        A = torch.randn(m, k, generator=g).half()
+        B = torch.randn(k, n, generator=g).half()
+        Ad, Bd = A.cuda(), B.cuda()
+        calls = 200 if m <= 1024 else 50
+        ms = time_batches(lambda i: wo.matmul(Ad, Bd), calls)
+        err = og.max_rel_err(wo.matmul(Ad[:256], Bd), og.gemm_ref(A[:256], B))
+        fl = 2.0 * m * n * k
+        line(family="gemm", M=m, N=n, K=k, plan=wo.gemm_plan(m, n, k), us=round(ms * 1e3, 2),
+             TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
+             frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4),
+             max_rel_err=float(f"{err:.3e}"))
+
+
+def fam_epilogue(wo):
+    import torch
+
+    from oracle import gemm as og
+
+    for s in (1024, 4096):
+        g = torch.Generator().manual_seed(42 + 1)
+        A = torch.randn(s, s, generator=g).half()
+        B = torch.randn(s, s, generator=g).half()
+        C = torch.randn(s, s, generator=g)
+        Ad, Bd, Cd = A.cuda(), B.cuda(), C.cuda()
+        calls = 200 if s <= 1024 else 50
+        fl = 2.0 * s * s * s
+        ref = og.gemm_ref(A[:256], B, 2.0, 0.5, C[:256])
+        ms = time_batches(lambda i: wo.gemm(Ad, Bd, 2.0, 0.5, Cd), calls)
+        err = og.max_rel_err(wo.gemm(Ad, Bd, 2.0, 0.5, Cd)[:256], ref)
+        line(family="epilogue", mode="out_of_place", M=s, N=s, K=s, us=round(ms * 1e3, 2),
+             TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
+             frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4),
+             max_rel_err=float(f"{err:.3e}"))
+        Ci = Cd.clone()
+        ms = time_batches(lambda i: wo.gemm_inplace(Ad, Bd, Ci, 2.0, 0.5), calls)
+        Ci = Cd.clone()
+        wo.gemm_inplace(Ad, Bd, Ci, 2.0, 0.5)
+        err = og.max_rel_err(Ci[:256], ref)
+        line(family="epilogue", mode="in_place", M=s, N=s, K=s, us=round(ms * 1e3, 2),
+             TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
+             frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4),
+             max_rel_err=float(f"{err:.3e}"))
+
+
+def fam_skinny(wo):
+    import torch
+
+    from oracle import gemm as og
+
+    shapes = [(m, n, 4096) for m in (1, 16, 64, 128) for n in (4096, 11008, 14336)] + \
+             [(m, 4096, 14336) for m in (1, 16, 64, 128)]
+    for (m, n, k) in shapes:
+        g = torch.Generator().manual_seed(42 + 2)
+        A = torch.randn(m, k, generator=g).half()
+        B = (torch.randn(k, n, generator=g) * 0.02).half()
+        nbytes = 2 * m * k + 2 * k * n + 4 * m * n
+        cp = copies_for(nbytes)
+        As = [A.cuda() for _ in range(cp)]
+        Bs = [B.cuda() for _ in range(cp)]
+        ms = time_batches(lambda i: wo.matmul(As[i % cp], Bs[i % cp]), 4 * cp)
+        err = og.max_rel_err(wo.matmul(As[0], Bs[0]), og.gemm_ref(A, B))
+        line(family="skinny", M=m, N=n, K=k, plan=wo.gemm_plan(m, n, k), us=round(ms * 1e3, 2),
+             bytes=nbytes, GBps=round(nbytes / (ms * 1e-3) / 1e9, 1),
+             frac_hbm=round(nbytes / (ms * 1e-3) / PEAK_HBM_BPS, 4),
+             TFLOPS=round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 2), rotation_copies=cp,
+             max_rel_err=float(f"{err:.3e}"))
+        del As, Bs
+
+
+def w4a16_case(wo, m, n, use_graph=True):
+    import torch
+
+    from oracle import gemm as og
+    from oracle import int4 as oi
+
+    kw, G = 4096, 128
+    A, q, s, z = oi.make_inputs(m, kw, n, G, seed=42 + 3)
+    pk0 = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
+    sd = torch.from_numpy(s).cuda()
+    zd = torch.from_numpy(oi.pack_zeros(z)).cuda()
+    Ad = A.cuda()
+    nbytes = kw * n // 2 + (kw // G) * n * 2 + (kw // G) * n // 2 + 2 * m * kw + 4 * m * n
+    cp = copies_for(nbytes)
+    pks = [pk0.clone() for _ in range(cp)]
+    sds = [sd.clone() for _ in range(cp)]
+    zds = [zd.clone() for _ in range(cp)]
+    Y0 = wo.matmul_int4(Ad, pk0, sd, zd, G)
+    err = og.max_rel_err(Y0, oi.w4a16_ref(A, q, s, z, G))
+    fn = lambda i: wo.matmul_int4(Ad, pks[i % cp], sds[i % cp], zds[i % cp], G)
+    if use_graph:
+        ms, outs = time_graph(fn, cp)
+        assert torch.equal(outs[0], Y0), "graph replay differs from eager"
+    else:
+        ms = time_batches(fn, 2 * cp)
+    fl = 2.0 * m * n * kw
+    return {"M": m, "N": n, "K": kw, "G": G, "bytes": nbytes, "us_per_call": round(ms * 1e3, 3),
+            "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(nbytes / (ms * 1e-3) / PEAK_HBM_BPS, 4),
+            "TFLOPS": round(fl / (ms * 1e-3) / 1e12, 2), "rotation_copies": cp,
+            "timing": "graph replay" if use_graph else "stream launches",
+            "max_rel_err": float(f"{err:.3e}")}
+
+
+def fam_w4a16(wo):
+    for m in (1, 16, 128, 2048):
+        for n in (4096, 14336):
+            r = w4a16_case(wo, m, n, use_graph=m <= 16)
+            r["family"] = "w4a16"
+            line(**r)
+
+
+def fam_flash(wo):
+    import torch
+
+    from oracle import attention as oatt
+    from oracle import gemm as og
+
+    B, H, S, D = 4, 32, 4096, 128
+    Q, Kt, V = oatt.make_inputs(B, H, S, D, seed=42 + 4)
+    Qd, Kd, Vd = Q.cuda(), Kt.cuda(), V.cuda()
+    for causal in (False, True):
+        ms = time_batches(lambda i: wo.flash_attention(Qd, Kd, Vd, causal, 1.0 / math.sqrt(D)), 10)
+        O = wo.flash_attention(Qd, Kd, Vd, causal, 1.0 / math.sqrt(D))
+        ref = oatt.sdpa_ref(Q[0:1, 0:1], Kt[0:1, 0:1], V[0:1, 0:1], causal)
+        err = og.max_rel_err(O[0:1, 0:1].float(), ref)
+        fl = 4.0 * B * H * S * S * D if not causal else 4.0 * B * H * D * S * (S + 1) / 2
+        line(family="flash", B=B, H=H, S=S, D=D, causal=causal, us=round(ms * 1e3, 1),
+             TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
+             frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4),
+             max_rel_err=float(f"{err:.3e}"))
+
+
+def fam_copy(wo):
+    """Plain device copy of a known size: the calibration for rocprofv3's FETCH_SIZE and
+    WRITE_SIZE counters (bytes the counters report per byte actually copied)."""
+    import torch
+
+    nbytes = 256 << 20
+    x = torch.ones(nbytes, dtype=torch.uint8, device="cuda")
+    y = torch.empty_like(x)
+    ms = time_batches(lambda i: y.copy_(x), 10)
+    line(family="copy", bytes=nbytes, us=round(ms * 1e3, 1),
+         GBps_read_plus_write=round(2 * nbytes / (ms * 1e-3) / 1e9, 1))
+
+
+FAMILIES = {"gemm": fam_gemm, "epilogue": fam_epilogue, "skinny": fam_skinny,
+            "w4a16": fam_w4a16, "flash": fam_flash, "copy": fam_copy}
+
+
+# ------------------------------------------------------------------------ headline --
 def gemm_bench(wo, steps, warmup):
     import torch
 
@@ -81,60 +316,6 @@ def gemm_bench(wo, steps, warmup):
 
     err = og.max_rel_err(C[:256], og.gemm_ref(A[:256].cpu(), B.cpu()))
     return ms_step, ms_kernel, err
-
-
-def w4a16_bench(wo, Nw):
-    """M=1 W4A16 decode: graph-replayed launches over rotating weight copies (> 512 MB)."""
-    import numpy as np
-    import torch
-
-    from oracle import gemm as og
-    from oracle import int4 as oi
-
-    Kw, G = 4096, 128
-    A, q, s, z = oi.make_inputs(1, Kw, Nw, G, seed=42 + 3)
-    pk0 = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
-    sd = torch.from_numpy(s).cuda()
-    zd = torch.from_numpy(oi.pack_zeros(z)).cuda()
-    Ad = A.cuda()
-    algo_bytes = Kw * Nw // 2 + (Kw // G) * Nw * 2 + (Kw // G) * Nw // 2 + 2 * Kw + 4 * Nw
-    copies = max(2, math.ceil(600e6 / algo_bytes))
-    pks = [pk0.clone() for _ in range(copies)]
-    sds = [sd.clone() for _ in range(copies)]
-    zds = [zd.clone() for _ in range(copies)]
-    Y0 = wo.matmul_int4(Ad, pk0, sd, zd, G)
-    err = og.max_rel_err(Y0, oi.w4a16_ref(A, q, s, z, G))
-    torch.cuda.synchronize()
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(stream):
-        for i in range(3):  # warm the allocator on the side stream before capture
-            wo.matmul_int4(Ad, pks[i % copies], sds[i % copies], zds[i % copies], G)
-    torch.cuda.current_stream().wait_stream(stream)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    outs = []
-    with torch.cuda.graph(graph):
-        for i in range(copies):
-            outs.append(wo.matmul_int4(Ad, pks[i], sds[i], zds[i], G))
-    graph.replay()
-    torch.cuda.synchronize()
-    assert torch.equal(outs[0], Y0), "graph replay differs from eager"
-    reps = 5
-    ts = []
-    for _ in range(reps):
-        s0, e0 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s0.record()
-        graph.replay()
-        e0.record()
-        torch.cuda.synchronize()
-        ts.append(s0.elapsed_time(e0) / copies)
-    assert torch.equal(outs[-1], outs[0]), "graph replays differ"
-    ms = statistics.median(ts)
-    return {"N": Nw, "K": Kw, "G": G, "bytes": algo_bytes, "us_per_call": round(ms * 1e3, 3),
-            "GBps": round(algo_bytes / (ms * 1e-3) / 1e9, 1),
-            "hbm_frac": round(algo_bytes / (ms * 1e-3) / PEAK_HBM_BPS, 4),
-            "rotation_copies": copies, "max_rel_err": float(f"{err:.3e}")}
 
 
 def cpu_baseline(seconds):
@@ -164,17 +345,7 @@ def cpu_baseline(seconds):
                       f"(oracle.gemm.gemm_ref), median {t * 1e3:.1f} ms"}
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); every GPU box "
-              "in this build has one MI355X. Run with --gpus 1.", file=sys.stderr)
-        sys.exit(2)
-    import torch
-
-    import wmma_ops_amd as wo
-
-    assert torch.cuda.is_available(), "bench.py needs a GPU"
+def headline(wo, args):
     ms_step, ms_kernel, err = gemm_bench(wo, args.steps, args.warmup)
     flops = 2.0 * M * N * K
     tflops = flops / (ms_step * 1e-3) / 1e12
@@ -183,8 +354,9 @@ def main():
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
-    line = {
-        "metric": "FP16 GEMM TFLOPS (% MFMA peak) @4096^3; W4A16 M=1 HBM GB/s",
+    plan = wo.gemm_plan(M, N, K)
+    out = {
+        "metric": METRIC,
         "value": round(tflops, 2),
         "unit": "TFLOPS",
         "n_gpus": 1,
@@ -198,20 +370,40 @@ def main():
         "data": "synthetic (seeded N(0,1) fp16 inputs, fp32 output)",
         "config": {"workload": "fp16 GEMM C[4096,4096] fp32 = A[4096,4096] @ B[4096,4096] "
                                "(configs[1], wmma_ops_amd.matmul)",
-                   "M": M, "N": N, "K": K, "plan": wo.gemm_plan(M, N, K)},
+                   "M": M, "N": N, "K": K, "plan": plan},
         "pct_mfma_peak": round(100.0 * tflops * 1e12 / PEAK_FP16_FLOPS, 2),
         "max_rel_err": float(f"{err:.3e}"),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_FP16_FLOPS / 1e12, "unit": "TFLOP/s",
                      "frac": round(achieved * 1e12 / PEAK_FP16_FLOPS, 4), "traffic": traffic,
-                     "kernel": "gemm_tiled_kernel<256,256,2,2,true>",
+                     "kernel": "gemm_mfma_kernel<256,256,32,2,4,4> (BMxBNxBK, waves MxN, stages)",
                      "kernel_us": round(ms_kernel * 1e3, 2)},
     }
     if not args.no_w4a16:
-        line["w4a16_m1"] = [w4a16_bench(wo, n) for n in (4096, 14336)]
+        out["w4a16_m1"] = [w4a16_case(wo, 1, n) for n in (4096, 14336)]
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
-    print(json.dumps(line), flush=True)
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); every GPU box "
+              "in this build has one MI355X. Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import wmma_ops_amd as wo
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.suite:
+        for name in ("gemm", "epilogue", "skinny", "w4a16", "flash"):
+            FAMILIES[name](wo)
+    elif args.workload:
+        FAMILIES[args.workload](wo)
+    else:
+        headline(wo, args)
 
 
 if __name__ == "__main__":

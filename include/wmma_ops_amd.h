@@ -125,9 +125,10 @@ int wmma_w4a16_gemm(const void* A, int64_t lda, const int32_t* packed, const voi
 
 /*
  * Flash-attention forward.  Q [B,H,Sq,D], K and V [B,H,Sk,D], O [B,H,Sq,D]; fp16,
- * contiguous.  O = softmax(scale * Q K^T (+ causal mask: key j <= query i when
- * Sq == Sk; with Sq != Sk the mask is aligned to the bottom right, key j <= i + Sk - Sq))
- * V, FP32 online softmax and accumulation.  D in {64, 128}.
+ * contiguous.  O = softmax(scale * Q K^T (+ causal mask: key j <= query i, aligned to
+ * the top left for any Sq, Sk, as torch's scaled_dot_product_attention(is_causal=True)))
+ * V, FP32 online softmax and accumulation.  D in {64, 128}.  A query row whose keys are
+ * all masked (i.e. none, since key 0 is always kept) cannot occur.
  * Replaces the documented (unbound) flash_attention(Q,K,V,causal=False,scale=-1.0)
  * (README.md:221-251).  A caller's scale <= 0 is resolved to 1/sqrt(D) before this call.
  */
