@@ -2,26 +2,29 @@
 //
 // The reference documents flash_attention(Q, K, V, causal=False, scale=-1.0) on
 // [B, H, N, D] fp16 tensors with default scale 1/sqrt(D) (README.md:221-251); its kernel
-// was removed.  This is a new MFMA design:
+// was removed.  This is a new MFMA design for CDNA4:
 //
-//  * A workgroup owns 128 queries of one (batch, head): 4 waves x 32 queries.
-//  * Scores are computed transposed, S^T = K Q^T, on MFMA 32x32x16 with K as the matrix
-//    A operand (rows = keys, read K-contiguous from LDS) and the wave's Q fragments as
-//    the B operand (held in registers for the whole kernel).  In the S^T accumulator
-//    every lane owns ONE query (lane%32) and 16 keys of each 32-key block; the
-//    other 16 keys of that query live in lane^32.  Row max and row sum are therefore
-//    lane-local plus one exchange with lane^32.
-//  * The probabilities stay in registers: the accumulator elements of one lane are
-//    exactly the K-operand a lane must supply for the PV product O^T = V^T P^T (P^T as
-//    the B operand, lane = query), so no cross-lane movement of P is needed.  V^T is
-//    staged in LDS (keys contiguous) by an 8x8 register transpose on the way in, and
-//    each lane reads the eight keys that pair with its P elements.
-//  * FP32 online softmax in base 2 (scale * log2 e folded into one multiply), FP32
-//    accumulation, fp16 output.  K/V tiles of 64 keys are double-buffered in LDS; the
-//    next tile's global loads are in flight during the current tile's math.
-//  * Causal (key j <= query i, the top-left convention of torch SDPA's is_causal): key
-//    tiles beyond the workgroup's last query are never loaded, fully masked tiles are
-//    skipped per wave, and the heaviest query blocks are dispatched first.
+//  * A workgroup owns 256 queries of one (batch, head): 8 waves x 32 queries, two waves
+//    per SIMD, so one wave's softmax (VALU) overlaps the other's matrix work (MFMA).
+//  * K/V tiles of 64 keys travel global -> LDS by buffer_load ... lds DMA into a 4-deep
+//    ring shared by the 8 waves (no VGPR staging); out-of-range keys arrive as zeros.  K
+//    rows and V rows are stored as in memory, XOR-swizzled by 16-byte chunk.
+//  * Scores are computed transposed, S^T = K Q^T, on v_mfma_f32_32x32x16_f16 with K as the
+//    A operand (ds_read_b128) and the wave's Q fragments as the B operand (registers for
+//    the whole kernel): every lane owns one query and 16 keys of each 32-key block (the
+//    other 16 sit in lane ^ 32), so row max and row sum are lane-local plus one exchange.
+//  * The probabilities stay in registers: a lane's score elements are exactly the B operand
+//    it must supply for O^T = V^T P^T.  The matching A operand -- V^T, i.e. 8 keys of one
+//    d column -- comes straight out of the row-major V tile with the gfx950 transposing
+//    read ds_read_b64_tr_b16 (4 keys per read).
+//  * One barrier per tile; the DMA of tile j+3 is issued right after it.
+//  * FP32 online softmax in base 2 (scale * log2 e folded into one FMA per score), with
+//    lazy rescaling: the running max is only moved (and O and the row sum rescaled) when
+//    a row's max grows by more than 2^8 in some lane of the wave, so P stays <= 2^8 in fp16.
+//  * Causal (key j <= query i, top-left aligned as torch SDPA's is_causal): key tiles past
+//    the workgroup's last query are never loaded, tiles past a wave's own last query are
+//    skipped by that wave, masks are applied only on tiles that cross the diagonal or the
+//    end of K, and the heaviest query blocks are dispatched first.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "plan.hpp"
@@ -36,210 +39,336 @@ struct FlashArgs {
     const f16* V;
     f16* O;
     int Sq, Sk;
-    int nqb;          // query blocks
+    int nqb;           // query blocks
     float scale_log2;  // scale * log2(e)
 };
 
-constexpr int FA_WAVES = 4;
-constexpr int FA_BQ = 32 * FA_WAVES;  // 128 queries per workgroup
-constexpr int FA_BKV = 64;            // keys per LDS tile
+constexpr int FA_WAVES = 8;                 // waves per workgroup (two per SIMD)
+constexpr int FA_WQ = 32;                   // queries per wave
+constexpr int FA_NQB = FA_WQ / 32;          // 32-query MFMA blocks per wave
+constexpr int FA_BQ = FA_WAVES * FA_WQ;     // queries per workgroup
+constexpr int FA_BKV = 64;                  // keys per tile
+constexpr int FA_NS = 4;                    // LDS ring depth
 constexpr float kNegInf = -__builtin_huge_valf();
+constexpr float kLazyMax = 8.0f;            // rescale only when a max grows by > 2^8
+
+template <int D>
+struct FaCfg {
+    static constexpr int DCH = D / 8;                  // 16-byte chunks per row
+    static constexpr int NDS = D / 16;                 // d-steps of S^T
+    static constexpr int NDB = D / 32;                 // 32-wide d blocks of O
+    static constexpr int TILE = FA_BKV * D * 2;        // bytes of one K (or V) tile
+    static constexpr int STAGE = 2 * TILE;             // K then V
+    static constexpr int DMA = TILE / 1024 / FA_WAVES; // 1 KB DMA instructions per wave per tile
+    static constexpr int PER_STAGE = 2 * DMA;          // vmcnt per stage
+    static_assert(TILE % (1024 * FA_WAVES) == 0, "DMA split");
+};
+
+// Row swizzles (16-byte chunk index XOR).  K rows are read by ds_read_b128 with 32 lanes
+// on 32 consecutive rows at one chunk; V rows by the transposing read, four consecutive
+// rows at one chunk pair.
+template <int D>
+__device__ __forceinline__ int swz_k(int row) {
+    return D == 128 ? (row & 15) : ((row ^ (row >> 3)) & 7);
+}
+template <int D>
+__device__ __forceinline__ int swz_v(int row) {
+    return D == 128 ? 4 * (row & 3) : 2 * (row & 3);
+}
+
+template <int D>
+struct FaLane {
+    uint32_t k_off[FaCfg<D>::DMA], v_off[FaCfg<D>::DMA];  // DMA source offsets in a tile
+    int k_row[FaCfg<D>::DMA], v_row[FaCfg<D>::DMA];       // key row of each DMA chunk
+    int dma_k, dma_v;                                     // this wave's DMA slice (uniform)
+    int k_addr[2];        // K fragment row base (bytes) for key blocks 0, 1
+    int k_sw[2];          // K swizzle of this lane's row in key blocks 0, 1
+    int v_addr[FaCfg<D>::NDB];  // first transposing-read address per d block
+    int h;                // lane / 32
+};
+
+// DMA of one K/V tile (kleft = valid keys in it; <= 0 loads zeros).
+template <int D>
+__device__ __forceinline__ void fa_dma(WMMA_LDS unsigned char* dst, const FaLane<D>& L,
+                                       __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+                                       int kleft) {
+    constexpr int DMA = FaCfg<D>::DMA;
+#pragma unroll
+    for (int i = 0; i < DMA; ++i)
+        lds_dma16(rk, L.k_row[i] < kleft ? L.k_off[i] : kOobOffset, dst + L.dma_k + i * 1024);
+#pragma unroll
+    for (int i = 0; i < DMA; ++i)
+        lds_dma16(rv, L.v_row[i] < kleft ? L.v_off[i] : kOobOffset,
+                  dst + FaCfg<D>::TILE + L.dma_v + i * 1024);
+}
+
+// S^T += K Q^T for both key blocks and both query blocks of one tile.
+template <int D>
+__device__ __forceinline__ void fa_scores(const WMMA_LDS unsigned char* s, const FaLane<D>& L,
+                                          const f16x8 (&qf)[FA_NQB][FaCfg<D>::NDS],
+                                          f32x16 (&S)[2][FA_NQB]) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < FA_NQB; ++qb) S[kb][qb] = f32x16{};
+#pragma unroll
+    for (int ds = 0; ds < FaCfg<D>::NDS; ++ds) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const int c = (2 * ds + L.h) ^ L.k_sw[kb];
+            const f16x8 kf = as_f16x8(*(const WMMA_LDS u32x4*)(s + L.k_addr[kb] + (c << 4)));
+#pragma unroll
+            for (int qb = 0; qb < FA_NQB; ++qb) S[kb][qb] = mfma32(kf, qf[qb][ds], S[kb][qb]);
+        }
+    }
+}
+
+// Online softmax of one tile for both query blocks.  Returns (through `resc`) whether O
+// must be rescaled before this tile's PV product, and the per-query factors in `alpha`.
+// Sets masked scores (keys past Sk or, causal, past the query) to -inf.
+__device__ __forceinline__ void fa_mask(f32x16 (&S)[2][FA_NQB], int kv0, int qrow0, int Sk,
+                                        bool causal, int h) {
+#pragma unroll
+    for (int qb = 0; qb < FA_NQB; ++qb) {
+        const int q = qrow0 + 32 * qb;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = kv0 + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
+                const bool ok = key < Sk && (!causal || key <= q);
+                S[kb][qb][r] = ok ? S[kb][qb][r] : kNegInf;
+            }
+    }
+}
+
+__device__ __forceinline__ void fa_softmax(f32x16 (&S)[2][FA_NQB], float c, float (&m_run)[FA_NQB],
+                                           float (&l_run)[FA_NQB], float (&alpha)[FA_NQB], bool& resc,
+                                           f16x8 (&P)[2][2][FA_NQB]) {
+    float mloc[FA_NQB];
+#pragma unroll
+    for (int qb = 0; qb < FA_NQB; ++qb) {
+        float mx = kNegInf;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, S[kb][qb][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mloc[qb] = mx * c;  // c > 0: max of the scaled scores
+    }
+    // Lazy rescale decision (wave-uniform).
+    bool need = false;
+#pragma unroll
+    for (int qb = 0; qb < FA_NQB; ++qb) need |= mloc[qb] > m_run[qb] + kLazyMax;
+    resc = __builtin_amdgcn_ballot_w64(need) != 0;
+#pragma unroll
+    for (int qb = 0; qb < FA_NQB; ++qb) {
+        // Selects, not branches, so the softmax stays one basic block.  A running max of
+        // -inf (no key seen yet) gives alpha = 0 and keeps exp2's argument finite.
+        const float mn = resc ? fmaxf(m_run[qb], mloc[qb]) : m_run[qb];
+        const float a = m_run[qb] == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(m_run[qb] - mn);
+        alpha[qb] = resc ? a : 1.0f;
+        m_run[qb] = mn;
+        l_run[qb] *= alpha[qb];
+        const float m = m_run[qb] == kNegInf ? 0.0f : m_run[qb];
+        float sum = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kb][qb][8 * hh + e], c, -m));
+                    sum += pv;
+                    P[kb][hh][qb][e] = (f16)pv;
+                }
+        l_run[qb] += sum;
+    }
+}
+
+// O^T += V^T P^T over the tile's four 16-key steps.
+template <int D>
+__device__ __forceinline__ void fa_pv(const WMMA_LDS unsigned char* s, const FaLane<D>& L,
+                                      const f16x8 (&P)[2][2][FA_NQB],
+                                      f32x16 (&O)[FaCfg<D>::NDB][FA_NQB]) {
+    constexpr int RB = D * 2;  // bytes per V row
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+        for (int db = 0; db < FaCfg<D>::NDB; ++db) {
+            const WMMA_LDS unsigned char* pv = s + FaCfg<D>::TILE + L.v_addr[db] + 16 * ks * RB;
+            const f16x4 lo = lds_read_tr16(pv);
+            const f16x4 hi = lds_read_tr16(pv + 8 * RB);
+            const f16x8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+            for (int qb = 0; qb < FA_NQB; ++qb) O[db][qb] = mfma32(vf, P[ks >> 1][ks & 1][qb], O[db][qb]);
+        }
+    }
+}
+
+// One main-loop iteration (tile j): barrier (tile j resident and visible in every wave,
+// tile j-1's buffer free), DMA of tile j+3 into that buffer, then S^T, softmax and PV of
+// tile j.  The two buffers are distinct and passed as __restrict__ so the compiler keeps
+// the DMA in flight across the LDS reads; the true DMA -> read ordering is the explicit
+// vmcnt wait + barrier.
+template <int D, bool CAUSAL>
+__device__ __forceinline__ void fa_iter(const WMMA_LDS unsigned char* __restrict__ cur,
+                                        WMMA_LDS unsigned char* __restrict__ dst,
+                                        const FaLane<D>& L, __amdgpu_buffer_rsrc_t rk,
+                                        __amdgpu_buffer_rsrc_t rv, int kleft_dma,
+                                        const f16x8 (&qf)[FA_NQB][FaCfg<D>::NDS],
+                                        f32x16 (&O)[FaCfg<D>::NDB][FA_NQB], float (&m_run)[FA_NQB],
+                                        float (&l_run)[FA_NQB], float c, int kv0, int qrow0, int Sk,
+                                        bool live, bool masked) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads are done
+    wait_vmcnt<(FA_NS - 2) * FaCfg<D>::PER_STAGE>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    fa_dma<D>(dst, L, rk, rv, kleft_dma);
+    if (!live) return;  // causal: every key of this tile is past this wave's queries
+
+    f32x16 S[2][FA_NQB];
+    fa_scores<D>(cur, L, qf, S);
+    if (masked) fa_mask(S, kv0, qrow0, Sk, CAUSAL, L.h);
+    float alpha[FA_NQB];
+    bool resc;
+    f16x8 P[2][2][FA_NQB];
+    fa_softmax(S, c, m_run, l_run, alpha, resc, P);
+    if (resc) {
+#pragma unroll
+        for (int db = 0; db < FaCfg<D>::NDB; ++db)
+#pragma unroll
+            for (int qb = 0; qb < FA_NQB; ++qb) O[db][qb] *= alpha[qb];
+    }
+    fa_pv<D>(cur, L, P, O);
+}
 
 template <int D, bool CAUSAL>
 __global__ void __launch_bounds__(FA_WAVES * kWave)
+__attribute__((amdgpu_waves_per_eu(FA_WAVES / 4, FA_WAVES / 4)))
 flash_fwd_kernel(FlashArgs p) {
-    constexpr int DCH = D / 8;                 // 16-byte chunks per K row
-    constexpr int K_CH = FA_BKV * DCH;         // chunks per K tile
-    constexpr int VT_CH = D * (FA_BKV / 8);    // chunks per V^T tile (8 per d row)
-    constexpr int NDB = D / 32;                // 32-wide d blocks of O
-    constexpr int NDS = D / 16;                // 16-deep d steps of QK^T
-    constexpr int NT = FA_WAVES * kWave;
-    // loaders: threads [0,VT_THREADS) transpose V 8x8 blocks, the rest copy K chunks.
-    constexpr int V_BLOCKS = (FA_BKV / 8) * (D / 8);
-    constexpr int VT_THREADS = V_BLOCKS;                // one block per thread
-    constexpr int K_THREADS = NT - VT_THREADS;
-    constexpr int K_PER = (K_CH + K_THREADS - 1) / K_THREADS;
-    static_assert(VT_THREADS < NT, "loader split");
-    static_assert(K_PER <= 8, "loader registers");
+    using C = FaCfg<D>;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[FA_NS * C::STAGE];
+    WMMA_LDS unsigned char* lds = (WMMA_LDS unsigned char*)smem;
 
-    __shared__ u32x4 sk[2][K_CH];
-    __shared__ u32x4 sv[2][VT_CH];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = lane >> 5, c32 = lane & 31;
     const int bh = blockIdx.x;
-    const int qb = CAUSAL ? (p.nqb - 1 - (int)blockIdx.y) : (int)blockIdx.y;
-    const int q0 = qb * FA_BQ;
-    const int qw = q0 + wave * 32;
+    const int qb_idx = CAUSAL ? (p.nqb - 1 - (int)blockIdx.y) : (int)blockIdx.y;
+    const int q0 = qb_idx * FA_BQ;
+    const int qw = q0 + wave * FA_WQ;
     const int Sq = p.Sq, Sk = p.Sk;
+    const float c = p.scale_log2;
 
     const f16* Qb = p.Q + (int64_t)bh * Sq * D;
     const f16* Kb = p.K + (int64_t)bh * Sk * D;
     const f16* Vb = p.V + (int64_t)bh * Sk * D;
     f16* Ob = p.O + (int64_t)bh * Sq * D;
 
-    // Q fragments (B operand): query qw + lane%32, d = 16*s + 8*h + 0..7.
-    f16x8 qf[NDS];
+    // Q fragments (B operand of S^T): query qw + 32 qb + lane%32, d = 16 ds + 8 h + 0..7.
+    f16x8 qf[FA_NQB][C::NDS];
     {
         const __amdgpu_buffer_rsrc_t rs = make_rsrc(Qb);
-        const int q = qw + c32;
 #pragma unroll
-        for (int s = 0; s < NDS; ++s)
-            qf[s] = as_f16x8(buf_load16(
-                rs, q < Sq ? (uint32_t)(((int64_t)q * D + 16 * s + 8 * h) * 2) : kOobOffset));
+        for (int qb = 0; qb < FA_NQB; ++qb) {
+            const int q = qw + 32 * qb + c32;
+#pragma unroll
+            for (int ds = 0; ds < C::NDS; ++ds)
+                qf[qb][ds] = as_f16x8(buf_load16(
+                    rs, q < Sq ? (uint32_t)(((int64_t)q * D + 16 * ds + 8 * h) * 2) : kOobOffset));
+        }
     }
 
-    f32x16 o[NDB];
+    FaLane<D> L;
+    L.h = h;
+    L.dma_k = wave * (C::DMA * 1024);
+    L.dma_v = wave * (C::DMA * 1024);
 #pragma unroll
-    for (int i = 0; i < NDB; ++i) o[i] = f32x16{};
-    float m_run = kNegInf, l_run = 0.0f;
+    for (int i = 0; i < C::DMA; ++i) {
+        const int P = 64 * (wave * C::DMA + i) + lane;
+        const int row = P / C::DCH, pc = P % C::DCH;
+        L.k_row[i] = row;
+        L.k_off[i] = (uint32_t)((row * D + 8 * (pc ^ swz_k<D>(row))) * 2);
+        L.v_row[i] = row;
+        L.v_off[i] = (uint32_t)((row * D + 8 * (pc ^ swz_v<D>(row))) * 2);
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        L.k_addr[kb] = (32 * kb + c32) * (D * 2);
+        L.k_sw[kb] = swz_k<D>(32 * kb + c32);
+    }
+    {
+        // transposing-read source lane s = 4 jj + aa of 16-lane group g: V row
+        // 4 (g / 2) + jj (+8 for the upper half, +16 per key step), columns
+        // 32 db + 16 (g % 2) + 4 aa .. +3.
+        const int g = lane >> 4, s16 = lane & 15, jj = s16 >> 2, aa = s16 & 3;
+        const int row = 4 * (g >> 1) + jj;
+        const int sw = swz_v<D>(row);
+#pragma unroll
+        for (int db = 0; db < C::NDB; ++db) {
+            const int col = 32 * db + 16 * (g & 1) + 4 * aa;
+            L.v_addr[db] = row * (D * 2) + (((col >> 3) ^ sw) << 4) + ((col & 7) << 1);
+        }
+    }
 
     const int kv_end = CAUSAL ? min(Sk, q0 + FA_BQ) : Sk;
-    const int nkv = (kv_end + FA_BKV - 1) / FA_BKV;
-
-    u32x4 pre[8];
-    auto gload = [&](int kv0) {
-        if (tid < VT_THREADS) {
-            const int kb8 = tid / (D / 8), db8 = tid % (D / 8);
-            const __amdgpu_buffer_rsrc_t rs = make_rsrc(Vb);
-#pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                const int key = kv0 + kb8 * 8 + r;
-                pre[r] = buf_load16(rs, key < Sk ? (uint32_t)(((int64_t)key * D + db8 * 8) * 2)
-                                                 : kOobOffset);
-            }
-        } else {
-            const __amdgpu_buffer_rsrc_t rs = make_rsrc(Kb);
-#pragma unroll
-            for (int i = 0; i < K_PER; ++i) {
-                const int c = (tid - VT_THREADS) + i * K_THREADS;
-                const int key = kv0 + c / DCH, ch = c % DCH;
-                if (K_CH % K_THREADS == 0 || c < K_CH)
-                    pre[i] = buf_load16(rs, key < Sk ? (uint32_t)(((int64_t)key * D + ch * 8) * 2)
-                                                     : kOobOffset);
-            }
-        }
-    };
-    auto sstore = [&](int buf) {
-        if (tid < VT_THREADS) {
-            const int kb8 = tid / (D / 8), db8 = tid % (D / 8);
-            u32x4 t[8];
-            transpose8x8(pre, t);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int d = db8 * 8 + j;
-                sv[buf][d * 8 + (kb8 ^ swz8(d))] = t[j];
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < K_PER; ++i) {
-                const int c = (tid - VT_THREADS) + i * K_THREADS;
-                const int key = c / DCH, ch = c % DCH;
-                if (K_CH % K_THREADS == 0 || c < K_CH) sk[buf][key * DCH + (ch ^ swz8(key))] = pre[i];
-            }
-        }
+    const int T = (kv_end + FA_BKV - 1) / FA_BKV;
+    // Tiles this wave needs (causal: keys <= its last query).
+    const int Tw = CAUSAL ? min(T, (qw + FA_WQ - 1) / FA_BKV + 1) : T;
+    auto rk_of = [&](int t) { return make_rsrc(Kb + (int64_t)min(t, T - 1) * FA_BKV * D); };
+    auto rv_of = [&](int t) { return make_rsrc(Vb + (int64_t)min(t, T - 1) * FA_BKV * D); };
+    auto kleft = [&](int t) { return t < T ? Sk - t * FA_BKV : 0; };
+    // A tile needs masking if it reaches past Sk or (causal) past this wave's first query.
+    auto masked = [&](int t) {
+        const int kv0 = t * FA_BKV;
+        return kv0 + FA_BKV > Sk || (CAUSAL && kv0 + FA_BKV - 1 > qw);
     };
 
-    if (nkv > 0) {
-        gload(0);
-        sstore(0);
+    f32x16 O[C::NDB][FA_NQB];
+#pragma unroll
+    for (int db = 0; db < C::NDB; ++db)
+#pragma unroll
+        for (int qb = 0; qb < FA_NQB; ++qb) O[db][qb] = f32x16{};
+    float m_run[FA_NQB], l_run[FA_NQB];
+#pragma unroll
+    for (int qb = 0; qb < FA_NQB; ++qb) {
+        m_run[qb] = kNegInf;
+        l_run[qb] = 0.0f;
     }
-    __syncthreads();
+    const int qrow0 = qw + c32;
 
-    const int myq = qw + c32;
-    for (int j = 0; j < nkv; ++j) {
-        const int cur = j & 1;
-        const int kv0 = j * FA_BKV;
-        const bool more = j + 1 < nkv;
-        if (more) gload(kv0 + FA_BKV);
-
-        const bool active = !CAUSAL || kv0 <= qw + 31;
-        if (active) {
-            // S^T = K Q^T for two 32-key sub-blocks.
-            f32x16 s[2] = {f32x16{}, f32x16{}};
+    if (T > 0) {
+        // Prologue: tiles 0 .. NS-2 in flight (tiles past the end load zeros).
 #pragma unroll
-            for (int ds = 0; ds < NDS; ++ds) {
-                const int ch = 2 * ds + h;
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-                    const int key = kb * 32 + c32;
-                    const f16x8 kf = as_f16x8(sk[cur][key * DCH + (ch ^ swz8(key))]);
-                    s[kb] = mfma32(kf, qf[ds], s[kb]);
-                }
-            }
-            // scale, mask, running max
-            float mloc = kNegInf;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = kv0 + kb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                    bool ok = key < Sk;
-                    if (CAUSAL) ok = ok && key <= myq;
-                    const float x = ok ? s[kb][r] * p.scale_log2 : kNegInf;
-                    s[kb][r] = x;
-                    mloc = fmaxf(mloc, x);
-                }
-            }
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-            const float m_new = fmaxf(m_run, mloc);
-            const float m_use = m_new == kNegInf ? 0.0f : m_new;
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-            m_run = m_new;
-            float lsum = 0.0f;
-            f16x8 pf[2][2];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float pv = __builtin_amdgcn_exp2f(s[kb][8 * hh + e] - m_use);
-                        lsum += pv;
-                        pf[kb][hh][e] = (f16)pv;
-                    }
-                }
-            }
-            l_run = l_run * alpha + lsum;
-#pragma unroll
-            for (int i = 0; i < NDB; ++i) o[i] *= alpha;
-            // O^T += V^T P^T.  MFMA (kb, hh) pairs element e of lane half h with key
-            // kb*32 + 16*hh + 4*h + (e < 4 ? e : e + 4).
-#pragma unroll
-            for (int db = 0; db < NDB; ++db) {
-                const int d = db * 32 + c32;
-                const u32x4* row = &sv[cur][d * 8];
-                const int sw = swz8(d);
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
-                        const int ch0 = 4 * kb + 2 * hh;  // chunk of keys base..base+7
-                        const u32x2 lo = reinterpret_cast<const u32x2*>(&row[ch0 ^ sw])[h];
-                        const u32x2 hi = reinterpret_cast<const u32x2*>(&row[(ch0 + 1) ^ sw])[h];
-                        const f16x8 vf = as_f16x8(u32x4{lo[0], lo[1], hi[0], hi[1]});
-                        o[db] = mfma32(vf, pf[kb][hh], o[db]);
-                    }
-                }
-            }
+        for (int s = 0; s < FA_NS - 1; ++s) fa_dma<D>(lds + s * C::STAGE, L, rk_of(s), rv_of(s), kleft(s));
+        for (int t = 0; t < T; ++t) {
+            const int tf = t + FA_NS - 1;
+            fa_iter<D, CAUSAL>(lds + (t % FA_NS) * C::STAGE, lds + (tf % FA_NS) * C::STAGE, L,
+                               rk_of(tf), rv_of(tf), kleft(tf), qf, O, m_run, l_run, c,
+                               t * FA_BKV, qrow0, Sk, t < Tw, masked(t));
         }
-        if (more) sstore(cur ^ 1);
-        __syncthreads();
+        wait_vmcnt<0>();
     }
 
-    // normalise and store: lane owns query myq, d = 32*db + 8*(r/4) + 4*h + r%4.
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (myq < Sq) {
+    // Normalise and store: lane owns query qw + 32 qb + lane%32, d = 32 db + 8 (r/4) +
+    // 4 h + r%4.
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
+    for (int qb = 0; qb < FA_NQB; ++qb) {
+        const int q = qrow0 + 32 * qb;
+        const float l_tot = l_run[qb] + __shfl_xor(l_run[qb], 32);
+        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        if (q < Sq) {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                f16x4 v;
+            for (int db = 0; db < C::NDB; ++db) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = (f16)(o[db][4 * g + e] * inv);
-                const int d = db * 32 + 8 * g + 4 * h;
-                *reinterpret_cast<f16x4*>(Ob + (int64_t)myq * D + d) = v;
+                for (int g = 0; g < 4; ++g) {
+                    f16x4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = (f16)(O[db][qb][4 * g + e] * inv);
+                    const int d = 32 * db + 8 * g + 4 * h;
+                    *reinterpret_cast<f16x4*>(Ob + (int64_t)q * D + d) = v;
+                }
             }
         }
     }
