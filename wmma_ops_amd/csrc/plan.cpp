@@ -82,7 +82,10 @@ int make_plan(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* ou
     p.tile_n = t.bn;
     int tiles = ceil_div(M, t.bm) * ceil_div(N, t.bn);
     int split = 1;
-    if (tiles > 0 && tiles * 2 <= num_cus && K >= 512) {
+    // Split K only when the chip is under-filled and the GEMM is big enough (>= 2^30
+    // multiply-adds) for the extra reduction launch to pay for itself.
+    if (tiles > 0 && tiles * 2 <= num_cus && K >= 512 &&
+        (int64_t)M * N * K >= (int64_t(1) << 30)) {
         split = std::min({num_cus / tiles, K / 256, kMaxSplitK});
         split = std::max(split, 1);
     }
