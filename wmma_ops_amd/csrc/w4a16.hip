@@ -114,6 +114,7 @@ struct W4Args {
     float* ws;            // partials [split][M][N]
     int split;
     int kc_per_split;     // 64-deep chunks per split
+    int pp_shift;         // decode-MFMA kernel: log2(G / 128)
 };
 
 // Per-lane group parameters: zs = (1024 + z, 1024 + z), ss = (s, s) as packed fp16 pairs.
@@ -438,10 +439,26 @@ w4a16_decode_kernel(W4Args p) {
     }
 }
 
-// --------------------------------------------- decode on the matrix pipe (M <= 16) --
-// Same data movement as w4a16_decode_kernel (one workgroup per 16-column slice, all 64
-// lanes of a wave load 1 KB of prepacked weights: slice column l%16, K run (l/16) of a
-// 128-deep pair-step), but the multiply-accumulate runs on v_mfma_f32_16x16x32_f16:
+// ---------------------------------------------- decode on the matrix pipe (M <= 4) --
+// One workgroup per 16-column slice (half of a 32-column prepacked tile) over the whole K
+// range, so no cross-workgroup reduction.  A wave load covers one 128-deep pair-step pp:
+// lane l reads slice column l%16, chunk 2*pp + l/32, K half (l/16)%2 -- 1 KB per
+// instruction in 256-byte runs.  Wave w owns pair-steps w + DM_NW * j; a round is DM_U of
+// them.
+//
+// Every wave is self-contained until the final cross-wave sum: it loads the activations of
+// ITS pair-steps only (lane l: chunk l%16 of pair-step l/16 of the round, one 16-byte load
+// per activation row), then the round's scales and zeros (ONE load each: lane l fetches
+// pair-step l/16 at column l%16; a lane shuffle later hands each lane its own), then the
+// DM_U weight loads, and stages its activations in a private LDS region.  No barrier sits
+// between a wave's loads and its MFMAs, so each wave computes as soon as its own data has
+// landed -- under a saturated memory system the waves of one workgroup finish issuing
+// their loads microseconds apart.  Vector loads return in order, so the activations and
+// group parameters are waited on before the weights, and pair-step u's MFMAs wait for
+// weight load u only.  Every load is unconditional (indices clamped into range): the code
+// is straight-line and each wait covers exactly the loads it needs.
+//
+// The multiply-accumulate runs on v_mfma_f32_16x16x32_f16:
 //   A operand (lane l: row l%16 = activation row m, K quarter l/16): the activations a',
 //     where a' = a at offsets {0,1,4,5} and a/16 at {2,3,6,7} of every 8 values;
 //   B operand (lane l: column l%16 = slice column n, same K quarter): the dequantised
@@ -452,147 +469,148 @@ w4a16_decode_kernel(W4Args p) {
 //     fp16(16 (q - z) s) = 16 W exactly (a power-of-two scale commutes with rounding),
 //     which the a/16 of the A operand cancels.  One shift, four v_and_or, four v_pk_add
 //     and four v_pk_mul per 8 weights, no shifts per nibble.
-// The accumulator runs over every group; only the final cross-wave sum remains.
-// Requires G % 128 == 0 (a pair-step never straddles two groups).
-// D layout: lane l holds column n = l%16 and rows m = 4*(l/16) + r (r < RR = ceil(M/4)).
+// The accumulator runs over every group; the eight waves' partials meet in LDS at the end.
+// Requires G = 128 * 2^j (a pair-step never straddles two groups).
+// D layout: lane l holds column n = l%16 and rows m = 4*(l/16) + r; rows 0..3 live in
+// lanes 0..15.
 constexpr int DM_NW = 8;
 constexpr int DM_U = 4;
+constexpr int DM_MAXM = 4;
+// LDS row stride (halves) of a wave's staged activations: DM_U pair-steps of 128 values
+// plus 16 bytes, so rows fall on different banks.
+constexpr int DM_ROW = DM_U * 128 + 8;
 
+template <int MM>
 struct DecodeMRound {
-    u32x4 w[DM_U];
-    uint32_t s[DM_U], z[DM_U];
+    u32x4 a[MM];    // activations: row m, pair-step l/16 of the round, chunk l%16
+    u32x4 w[DM_U];  // weights of pair-steps u
+    uint32_t s, z;  // raw scale / zero of (pair-step l/16 of the round, column l%16)
 };
 
-// LDS row stride (halves) of the staged activations: K plus 16 bytes, so the 16 rows
-// read by one MFMA operand fall on distinct banks.
-__host__ __device__ inline int dm_row(int K) { return K + 8; }
-size_t decode_mfma_lds_bytes(int M, int K) { return (size_t)M * dm_row(K) * 2; }
+// Staging buffers per wave: one when a single round covers K, else two (rounds alternate).
+__host__ __device__ constexpr int dm_nbuf(bool one) { return one ? 1 : 2; }
+bool decode_mfma_one(int K) { return K <= DM_NW * DM_U * 128; }
+size_t decode_mfma_lds_bytes(int M, int K) {
+    return (size_t)dm_nbuf(decode_mfma_one(K)) * DM_NW * M * DM_ROW * 2;
+}
 
-template <int ZF, bool ONE, int RR>
+// ONE: K <= DM_NW * DM_U * 128 -- a single round per wave, no second register set, so
+// the kernel fits 64 VGPRs and eight waves per SIMD stay resident.
+template <int ZF, bool ONE, int MM>
 __global__ void __launch_bounds__(DM_NW * kWave)
 __attribute__((amdgpu_waves_per_eu(ONE ? 8 : 4)))
 w4a16_decode_mfma_kernel(W4Args p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char dm_smem[];
-    const int K = p.K, M = p.M, RS = dm_row(K);
-    f16* sA = reinterpret_cast<f16*>(dm_smem);  // [M][RS] a'
-    __shared__ float red[DM_NW][16][16];
+    __shared__ float red[DM_NW][DM_MAXM][16];
+    const int K = p.K;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nt = blockIdx.x >> 1, sc = blockIdx.x & 1;
+    // Slice of this workgroup: each XCD walks a contiguous run of slices, so the four
+    // slices that share a 128-byte line of scales are served by one L2.
+    const int slice = xcd_remap(blockIdx.x, gridDim.x);
+    const int nt = slice >> 1, sc = slice & 1;
     const int col = lane & 15, sub = lane >> 4, dc = sub >> 1, h = sub & 1;
     const int n = 32 * nt + 16 * sc + col;
     const int KC = K / 64, KP = KC / 2;
-    const int cpr = K / 8, nchunk = M * cpr;
-
-    // Activation chunks first (see w4a16_decode_kernel).
-    constexpr int ABUF = 2;
-    u32x4 abuf[ABUF];
-#pragma unroll
-    for (int j = 0; j < ABUF; ++j) {
-        const int i = tid + j * DM_NW * kWave;
-        if (i < nchunk) {
-            const int m = i / cpr, c = i - m * cpr;
-            abuf[j] = *reinterpret_cast<const u32x4*>(p.A + (int64_t)m * p.lda + 8 * c);
-        }
-    }
+    // Staging buffers of this wave, each [MM][DM_ROW] halves.
+    f16* sbuf = reinterpret_cast<f16*>(dm_smem) + (size_t)wave * dm_nbuf(ONE) * MM * DM_ROW;
 
     const u32x4* wcol = p.W + (int64_t)nt * KC * 64 + 32 * h + 16 * sc + col;
-    auto load_one = [&](int pp, DecodeMRound& R, int u) {
-        R.w[u] = __builtin_nontemporal_load(wcol + (int64_t)(2 * pp + dc) * 64);
-        group_load<ZF>(p, (128 * pp) / p.G, n, &R.s[u], &R.z[u]);
-    };
-    auto load_round = [&](int r, DecodeMRound& R) {
-        const int pp0 = wave + DM_NW * DM_U * r;
-        if (pp0 + DM_NW * (DM_U - 1) < KP) {
+    auto load_round = [&](int r, DecodeMRound<MM>& R) {
+        // this lane's activation chunk / group parameters: pair-step `sub` of the round
+        const int ppl = min(wave + DM_NW * (DM_U * r + sub), KP - 1);
+        const int ka = 128 * ppl + 8 * col;
 #pragma unroll
-            for (int u = 0; u < DM_U; ++u) load_one(pp0 + DM_NW * u, R, u);
-        } else {
+        for (int m = 0; m < MM; ++m)
+            R.a[m] = *reinterpret_cast<const u32x4*>(p.A + (int64_t)m * p.lda + ka);
+        const int g = ppl >> p.pp_shift;  // G = 128 << pp_shift
+        R.s = __builtin_bit_cast(uint16_t, p.S[(int64_t)g * p.N + n]);
+        if constexpr (ZF == WMMA_ZEROS_PACKED)
+            R.z = (uint32_t)static_cast<const int32_t*>(p.Z)[(int64_t)g * (p.N / 8) + n / 8];
+        else
+            R.z = static_cast<const uint8_t*>(p.Z)[(int64_t)g * p.N + n];
 #pragma unroll
-            for (int u = 0; u < DM_U; ++u)
-                if (pp0 + DM_NW * u < KP) load_one(pp0 + DM_NW * u, R, u);
+        for (int u = 0; u < DM_U; ++u) {
+            const int pp = min(wave + DM_NW * (DM_U * r + u), KP - 1);
+            R.w[u] = __builtin_nontemporal_load(wcol + (int64_t)(2 * pp + dc) * 64);
         }
     };
-    const int rounds = ONE ? 1 : (KP - wave + DM_NW * DM_U - 1) / (DM_NW * DM_U);
-    DecodeMRound R0, R1;
-    load_round(0, R0);
 
-    // Stage a' (chunk i = 8 activations of row m).
-    auto stage_chunk = [&](int i, u32x4 v) {
-        const int m = i / cpr, c = i - m * cpr;
-        f16x8 a = as_f16x8(v);
-#pragma unroll
-        for (int e = 2; e < 8; e += 4) {
-            a[e] = a[e] * (f16)0.0625f;
-            a[e + 1] = a[e + 1] * (f16)0.0625f;
-        }
-        *reinterpret_cast<u32x4*>(sA + m * RS + 8 * c) = as_u32x4(a);
-    };
-#pragma unroll
-    for (int j = 0; j < ABUF; ++j) {
-        const int i = tid + j * DM_NW * kWave;
-        if (i < nchunk) stage_chunk(i, abuf[j]);
-    }
-    for (int i = tid + ABUF * DM_NW * kWave; i < nchunk; i += DM_NW * kWave) {
-        const int m = i / cpr, c = i - m * cpr;
-        stage_chunk(i, *reinterpret_cast<const u32x4*>(p.A + (int64_t)m * p.lda + 8 * c));
-    }
-    __syncthreads();
-
-    // A-operand row of this lane (rows >= M read row 0; those output rows are unused).
-    const f16* arow = sA + (col < M ? col : 0) * RS;
     uint32_t magic = 0x64006400u;
     asm volatile("" : "+v"(magic));  // keep the constant in a VGPR: one v_and_or per pair
     f32x4 d{};
-    auto compute_one = [&](int pp, const DecodeMRound& R, int u) {
-        const int k0 = 128 * pp + 64 * dc + 32 * h;
+    const int am = col < MM ? col : 0;  // A-operand row (rows >= M repeat row 0, unused)
+    auto compute_round = [&](int r, const DecodeMRound<MM>& R, f16* buf) {
+        // stage a' (this lane's chunk of every row)
+#pragma unroll
+        for (int m = 0; m < MM; ++m) {
+            f16x8 a = as_f16x8(R.a[m]);
+#pragma unroll
+            for (int e = 2; e < 8; e += 4) {
+                a[e] = a[e] * (f16)0.0625f;
+                a[e + 1] = a[e + 1] * (f16)0.0625f;
+            }
+            *reinterpret_cast<u32x4*>(buf + m * DM_ROW + 128 * sub + 8 * col) = as_u32x4(a);
+        }
+        uint32_t rs = R.s, rz = R.z;
+        asm volatile("" : "+v"(rs), "+v"(rz));  // no work on them hoisted up to their load
         uint32_t z;
         if constexpr (ZF == WMMA_ZEROS_PACKED)
-            z = (R.z[u] >> (4 * (n & 7))) & 0xFu;
+            z = (rz >> (4 * (n & 7))) & 0xFu;
         else
-            z = R.z[u] & 0xFu;
-        const uint32_t z1 = 0x6400u | z, z16 = 0x6400u | (z << 4);
-        const f16x2 zs1 = as_h2(z1 | (z1 << 16)), zs16 = as_h2(z16 | (z16 << 16));
-        const f16x2 ss = as_h2(R.s[u] | (R.s[u] << 16));
+            z = rz & 0xFu;
+        const int sz = (int)(rs | (z << 16));
+        const f16* arow = buf + am * DM_ROW + 32 * sub;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const uint32_t x = R.w[u][w], x8 = x >> 8;
-            u32x4 bv;
-            bv[0] = as_u32((as_h2((x & 0x000F000Fu) | magic) - zs1) * ss);
-            bv[1] = as_u32((as_h2((x & 0x00F000F0u) | magic) - zs16) * ss);
-            bv[2] = as_u32((as_h2((x8 & 0x000F000Fu) | magic) - zs1) * ss);
-            bv[3] = as_u32((as_h2((x8 & 0x00F000F0u) | magic) - zs16) * ss);
-            const f16x8 av = as_f16x8(*reinterpret_cast<const u32x4*>(arow + k0 + 8 * w));
-            d = mfma16(av, as_f16x8(bv), d);
-        }
-    };
-    auto compute_round = [&](int r, const DecodeMRound& R) {
-        const int pp0 = wave + DM_NW * DM_U * r;
-        if (pp0 + DM_NW * (DM_U - 1) < KP) {
+        for (int u = 0; u < DM_U; ++u) {
+            const uint32_t v = (uint32_t)__shfl(sz, 16 * u + col);
+            const int pp = wave + DM_NW * (DM_U * r + u);
+            if (pp < KP) {
+                const uint32_t zz = v >> 16, s = v & 0xFFFFu;
+                const uint32_t z1 = 0x6400u | zz, z16 = 0x6400u | (zz << 4);
+                const f16x2 zs1 = as_h2(z1 | (z1 << 16)), zs16 = as_h2(z16 | (z16 << 16));
+                const f16x2 ss = as_h2(s | (s << 16));
 #pragma unroll
-            for (int u = 0; u < DM_U; ++u) compute_one(pp0 + DM_NW * u, R, u);
-        } else {
-#pragma unroll
-            for (int u = 0; u < DM_U; ++u)
-                if (pp0 + DM_NW * u < KP) compute_one(pp0 + DM_NW * u, R, u);
-        }
-    };
-    if constexpr (ONE) {
-        compute_round(0, R0);
-    } else {
-        for (int r = 0; r < rounds; r += 2) {
-            if (r + 1 < rounds) load_round(r + 1, R1);
-            compute_round(r, R0);
-            if (r + 1 < rounds) {
-                if (r + 2 < rounds) load_round(r + 2, R0);
-                compute_round(r + 1, R1);
+                for (int w = 0; w < 4; ++w) {
+                    const uint32_t x = R.w[u][w], x8 = x >> 8;
+                    u32x4 bv;
+                    bv[0] = as_u32((as_h2((x & 0x000F000Fu) | magic) - zs1) * ss);
+                    bv[1] = as_u32((as_h2((x & 0x00F000F0u) | magic) - zs16) * ss);
+                    bv[2] = as_u32((as_h2((x8 & 0x000F000Fu) | magic) - zs1) * ss);
+                    bv[3] = as_u32((as_h2((x8 & 0x00F000F0u) | magic) - zs16) * ss);
+                    const f16x8 av = as_f16x8(*reinterpret_cast<const u32x4*>(arow + 128 * u + 8 * w));
+                    d = mfma16(av, as_f16x8(bv), d);
+                }
             }
         }
+    };
+
+    if constexpr (ONE) {
+        DecodeMRound<MM> R0;
+        load_round(0, R0);
+        compute_round(0, R0, sbuf);
+    } else {
+        // Round r+1 in flight while round r is computed; straight-line body (the loads
+        // past the last round are clamped re-loads of it).  Staging buffers alternate, so
+        // a wave's LDS writes for round r+1 never race its reads of round r.
+        const int rounds = (KP - wave + DM_NW * DM_U - 1) / (DM_NW * DM_U);
+        DecodeMRound<MM> R0, R1;
+        load_round(0, R0);
+        load_round(1, R1);
+        for (int r = 0; r < rounds; r += 2) {
+            compute_round(r, R0, sbuf);
+            load_round(r + 2, R0);
+            if (r + 1 < rounds) compute_round(r + 1, R1, sbuf + MM * DM_ROW);
+            load_round(r + 3, R1);
+        }
     }
-    // d[r]: activation row 4*sub + r, slice column col.
+    // Rows 0..3 are d[0..3] of lanes 0..15.
+    if (sub == 0) {
 #pragma unroll
-    for (int r = 0; r < RR; ++r) red[wave][4 * sub + r][col] = d[r];
+        for (int q = 0; q < DM_MAXM; ++q) red[wave][q][col] = d[q];
+    }
     __syncthreads();
-    if (tid < 16 * M) {
+    if (tid < 16 * MM) {
         const int m = tid >> 4, c = tid & 15;
         float v = red[0][m][c];
 #pragma unroll
@@ -604,7 +622,7 @@ w4a16_decode_mfma_kernel(W4Args p) {
 template <int ZF, bool ONE>
 void launch_decode_mfma(const W4Args& a, int M, dim3 grid, dim3 block, size_t lds,
                         hipStream_t stream) {
-    switch ((M + 3) / 4) {
+    switch (M) {
         case 1: hipLaunchKernelGGL((w4a16_decode_mfma_kernel<ZF, ONE, 1>), grid, block, lds, stream, a); break;
         case 2: hipLaunchKernelGGL((w4a16_decode_mfma_kernel<ZF, ONE, 2>), grid, block, lds, stream, a); break;
         case 3: hipLaunchKernelGGL((w4a16_decode_mfma_kernel<ZF, ONE, 3>), grid, block, lds, stream, a); break;
@@ -805,7 +823,7 @@ W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
     pl.k_per_split = K;
     const bool slices_ok = N / 16 >= num_cus / 2 && K % 128 == 0;
     (void)aligned;
-    if (M >= 1 && M <= 16 && slices_ok && G % 128 == 0 &&
+    if (M >= 1 && M <= DM_MAXM && slices_ok && G % 128 == 0 && ((G / 128) & (G / 128 - 1)) == 0 &&
         decode_mfma_lds_bytes(M, K) <= kDecodeLdsMax) {
         pl.kind = W4_DECODE_MFMA;
         return pl;
@@ -846,7 +864,7 @@ hipError_t launch_w4a16_zf(const W4Args& a, const W4A16Launch& w, hipStream_t st
     if (pl.kind == W4_DECODE_MFMA) {
         const size_t lds = decode_mfma_lds_bytes(w.M, w.K);
         const dim3 grid(w.N / 16), block(DM_NW * kWave);
-        if (w.K <= DM_NW * DM_U * 128)
+        if (decode_mfma_one(w.K))
             launch_decode_mfma<ZF, true>(a, w.M, grid, block, lds, stream);
         else
             launch_decode_mfma<ZF, false>(a, w.M, grid, block, lds, stream);
@@ -913,6 +931,8 @@ hipError_t launch_w4a16(const W4A16Launch& w, hipStream_t stream) {
     a.ws = static_cast<float*>(w.workspace);
     a.split = w.plan.split;
     a.kc_per_split = w.plan.k_per_split / 64;
+    a.pp_shift = 0;
+    while (w.G >= 128 && (128 << (a.pp_shift + 1)) <= w.G) ++a.pp_shift;
     if (w.zeros_format == WMMA_ZEROS_PACKED) return launch_w4a16_zf<WMMA_ZEROS_PACKED>(a, w, stream);
     return launch_w4a16_zf<WMMA_ZEROS_U8>(a, w, stream);
 }
