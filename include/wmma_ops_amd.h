@@ -113,6 +113,24 @@ int wmma_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q, void* str
 /* Workspace bytes wmma_w4a16_gemm needs (fp32 split-K partials). */
 size_t wmma_w4a16_workspace_size(int M, int N, int K, int group_size);
 
+#define WMMA_W4_KERNEL_DECODE_MFMA 0  /* M <= 4: one workgroup per 16 columns, matrix pipe */
+#define WMMA_W4_KERNEL_DECODE 1       /* M <= 4, other group sizes: VALU dot products      */
+#define WMMA_W4_KERNEL_GEMV_SPLIT 2   /* M <= 4, narrow N: 32 columns per workgroup, split-K */
+#define WMMA_W4_KERNEL_MFMA 3         /* larger M: tiled MFMA kernel                         */
+#define WMMA_W4_KERNEL_SKINNY 4       /* 4 < M <= 32: 32 columns per workgroup, matrix pipe */
+
+typedef struct wmma_w4a16_plan {
+    int kernel;             /* WMMA_W4_KERNEL_*                                           */
+    int split_k;            /* K partitions (1 = no split, no workspace)                  */
+    int k_per_split;        /* K elements per partition                                   */
+    size_t workspace_bytes; /* fp32 partial sums: split_k * M * N * 4, 0 when split_k==1  */
+} wmma_w4a16_plan;
+
+/* Host-only planner for wmma_w4a16_gemm on a device with `num_cus` compute units, for
+ * 8-byte-aligned scales (the case of every torch allocation).  No reference counterpart;
+ * the W4A16 analogue of wmma_gemm_plan_make. */
+int wmma_w4a16_plan_make(int M, int N, int K, int group_size, int num_cus, wmma_w4a16_plan* out);
+
 /*
  * Y[M,N] (fp32) = A[M,K] (fp16) @ W[K,N], W[k][n] = fp16((q[k][n] - z[k/G][n]) * s[k/G][n])
  * (dequantised value rounded once to fp16).  packed: output of wmma_int4_prepack.

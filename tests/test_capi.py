@@ -112,6 +112,36 @@ def test_plan_make(lib):
     assert lib.wmma_gemm_plan_make(10, 10, 10, -1, 256, None) == INVALID
 
 
+class W4Plan(ctypes.Structure):
+    _fields_ = [("kernel", ctypes.c_int), ("split_k", ctypes.c_int), ("k_per_split", ctypes.c_int),
+                ("workspace_bytes", ctypes.c_size_t)]
+
+
+def test_w4a16_plan_make(lib):
+    lib.wmma_w4a16_plan_make.argtypes = [ctypes.c_int] * 5 + [ctypes.POINTER(W4Plan)]
+    p = W4Plan()
+
+    def plan(M, N, K, G=128):
+        assert lib.wmma_w4a16_plan_make(M, N, K, G, 256, ctypes.byref(p)) == OK
+        return (p.kernel, p.split_k, p.k_per_split, p.workspace_bytes)
+
+    assert plan(1, 14336, 4096)[:2] == (0, 1)          # decode on the matrix pipe
+    assert plan(4, 4096, 4096)[:2] == (0, 1)
+    assert plan(16, 14336, 4096) == (4, 1, 4096, 0)    # skinny, 448 tiles: no split
+    k, s, kps, ws = plan(16, 4096, 4096)               # skinny, 128 tiles: K split
+    assert (k, s, kps) == (4, 4, 1024) and ws == 4 * 16 * 4096 * 4
+    assert plan(32, 14336, 4096)[0] == 4
+    assert plan(33, 14336, 4096)[0] == 3               # tiled MFMA beyond 32 rows
+    assert plan(16, 14336, 4096, 64)[0] == 3           # G not 128 * 2^j
+    assert plan(16, 14336, 4608, 384)[0] == 3
+    for M, N, K, G in [(5, 1024, 4224, 128), (17, 352, 1536, 256), (2048, 14336, 4096, 128)]:
+        k, s, kps, ws = plan(M, N, K, G)
+        assert kps * (s - 1) < K <= kps * s
+        assert ws == (s * M * N * 4 if s > 1 else 0)
+    assert lib.wmma_w4a16_plan_make(16, 100, 4096, 128, 256, ctypes.byref(p)) == INVALID
+    assert lib.wmma_w4a16_plan_make(16, 4096, 4096, 128, 256, None) == INVALID
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (16, 11008, 4096), (64, 14336, 4096),
                                    (128, 4096, 14336), (512, 512, 512), (1024, 1024, 1024),
                                    (2048, 2048, 2048), (4096, 4096, 2048), (300, 70, 5000)])

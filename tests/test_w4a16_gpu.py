@@ -69,6 +69,29 @@ def test_w4a16_group_sizes_and_u8_zeros(wo, M, K, N, G):
     assert torch.equal(Yp, Yu)
 
 
+# The 4 < M <= 32 matrix-pipe kernel: one and two 16-row blocks, K split over workgroups
+# (N=4096), a ragged last split (K=4224: 33 pair-steps), G=256 (two pair-steps per group),
+# a tile count that is not a multiple of the XCD count (N=352), lda > K, both zero formats.
+@pytest.mark.parametrize("M", [5, 8, 16, 17, 31, 32])
+@pytest.mark.parametrize("K,N,G", [(4096, 4096, 128), (4224, 1024, 128), (1536, 352, 256)])
+def test_w4a16_skinny(wo, M, K, N, G):
+    plan = wo.w4a16_plan(M, N, K, G)
+    report("w4a16_skinny", M=M, K=K, N=N, G=G, plan=plan)
+    assert plan[0] == 4
+    A, q, s, z = oi.make_inputs(M, K, N, G, seed=7 * M + K + N)
+    ref = oi.w4a16_ref(A, q, s, z, G)
+    pk = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
+    sd = torch.from_numpy(s).cuda()
+    Abig = torch.zeros(M, K + 64, dtype=torch.half)
+    Abig[:, :K] = A
+    Ad = Abig.cuda()[:, :K]  # lda = K + 64
+    Yp = wo.matmul_int4(Ad, pk, sd, torch.from_numpy(oi.pack_zeros(z)).cuda(), G)
+    Yu = wo.matmul_int4(Ad, pk, sd, torch.from_numpy(z).cuda(), G)
+    assert torch.isfinite(Yp).all()
+    assert og.max_rel_err(Yp, ref) <= 1e-3
+    assert torch.equal(Yp, Yu)
+
+
 def test_w4a16_zero_when_q_equals_z(wo):
     K, N, G = 256, 64, 128
     q = np.full((K, N), 9, dtype=np.uint8)

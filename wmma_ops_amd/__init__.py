@@ -43,6 +43,7 @@ unprepack_int4 = _C.unprepack_int4
 unpack_int4 = _C.unpack_int4
 matmul_int4 = _C.matmul_int4
 gemm_plan = _C.gemm_plan
+w4a16_plan = _C.w4a16_plan
 
 # The reference binds 13 more matmul_* names, each a gfx1151 tuning experiment computing
 # the same C = A @ B (wmma_gemm.hip:2122-2137).  They resolve to the planner-driven MFMA
@@ -60,5 +61,5 @@ TILE_CONFIGS = {0: (64, 64), 1: (128, 64), 2: (256, 64), 3: (128, 128), 4: (256,
 __all__ = [
     "matmul", "matmul_adaptive", "matmul_tiled", "gemm", "gemm_inplace", "gemm_adaptive",
     "flash_attention", "prepack_int4", "unprepack_int4", "unpack_int4", "matmul_int4",
-    "gemm_plan", "TILE_CONFIGS", "LIBRARY_PATH", "HEADER_PATH", *_REFERENCE_VARIANTS,
+    "gemm_plan", "w4a16_plan", "TILE_CONFIGS", "LIBRARY_PATH", "HEADER_PATH", *_REFERENCE_VARIANTS,
 ]

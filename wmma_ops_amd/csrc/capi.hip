@@ -204,6 +204,20 @@ size_t wmma_w4a16_workspace_size(int M, int N, int K, int group_size) {
     return need;
 }
 
+int wmma_w4a16_plan_make(int M, int N, int K, int group_size, int num_cus, wmma_w4a16_plan* out) {
+    if (!out) return fail(WMMA_ERR_INVALID_ARG, "NULL plan");
+    if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0 || N % 32 != 0 || group_size <= 0 ||
+        group_size % 32 != 0 || K % group_size != 0)
+        return fail(WMMA_ERR_INVALID_ARG, "invalid W4A16 shape M=%d N=%d K=%d G=%d", M, N, K,
+                    group_size);
+    const W4A16Plan pl = w4a16_plan(M, N, K, group_size, num_cus > 0 ? num_cus : current_cus(), true);
+    out->kernel = pl.kind;
+    out->split_k = pl.split;
+    out->k_per_split = pl.k_per_split;
+    out->workspace_bytes = pl.split > 1 ? (size_t)pl.split * M * N * sizeof(float) : 0;
+    return ok();
+}
+
 int wmma_w4a16_gemm(const void* A, int64_t lda, const int32_t* packed, const void* scales,
                     const void* zeros, int zeros_format, int M, int N, int K, int group_size,
                     float* Y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {

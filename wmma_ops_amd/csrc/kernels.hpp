@@ -34,10 +34,11 @@ hipError_t launch_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q,
 
 // W4A16 kernel families.
 enum W4A16Kind {
-    W4_DECODE_MFMA = 0,  // M <= 16, G % 128 == 0: one workgroup per 16 columns, matrix-pipe dots
+    W4_DECODE_MFMA = 0,  // M <= 4, G = 128 * 2^j: one workgroup per 16 columns, matrix-pipe dots
     W4_DECODE = 1,       // M <= 4: one workgroup per 16 columns, VALU dots
     W4_GEMV_SPLIT = 2,   // M <= 4, other shapes: 32 columns per workgroup, K split + reduce
     W4_MFMA = 3,         // larger M: tiled MFMA kernel, K split + reduce when few tiles
+    W4_SKINNY = 4,       // 4 < M <= 32: 32 columns per workgroup, K split + reduce when few tiles
 };
 
 struct W4A16Plan {

@@ -294,6 +294,15 @@ std::vector<int64_t> gemm_plan(int64_t M, int64_t N, int64_t K, int64_t tile_cfg
             (int64_t)p.workspace_bytes};
 }
 
+// W4A16 planner introspection: (kernel, split_k, k_per_split, workspace_bytes).
+std::vector<int64_t> w4a16_plan(int64_t M, int64_t N, int64_t K, int64_t group_size,
+                                int64_t num_cus) {
+    wmma_w4a16_plan p{};
+    check_status(wmma_w4a16_plan_make((int)M, (int)N, (int)K, (int)group_size, (int)num_cus, &p),
+                 "wmma_w4a16_plan_make");
+    return {p.kernel, p.split_k, p.k_per_split, (int64_t)p.workspace_bytes};
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -318,6 +327,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("matmul_int4", &matmul_int4, "W4A16 dequant GEMM: fp16 A @ int4 W -> fp32",
           py::arg("A"), py::arg("packed"), py::arg("scales"), py::arg("zeros"),
           py::arg("group_size") = 128);
+    m.def("w4a16_plan", &w4a16_plan, "Planner decision for a W4A16 shape", py::arg("M"),
+          py::arg("N"), py::arg("K"), py::arg("group_size") = 128, py::arg("num_cus") = 256);
     m.def("gemm_plan", &gemm_plan, "Planner decision for a GEMM shape", py::arg("M"), py::arg("N"),
           py::arg("K"), py::arg("tile_cfg") = -1, py::arg("num_cus") = 256);
 }

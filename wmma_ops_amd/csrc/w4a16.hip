@@ -630,6 +630,167 @@ void launch_decode_mfma(const W4Args& a, int M, dim3 grid, dim3 block, size_t ld
     }
 }
 
+// ------------------------------------------------ skinny (4 < M <= 32) on the matrix pipe --
+// Memory-bound like decode (every weight is used by at most 32 rows), so the structure is
+// the decode kernel's: every wave issues all its loads up front and then works through
+// them in arrival order, with no barrier before the final cross-wave sum.  Differences:
+//  * a workgroup covers a whole 32-column prepacked tile (both 16-column halves), so each
+//    activation fragment feeds two MFMAs;
+//  * the activations come straight from L2 into registers in the MFMA A-operand layout --
+//    lane l: row 16*b + l%16 (clamped to M-1; those rows are never stored), K quarter l/16,
+//    i.e. 64 contiguous bytes per lane per pair-step -- then a' = a with offsets {2,3,6,7}
+//    of every 8 scaled by 1/16 (two v_pk_mul) to cancel the 16x of those weight pairs;
+//  * SK_U pair-steps per wave; when the 32-column tiles alone cannot fill the chip the K
+//    range is split over blockIdx.y (SK_NW * SK_U pair-steps per split) and the partials
+//    go to the workspace for w4a16_reduce_kernel.
+// The B operand is the decode kernel's: W = fp16((q - z) s) rounded once per weight.
+// D layout per 16-row block b and half sc: lane l holds column 32*nt + 16*sc + l%16 and
+// rows 16*b + 4*(l/16) + r.
+constexpr int SK_NW = 8;
+
+template <int ZF, int MB, int U>
+__global__ void __launch_bounds__(SK_NW * kWave)
+w4a16_skinny_kernel(W4Args p) {
+    __shared__ float red[SK_NW][MB * 16][33];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nt = xcd_remap(blockIdx.x, gridDim.x);
+    const int col = lane & 15, sub = lane >> 4, dc = sub >> 1, h = sub & 1;
+    const int K = p.K, M = p.M, KC = K / 64, KP = KC / 2;
+    const int kp0 = blockIdx.y * (SK_NW * U);
+
+    // Group parameters: lane l fetches pair-step min(l/16, U-1) of this wave for both
+    // 16-column halves; a lane shuffle later hands each lane its own.
+    uint32_t sraw[2], zraw[2];
+    {
+        const int ppl = min(kp0 + wave + SK_NW * min(sub, U - 1), KP - 1);
+        const int g = ppl >> p.pp_shift;  // G = 128 << pp_shift
+#pragma unroll
+        for (int sc = 0; sc < 2; ++sc) {
+            const int n = 32 * nt + 16 * sc + col;
+            sraw[sc] = __builtin_bit_cast(uint16_t, p.S[(int64_t)g * p.N + n]);
+            if constexpr (ZF == WMMA_ZEROS_PACKED)
+                zraw[sc] = (uint32_t)static_cast<const int32_t*>(p.Z)[(int64_t)g * (p.N / 8) + n / 8];
+            else
+                zraw[sc] = static_cast<const uint8_t*>(p.Z)[(int64_t)g * p.N + n];
+        }
+    }
+    // Activations and weights, pair-step by pair-step (clamped: every load is issued).
+    u32x4 av[U][MB][4], wv[U][2];
+    const u32x4* wbase = p.W + (int64_t)nt * KC * 64 + 32 * h + col;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int pp = min(kp0 + wave + SK_NW * u, KP - 1);
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            const int row = min(16 * b + col, M - 1);
+            const f16* ap = p.A + (int64_t)row * p.lda + 128 * pp + 32 * sub;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) av[u][b][q] = *reinterpret_cast<const u32x4*>(ap + 8 * q);
+        }
+#pragma unroll
+        for (int sc = 0; sc < 2; ++sc)
+            wv[u][sc] = __builtin_nontemporal_load(wbase + 16 * sc + (int64_t)(2 * pp + dc) * 64);
+    }
+
+    asm volatile("" : "+v"(sraw[0]), "+v"(sraw[1]), "+v"(zraw[0]), "+v"(zraw[1]));
+    int sz[2];
+#pragma unroll
+    for (int sc = 0; sc < 2; ++sc) {
+        uint32_t z;
+        if constexpr (ZF == WMMA_ZEROS_PACKED)
+            z = (zraw[sc] >> (4 * ((32 * nt + 16 * sc + col) & 7))) & 0xFu;
+        else
+            z = zraw[sc] & 0xFu;
+        sz[sc] = (int)(sraw[sc] | (z << 16));
+    }
+    uint32_t magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));
+    f32x4 d[MB][2];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) d[b][0] = d[b][1] = f32x4{};
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        uint32_t v[2];
+#pragma unroll
+        for (int sc = 0; sc < 2; ++sc) v[sc] = (uint32_t)__shfl(sz[sc], 16 * u + col);
+        if (kp0 + wave + SK_NW * u < KP) {  // uniform
+            f16x8 a[MB][4];
+#pragma unroll
+            for (int b = 0; b < MB; ++b)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    a[b][q] = as_f16x8(av[u][b][q]);
+#pragma unroll
+                    for (int e = 2; e < 8; e += 4) {
+                        a[b][q][e] = a[b][q][e] * (f16)0.0625f;
+                        a[b][q][e + 1] = a[b][q][e + 1] * (f16)0.0625f;
+                    }
+                }
+#pragma unroll
+            for (int sc = 0; sc < 2; ++sc) {
+                const uint32_t zz = v[sc] >> 16, s = v[sc] & 0xFFFFu;
+                const uint32_t z1 = 0x6400u | zz, z16 = 0x6400u | (zz << 4);
+                const f16x2 zs1 = as_h2(z1 | (z1 << 16)), zs16 = as_h2(z16 | (z16 << 16));
+                const f16x2 ss = as_h2(s | (s << 16));
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t x = wv[u][sc][q], x8 = x >> 8;
+                    u32x4 bv;
+                    bv[0] = as_u32((as_h2((x & 0x000F000Fu) | magic) - zs1) * ss);
+                    bv[1] = as_u32((as_h2((x & 0x00F000F0u) | magic) - zs16) * ss);
+                    bv[2] = as_u32((as_h2((x8 & 0x000F000Fu) | magic) - zs1) * ss);
+                    bv[3] = as_u32((as_h2((x8 & 0x00F000F0u) | magic) - zs16) * ss);
+#pragma unroll
+                    for (int b = 0; b < MB; ++b) d[b][sc] = mfma16(a[b][q], as_f16x8(bv), d[b][sc]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int sc = 0; sc < 2; ++sc)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[wave][16 * b + 4 * sub + r][16 * sc + col] = d[b][sc][r];
+    __syncthreads();
+    const bool partial = gridDim.y > 1;
+    for (int i = tid; i < M * 32; i += SK_NW * kWave) {
+        const int m = i >> 5, c = i & 31;
+        float acc = red[0][m][c];
+#pragma unroll
+        for (int w = 1; w < SK_NW; ++w) acc += red[w][m][c];
+        const int n = 32 * nt + c;
+        if (partial)
+            p.ws[((int64_t)blockIdx.y * M + m) * p.N + n] = acc;
+        else
+            p.Y[(int64_t)m * p.ldy + n] = acc;
+    }
+}
+
+// Pair-steps per wave for the skinny kernel: as many as possible (fewer splits) while the
+// 32-column tiles times the K splits still give about 1.5 workgroups per CU.
+int skinny_u(int M, int N, int K, int num_cus) {
+    const int tiles = N / 32, KP = K / 128;
+    const int umax = M > 16 ? 2 : 4;
+    for (int u = umax; u > 1; u /= 2) {
+        const int splits = ceil_div(KP, SK_NW * u);
+        if ((int64_t)tiles * splits * 2 >= (int64_t)num_cus * 3) return u;
+    }
+    return 1;
+}
+
+template <int ZF, int MB>
+void launch_skinny_mb(const W4Args& a, int U, dim3 grid, hipStream_t stream) {
+    const dim3 block(SK_NW * kWave);
+    if (U == 4)
+        hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, (MB == 1 ? 4 : 2)>), grid, block, 0, stream, a);
+    else if (U == 2)
+        hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, 2>), grid, block, 0, stream, a);
+    else
+        hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, 1>), grid, block, 0, stream, a);
+}
+
 // ------------------------------------------------------------------ MFMA (M > GV_MAXM) --
 // D = W^T A^T on MFMA 32x32x16: matrix rows are weight columns n, matrix columns are
 // activation rows m.  Workgroup: 4 waves along N, each wave WNT 32-column tiles; the
@@ -810,11 +971,13 @@ hipError_t launch_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q,
 }
 
 // Host-only: choose the kernel and K split.
-//   decode-mfma  M <= 16, G % 128 == 0, K % 128 == 0, the staged activations fit LDS and
+//   decode-mfma  M <= 4, G = 128 * 2^j, K % 128 == 0, the staged activations fit LDS and
 //                the 16-column slices give at least half a workgroup per CU.
 //   decode       M <= 4 with the same slice condition, other group sizes.
 //   gemv-split   other M <= 4 shapes: one workgroup per 32 columns, K split (plus a reduce
 //                pass) only when fewer than 2*CUs workgroups would exist.
+//   skinny       4 < M <= 32 with G = 128 * 2^j: 32 columns per workgroup, K split (plus
+//                a reduce pass) only when the tiles alone give under 1.5 workgroups per CU.
 //   mfma         everything else.
 W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
     if (num_cus <= 0) num_cus = 256;
@@ -830,6 +993,13 @@ W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
     }
     if (w4a16_use_decode(M, N, K, num_cus)) {
         pl.kind = W4_DECODE;
+        return pl;
+    }
+    if (M > DM_MAXM && M <= 32 && K % 128 == 0 && G % 128 == 0 && ((G / 128) & (G / 128 - 1)) == 0) {
+        const int u = skinny_u(M, N, K, num_cus);
+        pl.kind = W4_SKINNY;
+        pl.k_per_split = SK_NW * u * 128;
+        pl.split = ceil_div(K, pl.k_per_split);
         return pl;
     }
     const int KC = K / 64;
@@ -890,7 +1060,14 @@ hipError_t launch_w4a16_zf(const W4Args& a, const W4A16Launch& w, hipStream_t st
         }
         return hipGetLastError();
     }
-    if (pl.kind == W4_GEMV_SPLIT) {
+    if (pl.kind == W4_SKINNY) {
+        const int U = pl.k_per_split / (SK_NW * 128);
+        const dim3 grid(ntiles, pl.split);
+        if (w.M <= 16)
+            launch_skinny_mb<ZF, 1>(a, U, grid, stream);
+        else
+            launch_skinny_mb<ZF, 2>(a, U, grid, stream);
+    } else if (pl.kind == W4_GEMV_SPLIT) {
         hipLaunchKernelGGL((w4a16_gemv_kernel<ZF>), dim3(ntiles, pl.split), dim3(GV_NW * kWave), 0,
                            stream, a);
     } else {
