@@ -131,8 +131,9 @@ def test_w4a16_plan_make(lib):
     k, s, kps, ws = plan(16, 4096, 4096)               # skinny, 128 tiles: K split
     assert (k, s, kps) == (4, 4, 1024) and ws == 4 * 16 * 4096 * 4
     assert plan(32, 14336, 4096)[0] == 4
-    assert plan(33, 14336, 4096)[0] == 3               # tiled MFMA beyond 32 rows
-    assert plan(16, 14336, 4096, 64)[0] == 3           # G not 128 * 2^j
+    assert plan(33, 14336, 4096)[0] == 5               # LDS-DMA GEMM beyond 32 rows
+    assert plan(2048, 14336, 4096)[:2] == (5, 1)
+    assert plan(16, 14336, 4096, 64)[0] == 3           # G not 128 * 2^j: older tiled kernel
     assert plan(16, 14336, 4608, 384)[0] == 3
     for M, N, K, G in [(5, 1024, 4224, 128), (17, 352, 1536, 256), (2048, 14336, 4096, 128)]:
         k, s, kps, ws = plan(M, N, K, G)

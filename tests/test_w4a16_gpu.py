@@ -92,6 +92,31 @@ def test_w4a16_skinny(wo, M, K, N, G):
     assert torch.equal(Yp, Yu)
 
 
+# The M > 32 LDS-DMA kernel: both tile configurations (128x128 below 512 rows, 256x256
+# from 512), partial M and N tiles, K shorter than the stage ring (K=192), K split
+# (M=64, N=1024: few tiles), G=32 (the two K halves of a chunk in different groups), lda > K,
+# both zero formats.
+@pytest.mark.parametrize("M,K,N,G", [(33, 1024, 4096, 128), (64, 2048, 1024, 64), (200, 192, 288, 32),
+                                     (512, 1024, 2048, 128), (600, 512, 288, 256),
+                                     (1030, 2048, 1056, 128)])
+def test_w4a16_gemm_tiles(wo, M, K, N, G):
+    plan = wo.w4a16_plan(M, N, K, G)
+    report("w4a16_gemm", M=M, K=K, N=N, G=G, plan=plan)
+    assert plan[0] == 5
+    A, q, s, z = oi.make_inputs(M, K, N, G, seed=3 * M + K + N + G)
+    ref = oi.w4a16_ref(A, q, s, z, G)
+    pk = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
+    sd = torch.from_numpy(s).cuda()
+    Abig = torch.zeros(M, K + 32, dtype=torch.half)
+    Abig[:, :K] = A
+    Ad = Abig.cuda()[:, :K]  # lda = K + 32
+    Yp = wo.matmul_int4(Ad, pk, sd, torch.from_numpy(oi.pack_zeros(z)).cuda(), G)
+    Yu = wo.matmul_int4(Ad, pk, sd, torch.from_numpy(z).cuda(), G)
+    assert torch.isfinite(Yp).all()
+    assert og.max_rel_err(Yp, ref) <= 1e-3
+    assert torch.equal(Yp, Yu)
+
+
 def test_w4a16_zero_when_q_equals_z(wo):
     K, N, G = 256, 64, 128
     q = np.full((K, N), 9, dtype=np.uint8)

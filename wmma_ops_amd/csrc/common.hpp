@@ -47,6 +47,9 @@ __device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t
 __device__ __forceinline__ uint16_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
     return __builtin_amdgcn_raw_buffer_load_b16(r, byte_off, 0, 0);
 }
+__device__ __forceinline__ uint8_t buf_load1(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_amdgcn_raw_buffer_load_b8(r, byte_off, 0, 0);
+}
 
 // v_mfma_f32_32x32x16_f16: D(32x32 fp32) += A(32x16) * B(16x32).
 // Lane l supplies row l%32 of A and column l%32 of B, eight K values each (the K half is

@@ -39,6 +39,7 @@ enum W4A16Kind {
     W4_GEMV_SPLIT = 2,   // M <= 4, other shapes: 32 columns per workgroup, K split + reduce
     W4_MFMA = 3,         // larger M: tiled MFMA kernel, K split + reduce when few tiles
     W4_SKINNY = 4,       // 4 < M <= 32: 32 columns per workgroup, K split + reduce when few tiles
+    W4_GEMM = 5,         // M > 32: LDS-DMA MFMA GEMM, K split + reduce when few tiles
 };
 
 struct W4A16Plan {

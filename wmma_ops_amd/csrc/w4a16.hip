@@ -791,6 +791,247 @@ void launch_skinny_mb(const W4Args& a, int U, dim3 grid, hipStream_t stream) {
         hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, 1>), grid, block, 0, stream, a);
 }
 
+// ------------------------------------------------------ W4A16 GEMM (M > 32), LDS-DMA --
+// Output tile BM x BN per workgroup, WM x WN waves, wave tile TM x TN = FM x FN MFMA
+// 32x32x16 tiles.  K advances in 64-deep stages (one prepacked block row):
+//   activations A[BM][64] fp16 travel global -> LDS by buffer_load ... lds into an NS-deep
+//     ring; rows of eight 16-byte chunks, chunk c of row r stored at c ^ swz8(r)
+//     (conflict-free for the 16-row ds_read_b128 pattern below);
+//   weights: each wave loads its FN prepacked blocks (1 KB each; lane l: the four words of
+//     column l%32, K half l/32) plus that lane's scale and zero straight into registers,
+//     into a ring NS stages deep -- the stage issued NS-1 stages ahead never overwrites the
+//     one being dequantised.
+// k-step j of a stage (j = 0..3) uses word j of every lane: K offsets 32*(l/32) + 8j .. +7,
+// matched on the A side by chunk 4*(l/32) + j of the lane's row.  Dequantisation per word:
+// pair i = ((w >> 4i) & 0x000F000F) | 0x6400.. (= 1024 + q, exact), minus (1024 + z)
+// (exact), times s (one fp16 rounding) -- W = fp16((q - z) s), the A operand stays raw.
+// One barrier per stage, after this wave's share of the stage has landed (vmcnt): from
+// then on every wave's copy is visible and every wave has finished reading the slot the
+// new DMA overwrites.
+constexpr int W4G_MAXSTAGES = 4;
+
+template <int FN>
+struct W4GSlot {
+    u32x4 w[FN];
+    uint32_t s[FN], z[FN];
+};
+
+template <int BM, int BN, int WM, int WN, int NS, int ZF>
+struct W4GCfg {
+    static constexpr int NW = WM * WN, TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+    static constexpr int A_BYTES = BM * 128;
+    static constexpr int A_DMA = A_BYTES / (1024 * NW);
+    static constexpr int PER = A_DMA + 3 * FN;  // vmcnt events per stage per wave
+    static_assert(A_BYTES % (1024 * NW) == 0, "A stage must split into 1 KB DMAs per wave");
+    static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32");
+    static_assert(NS >= 3 && NS <= W4G_MAXSTAGES && (NS - 2) * PER < 64, "vmcnt range");
+};
+
+struct W4GLane {
+    uint32_t a_off[8];  // A DMA source offsets (row part; kOobOffset for rows >= M)
+    int a_dst;          // this wave's DMA slice of a stage
+    int a_addr[8];      // byte offset of the lane's A row in a stage (per i < FM)
+    int a_sw[8];        // its swizzle
+    uint32_t w_off[4];  // weight block offset of column tile j at K chunk 0 (kOobOffset: none)
+    uint32_t s_off[4], z_off[4];  // scale / zero offset of column tile j at group 0
+    int h;
+};
+
+// Issue the loads of global K chunk kc (kc < 0: nothing real -- every lane reads out of
+// range, so the event count stays uniform) into LDS slot dst and register slot R.  The
+// per-lane base offsets already carry kOobOffset for rows / columns outside the matrix;
+// adding a K offset (< 2^31) keeps them out of range, so no lane needs a branch.
+template <class C, int ZF>
+__device__ __forceinline__ void w4g_issue(const W4Args& p, const W4GLane& L,
+                                          __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rw,
+                                          __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rz,
+                                          int kc, WMMA_LDS unsigned char* __restrict__ dst,
+                                          W4GSlot<C::FN>& R) {
+    const bool live = kc >= 0;  // uniform
+    const uint32_t dead = live ? 0u : kOobOffset;
+    const uint32_t k = live ? (uint32_t)kc : 0u;
+#pragma unroll
+    for (int i = 0; i < C::A_DMA; ++i)
+        lds_dma16(ra, (L.a_off[i] + k * 128u) | dead, dst + L.a_dst + i * 1024);
+    const uint32_t g = (64u * k + 32u * (uint32_t)L.h) / (uint32_t)p.G;
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) {
+        R.w[j] = buf_load16(rw, (L.w_off[j] + k * 1024u) | dead);
+        R.s[j] = buf_load2(rs, (L.s_off[j] + g * (uint32_t)p.N * 2u) | dead);
+        if constexpr (ZF == WMMA_ZEROS_PACKED)
+            R.z[j] = buf_load4(rz, (L.z_off[j] + g * (uint32_t)(p.N / 8) * 4u) | dead);
+        else
+            R.z[j] = buf_load1(rz, (L.z_off[j] + g * (uint32_t)p.N) | dead);
+    }
+}
+
+// One stage, after its wait + barrier: issue stage t + NS - 1 (global chunk kc_next, or -1)
+// into LDS slot dst and register slot Rn, then dequantise this stage's weights (slot R) and
+// run its 4 x FM x FN MFMAs on the activations in LDS slot cur.  cur and dst are distinct
+// slots, declared __restrict__ so the compiler keeps the DMA in flight across the reads;
+// the ordering between a DMA and later reads of the same slot is the wait + barrier.
+template <class C, int ZF>
+__device__ __forceinline__ void w4g_stage(const W4Args& p, const W4GLane& L,
+                                          __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rw,
+                                          __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rz,
+                                          const WMMA_LDS unsigned char* __restrict__ cur,
+                                          WMMA_LDS unsigned char* __restrict__ dst, int kc_next,
+                                          const W4GSlot<C::FN>& R, W4GSlot<C::FN>& Rn,
+                                          bool compute, int lane, uint32_t magic,
+                                          f32x16 (&acc)[C::FM][C::FN]) {
+    w4g_issue<C, ZF>(p, L, ra, rw, rs, rz, kc_next, dst, Rn);
+    if (!compute) return;
+    f16x2 zs[C::FN], ss[C::FN];
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) {
+        uint32_t z;
+        if constexpr (ZF == WMMA_ZEROS_PACKED)
+            z = (R.z[j] >> (4 * (lane & 7))) & 0xFu;  // column % 8 == lane % 8
+        else
+            z = R.z[j] & 0xFu;
+        const uint32_t zh = 0x6400u | z, sv = R.s[j] & 0xFFFFu;
+        zs[j] = as_h2(zh | (zh << 16));
+        ss[j] = as_h2(sv | (sv << 16));
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        f16x8 b[C::FN];
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j) {
+            const uint32_t x = R.w[j][ks];
+            u32x4 bv;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                bv[q] = as_u32((as_h2(((x >> (4 * q)) & 0x000F000Fu) | magic) - zs[j]) * ss[j]);
+            b[j] = as_f16x8(bv);
+        }
+        f16x8 a[C::FM];
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i) {
+            const int c = (4 * L.h + ks) ^ L.a_sw[i];
+            a[i] = as_f16x8(*(const WMMA_LDS u32x4*)(cur + L.a_addr[i] + (c << 4)));
+        }
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::FN; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int NS, int ZF>
+__global__ void __launch_bounds__(WM * WN * kWave)
+__attribute__((amdgpu_waves_per_eu(2, 2)))
+w4a16_gemm_kernel(W4Args p) {
+    using C = W4GCfg<BM, BN, WM, WN, NS, ZF>;
+    constexpr int FM = C::FM, FN = C::FN, TM = C::TM, TN = C::TN;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * C::A_BYTES];
+    WMMA_LDS unsigned char* lds = (WMMA_LDS unsigned char*)smem;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
+    int tm, tn;
+    grouped_tile(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, 4, &tm, &tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int KC = p.K / 64;
+    const int kc0 = blockIdx.y * p.kc_per_split;
+    const int nk = max(0, min(KC, kc0 + p.kc_per_split) - kc0);
+
+    W4GLane L;
+#pragma unroll
+    for (int i = 0; i < C::A_DMA; ++i) {
+        const int P = 64 * (wave * C::A_DMA + i) + lane;
+        const int r = P >> 3, c = (P & 7) ^ swz8(r);
+        L.a_off[i] = m0 + r < p.M ? (uint32_t)((r * p.lda + 8 * c) * 2) : kOobOffset;
+    }
+    L.a_dst = wave * C::A_DMA * 1024;
+    L.h = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int r = wm * TM + 32 * i + (lane & 31);
+        L.a_addr[i] = r * 128;
+        L.a_sw[i] = swz8(r);
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int n = n0 + wn * TN + 32 * j + (lane & 31);
+        const bool ok = n < p.N;
+        const int ntile = n >> 5;
+        L.w_off[j] = ok ? (uint32_t)(((int64_t)ntile * KC * 64 + lane) * 16) : kOobOffset;
+        L.s_off[j] = ok ? (uint32_t)n * 2u : kOobOffset;
+        if constexpr (ZF == WMMA_ZEROS_PACKED)
+            L.z_off[j] = ok ? (uint32_t)(n >> 3) * 4u : kOobOffset;
+        else
+            L.z_off[j] = ok ? (uint32_t)n : kOobOffset;
+    }
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A + (int64_t)m0 * p.lda);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.S);
+    const __amdgpu_buffer_rsrc_t rz = make_rsrc(p.Z);
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
+    uint32_t magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));
+
+    W4GSlot<FN> ring[NS];
+    if (nk > 0) {
+        // Prologue: stages 0 .. NS-2 in flight.
+#pragma unroll
+        for (int q = 0; q < NS - 1; ++q)
+            w4g_issue<C, ZF>(p, L, ra, rw, rs, rz, q < nk ? kc0 + q : -1, lds + q * C::A_BYTES, ring[q]);
+        // Main loop, unrolled by NS so every register-ring slot is a static index.  Stage
+        // t reads LDS slot t % NS and ring[t % NS]; it issues stage t + NS - 1 into LDS slot
+        // (t - 1) % NS and ring[(t - 1) % NS], both free once this stage's barrier passed.
+        for (int t0 = 0; t0 < nk; t0 += NS) {
+#pragma unroll
+            for (int q = 0; q < NS; ++q) {
+                const int t = t0 + q;
+                wait_vmcnt<(NS - 2) * C::PER>();
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                const int tn_ = t + NS - 1;
+                w4g_stage<C, ZF>(p, L, ra, rw, rs, rz, lds + q * C::A_BYTES,
+                                 lds + ((q + NS - 1) % NS) * C::A_BYTES,
+                                 tn_ < nk ? kc0 + tn_ : -1, ring[q], ring[(q + NS - 1) % NS],
+                                 t < nk, lane, magic, acc);
+            }
+        }
+        wait_vmcnt<0>();
+    }
+
+    // Epilogue.  D: lane column lane%32, element r -> row 8*(r/4) + 4*(lane/32) + r%4.
+    const bool partial = gridDim.y > 1;
+    float* out = partial ? p.ws + (size_t)blockIdx.y * (size_t)p.M * (size_t)p.N : p.Y;
+    const int64_t ldo = partial ? (int64_t)p.N : p.ldy;
+    const int row0 = m0 + wm * TM + 4 * L.h, col0 = n0 + wn * TN + (lane & 31);
+    const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = row0 + 32 * i + 8 * (r >> 2) + (r & 3), col = col0 + 32 * j;
+                if (full || (row < p.M && col < p.N)) out[(int64_t)row * ldo + col] = acc[i][j][r];
+            }
+}
+
+// W4A16 GEMM configurations: BM x BN, WM x WN waves, NS stages.
+//   big  256 x 256, 2 x 4 waves, 4 stages (128 KB LDS): M >= 512
+//   mid  128 x 128, 2 x 2 waves, 4 stages (64 KB LDS):  32 < M < 512
+template <int ZF>
+void launch_w4g(const W4Args& a, int cfg, dim3 grid, hipStream_t stream) {
+    if (cfg == 0)
+        hipLaunchKernelGGL((w4a16_gemm_kernel<256, 256, 2, 4, 4, ZF>), grid, dim3(8 * kWave), 0, stream, a);
+    else
+        hipLaunchKernelGGL((w4a16_gemm_kernel<128, 128, 2, 2, 4, ZF>), grid, dim3(4 * kWave), 0, stream, a);
+}
+
 // ------------------------------------------------------------------ MFMA (M > GV_MAXM) --
 // D = W^T A^T on MFMA 32x32x16: matrix rows are weight columns n, matrix columns are
 // activation rows m.  Workgroup: 4 waves along N, each wave WNT 32-column tiles; the
@@ -978,7 +1219,9 @@ hipError_t launch_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q,
 //                pass) only when fewer than 2*CUs workgroups would exist.
 //   skinny       4 < M <= 32 with G = 128 * 2^j: 32 columns per workgroup, K split (plus
 //                a reduce pass) only when the tiles alone give under 1.5 workgroups per CU.
-//   mfma         everything else.
+//   gemm         M > 32: LDS-DMA MFMA GEMM (256x256 tiles from 512 rows, else 128x128),
+//                K split (plus a reduce pass) only when the tiles cannot fill the chip.
+//   mfma         everything else (M <= 32 shapes the kernels above do not take).
 W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
     if (num_cus <= 0) num_cus = 256;
     W4A16Plan pl{};
@@ -1003,6 +1246,20 @@ W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
         return pl;
     }
     const int KC = K / 64;
+    if (M > 32) {
+        // LDS-DMA W4A16 GEMM: big tiles from 512 rows, K split only to fill the chip.
+        const bool big = M >= 512;
+        const int bm = big ? 256 : 128, bn = big ? 256 : 128;
+        const int64_t tiles = (int64_t)ceil_div(M, bm) * ceil_div(N, bn);
+        int s = 1;
+        if (tiles < num_cus) s = (int)std::min<int64_t>(ceil_div64(num_cus, tiles), 4);
+        s = std::max(1, std::min(s, KC / 4));
+        const int kcps = ceil_div(KC, s);
+        pl.kind = W4_GEMM;
+        pl.split = ceil_div(KC, kcps);
+        pl.k_per_split = kcps * 64;
+        return pl;
+    }
     const bool use_mfma = M > GV_MAXM;
     int64_t blocks;
     if (!use_mfma) {
@@ -1060,7 +1317,12 @@ hipError_t launch_w4a16_zf(const W4Args& a, const W4A16Launch& w, hipStream_t st
         }
         return hipGetLastError();
     }
-    if (pl.kind == W4_SKINNY) {
+    if (pl.kind == W4_GEMM) {
+        const bool big = w.M >= 512;
+        const int bm = big ? 256 : 128, bn = big ? 256 : 128;
+        const dim3 grid(ceil_div(w.M, bm) * ceil_div(w.N, bn), pl.split);
+        launch_w4g<ZF>(a, big ? 0 : 1, grid, stream);
+    } else if (pl.kind == W4_SKINNY) {
         const int U = pl.k_per_split / (SK_NW * 128);
         const dim3 grid(ntiles, pl.split);
         if (w.M <= 16)
