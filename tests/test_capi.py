@@ -128,8 +128,11 @@ def test_w4a16_plan_make(lib):
     assert plan(1, 14336, 4096)[:2] == (0, 1)          # decode on the matrix pipe
     assert plan(4, 4096, 4096)[:2] == (0, 1)
     assert plan(16, 14336, 4096) == (4, 1, 4096, 0)    # skinny, 448 tiles: no split
-    k, s, kps, ws = plan(16, 4096, 4096)               # skinny, 128 tiles: K split
-    assert (k, s, kps) == (4, 4, 1024) and ws == 4 * 16 * 4096 * 4
+    assert plan(16, 4096, 4096) == (4, 1, 4096, 0)     # skinny, 128 tiles: half the CUs, no split
+    k, s, kps, ws = plan(16, 2048, 4096)               # skinny, 64 tiles: K split
+    assert (k, s, kps) == (4, 2, 2048) and ws == 2 * 16 * 2048 * 4
+    assert plan(128, 14336, 4096)[:2] == (5, 2)        # 112 tiles of 128x128: split 2
+    assert plan(2048, 4096, 4096)[:2] == (5, 2)
     assert plan(32, 14336, 4096)[0] == 4
     assert plan(33, 14336, 4096)[0] == 5               # LDS-DMA GEMM beyond 32 rows
     assert plan(2048, 14336, 4096)[:2] == (5, 1)

@@ -70,7 +70,7 @@ def test_w4a16_group_sizes_and_u8_zeros(wo, M, K, N, G):
 
 
 # The 4 < M <= 32 matrix-pipe kernel: one and two 16-row blocks, K split over workgroups
-# (N=4096), a ragged last split (K=4224: 33 pair-steps), G=256 (two pair-steps per group),
+# (N=1024, N=352; and N=4096 for M > 16), a ragged last split (K=4224: 33 pair-steps), G=256,
 # a tile count that is not a multiple of the XCD count (N=352), lda > K, both zero formats.
 @pytest.mark.parametrize("M", [5, 8, 16, 17, 31, 32])
 @pytest.mark.parametrize("K,N,G", [(4096, 4096, 128), (4224, 1024, 128), (1536, 352, 256)])

@@ -768,14 +768,15 @@ w4a16_skinny_kernel(W4Args p) {
     }
 }
 
-// Pair-steps per wave for the skinny kernel: as many as possible (fewer splits) while the
-// 32-column tiles times the K splits still give about 1.5 workgroups per CU.
+// Pair-steps per wave for the skinny kernel: as many as possible (fewer splits, no reduce
+// pass) while the 32-column tiles times the K splits still give half a workgroup per CU --
+// measured on MI355X, 128 unsplit workgroups beat 512 split ones plus the reduce pass.
 int skinny_u(int M, int N, int K, int num_cus) {
     const int tiles = N / 32, KP = K / 128;
     const int umax = M > 16 ? 2 : 4;
     for (int u = umax; u > 1; u /= 2) {
         const int splits = ceil_div(KP, SK_NW * u);
-        if ((int64_t)tiles * splits * 2 >= (int64_t)num_cus * 3) return u;
+        if ((int64_t)tiles * splits * 2 >= (int64_t)num_cus) return u;
     }
     return 1;
 }
@@ -1218,7 +1219,7 @@ hipError_t launch_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q,
 //   gemv-split   other M <= 4 shapes: one workgroup per 32 columns, K split (plus a reduce
 //                pass) only when fewer than 2*CUs workgroups would exist.
 //   skinny       4 < M <= 32 with G = 128 * 2^j: 32 columns per workgroup, K split (plus
-//                a reduce pass) only when the tiles alone give under 1.5 workgroups per CU.
+//                a reduce pass) only when the tiles alone give under half a workgroup per CU.
 //   gemm         M > 32: LDS-DMA MFMA GEMM (256x256 tiles from 512 rows, else 128x128),
 //                K split (plus a reduce pass) only when the tiles cannot fill the chip.
 //   mfma         everything else (M <= 32 shapes the kernels above do not take).
@@ -1251,8 +1252,10 @@ W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
         const bool big = M >= 512;
         const int bm = big ? 256 : 128, bn = big ? 256 : 128;
         const int64_t tiles = (int64_t)ceil_div(M, bm) * ceil_div(N, bn);
+        // Split only while every split keeps at least one CU's worth of tiles: the partial
+        // sums cost a second pass over M x N fp32 per split.
         int s = 1;
-        if (tiles < num_cus) s = (int)std::min<int64_t>(ceil_div64(num_cus, tiles), 4);
+        if (tiles < num_cus) s = (int)std::min<int64_t>(std::max<int64_t>(num_cus / tiles, 1), 4);
         s = std::max(1, std::min(s, KC / 4));
         const int kcps = ceil_div(KC, s);
         pl.kind = W4_GEMM;
