@@ -61,6 +61,28 @@ def test_flash_invariants(wo):
     assert torch.allclose(Oc[0, :, 0].float().cpu(), V[0, :, 0].float(), atol=1e-3)
 
 
+# Scores that climb by ~46 (in log2 units) every 64-key tile, and isolated spikes late in
+# the sequence: the running max must move mid-sequence (rescale of O and the row sum, tile
+# recomputed) -- the path ordinary N(0,1) inputs only take on the first tile.
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("pattern", ["ramp", "spikes"])
+def test_flash_running_max_moves(wo, causal, pattern):
+    B, H, S, D = 1, 2, 1024, 128
+    g = torch.Generator().manual_seed(11)
+    Q = (torch.ones(B, H, S, D) + 0.1 * torch.randn(B, H, S, D, generator=g))
+    if pattern == "ramp":
+        t = 0.05 * torch.arange(S, dtype=torch.float32)          # score ~ 0.57 * key index
+        K = torch.ones(B, H, S, D) * t[None, None, :, None]
+    else:
+        K = 0.5 * torch.randn(B, H, S, D, generator=g)
+        K[:, :, [300, 301, 700, 1000]] += 6.0                      # +68 in the score
+    V = torch.randn(B, H, S, D, generator=g)
+    Q, K, V = Q.half(), K.half(), V.half()
+    report("flash_max_moves", pattern=pattern, causal=causal)
+    O = wo.flash_attention(Q.cuda(), K.cuda(), V.cuda(), causal=causal)
+    _check(O, oatt.sdpa_ref(Q, K, V, causal))
+
+
 def test_flash_errors(wo):
     x = torch.zeros(1, 1, 8, 96, dtype=torch.half, device="cuda")
     with pytest.raises(RuntimeError, match="head_dim"):

@@ -18,9 +18,10 @@
 //    d column -- comes straight out of the row-major V tile with the gfx950 transposing
 //    read ds_read_b64_tr_b16 (4 keys per read).
 //  * One barrier per tile; the DMA of tile j+3 is issued right after it.
-//  * FP32 online softmax in base 2 (scale * log2 e folded into one FMA per score), with
-//    lazy rescaling: the running max is only moved (and O and the row sum rescaled) when
-//    a row's max grows by more than 2^8 in some lane of the wave, so P stays <= 2^8 in fp16.
+//  * FP32 online softmax in base 2 (scale * log2 e folded into one FMA per score) against a
+//    stale running max: no per-tile row max; the running max is only moved (and O and the
+//    row sum rescaled, the tile recomputed) when some probability could reach 2^15, which
+//    the lane's partial sum shows, so P stays below 2^15 in fp16.
 //  * Causal (key j <= query i, top-left aligned as torch SDPA's is_causal): key tiles past
 //    the workgroup's last query are never loaded, tiles past a wave's own last query are
 //    skipped by that wave, masks are applied only on tiles that cross the diagonal or the
@@ -50,7 +51,6 @@ constexpr int FA_BQ = FA_WAVES * FA_WQ;     // queries per workgroup
 constexpr int FA_BKV = 64;                  // keys per tile
 constexpr int FA_NS = 4;                    // LDS ring depth
 constexpr float kNegInf = -__builtin_huge_valf();
-constexpr float kLazyMax = 8.0f;            // rescale only when a max grows by > 2^8
 
 template <int D>
 struct FaCfg {
@@ -123,8 +123,6 @@ __device__ __forceinline__ void fa_scores(const WMMA_LDS unsigned char* s, const
     }
 }
 
-// Online softmax of one tile for both query blocks.  Returns (through `resc`) whether O
-// must be rescaled before this tile's PV product, and the per-query factors in `alpha`.
 // Sets masked scores (keys past Sk or, causal, past the query) to -inf.
 __device__ __forceinline__ void fa_mask(f32x16 (&S)[2][FA_NQB], int kv0, int qrow0, int Sk,
                                         bool causal, int h) {
@@ -142,48 +140,68 @@ __device__ __forceinline__ void fa_mask(f32x16 (&S)[2][FA_NQB], int kv0, int qro
     }
 }
 
+// Online softmax of one tile, both query blocks (base 2, FP32), with a stale running max.
+// Returns (through `resc`) whether O must be rescaled by `alpha` before this tile's PV.  The probabilities
+// are computed straight against the running max m_run, p = exp2(c*s - m_run), with no
+// per-tile max: that max is only needed when some p could leave fp16's range, and every
+// such case shows in the lane's partial sum (p <= sum), so a wave-uniform check of
+// "sum > 2^15 or no key seen yet" decides.  Only then is the tile's max taken (one
+// cross-lane exchange), m_run raised, O and l rescaled by alpha = exp2(m_old - m_new) and
+// the tile recomputed -- on the first tile, and after that only when a row's max grows by
+// more than 2^15.  Otherwise every p < 2^15 < 65504, so P converts to fp16 safely.  The
+// row sum uses four independent partial sums (short dependency chains).
+__device__ __forceinline__ void fa_exp_tile(const f32x16 (&S)[2][FA_NQB], int qb, float c, float m,
+                                            f16x8 (&P)[2][2][FA_NQB], float& sum) {
+    float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kb][qb][8 * hh + e], c, -m));
+                s4[e & 3] += pv;
+                P[kb][hh][qb][e] = (f16)pv;
+            }
+    sum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+}
+
 __device__ __forceinline__ void fa_softmax(f32x16 (&S)[2][FA_NQB], float c, float (&m_run)[FA_NQB],
                                            float (&l_run)[FA_NQB], float (&alpha)[FA_NQB], bool& resc,
                                            f16x8 (&P)[2][2][FA_NQB]) {
-    float mloc[FA_NQB];
-#pragma unroll
-    for (int qb = 0; qb < FA_NQB; ++qb) {
-        float mx = kNegInf;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, S[kb][qb][r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        mloc[qb] = mx * c;  // c > 0: max of the scaled scores
-    }
-    // Lazy rescale decision (wave-uniform).
+    constexpr float kSumMax = 32768.0f;  // 2^15
+    float sum[FA_NQB];
     bool need = false;
 #pragma unroll
-    for (int qb = 0; qb < FA_NQB; ++qb) need |= mloc[qb] > m_run[qb] + kLazyMax;
-    resc = __builtin_amdgcn_ballot_w64(need) != 0;
-#pragma unroll
     for (int qb = 0; qb < FA_NQB; ++qb) {
-        // Selects, not branches, so the softmax stays one basic block.  A running max of
-        // -inf (no key seen yet) gives alpha = 0 and keeps exp2's argument finite.
-        const float mn = resc ? fmaxf(m_run[qb], mloc[qb]) : m_run[qb];
-        const float a = m_run[qb] == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(m_run[qb] - mn);
-        alpha[qb] = resc ? a : 1.0f;
-        m_run[qb] = mn;
-        l_run[qb] *= alpha[qb];
-        const float m = m_run[qb] == kNegInf ? 0.0f : m_run[qb];
-        float sum = 0.0f;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kb][qb][8 * hh + e], c, -m));
-                    sum += pv;
-                    P[kb][hh][qb][e] = (f16)pv;
-                }
-        l_run[qb] += sum;
+        const bool fresh = m_run[qb] == kNegInf;
+        fa_exp_tile(S, qb, c, fresh ? 0.0f : m_run[qb], P, sum[qb]);
+        need |= fresh || !(sum[qb] <= kSumMax);  // also catches inf / NaN
     }
+    resc = __builtin_amdgcn_ballot_w64(need) != 0;
+    if (resc) {  // wave-uniform, rare
+#pragma unroll
+        for (int qb = 0; qb < FA_NQB; ++qb) {
+            float mx = kNegInf;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, S[kb][qb][r]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mn = fmaxf(m_run[qb], mx * c);  // c > 0: max of the scaled scores
+            // A running max of -inf (no key seen yet) gives alpha = 0 and keeps exp2's
+            // argument finite.
+            alpha[qb] = m_run[qb] == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(m_run[qb] - mn);
+            m_run[qb] = mn;
+            l_run[qb] *= alpha[qb];
+            fa_exp_tile(S, qb, c, mn == kNegInf ? 0.0f : mn, P, sum[qb]);
+        }
+    } else {
+#pragma unroll
+        for (int qb = 0; qb < FA_NQB; ++qb) alpha[qb] = 1.0f;
+    }
+#pragma unroll
+    for (int qb = 0; qb < FA_NQB; ++qb) l_run[qb] += sum[qb];
 }
 
 // O^T += V^T P^T over the tile's four 16-key steps.
