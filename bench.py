@@ -8,8 +8,10 @@
 Default run (the driver's contract): ONE JSON line for the headline metric of
 BASELINE.json, "FP16 GEMM TFLOPS (% MFMA peak) @4096^3; W4A16 M=1 HBM GB/s".
 A step is one wmma_ops_amd.matmul of the 4096^3 FP16 GEMM: A[4096,4096] and
-B[4096,4096] fp16 ~ N(0,1) (seed 42 + 1), fp32 output, inputs resident in HBM.  W warmup
-steps, then K timed steps between two synchronisations; `value` = 2*M*N*K / time.
+B[4096,4096] fp16 ~ N(0,1) (seed 42 + 1), fp32 output, inputs resident in HBM.  The same
+step first runs for 100 ms of GPU time (the clock ramps up under sustained load: timed
+from idle, the first tens of launches run 10-15% slower), then W warmup steps, then K
+timed steps between two synchronisations; `value` = 2*M*N*K / time.
 `roofline.achieved` divides the same FLOPs by the kernel's mean duration measured with
 HIP events on the stream the kernel is launched on (the current stream).  The W4A16 M=1
 decode figures (configs[3], K=4096, N in {4096, 14336}, G=128) ride along in the same
@@ -53,8 +55,8 @@ METRIC = "FP16 GEMM TFLOPS (% MFMA peak) @4096^3; W4A16 M=1 HBM GB/s"
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[1])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-w4a16", action="store_true", help="skip the W4A16 decode figures")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -64,13 +66,32 @@ def parse():
 
 
 # ---------------------------------------------------------------------------- timing --
+SETTLE_MS = 100.0  # sustained load before any timing: the GPU's clock ramps up over ~50 ms
+
+
+def settle(fn, ms=SETTLE_MS):
+    """Runs fn(i) back to back until `ms` of GPU time have passed, so that the timed calls
+    that follow see the clock a sustained workload runs at, not the idle one."""
+    import torch
+
+    spent, i = 0.0, 0
+    while spent < ms:
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(16):
+            fn(i)
+            i += 1
+        e.record()
+        e.synchronize()
+        spent += s.elapsed_time(e)
+
+
 def time_batches(fn, calls, batches=5):
     """Median over `batches` of (event-timed batch of `calls` back-to-back calls)/calls,
     in ms.  fn(i) runs call i (so inputs can rotate)."""
     import torch
 
-    for i in range(min(calls, 3)):
-        fn(i)
+    settle(fn)
     torch.cuda.synchronize()
     out = []
     for _ in range(batches):
@@ -103,6 +124,7 @@ def time_graph(fn, copies, batches=5):
             outs.append(fn(i))
     graph.replay()
     torch.cuda.synchronize()
+    settle(lambda i: graph.replay())
     ts = []
     for _ in range(batches):
         s0, e0 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -287,6 +309,7 @@ def gemm_bench(wo, steps, warmup):
     g = torch.Generator().manual_seed(42 + 1)
     A = torch.randn(M, K, generator=g).half().cuda()
     B = torch.randn(K, N, generator=g).half().cuda()
+    settle(lambda i: wo.matmul(A, B))
     for _ in range(warmup):
         wo.matmul(A, B)
     torch.cuda.synchronize()

@@ -117,6 +117,44 @@ def test_w4a16_gemm_tiles(wo, M, K, N, G):
     assert torch.equal(Yp, Yu)
 
 
+# The M <= 2 decode kernel applies s and z to each 128-deep partial sum: the MFMA sees the
+# nibbles offset by 1024 and the offset is subtracted through fp32 sums of the activations.
+# Activations with a large common mean or outlier channels make that offset term large
+# against the result, which is where a cancellation mistake would show.
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("kind", ["mean4", "outliers"])
+def test_w4a16_decode_offset_cancellation(wo, M, kind):
+    K, N, G = 4096, 512, 128
+    report("w4a16_offset", M=M, kind=kind)
+    A, q, s, z = oi.make_inputs(M, K, N, G, seed=7 + M)
+    if kind == "mean4":
+        A = (4.0 + 0.5 * A.float()).half()
+    else:
+        A = A.clone()
+        A[:, ::512] *= 64.0
+    ref = oi.w4a16_ref(A, q, s, z, G)
+    pk = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
+    for zeros in (oi.pack_zeros(z), z):
+        Y = wo.matmul_int4(A.cuda(), pk, torch.from_numpy(s).cuda(), torch.from_numpy(zeros).cuda(), G)
+        err = og.max_rel_err(Y, ref)
+        assert err <= 1e-3, err
+
+
+@pytest.mark.parametrize("M", [1, 2])
+def test_w4a16_decode_q_equals_z_cancels(wo, M):
+    # q == z everywhere: the result is a difference of two fp32 sums of the same terms,
+    # zero up to their rounding (far below the offset term 1024 s sum|a|).
+    K, N, G = 4096, 256, 128
+    q = np.random.default_rng(3).integers(0, 16, (K // G, N), dtype=np.uint8)
+    zq = np.repeat(q, G, axis=0)
+    s = np.full((K // G, N), 0.01, dtype=np.float16)
+    A = torch.randn(M, K, generator=torch.Generator().manual_seed(5)).half()
+    pk = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(zq)).cuda())
+    Y = wo.matmul_int4(A.cuda(), pk, torch.from_numpy(s).cuda(), torch.from_numpy(q).cuda(), G)
+    offset = 1024 * 0.01 * A.float().abs().sum(dim=1, keepdim=True)
+    assert (Y.cpu().abs() <= 1e-5 * offset).all(), float((Y.cpu().abs() / offset).max())
+
+
 def test_w4a16_zero_when_q_equals_z(wo):
     K, N, G = 256, 64, 128
     q = np.full((K, N), 9, dtype=np.uint8)

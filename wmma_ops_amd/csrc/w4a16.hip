@@ -458,19 +458,26 @@ w4a16_decode_kernel(W4Args p) {
 // weight load u only.  Every load is unconditional (indices clamped into range): the code
 // is straight-line and each wait covers exactly the loads it needs.
 //
-// The multiply-accumulate runs on v_mfma_f32_16x16x32_f16:
+// The multiply-accumulate runs on v_mfma_f32_16x16x32_f16, with the scale and zero point
+// applied to each pair-step's partial sum rather than to every weight:
 //   A operand (lane l: row l%16 = activation row m, K quarter l/16): the activations a',
 //     where a' = a at offsets {0,1,4,5} and a/16 at {2,3,6,7} of every 8 values;
-//   B operand (lane l: column l%16 = slice column n, same K quarter): the dequantised
-//     weights of one prepacked word, W = fp16((q - z) s).  (w & 0x000F000F) | 0x6400..
-//     is the fp16 pair (1024 + q0, 1024 + q1); minus (1024 + z) it is exactly q - z, and
-//     one fp16 multiply by s rounds once, as the definition requires.  The pairs at
-//     offsets {2,3,6,7} come out of (w & 0x00F000F0) | 0x6400.. as 1024 + 16 q, giving
-//     fp16(16 (q - z) s) = 16 W exactly (a power-of-two scale commutes with rounding),
-//     which the a/16 of the A operand cancels.  One shift, four v_and_or, four v_pk_add
-//     and four v_pk_mul per 8 weights, no shifts per nibble.
-// The accumulator runs over every group; the eight waves' partials meet in LDS at the end.
-// Requires G = 128 * 2^j (a pair-step never straddles two groups).
+//   B operand (lane l: column l%16 = slice column n, same K quarter): the raw nibbles of
+//     one prepacked word as fp16.  (w & 0x000F000F) | 0x6400.. is the exact fp16 pair
+//     (1024 + q0, 1024 + q1); the pairs at offsets {2,3,6,7} come out of
+//     (w & 0x00F000F0) | 0x6400.. as 1024 + 16 q, which the a/16 of the A operand turns
+//     back into 64 + q.  One shift and four v_and_or per 8 weights.
+//   Per pair-step t (128 values of K, inside one group g):
+//     sum_k a_k (q_k - z) s = s (D_t - 1024 P_t - z Q_t),
+//     D_t = sum a' B (four MFMAs into a fresh accumulator), P_t = sum a', Q_t = sum a.
+//   The lane that loaded pair-step t's activation chunk sums its 8 values (v_dot2 against
+//   ones), a 16-lane DPP reduction gives P_t and Q_t for the whole pair-step, and that same
+//   lane holds s and z of (t, its column), so it adds s (1024 P_t + z Q_t) to a private
+//   correction that is reduced once at the end.  The products are exact and the sums are
+//   fp32, so the result differs from the fp16-rounded dequantised weights of the definition
+//   by at most their rounding (2^-11 of each weight).
+// The eight waves' partials meet in LDS at the end.  Requires G = 128 * 2^j (a pair-step
+// never straddles two groups).
 // D layout: lane l holds column n = l%16 and rows m = 4*(l/16) + r; rows 0..3 live in
 // lanes 0..15.
 constexpr int DM_NW = 8;
@@ -479,6 +486,20 @@ constexpr int DM_MAXM = 4;
 // LDS row stride (halves) of a wave's staged activations: DM_U pair-steps of 128 values
 // plus 16 bytes, so rows fall on different banks.
 constexpr int DM_ROW = DM_U * 128 + 8;
+
+// Sum over the 16 lanes of each DPP row, returned in every lane of the row.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f32<0x141>(v);  // row_half_mirror
+    v += dpp_f32<0x140>(v);  // row_mirror
+    return v;
+}
 
 template <int MM>
 struct DecodeMRound {
@@ -538,12 +559,33 @@ w4a16_decode_mfma_kernel(W4Args p) {
 
     uint32_t magic = 0x64006400u;
     asm volatile("" : "+v"(magic));  // keep the constant in a VGPR: one v_and_or per pair
-    f32x4 d{};
+    // DEFER: scale and zero applied per pair-step (fewer VALU operations for one or two
+    // rows; from three rows on the per-row sums cost as much as they save).
+    constexpr bool DEFER = MM <= 2;
+    f32x4 d{};              // exact path: accumulator over all pair-steps
+    float y[MM], corr[MM];  // deferred path: sum of s D_t (lanes 0..15); this lane's corrections
+#pragma unroll
+    for (int m = 0; m < MM; ++m) y[m] = corr[m] = 0.0f;
     const int am = col < MM ? col : 0;  // A-operand row (rows >= M repeat row 0, unused)
+    const f16x2 ones = {(f16)1.0f, (f16)1.0f};
     auto compute_round = [&](int r, const DecodeMRound<MM>& R, f16* buf) {
-        // stage a' (this lane's chunk of every row)
+        // This lane's pair-step: its activation chunk, scale and zero.
+        const bool lane_live = wave + DM_NW * (DM_U * r + sub) < KP;
+        float P[MM], Q[MM];
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
+            if constexpr (DEFER) {
+                // 1024 P and Q of the pair-step (offsets {0,1,4,5} in e1, {2,3,6,7} in e2)
+                const float e1 = __builtin_amdgcn_fdot2(
+                    as_h2(R.a[m][0]), ones,
+                    __builtin_amdgcn_fdot2(as_h2(R.a[m][2]), ones, 0.0f, false), false);
+                const float e2 = __builtin_amdgcn_fdot2(
+                    as_h2(R.a[m][1]), ones,
+                    __builtin_amdgcn_fdot2(as_h2(R.a[m][3]), ones, 0.0f, false), false);
+                P[m] = row16_sum(__builtin_fmaf(e2, 64.0f, e1 * 1024.0f));
+                Q[m] = row16_sum(e1 + e2);
+            }
+            // stage a' (this lane's chunk of row m)
             f16x8 a = as_f16x8(R.a[m]);
 #pragma unroll
             for (int e = 2; e < 8; e += 4) {
@@ -559,27 +601,48 @@ w4a16_decode_mfma_kernel(W4Args p) {
             z = (rz >> (4 * (n & 7))) & 0xFu;
         else
             z = rz & 0xFu;
+        if constexpr (DEFER) {
+            const float sf = lane_live ? (float)__builtin_bit_cast(f16, (uint16_t)rs) : 0.0f;
+            const float zf = (float)z;
+#pragma unroll
+            for (int m = 0; m < MM; ++m)
+                corr[m] = __builtin_fmaf(sf, __builtin_fmaf(zf, Q[m], P[m]), corr[m]);
+        }
         const int sz = (int)(rs | (z << 16));
         const f16* arow = buf + am * DM_ROW + 32 * sub;
 #pragma unroll
         for (int u = 0; u < DM_U; ++u) {
-            const uint32_t v = (uint32_t)__shfl(sz, 16 * u + col);
+            const uint32_t v = (uint32_t)__shfl(DEFER ? (int)rs : sz, 16 * u + col);
             const int pp = wave + DM_NW * (DM_U * r + u);
             if (pp < KP) {
                 const uint32_t zz = v >> 16, s = v & 0xFFFFu;
                 const uint32_t z1 = 0x6400u | zz, z16 = 0x6400u | (zz << 4);
                 const f16x2 zs1 = as_h2(z1 | (z1 << 16)), zs16 = as_h2(z16 | (z16 << 16));
                 const f16x2 ss = as_h2(s | (s << 16));
+                f32x4 acc = DEFER ? f32x4{} : d;
 #pragma unroll
                 for (int w = 0; w < 4; ++w) {
                     const uint32_t x = R.w[u][w], x8 = x >> 8;
                     u32x4 bv;
-                    bv[0] = as_u32((as_h2((x & 0x000F000Fu) | magic) - zs1) * ss);
-                    bv[1] = as_u32((as_h2((x & 0x00F000F0u) | magic) - zs16) * ss);
-                    bv[2] = as_u32((as_h2((x8 & 0x000F000Fu) | magic) - zs1) * ss);
-                    bv[3] = as_u32((as_h2((x8 & 0x00F000F0u) | magic) - zs16) * ss);
+                    bv[0] = (x & 0x000F000Fu) | magic;
+                    bv[1] = (x & 0x00F000F0u) | magic;
+                    bv[2] = (x8 & 0x000F000Fu) | magic;
+                    bv[3] = (x8 & 0x00F000F0u) | magic;
+                    if constexpr (!DEFER) {  // W = fp16((q - z) s), 16 W at {2,3,6,7}
+                        bv[0] = as_u32((as_h2(bv[0]) - zs1) * ss);
+                        bv[1] = as_u32((as_h2(bv[1]) - zs16) * ss);
+                        bv[2] = as_u32((as_h2(bv[2]) - zs1) * ss);
+                        bv[3] = as_u32((as_h2(bv[3]) - zs16) * ss);
+                    }
                     const f16x8 av = as_f16x8(*reinterpret_cast<const u32x4*>(arow + 128 * u + 8 * w));
-                    d = mfma16(av, as_f16x8(bv), d);
+                    acc = mfma16(av, as_f16x8(bv), acc);
+                }
+                if constexpr (DEFER) {
+                    const float sf = (float)__builtin_bit_cast(f16, (uint16_t)s);
+#pragma unroll
+                    for (int m = 0; m < MM; ++m) y[m] = __builtin_fmaf(sf, acc[m], y[m]);
+                } else {
+                    d = acc;
                 }
             }
         }
@@ -604,10 +667,18 @@ w4a16_decode_mfma_kernel(W4Args p) {
             load_round(r + 3, R1);
         }
     }
-    // Rows 0..3 are d[0..3] of lanes 0..15.
+    // Rows 0..MM-1 live in lanes 0..15 (d[m], or y[m] less the corrections of the four
+    // lanes of the column, one per pair-step of a round).
+    if constexpr (DEFER) {
+#pragma unroll
+        for (int m = 0; m < MM; ++m) {
+            corr[m] += __shfl_xor(corr[m], 16);
+            corr[m] += __shfl_xor(corr[m], 32);
+        }
+    }
     if (sub == 0) {
 #pragma unroll
-        for (int q = 0; q < DM_MAXM; ++q) red[wave][q][col] = d[q];
+        for (int m = 0; m < MM; ++m) red[wave][m][col] = DEFER ? y[m] - corr[m] : d[m];
     }
     __syncthreads();
     if (tid < 16 * MM) {
