@@ -146,4 +146,41 @@ __device__ __forceinline__ void grouped_tile(int pid, int tiles_m, int tiles_n, 
     *tn = in / gsize;
 }
 
+// Sum of split-K partials p[s * stride + 0 .. W-1] over s = 0, 1, ..., split-1, added in
+// that order (the fixed order every split-K path shares, so results do not depend on
+// scheduling).  The loads of eight splits are issued before any is waited on: a split-K
+// reduction is one memory round trip per eight splits, not one per split.
+template <int W>
+struct FVec;
+template <>
+struct FVec<1> {
+    using T = float;
+};
+template <>
+struct FVec<4> {
+    using T = f32x4;
+};
+template <int W>
+__device__ __forceinline__ void splitk_sum(const float* p, int64_t stride, int split,
+                                           float (&v)[W]) {
+    using T = typename FVec<W>::T;
+    constexpr int B = 8;
+    T acc{};
+    for (int s0 = 0; s0 < split; s0 += B) {
+        T t[B];
+#pragma unroll
+        for (int u = 0; u < B; ++u)  // clamped index: every load unconditional
+            t[u] = *reinterpret_cast<const T*>(p + (int64_t)min(s0 + u, split - 1) * stride);
+#pragma unroll
+        for (int u = 0; u < B; ++u)
+            if (s0 + u < split) acc += t[u];
+    }
+    if constexpr (W == 1) {
+        v[0] = acc;
+    } else {
+#pragma unroll
+        for (int e = 0; e < W; ++e) v[e] = acc[e];
+    }
+}
+
 }  // namespace wmma_amd

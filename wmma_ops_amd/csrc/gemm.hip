@@ -661,21 +661,28 @@ gemm_skinny_kernel(GemmArgs p) {
 }
 
 // ------------------------------------------------------------------------------------
-// Split-K reduction + epilogue: out = alpha * sum_s ws[s] (+ beta * C_in).
+// Split-K reduction + epilogue: out = alpha * sum_s ws[s] (+ beta * C_in).  One thread per
+// W columns of a row (W = 4 when N is a multiple of 4 and the workspace 16-byte aligned).
 // ------------------------------------------------------------------------------------
+template <int W>
 __global__ void __launch_bounds__(256)
 splitk_reduce_kernel(const float* ws, int split, const float* Cin, int64_t ldcin, float* Cout,
                      int64_t ldc, int M, int N, float alpha, float beta) {
     const int64_t total = (int64_t)M * N;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     const bool use_c = beta != 0.0f && Cin != nullptr;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-        const int64_t row = i / N, col = i % N;
-        float v = ws[i];
-        for (int s = 1; s < split; ++s) v += ws[(int64_t)s * total + i];
-        v = alpha * v;
-        if (use_c) v += beta * Cin[row * ldcin + col];
-        Cout[row * ldc + col] = v;
+    const int nv = (N + W - 1) / W;
+    for (int row = blockIdx.y; row < M; row += gridDim.y) {
+        for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < nv; q += gridDim.x * blockDim.x) {
+            const int col = q * W;
+            float v[W];
+            splitk_sum<W>(ws + (int64_t)row * N + col, total, split, v);
+#pragma unroll
+            for (int e = 0; e < W; ++e) {
+                float r = alpha * v[e];
+                if (use_c) r += beta * Cin[(int64_t)row * ldcin + col + e];
+                Cout[(int64_t)row * ldc + col + e] = r;
+            }
+        }
     }
 }
 
@@ -766,11 +773,16 @@ hipError_t launch_gemm(const GemmLaunch& g, hipStream_t stream) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || pl.split_k <= 1) return e;
 
-    const int64_t total = (int64_t)g.M * g.N;
-    int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream,
-                       static_cast<const float*>(g.workspace), pl.split_k, g.C_in, g.ldc_in,
-                       g.C_out, g.ldc, g.M, g.N, g.alpha, g.beta);
+    const bool vec4 = g.N % 4 == 0 && (reinterpret_cast<uintptr_t>(g.workspace) & 15u) == 0;
+    const int nv = vec4 ? g.N / 4 : g.N;
+    const dim3 grid(std::min(ceil_div(nv, 256), 64), std::min(g.M, 65535));
+    const float* ws = static_cast<const float*>(g.workspace);
+    if (vec4)
+        hipLaunchKernelGGL(splitk_reduce_kernel<4>, grid, dim3(256), 0, stream, ws, pl.split_k,
+                           g.C_in, g.ldc_in, g.C_out, g.ldc, g.M, g.N, g.alpha, g.beta);
+    else
+        hipLaunchKernelGGL(splitk_reduce_kernel<1>, grid, dim3(256), 0, stream, ws, pl.split_k,
+                           g.C_in, g.ldc_in, g.C_out, g.ldc, g.M, g.N, g.alpha, g.beta);
     return hipGetLastError();
 }
 

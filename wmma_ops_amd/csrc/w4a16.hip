@@ -1229,14 +1229,19 @@ w4a16_mfma_kernel(W4Args p) {
     }
 }
 
+template <int W>
 __global__ void __launch_bounds__(256)
 w4a16_reduce_kernel(const float* ws, int split, float* Y, int64_t ldy, int M, int N) {
     const int64_t total = (int64_t)M * N;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        float v = ws[i];
-        for (int s = 1; s < split; ++s) v += ws[(int64_t)s * total + i];
-        Y[(i / N) * ldy + i % N] = v;
+    const int nv = (N + W - 1) / W;
+    for (int row = blockIdx.y; row < M; row += gridDim.y) {
+        for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < nv; q += gridDim.x * blockDim.x) {
+            const int col = q * W;
+            float v[W];
+            splitk_sum<W>(ws + (int64_t)row * N + col, total, split, v);
+#pragma unroll
+            for (int e = 0; e < W; ++e) Y[(int64_t)row * ldy + col + e] = v[e];
+        }
     }
 }
 
@@ -1419,9 +1424,16 @@ hipError_t launch_w4a16_zf(const W4Args& a, const W4A16Launch& w, hipStream_t st
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || pl.split <= 1) return e;
-    const int64_t total = (int64_t)w.M * w.N;
-    hipLaunchKernelGGL(w4a16_reduce_kernel, dim3(grid_for(total, 256)), dim3(256), 0, stream,
-                       static_cast<const float*>(w.workspace), pl.split, w.Y, w.ldy, w.M, w.N);
+    const bool vec4 = w.N % 4 == 0 && (reinterpret_cast<uintptr_t>(w.workspace) & 15u) == 0;
+    const int nv = vec4 ? w.N / 4 : w.N;
+    const dim3 grid(std::min(ceil_div(nv, 256), 64), std::min(w.M, 65535));
+    const float* ws = static_cast<const float*>(w.workspace);
+    if (vec4)
+        hipLaunchKernelGGL(w4a16_reduce_kernel<4>, grid, dim3(256), 0, stream, ws, pl.split, w.Y,
+                           w.ldy, w.M, w.N);
+    else
+        hipLaunchKernelGGL(w4a16_reduce_kernel<1>, grid, dim3(256), 0, stream, ws, pl.split, w.Y,
+                           w.ldy, w.M, w.N);
     return hipGetLastError();
 }
 
