@@ -100,6 +100,56 @@ def test_skinny_split_k(wo, M, N, K):
     _check(wo.matmul(A.cuda(), B.cuda()), ref)
 
 
+def _capi():
+    import ctypes
+    import os
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                                   "wmma_ops_amd", "libwmma_ops_amd.so"))
+    vp, i64, i32, f32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    lib.wmma_gemm_workspace_size.restype = sz
+    lib.wmma_gemm_workspace_size.argtypes = [i32, i32, i32, i32]
+    lib.wmma_gemm_f16f32.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32,
+                                     f32, f32, i32, vp, sz, vp]
+    return lib
+
+
+# Split-K partials go through a caller workspace whose contents are arbitrary: a workspace
+# of random bytes, the same workspace again and re-randomised must all give the same bits
+# (fixed summation order), within tolerance of the oracle, and so must the in-place
+# epilogue through the same workspace.
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (16, 14336, 4096), (5, 1024, 14336),
+                                   (3, 4096, 520)])
+def test_skinny_split_k_any_workspace(wo, M, N, K):
+    report("skinny_ws", M=M, N=N, K=K, plan=wo.gemm_plan(M, N, K))
+    lib = _capi()
+    A, B = _inputs(M, N, K, 77 + M, bstd=0.02)
+    ref = og.gemm_ref(A, B)
+    Ad, Bd = A.cuda(), B.cuda()
+    need = lib.wmma_gemm_workspace_size(M, N, K, -1)
+    assert need > 0 and wo.gemm_plan(M, N, K)[4] > 1
+    g = torch.Generator(device="cuda").manual_seed(M + N)
+    ws = torch.randint(0, 256, (need,), dtype=torch.uint8, device="cuda", generator=g)
+    stream = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for rnd in range(3):
+        if rnd == 2:
+            ws.random_(0, 256, generator=g)
+        C = torch.full((M, N), float("nan"), device="cuda")
+        rc = lib.wmma_gemm_f16f32(Ad.data_ptr(), K, Bd.data_ptr(), N, None, N, C.data_ptr(), N,
+                                  M, N, K, 1.0, 0.0, -1, ws.data_ptr(), need, stream)
+        assert rc == 0
+        outs.append(C)
+    torch.cuda.synchronize()
+    _check(outs[0], ref)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    Cin = torch.randn(M, N, generator=torch.Generator().manual_seed(3))
+    Ci = Cin.cuda()
+    rc = lib.wmma_gemm_f16f32(Ad.data_ptr(), K, Bd.data_ptr(), N, Ci.data_ptr(), N, Ci.data_ptr(), N,
+                              M, N, K, 2.0, 0.5, -1, ws.data_ptr(), need, stream)
+    assert rc == 0
+    _check(Ci, og.gemm_ref(A, B, 2.0, 0.5, Cin))
+
+
 def test_skinny_epilogue_in_place(wo):
     A, B = _inputs(16, 4096, 4096, 11, bstd=0.02)
     C = torch.randn(16, 4096, generator=torch.Generator().manual_seed(12))

@@ -567,7 +567,7 @@ gemm_skinny_kernel(GemmArgs p) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar descriptors
     const int q = lane >> 4;   // K quarter
     const int c16 = lane & 15;
     const int n0 = blockIdx.x * SK_COLS;
@@ -583,21 +583,52 @@ gemm_skinny_kernel(GemmArgs p) {
     const bool m_ok = c16 < M;
     const int ncol = n0 + 8 * c16;
 
+    if constexpr (VEC) {
+        // Straight-line double buffering: slab i+1's loads are in flight while slab i is
+        // transposed and multiplied.  Every load is unconditional -- rows past kend and
+        // columns past N come back as zeros through the buffer range check -- so each
+        // wait covers exactly the slab it needs; slabs past the end are all zeros.
+        struct Slab {
+            u32x4 b[8];
+            u32x4 a;
+        };
+        constexpr int STEP = SK_WAVES * 32;
+        const int nsl = (kend - kbeg + STEP - 1) / STEP;  // slabs per wave (uniform)
+        auto load = [&](int i, Slab& S) {
+            const int k0 = kbeg + wave * 32 + i * STEP;
+            const int ka = k0 + 8 * q;
+            const __amdgpu_buffer_rsrc_t b_rs = make_rsrc(p.B + (int64_t)k0 * p.ldb + n0);
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                const bool ok = (ka + r < kend) && (ncol < N);
+                S.b[r] = buf_load16_nt(b_rs, ok ? (uint32_t)(((8 * q + r) * p.ldb + 8 * c16) * 2)
+                                                : kOobOffset);
+            }
+            S.a = buf_load16(a_rs, (m_ok && ka < kend) ? (uint32_t)((c16 * p.lda + ka) * 2)
+                                                       : kOobOffset);
+        };
+        auto compute = [&](const Slab& S) {
+            u32x4 bt[8];
+            transpose8x8(S.b, bt);
+            const f16x8 a8 = as_f16x8(S.a);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] = mfma16(as_f16x8(bt[j]), a8, acc[j]);
+        };
+        Slab S0, S1;
+        load(0, S0);
+        for (int i = 0; i < nsl; i += 2) {
+            load(i + 1, S1);
+            compute(S0);
+            load(i + 2, S0);
+            compute(S1);
+        }
+    } else {
     for (int k0 = kbeg + wave * 32; k0 < kend; k0 += SK_WAVES * 32) {
         const __amdgpu_buffer_rsrc_t b_rs = make_rsrc(p.B + (int64_t)k0 * p.ldb + n0);
         u32x4 rb[8];
         u32x4 av;
         const int ka = k0 + 8 * q;
-        if constexpr (VEC) {
-#pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                const bool ok = (ka + r < kend) && (ncol < N);
-                rb[r] = buf_load16(b_rs, ok ? (uint32_t)(((8 * q + r) * p.ldb + 8 * c16) * 2)
-                                            : kOobOffset);
-            }
-            const bool ok = m_ok && ka < kend;
-            av = buf_load16(a_rs, ok ? (uint32_t)((c16 * p.lda + ka) * 2) : kOobOffset);
-        } else {
+        {
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
                 u32x4 v4;
@@ -633,6 +664,7 @@ gemm_skinny_kernel(GemmArgs p) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[j] = mfma16(as_f16x8(bt[j]), a8, acc[j]);
     }
+    }
 
     // D of MFMA j: lane holds m = lane%16, rows 4*(lane/16)+r -> column 8*(4q+r)+j.
 #pragma unroll
@@ -641,21 +673,31 @@ gemm_skinny_kernel(GemmArgs p) {
         for (int r = 0; r < 4; ++r) red[wave][c16][8 * (4 * q + r) + j] = acc[j][r];
     __syncthreads();
 
-    const bool partial = p.split > 1;
-    float* out = partial ? p.ws + (size_t)blockIdx.y * (size_t)M * (size_t)N : p.Cout;
-    const int64_t ldo = partial ? (int64_t)N : p.ldc;
-    const bool use_c = !partial && p.beta != 0.0f && p.Cin != nullptr;
+    const bool use_c = p.beta != 0.0f && p.Cin != nullptr;
+    if (p.split == 1) {
+        for (int idx = tid; idx < kSkinnyMaxM * SK_COLS; idx += SK_WAVES * kWave) {
+            const int m = idx / SK_COLS, n = idx % SK_COLS;
+            if (m < M && n0 + n < N) {
+                float v = red[0][m][n];
+#pragma unroll
+                for (int w = 1; w < SK_WAVES; ++w) v += red[w][m][n];
+                v = p.alpha * v;
+                if (use_c) v += p.beta * p.Cin[(int64_t)m * p.ldcin + n0 + n];
+                p.Cout[(int64_t)m * p.ldc + n0 + n] = v;
+            }
+        }
+        return;
+    }
+    // Split K: this workgroup's partial goes to the workspace; splitk_reduce_kernel sums
+    // the partials in split order and applies the epilogue.
+    float* part = p.ws + (size_t)blockIdx.y * (size_t)M * (size_t)N;
     for (int idx = tid; idx < kSkinnyMaxM * SK_COLS; idx += SK_WAVES * kWave) {
         const int m = idx / SK_COLS, n = idx % SK_COLS;
         if (m < M && n0 + n < N) {
             float v = red[0][m][n];
 #pragma unroll
             for (int w = 1; w < SK_WAVES; ++w) v += red[w][m][n];
-            if (!partial) {
-                v = p.alpha * v;
-                if (use_c) v += p.beta * p.Cin[(int64_t)m * p.ldcin + n0 + n];
-            }
-            out[(int64_t)m * ldo + n0 + n] = v;
+            part[(int64_t)m * N + n0 + n] = v;
         }
     }
 }

@@ -45,15 +45,30 @@ int make_plan(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* ou
     }
 
     if (M <= kSkinnyMaxM && M > 0 && N > 0 && K > 0) {
-        // Streaming kernel: each workgroup owns kSkinnyBlockN columns and one K range;
-        // split K until the chip holds about two workgroups per CU.
+        // Streaming kernel: each workgroup owns kSkinnyBlockN columns and one K range.
+        // The launch lasts as long as the busiest CU, which streams ceil(W / CUs) of the
+        // W = tiles x split workgroups, each 1/W of the bytes: pick the split that
+        // minimises ceil(W / CUs) / W over W <= 3 x CUs (measured on MI355X: a split that
+        // leaves some CUs one workgroup more than the rest costs 10-25%, and beyond three
+        // workgroups per CU the extra partial sums cost more than the balance gains), the
+        // smaller split on a tie (fewer partial sums to write and reduce).
         p.kernel = WMMA_KERNEL_SKINNY;
         p.tile_cfg = -1;
         p.tile_m = kSkinnyMaxM;
         p.tile_n = kSkinnyBlockN;
-        int tiles = ceil_div(N, kSkinnyBlockN);
-        int want = std::max(1, (2 * num_cus + tiles - 1) / tiles);
-        int split = std::min({want, std::max(1, K / 256), kMaxSplitK});
+        const int tiles = ceil_div(N, kSkinnyBlockN);
+        const int smax = std::min(std::max(1, K / 256), kMaxSplitK);
+        int split = 1;
+        double best = 1e300;
+        for (int sp = 1; sp <= smax; ++sp) {
+            const int64_t w = (int64_t)tiles * sp;
+            if (sp > 1 && w > 3 * (int64_t)num_cus) break;
+            const double cost = (double)ceil_div64(w, num_cus) / (double)w;
+            if (cost < best * 0.99) {
+                best = cost;
+                split = sp;
+            }
+        }
         finish_split(M, N, K, tiles, split, &p);
         *out = p;
         return WMMA_OK;
