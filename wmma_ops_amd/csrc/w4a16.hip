@@ -1324,10 +1324,16 @@ W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
     }
     const int KC = K / 64;
     if (M > 32) {
-        // LDS-DMA W4A16 GEMM: big tiles from 512 rows, K split only to fill the chip.
-        const bool big = M >= 512;
+        // LDS-DMA W4A16 GEMM: 256x256 tiles when they alone occupy at least 3/4 of the
+        // CUs (from 512 rows), else 128x128 tiles; K split only to fill the chip.
+        // (Measured: M = 2048, N = 4096 -- 128 big tiles need a 2-way split whose
+        // partial-sum pass costs 16 us of 90, 512 small tiles none; M = 1024, N = 14336 --
+        // 224 big tiles beat 896 small ones by 20%.)
+        const int64_t big_tiles = (int64_t)ceil_div(M, 256) * ceil_div(N, 256);
+        const bool big = M >= 512 && 4 * big_tiles >= 3 * (int64_t)num_cus;
         const int bm = big ? 256 : 128, bn = big ? 256 : 128;
         const int64_t tiles = (int64_t)ceil_div(M, bm) * ceil_div(N, bn);
+        pl.big = big ? 1 : 0;
         // Split only while every split keeps at least one CU's worth of tiles: the partial
         // sums cost a second pass over M x N fp32 per split.
         int s = 1;
@@ -1397,7 +1403,7 @@ hipError_t launch_w4a16_zf(const W4Args& a, const W4A16Launch& w, hipStream_t st
         return hipGetLastError();
     }
     if (pl.kind == W4_GEMM) {
-        const bool big = w.M >= 512;
+        const bool big = pl.big != 0;
         const int bm = big ? 256 : 128, bn = big ? 256 : 128;
         const dim3 grid(ceil_div(w.M, bm) * ceil_div(w.N, bn), pl.split);
         launch_w4g<ZF>(a, big ? 0 : 1, grid, stream);
