@@ -1094,14 +1094,17 @@ w4a16_gemm_kernel(W4Args p) {
 }
 
 // W4A16 GEMM configurations: BM x BN, WM x WN waves, NS stages.
-//   big  256 x 256, 2 x 4 waves, 4 stages (128 KB LDS): M >= 512
-//   mid  128 x 128, 2 x 2 waves, 4 stages (64 KB LDS):  32 < M < 512
+//   big  256 x 256, 2 x 4 waves, 4 stages (128 KB LDS): from 512 rows
+//   mid  128 x 128, 1 x 4 waves, 4 stages (64 KB LDS):  otherwise.  One wave row, so each
+//        weight of the tile is dequantised once (a 2 x 2 grid dequantises every weight in
+//        both wave rows; measured 4-11% slower at M = 64..256).  6 or 8 stages measured no
+//        faster.
 template <int ZF>
 void launch_w4g(const W4Args& a, int cfg, dim3 grid, hipStream_t stream) {
     if (cfg == 0)
         hipLaunchKernelGGL((w4a16_gemm_kernel<256, 256, 2, 4, 4, ZF>), grid, dim3(8 * kWave), 0, stream, a);
     else
-        hipLaunchKernelGGL((w4a16_gemm_kernel<128, 128, 2, 2, 4, ZF>), grid, dim3(4 * kWave), 0, stream, a);
+        hipLaunchKernelGGL((w4a16_gemm_kernel<128, 128, 1, 4, 4, ZF>), grid, dim3(4 * kWave), 0, stream, a);
 }
 
 // ------------------------------------------------------------------ MFMA (M > GV_MAXM) --
