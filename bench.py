@@ -23,7 +23,7 @@ Workload families (--workload):
   epilogue   configs[1]: C = 2.0*A@B + 0.5*C, out-of-place and in-place, 1024^3/4096^3
   skinny     configs[2]: M in {1,16,64,128} x N in {4096,11008,14336}, K=4096; K=14336,N=4096
   w4a16      configs[3]: M in {1,16,128,2048} x N in {4096,14336}, K=4096, G=128
-  flash      configs[4]: [4,32,4096,128], causal and non-causal
+  flash      configs[4]: [4,32,4096,128], causal and non-causal; and with 8 K/V heads (GQA)
   copy       a plain 256 MiB device copy (calibrates the rocprofv3 byte counters)
 HBM-bound cases rotate their inputs over more than 512 MB (twice the 256 MB MALL) so the
 bytes really come from HBM; microsecond-scale kernels are replayed from a HIP graph.
@@ -271,18 +271,23 @@ def fam_flash(wo):
     from oracle import gemm as og
 
     B, H, S, D = 4, 32, 4096, 128
-    Q, Kt, V = oatt.make_inputs(B, H, S, D, seed=42 + 4)
-    Qd, Kd, Vd = Q.cuda(), Kt.cuda(), V.cuda()
-    for causal in (False, True):
-        ms = time_batches(lambda i: wo.flash_attention(Qd, Kd, Vd, causal, 1.0 / math.sqrt(D)), 10)
-        O = wo.flash_attention(Qd, Kd, Vd, causal, 1.0 / math.sqrt(D))
-        ref = oatt.sdpa_ref(Q[0:1, 0:1], Kt[0:1, 0:1], V[0:1, 0:1], causal)
-        err = og.max_rel_err(O[0:1, 0:1].float(), ref)
-        fl = 4.0 * B * H * S * S * D if not causal else 4.0 * B * H * D * S * (S + 1) / 2
-        line(family="flash", B=B, H=H, S=S, D=D, causal=causal, us=round(ms * 1e3, 1),
-             TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
-             frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4),
-             max_rel_err=float(f"{err:.3e}"))
+    # configs[4] (multi-head), then the same with 8 key/value heads (grouped-query attention,
+    # the extension of the documented API; same FLOPs, a quarter of the K/V bytes)
+    for Hkv in (H, 8):
+        Q, Kt, V = oatt.make_inputs(B, H, S, D, seed=42 + 4, Hkv=Hkv)
+        Qd, Kd, Vd = Q.cuda(), Kt.cuda(), V.cuda()
+        g = H // Hkv
+        for causal in (False, True):
+            ms = time_batches(lambda i: wo.flash_attention(Qd, Kd, Vd, causal, 1.0 / math.sqrt(D)), 10)
+            O = wo.flash_attention(Qd, Kd, Vd, causal, 1.0 / math.sqrt(D))
+            ref = oatt.sdpa_ref(Q[0:1, 0:g], Kt[0:1, 0:1], V[0:1, 0:1], causal)
+            err = og.max_rel_err(O[0:1, 0:g].float(), ref)
+            fl = 4.0 * B * H * S * S * D if not causal else 4.0 * B * H * D * S * (S + 1) / 2
+            line(family="flash", B=B, H=H, Hkv=Hkv, S=S, D=D, causal=causal, us=round(ms * 1e3, 1),
+                 TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
+                 frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4),
+                 max_rel_err=float(f"{err:.3e}"))
+        del Qd, Kd, Vd
 
 
 def fam_copy(wo):

@@ -154,6 +154,18 @@ int wmma_w4a16_gemm(const void* A, int64_t lda, const int32_t* packed, const voi
 int wmma_flash_attn_fwd(const void* Q, const void* K, const void* V, void* O, int B, int H,
                         int Sq, int Sk, int D, float scale, int causal, void* stream);
 
+/*
+ * The same with grouped-query / multi-query attention: K and V are [B,Hkv,Sk,D] with
+ * H % Hkv == 0, and query head h reads key/value head h / (H/Hkv) -- the head mapping of
+ * torch's scaled_dot_product_attention(enable_gqa=True).  Hkv == H is
+ * wmma_flash_attn_fwd.  No counterpart in the reference: its documented flash_attention
+ * (README.md:221-251) takes equal head counts; this is the grouped-query extension of
+ * that API.
+ */
+int wmma_flash_attn_fwd_gqa(const void* Q, const void* K, const void* V, void* O, int B, int H,
+                            int Hkv, int Sq, int Sk, int D, float scale, int causal,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,20 +19,34 @@ def resolve_scale(D: int, scale: float) -> float:
     return scale if scale > 0 else 1.0 / math.sqrt(D)
 
 
+def expand_kv(X, heads: int):
+    """Grouped-query attention: key/value head j serves query heads j*g .. j*g+g-1,
+    g = heads / X.shape[1] (torch SDPA's enable_gqa mapping)."""
+    hkv = X.shape[1]
+    assert heads % hkv == 0
+    g = heads // hkv
+    if isinstance(X, np.ndarray):
+        return np.repeat(X, g, axis=1)
+    return X.repeat_interleave(g, dim=1)
+
+
 def sdpa_ref(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, causal: bool = False,
              scale: float = -1.0) -> torch.Tensor:
-    """FP32 scaled-dot-product attention on the CPU (the library routine)."""
+    """FP32 scaled-dot-product attention on the CPU (the library routine); K/V may carry
+    fewer heads than Q (grouped-query attention, expanded by expand_kv)."""
     sc = resolve_scale(Q.shape[-1], scale)
-    return F.scaled_dot_product_attention(Q.detach().cpu().float(), K.detach().cpu().float(),
-                                          V.detach().cpu().float(), is_causal=causal, scale=sc)
+    H = Q.shape[1]
+    K, V = expand_kv(K.detach().cpu().float(), H), expand_kv(V.detach().cpu().float(), H)
+    return F.scaled_dot_product_attention(Q.detach().cpu().float(), K, V, is_causal=causal,
+                                          scale=sc)
 
 
 def attention_naive_f64(Q: np.ndarray, K: np.ndarray, V: np.ndarray, causal: bool = False,
                         scale: float = -1.0) -> np.ndarray:
     """Explicit float64 softmax(scale * Q K^T + mask) V, for tiny shapes."""
     Q = np.asarray(Q, dtype=np.float64)
-    K = np.asarray(K, dtype=np.float64)
-    V = np.asarray(V, dtype=np.float64)
+    K = expand_kv(np.asarray(K, dtype=np.float64), Q.shape[1])
+    V = expand_kv(np.asarray(V, dtype=np.float64), Q.shape[1])
     sc = resolve_scale(Q.shape[-1], scale)
     S = np.einsum("...qd,...kd->...qk", Q, K) * sc
     if causal:
@@ -45,11 +59,13 @@ def attention_naive_f64(Q: np.ndarray, K: np.ndarray, V: np.ndarray, causal: boo
     return np.einsum("...qk,...kd->...qd", P, V)
 
 
-def make_inputs(B: int, H: int, S: int, D: int, seed: int, Sk: int | None = None):
-    """Seeded Q, K, V ~ N(0, 1) in fp16."""
+def make_inputs(B: int, H: int, S: int, D: int, seed: int, Sk: int | None = None,
+                Hkv: int | None = None):
+    """Seeded Q [B,H,S,D], K and V [B,Hkv,Sk,D] ~ N(0, 1) in fp16 (Hkv defaults to H)."""
     g = torch.Generator().manual_seed(seed)
     Sk = S if Sk is None else Sk
+    Hkv = H if Hkv is None else Hkv
     Q = torch.randn(B, H, S, D, generator=g).half()
-    K = torch.randn(B, H, Sk, D, generator=g).half()
-    V = torch.randn(B, H, Sk, D, generator=g).half()
+    K = torch.randn(B, Hkv, Sk, D, generator=g).half()
+    V = torch.randn(B, Hkv, Sk, D, generator=g).half()
     return Q, K, V

@@ -41,6 +41,7 @@ def lib():
     L.wmma_int4_unpack.argtypes = [vp, i32, i32, vp, vp]
     L.wmma_w4a16_gemm.argtypes = [vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, vp, i64, vp, sz, vp]
     L.wmma_flash_attn_fwd.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, i32, vp]
+    L.wmma_flash_attn_fwd_gqa.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, vp]
     return L
 
 
@@ -188,6 +189,12 @@ def test_flash_validation_codes(lib):
     assert f(O=None) == INVALID
     assert f(O=FAKE + 8) == MISALIGNED
     assert f(S=0) == OK
+    g = lambda H, Hkv: lib.wmma_flash_attn_fwd_gqa(FAKE, FAKE, FAKE, FAKE, 1, H, Hkv, 128, 128, 128,
+                                                    0.1, 0, None)
+    assert g(8, 3) == INVALID                      # key/value heads must divide query heads
+    assert b"must divide" in lib.wmma_last_error()
+    assert g(8, 0) == INVALID
+    assert g(0, 0) == OK                           # no heads: nothing to do
 
 
 # ---------------------------------------------------------------- torch layer on CPU --

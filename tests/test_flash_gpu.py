@@ -83,6 +83,33 @@ def test_flash_running_max_moves(wo, causal, pattern):
     _check(O, oatt.sdpa_ref(Q, K, V, causal))
 
 
+# Grouped-query / multi-query attention: K and V carry Hkv heads, query head h reads
+# key/value head h // (H / Hkv) (torch SDPA's enable_gqa mapping).
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,H,Hkv,Sq,Sk,D", [(2, 8, 2, 300, 300, 128), (1, 8, 1, 257, 257, 64),
+                                             (2, 4, 4, 128, 128, 64), (1, 6, 3, 100, 333, 128),
+                                             (1, 32, 8, 1024, 1024, 128)])
+def test_flash_gqa(wo, causal, B, H, Hkv, Sq, Sk, D):
+    report("flash_gqa", B=B, H=H, Hkv=Hkv, Sq=Sq, Sk=Sk, D=D, causal=causal)
+    Q, K, V = oatt.make_inputs(B, H, Sq, D, seed=H * 100 + Hkv + Sq, Sk=Sk, Hkv=Hkv)
+    O = wo.flash_attention(Q.cuda(), K.cuda(), V.cuda(), causal=causal)
+    _check(O, oatt.sdpa_ref(Q, K, V, causal))
+
+
+def test_flash_gqa_head_mapping(wo):
+    # V constant within each key/value head j (value j + 1): query head h must output
+    # h // g + 1 everywhere (to within the rounding of the softmax weights), whatever the
+    # scores.
+    H, Hkv, D = 8, 2, 64
+    Q, K, _ = oatt.make_inputs(2, H, 200, D, seed=9, Hkv=Hkv)
+    V = (torch.arange(1, Hkv + 1, dtype=torch.float16).view(1, Hkv, 1, 1)
+         * torch.ones(2, Hkv, 200, D)).half()
+    O = wo.flash_attention(Q.cuda(), K.cuda(), V.cuda(), causal=True).cpu()
+    for h in range(H):
+        want = float(h // (H // Hkv) + 1)
+        assert torch.allclose(O[:, h].float(), torch.full((2, 200, D), want), atol=2e-3 * want), h
+
+
 def test_flash_errors(wo):
     x = torch.zeros(1, 1, 8, 96, dtype=torch.half, device="cuda")
     with pytest.raises(RuntimeError, match="head_dim"):
@@ -90,3 +117,7 @@ def test_flash_errors(wo):
     y = torch.zeros(1, 1, 8, 64, dtype=torch.float32, device="cuda")
     with pytest.raises(RuntimeError, match="float16"):
         wo.flash_attention(y, y, y)
+    q = torch.zeros(1, 6, 8, 64, dtype=torch.half, device="cuda")
+    kv = torch.zeros(1, 4, 8, 64, dtype=torch.half, device="cuda")
+    with pytest.raises(RuntimeError, match="K/V heads must divide Q heads"):
+        wo.flash_attention(q, kv, kv)

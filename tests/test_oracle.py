@@ -229,3 +229,28 @@ def test_sdpa_invariants():
     assert torch.allclose(oatt.sdpa_ref(Q, K[:, :, perm], V[:, :, perm]), oatt.sdpa_ref(Q, K, V), atol=1e-6)
     # default scale is 1/sqrt(D)
     assert oatt.resolve_scale(128, -1.0) == pytest.approx(1 / np.sqrt(128))
+
+
+# Grouped-query attention: key/value head j serves query heads j*g .. j*g+g-1.
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("H,Hkv", [(4, 2), (6, 1), (8, 4)])
+def test_sdpa_ref_gqa_matches_torch_enable_gqa(causal, H, Hkv):
+    Q, K, V = oatt.make_inputs(2, H, 11, 16, seed=H * 10 + Hkv, Sk=13, Hkv=Hkv)
+    got = oatt.sdpa_ref(Q, K, V, causal)
+    lib = torch.nn.functional.scaled_dot_product_attention(Q.float(), K.float(), V.float(),
+                                                           is_causal=causal, enable_gqa=True)
+    assert torch.allclose(got, lib, atol=1e-6)
+    ref = oatt.attention_naive_f64(Q.numpy(), K.numpy(), V.numpy(), causal)
+    assert np.allclose(got.double().numpy(), ref, atol=2e-6)
+
+
+def test_gqa_head_mapping_closed_form():
+    # V rows constant within each key/value head j (value c_j): every output of query head h
+    # equals c_{h // g} (up to the rounding of the softmax weights' sum), whatever the
+    # scores -- pins which head is read.
+    H, Hkv, D = 6, 3, 16
+    Q, K, _ = oatt.make_inputs(1, H, 7, D, seed=3, Hkv=Hkv)
+    c = torch.arange(1, Hkv + 1, dtype=torch.float16).view(1, Hkv, 1, 1) * torch.ones(1, Hkv, 7, D).half()
+    O = oatt.sdpa_ref(Q, K, c)
+    for h in range(H):
+        assert torch.allclose(O[0, h], torch.full_like(O[0, h], float(h // (H // Hkv) + 1)), atol=1e-6)

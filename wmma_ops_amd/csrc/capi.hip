@@ -266,12 +266,14 @@ int wmma_w4a16_gemm(const void* A, int64_t lda, const int32_t* packed, const voi
 }
 
 // ----------------------------------------------------------------------------- flash --
-int wmma_flash_attn_fwd(const void* Q, const void* K, const void* V, void* O, int B, int H,
-                        int Sq, int Sk, int D, float scale, int causal, void* stream) {
+int wmma_flash_attn_fwd_gqa(const void* Q, const void* K, const void* V, void* O, int B, int H,
+                            int Hkv, int Sq, int Sk, int D, float scale, int causal, void* stream) {
     if (B < 0 || H < 0 || Sq < 0 || Sk < 0) return fail(WMMA_ERR_INVALID_ARG, "negative dimension");
     if (D != 64 && D != 128) return fail(WMMA_ERR_UNSUPPORTED, "head_dim %d (supported: 64, 128)", D);
     if (!(scale > 0.0f) || !std::isfinite(scale))
         return fail(WMMA_ERR_INVALID_ARG, "scale must be positive and finite");
+    if (H > 0 && (Hkv <= 0 || H % Hkv != 0))
+        return fail(WMMA_ERR_INVALID_ARG, "key/value heads (%d) must divide query heads (%d)", Hkv, H);
     if (B == 0 || H == 0 || Sq == 0) return ok();
     if (Sk == 0) return fail(WMMA_ERR_INVALID_ARG, "Sk must be positive when Sq > 0");
     if (!Q || !K || !V || !O) return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
@@ -287,12 +289,18 @@ int wmma_flash_attn_fwd(const void* Q, const void* K, const void* V, void* O, in
     f.O = O;
     f.B = B;
     f.H = H;
+    f.Hkv = Hkv;
     f.Sq = Sq;
     f.Sk = Sk;
     f.D = D;
     f.scale = scale;
     f.causal = causal != 0;
     return hip_status(launch_flash_fwd(f, static_cast<hipStream_t>(stream)), "flash launch");
+}
+
+int wmma_flash_attn_fwd(const void* Q, const void* K, const void* V, void* O, int B, int H,
+                        int Sq, int Sk, int D, float scale, int causal, void* stream) {
+    return wmma_flash_attn_fwd_gqa(Q, K, V, O, B, H, H, Sq, Sk, D, scale, causal, stream);
 }
 
 }  // extern "C"

@@ -42,6 +42,7 @@ struct FlashArgs {
     int Sq, Sk;
     int nqb;           // query blocks
     float scale_log2;  // scale * log2(e)
+    int group;         // query heads per key/value head (1: multi-head attention)
 };
 
 constexpr int FA_WAVES = 8;                 // waves per workgroup (two per SIMD)
@@ -298,9 +299,12 @@ flash_fwd_kernel(FlashArgs p) {
     const int Sq = p.Sq, Sk = p.Sk;
     const float c = p.scale_log2;
 
+    // Grouped-query attention: query heads bh of one batch entry come in runs of `group`
+    // that share key/value head bh / group (heads are the inner index of both).
+    const int kvh = bh / p.group;
     const f16* Qb = p.Q + (int64_t)bh * Sq * D;
-    const f16* Kb = p.K + (int64_t)bh * Sk * D;
-    const f16* Vb = p.V + (int64_t)bh * Sk * D;
+    const f16* Kb = p.K + (int64_t)kvh * Sk * D;
+    const f16* Vb = p.V + (int64_t)kvh * Sk * D;
     f16* Ob = p.O + (int64_t)bh * Sq * D;
 
     // Q fragments (B operand of S^T): query qw + 32 qb + lane%32, d = 16 ds + 8 h + 0..7.
@@ -431,6 +435,7 @@ hipError_t launch_flash_fwd(const FlashLaunch& f, hipStream_t stream) {
     a.Sq = f.Sq;
     a.Sk = f.Sk;
     a.nqb = ceil_div(f.Sq, FA_BQ);
+    a.group = f.H / f.Hkv;
     a.scale_log2 = f.scale * 1.4426950408889634f;
     const int BH = f.B * f.H;
     if (f.D == 128)

@@ -73,6 +73,7 @@ struct FlashLaunch {
     const void* V;
     void* O;
     int B, H, Sq, Sk, D;
+    int Hkv;  // key/value heads (H % Hkv == 0; H for multi-head attention)
     float scale;
     bool causal;
 };

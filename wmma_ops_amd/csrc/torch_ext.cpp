@@ -163,7 +163,9 @@ void gemm_inplace(torch::Tensor A, torch::Tensor B, torch::Tensor C, double alph
 }
 
 // flash_attention(Q, K, V, causal=False, scale=-1.0) (README.md:221-251): Q [B,H,Sq,D],
-// K/V [B,H,Sk,D] fp16; scale <= 0 selects 1/sqrt(D).  Returns fp16 [B,H,Sq,D].
+// K/V [B,Hkv,Sk,D] fp16 with Hkv dividing H (Hkv < H: grouped-query attention, query head h
+// reads key/value head h / (H/Hkv)); scale <= 0 selects 1/sqrt(D).  Returns fp16
+// [B,H,Sq,D].
 torch::Tensor flash_attention(torch::Tensor Q, torch::Tensor K, torch::Tensor V, bool causal,
                               double scale) {
     TORCH_CHECK(Q.is_cuda() && K.is_cuda() && V.is_cuda(), "Inputs must be CUDA tensors");
@@ -174,8 +176,10 @@ torch::Tensor flash_attention(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
                 "Inputs must be float16");
     TORCH_CHECK(Q.dim() == 4 && K.dim() == 4 && V.dim() == 4, "Inputs must be 4D [B, H, N, D]");
     TORCH_CHECK(K.sizes() == V.sizes(), "K and V must have the same shape");
-    TORCH_CHECK(Q.size(0) == K.size(0) && Q.size(1) == K.size(1) && Q.size(3) == K.size(3),
-                "Q and K must agree in batch, heads and head_dim");
+    TORCH_CHECK(Q.size(0) == K.size(0) && Q.size(3) == K.size(3),
+                "Q and K must agree in batch and head_dim");
+    TORCH_CHECK(K.size(1) > 0 && Q.size(1) % K.size(1) == 0,
+                "K/V heads must divide Q heads");
     const int64_t D = Q.size(3);
     TORCH_CHECK(D == 64 || D == 128, "head_dim must be 64 or 128");
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(Q.device());
@@ -184,10 +188,11 @@ torch::Tensor flash_attention(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
     V = V.contiguous();
     const float sc = scale > 0.0 ? (float)scale : (float)(1.0 / std::sqrt((double)D));
     auto O = torch::empty_like(Q);
-    int rc = wmma_flash_attn_fwd(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(),
-                                 (int)Q.size(0), (int)Q.size(1), (int)Q.size(2), (int)K.size(2),
-                                 (int)D, sc, causal ? 1 : 0, current_stream(Q));
-    check_status(rc, "wmma_flash_attn_fwd");
+    int rc = wmma_flash_attn_fwd_gqa(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(),
+                                     (int)Q.size(0), (int)Q.size(1), (int)K.size(1),
+                                     (int)Q.size(2), (int)K.size(2), (int)D, sc, causal ? 1 : 0,
+                                     current_stream(Q));
+    check_status(rc, "wmma_flash_attn_fwd_gqa");
     return O;
 }
 
