@@ -230,9 +230,11 @@ def w4a16_case(wo, m, n, use_graph=True):
 
     kw, G = 4096, 128
     A, q, s, z = oi.make_inputs(m, kw, n, G, seed=42 + 3)
+    # one-time layout conversions (outside the timed region): weights to the MFMA layout,
+    # scales/zeros to the slice-major layout (same bytes, contiguous per 16 columns)
     pk0 = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
-    sd = torch.from_numpy(s).cuda()
-    zd = torch.from_numpy(oi.pack_zeros(z)).cuda()
+    sd, zd = wo.prepack_int4_params(torch.from_numpy(s).cuda(),
+                                    torch.from_numpy(oi.pack_zeros(z)).cuda())
     Ad = A.cuda()
     nbytes = kw * n // 2 + (kw // G) * n * 2 + (kw // G) * n // 2 + 2 * m * kw + 4 * m * n
     cp = copies_for(nbytes)

@@ -109,6 +109,21 @@ int wmma_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q, void* str
 
 #define WMMA_ZEROS_PACKED 0  /* zeros int32 [K/G, N/8]; z[g][n] in bits 4*(n%8).. of [g][n/8] */
 #define WMMA_ZEROS_U8 1      /* zeros uint8 [K/G, N]                                       */
+#define WMMA_ZEROS_SLICED 2  /* scales AND zeros in the slice-major layout of
+                                wmma_int4_prepack_params: scales fp16 [N/16][K/G][16],
+                                zeros int32 [N/16][K/G][2] (word w: columns 16*i+8w.., nibble
+                                n%8) -- a 16-column slice's parameters are contiguous      */
+
+/*
+ * Group parameters to the slice-major layout (WMMA_ZEROS_SLICED), bit-exact: scales
+ * fp16 [K/G, N] -> scales_out [N/16][K/G][16]; zeros (WMMA_ZEROS_PACKED int32 [K/G, N/8]
+ * or WMMA_ZEROS_U8 uint8 [K/G, N]) -> zeros_out int32 [N/16][K/G][2].  A one-time layout
+ * conversion like wmma_int4_prepack: the decode kernel reads a slice's parameters as one
+ * contiguous run.  N % 32 == 0, K % group_size == 0.  No reference counterpart.
+ */
+int wmma_int4_prepack_params(const void* scales, const void* zeros, int zeros_format, int K,
+                             int N, int group_size, void* scales_out, int32_t* zeros_out,
+                             void* stream);
 
 /* Workspace bytes wmma_w4a16_gemm needs (fp32 split-K partials). */
 size_t wmma_w4a16_workspace_size(int M, int N, int K, int group_size);
@@ -135,7 +150,8 @@ int wmma_w4a16_plan_make(int M, int N, int K, int group_size, int num_cus, wmma_
 /*
  * Y[M,N] (fp32) = A[M,K] (fp16) @ W[K,N], W[k][n] = fp16((q[k][n] - z[k/G][n]) * s[k/G][n])
  * (dequantised value rounded once to fp16).  packed: output of wmma_int4_prepack.
- * scales: fp16 [K/G, N].  zeros: per zeros_format.  G = group_size, G % 32 == 0, K % G == 0.
+ * scales: fp16 [K/G, N] (or [N/16][K/G][16] with WMMA_ZEROS_SLICED).  zeros: per
+ * zeros_format.  G = group_size, G % 32 == 0, K % G == 0.
  * No reference counterpart (BASELINE-defined W4A16 path).
  */
 int wmma_w4a16_gemm(const void* A, int64_t lda, const int32_t* packed, const void* scales,

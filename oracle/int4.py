@@ -54,6 +54,19 @@ def pack_zeros(z: np.ndarray) -> np.ndarray:
     return out.view(np.int32)
 
 
+def slice_params(s: np.ndarray, z: np.ndarray):
+    """Slice-major group parameters (this library's WMMA_ZEROS_SLICED layout):
+    scales fp16 [K/G, N] -> [N/16, K/G, 16]; uint8 zeros [K/G, N] -> int32 [N/16, K/G, 2]
+    where word w of (slice i, group g) packs z[g][16 i + 8 w + j] into nibble j."""
+    s = np.asarray(s)
+    z = np.asarray(z, dtype=np.uint8)
+    ng, N = s.shape
+    assert N % 16 == 0 and z.shape == (ng, N)
+    s_sl = np.ascontiguousarray(s.reshape(ng, N // 16, 16).transpose(1, 0, 2))
+    z_sl = pack_zeros(z.reshape(ng, N // 16, 16).transpose(1, 0, 2).reshape(N // 16 * ng, 16))
+    return s_sl, np.ascontiguousarray(z_sl.reshape(N // 16, ng, 2))
+
+
 def unpack_zeros(zp: np.ndarray) -> np.ndarray:
     w = np.asarray(zp).view(np.uint32)
     ng, n8 = w.shape

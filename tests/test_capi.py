@@ -39,6 +39,7 @@ def lib():
     L.wmma_w4a16_workspace_size.restype = sz
     L.wmma_int4_prepack.argtypes = [vp, i32, i32, vp, vp]
     L.wmma_int4_unpack.argtypes = [vp, i32, i32, vp, vp]
+    L.wmma_int4_prepack_params.argtypes = [vp, vp, i32, i32, i32, i32, vp, vp, vp]
     L.wmma_w4a16_gemm.argtypes = [vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, vp, i64, vp, sz, vp]
     L.wmma_flash_attn_fwd.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, i32, vp]
     L.wmma_flash_attn_fwd_gqa.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, vp]
@@ -178,6 +179,17 @@ def test_int4_validation_codes(lib):
     assert w(A=FAKE + 2) == MISALIGNED
     assert w(lda=100) == INVALID
     assert w(M=0) == OK
+
+
+def test_prepack_params_validation_codes(lib):
+    f = lambda **kw: lib.wmma_int4_prepack_params(kw.get("s", FAKE), FAKE, kw.get("zf", 0), kw.get("K", 256),
+                                                  kw.get("N", 64), kw.get("G", 64), FAKE, kw.get("zo", FAKE), None)
+    assert f(N=48) == UNSUPPORTED          # N % 32
+    assert f(G=96) == INVALID              # group size must divide K
+    assert f(zf=2) == INVALID              # already sliced
+    assert f(s=None) == INVALID
+    assert f(s=FAKE + 1) == MISALIGNED
+    assert f(zo=FAKE + 2) == MISALIGNED
 
 
 def test_flash_validation_codes(lib):

@@ -254,3 +254,22 @@ def test_gqa_head_mapping_closed_form():
     O = oatt.sdpa_ref(Q, K, c)
     for h in range(H):
         assert torch.allclose(O[0, h], torch.full_like(O[0, h], float(h // (H // Hkv) + 1)), atol=1e-6)
+
+
+def test_slice_params_layout():
+    # every element lands where the sliced layout puts it, and the layout is a bijection
+    rng = np.random.default_rng(5)
+    ng, N = 6, 64
+    sc = rng.standard_normal((ng, N)).astype(np.float16)
+    z = rng.integers(0, 16, (ng, N), dtype=np.uint8)
+    s_sl, z_sl = oi.slice_params(sc, z)
+    assert s_sl.shape == (N // 16, ng, 16) and z_sl.shape == (N // 16, ng, 2) and z_sl.dtype == np.int32
+    zw = z_sl.view(np.uint32)
+    for g in range(ng):
+        for n in range(N):
+            assert s_sl[n // 16, g, n % 16] == sc[g, n]
+            assert (zw[n // 16, g, (n // 8) % 2] >> (4 * (n % 8))) & 0xF == z[g, n]
+    assert sorted(s_sl.ravel().tolist()) == sorted(sc.ravel().tolist())
+    # the packed-zeros words of a slice are the standard packed words, regrouped
+    zp = oi.pack_zeros(z)
+    assert np.array_equal(z_sl.reshape(N // 16, ng, 2).transpose(1, 0, 2).reshape(ng, N // 8), zp)

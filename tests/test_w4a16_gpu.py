@@ -155,6 +155,32 @@ def test_w4a16_decode_q_equals_z_cancels(wo, M):
     assert (Y.cpu().abs() <= 1e-5 * offset).all(), float((Y.cpu().abs() / offset).max())
 
 
+# Slice-major group parameters (prepack_int4_params): a bit-exact layout conversion, and
+# every kernel reads them to the same bits as the standard [K/G, N] layout.
+def test_prepack_params_bit_exact(wo):
+    d = np.load(GOLDEN)
+    for zeros in (d["zeros_packed"], d["zeros_u8"]):
+        s_sl, z_sl = wo.prepack_int4_params(torch.from_numpy(d["scales"]).cuda(),
+                                            torch.from_numpy(zeros).cuda())
+        ws, wz = oi.slice_params(d["scales"], d["zeros_u8"])
+        assert np.array_equal(s_sl.cpu().numpy().view(np.uint16), ws.view(np.uint16))
+        assert np.array_equal(z_sl.cpu().numpy(), wz)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 16, 17, 32, 33, 128, 300])
+@pytest.mark.parametrize("K,N,G", [(4096, 1024, 128), (1024, 352, 64), (2048, 160, 256), (512, 96, 32)])
+def test_w4a16_sliced_params_same_bits(wo, M, K, N, G):
+    report("w4a16_sliced", M=M, K=K, N=N, G=G)
+    A, q, s, z = oi.make_inputs(M, K, N, G, seed=M * 7 + N + G)
+    pk = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
+    Ad, sd, zd = A.cuda(), torch.from_numpy(s).cuda(), torch.from_numpy(oi.pack_zeros(z)).cuda()
+    Y = wo.matmul_int4(Ad, pk, sd, zd, G)
+    s_sl, z_sl = wo.prepack_int4_params(sd, zd)
+    Ys = wo.matmul_int4(Ad, pk, s_sl, z_sl, G)
+    assert torch.equal(Y, Ys)
+    assert og.max_rel_err(Ys, oi.w4a16_ref(A, q, s, z, G)) <= 1e-3
+
+
 def test_w4a16_zero_when_q_equals_z(wo):
     K, N, G = 256, 64, 128
     q = np.full((K, N), 9, dtype=np.uint8)
@@ -188,5 +214,8 @@ def test_w4a16_errors(wo):
         wo.matmul_int4(A, pk, s.float(), z, 64)
     with pytest.raises(RuntimeError, match="Inner dimensions must match"):
         wo.matmul_int4(torch.zeros(1, 32, dtype=torch.half, device="cuda"), pk, s, z, 64)
+    s3 = torch.zeros(4, 1, 16, dtype=torch.half, device="cuda")
+    with pytest.raises(RuntimeError, match="sliced zeros must be int32"):
+        wo.matmul_int4(A, pk, s3, z, 64)
     with pytest.raises(RuntimeError, match="must be a multiple of 64"):
         wo.prepack_int4(torch.zeros(3, 64, dtype=torch.int32, device="cuda"))

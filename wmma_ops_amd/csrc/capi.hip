@@ -192,6 +192,27 @@ int wmma_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q, void* str
                       "int4 unpack launch");
 }
 
+int wmma_int4_prepack_params(const void* scales, const void* zeros, int zeros_format, int K,
+                             int N, int group_size, void* scales_out, int32_t* zeros_out,
+                             void* stream) {
+    if (int rc = check_int4_shape(K, N)) return rc;
+    if (group_size <= 0 || K % group_size != 0)
+        return fail(WMMA_ERR_INVALID_ARG, "group_size (%d) must divide K (%d)", group_size, K);
+    if (zeros_format != WMMA_ZEROS_PACKED && zeros_format != WMMA_ZEROS_U8)
+        return fail(WMMA_ERR_INVALID_ARG, "zeros format %d cannot be sliced", zeros_format);
+    if (!scales || !zeros || !scales_out || !zeros_out) return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
+    if ((reinterpret_cast<uintptr_t>(scales) & 1u) != 0 ||
+        (reinterpret_cast<uintptr_t>(scales_out) & 1u) != 0)
+        return fail(WMMA_ERR_MISALIGNED, "scales must be 2-byte aligned");
+    if ((zeros_format == WMMA_ZEROS_PACKED && (reinterpret_cast<uintptr_t>(zeros) & 3u) != 0) ||
+        (reinterpret_cast<uintptr_t>(zeros_out) & 3u) != 0)
+        return fail(WMMA_ERR_MISALIGNED, "packed zeros must be 4-byte aligned");
+    return hip_status(launch_int4_params_slice(scales, zeros, zeros_format, K / group_size, N,
+                                               scales_out, zeros_out,
+                                               static_cast<hipStream_t>(stream)),
+                      "int4 params launch");
+}
+
 size_t wmma_w4a16_workspace_size(int M, int N, int K, int group_size) {
     if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0 || group_size <= 0) return 0;
     // The plan depends on operand alignment only through the choice of the matrix-pipe
@@ -227,7 +248,8 @@ int wmma_w4a16_gemm(const void* A, int64_t lda, const int32_t* packed, const voi
         return fail(WMMA_ERR_UNSUPPORTED,
                     "group_size (%d) must be a positive multiple of 32 dividing K (%d)", group_size,
                     K);
-    if (zeros_format != WMMA_ZEROS_PACKED && zeros_format != WMMA_ZEROS_U8)
+    if (zeros_format != WMMA_ZEROS_PACKED && zeros_format != WMMA_ZEROS_U8 &&
+        zeros_format != WMMA_ZEROS_SLICED)
         return fail(WMMA_ERR_INVALID_ARG, "unknown zeros format %d", zeros_format);
     if (M == 0) return ok();
     if (!A || !packed || !scales || !zeros || !Y) return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
@@ -237,13 +259,13 @@ int wmma_w4a16_gemm(const void* A, int64_t lda, const int32_t* packed, const voi
     if (!aligned16(packed)) return fail(WMMA_ERR_MISALIGNED, "packed weights must be 16-byte aligned");
     if ((reinterpret_cast<uintptr_t>(scales) & 1u) != 0)
         return fail(WMMA_ERR_MISALIGNED, "scales must be 2-byte aligned");
-    if (zeros_format == WMMA_ZEROS_PACKED && (reinterpret_cast<uintptr_t>(zeros) & 3u) != 0)
+    if (zeros_format != WMMA_ZEROS_U8 && (reinterpret_cast<uintptr_t>(zeros) & 3u) != 0)
         return fail(WMMA_ERR_MISALIGNED, "packed zeros must be 4-byte aligned");
     if ((int64_t)M * lda * 2 > kMaxOffset)
         return fail(WMMA_ERR_UNSUPPORTED, "activation matrix too large for 32-bit offsets");
     W4A16Launch w{};
     const bool aligned = (reinterpret_cast<uintptr_t>(scales) & 7u) == 0 &&
-                         (zeros_format == WMMA_ZEROS_PACKED ||
+                         (zeros_format != WMMA_ZEROS_U8 ||
                           (reinterpret_cast<uintptr_t>(zeros) & 3u) == 0);
     w.plan = w4a16_plan(M, N, K, group_size, current_cus(), aligned);
     const size_t need = w.plan.split > 1 ? (size_t)w.plan.split * M * N * sizeof(float) : 0;

@@ -29,6 +29,10 @@ hipError_t launch_int4_prepack(const int32_t* qweight, int K, int N, int32_t* pa
                                hipStream_t stream);
 hipError_t launch_int4_unprepack(const int32_t* packed, int K, int N, int32_t* qweight,
                                  hipStream_t stream);
+// Scales [KG][N] and zeros (packed or uint8) to the slice-major layout (WMMA_ZEROS_SLICED).
+hipError_t launch_int4_params_slice(const void* scales, const void* zeros, int zeros_format,
+                                    int KG, int N, void* scales_out, int32_t* zeros_out,
+                                    hipStream_t stream);
 hipError_t launch_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q,
                               hipStream_t stream);
 

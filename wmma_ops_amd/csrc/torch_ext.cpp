@@ -241,8 +241,43 @@ torch::Tensor unpack_int4(torch::Tensor qweight) {
     return out;
 }
 
+// prepack_int4_params(scales[K/G, N] fp16, zeros[K/G, N/8] int32 or [K/G, N] uint8)
+//   -> (scales [N/16, K/G, 16] fp16, zeros [N/16, K/G, 2] int32): the slice-major layout
+//   matmul_int4 also accepts (a 16-column slice's parameters contiguous).
+std::vector<torch::Tensor> prepack_int4_params(torch::Tensor scales, torch::Tensor zeros) {
+    TORCH_CHECK(scales.is_cuda() && zeros.is_cuda(), "Inputs must be CUDA tensors");
+    TORCH_CHECK(scales.device() == zeros.device(), "Inputs must be on same device");
+    TORCH_CHECK(scales.dtype() == torch::kFloat16 && scales.dim() == 2,
+                "scales must be float16 [K/group_size, N]");
+    const int64_t ng = scales.size(0), N = scales.size(1);
+    TORCH_CHECK(N % 32 == 0 && ng > 0, "N must be a multiple of 32");
+    int zfmt;
+    if (zeros.dtype() == torch::kInt32) {
+        TORCH_CHECK(zeros.dim() == 2 && zeros.size(0) == ng && zeros.size(1) * 8 == N,
+                    "packed zeros must be int32 [K/group_size, N/8]");
+        zfmt = WMMA_ZEROS_PACKED;
+    } else {
+        TORCH_CHECK(zeros.dtype() == torch::kUInt8 && zeros.dim() == 2 && zeros.size(0) == ng &&
+                        zeros.size(1) == N,
+                    "zeros must be int32 [K/group_size, N/8] or uint8 [K/group_size, N]");
+        zfmt = WMMA_ZEROS_U8;
+    }
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(scales.device());
+    scales = scales.contiguous();
+    zeros = zeros.contiguous();
+    auto so = torch::empty({N / 16, ng, 16}, scales.options());
+    auto zo = torch::empty({N / 16, ng, 2}, torch::dtype(torch::kInt32).device(scales.device()));
+    // K and group_size only enter through K / group_size = ng: pass K = 64 ng, G = 64.
+    int rc = wmma_int4_prepack_params(scales.data_ptr(), zeros.data_ptr(), zfmt, (int)(64 * ng),
+                                      (int)N, 64, so.data_ptr(), zo.data_ptr<int32_t>(),
+                                      current_stream(scales));
+    check_status(rc, "wmma_int4_prepack_params");
+    return {so, zo};
+}
+
 // matmul_int4(A[M,K] fp16, packed (from prepack_int4), scales[K/G, N] fp16,
-//             zeros[K/G, N/8] int32 packed or [K/G, N] uint8, group_size=128) -> fp32 [M, N]
+//             zeros[K/G, N/8] int32 packed or [K/G, N] uint8, group_size=128) -> fp32 [M, N];
+// or scales and zeros as returned by prepack_int4_params.
 torch::Tensor matmul_int4(torch::Tensor A, torch::Tensor packed, torch::Tensor scales,
                           torch::Tensor zeros, int64_t group_size) {
     TORCH_CHECK(A.is_cuda() && packed.is_cuda() && scales.is_cuda() && zeros.is_cuda(),
@@ -257,11 +292,19 @@ torch::Tensor matmul_int4(torch::Tensor A, torch::Tensor packed, torch::Tensor s
     TORCH_CHECK(A.size(1) == K, "Inner dimensions must match");
     TORCH_CHECK(group_size > 0 && K % group_size == 0, "group_size must divide K");
     const int64_t ng = K / group_size;
-    TORCH_CHECK(scales.dtype() == torch::kFloat16 && scales.dim() == 2 && scales.size(0) == ng &&
-                    scales.size(1) == N,
-                "scales must be float16 [K/group_size, N]");
     int zfmt;
-    if (zeros.dtype() == torch::kInt32) {
+    if (scales.dim() == 3) {  // slice-major parameters from prepack_int4_params
+        TORCH_CHECK(scales.dtype() == torch::kFloat16 && scales.size(0) * 16 == N &&
+                        scales.size(1) == ng && scales.size(2) == 16,
+                    "sliced scales must be float16 [N/16, K/group_size, 16]");
+        TORCH_CHECK(zeros.dtype() == torch::kInt32 && zeros.dim() == 3 &&
+                        zeros.size(0) * 16 == N && zeros.size(1) == ng && zeros.size(2) == 2,
+                    "sliced zeros must be int32 [N/16, K/group_size, 2]");
+        zfmt = WMMA_ZEROS_SLICED;
+    } else if (!(scales.dtype() == torch::kFloat16 && scales.dim() == 2 &&
+                 scales.size(0) == ng && scales.size(1) == N)) {
+        TORCH_CHECK(false, "scales must be float16 [K/group_size, N]");
+    } else if (zeros.dtype() == torch::kInt32) {
         TORCH_CHECK(zeros.dim() == 2 && zeros.size(0) == ng && zeros.size(1) * 8 == N,
                     "packed zeros must be int32 [K/group_size, N/8]");
         zfmt = WMMA_ZEROS_PACKED;
@@ -329,6 +372,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("prepack_int4", &prepack_int4, "GPTQ int4 qweight [K/8,N] -> MFMA layout", py::arg("qweight"));
     m.def("unprepack_int4", &unprepack_int4, "Inverse of prepack_int4", py::arg("packed"));
     m.def("unpack_int4", &unpack_int4, "GPTQ int4 qweight [K/8,N] -> uint8 [K,N]", py::arg("qweight"));
+    m.def("prepack_int4_params", &prepack_int4_params,
+          "scales/zeros -> slice-major layout accepted by matmul_int4", py::arg("scales"),
+          py::arg("zeros"));
     m.def("matmul_int4", &matmul_int4, "W4A16 dequant GEMM: fp16 A @ int4 W -> fp32",
           py::arg("A"), py::arg("packed"), py::arg("scales"), py::arg("zeros"),
           py::arg("group_size") = 128);

@@ -100,6 +100,35 @@ int4_unpack_kernel(const int32_t* __restrict__ qw, int K, int N, uint8_t* __rest
     }
 }
 
+// Group parameters to the slice-major layout (WMMA_ZEROS_SLICED): one thread per
+// (16-column slice, group) writes the slice's 16 scales and its two zero words.
+template <int ZF>
+__global__ void __launch_bounds__(256)
+int4_params_slice_kernel(const uint16_t* __restrict__ s, const void* __restrict__ z, int KG, int N,
+                         uint16_t* __restrict__ s_out, int32_t* __restrict__ z_out) {
+    const int64_t total = (int64_t)(N / 16) * KG;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const int slice = (int)(t / KG), g = (int)(t % KG);
+        const int64_t row = (int64_t)g * N + 16 * slice;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s_out[t * 16 + e] = s[row + e];
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            uint32_t word;
+            if constexpr (ZF == WMMA_ZEROS_PACKED) {
+                word = (uint32_t)static_cast<const int32_t*>(z)[(int64_t)g * (N / 8) + 2 * slice + w];
+            } else {
+                word = 0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    word |= ((uint32_t)static_cast<const uint8_t*>(z)[row + 8 * w + j] & 0xFu) << (4 * j);
+            }
+            z_out[t * 2 + w] = (int32_t)word;
+        }
+    }
+}
+
 // --------------------------------------------------------------------- dequantisation --
 struct W4Args {
     const f16* A;
@@ -115,7 +144,33 @@ struct W4Args {
     int split;
     int kc_per_split;     // 64-deep chunks per split
     int pp_shift;         // decode-MFMA kernel: log2(G / 128)
+    int kg;               // K / G (groups)
 };
+
+// Element index of scale s[g][n], and of the zeros element (int32 word of eight nibbles,
+// nibble n % 8; or byte) holding z[g][n], per zeros format ZF:
+//   WMMA_ZEROS_PACKED  scales [K/G][N], zero words [K/G][N/8]
+//   WMMA_ZEROS_U8      scales [K/G][N], zero bytes [K/G][N]
+//   WMMA_ZEROS_SLICED  scales [N/16][K/G][16], zero words [N/16][K/G][2]: every 16-column
+//                      slice's parameters for all groups are one contiguous run, so a
+//                      workgroup that streams a slice over all of K reads them in 1 KB /
+//                      256-byte runs instead of 32-byte pieces of K/G rows.
+template <int ZF>
+__device__ __forceinline__ int64_t s_index(const W4Args& p, int g, int n) {
+    if constexpr (ZF == WMMA_ZEROS_SLICED)
+        return ((int64_t)(n >> 4) * p.kg + g) * 16 + (n & 15);
+    else
+        return (int64_t)g * p.N + n;
+}
+template <int ZF>
+__device__ __forceinline__ int64_t z_index(const W4Args& p, int g, int n) {
+    if constexpr (ZF == WMMA_ZEROS_SLICED)
+        return ((int64_t)(n >> 4) * p.kg + g) * 2 + ((n >> 3) & 1);
+    else if constexpr (ZF == WMMA_ZEROS_PACKED)
+        return (int64_t)g * (p.N / 8) + n / 8;
+    else
+        return (int64_t)g * p.N + n;
+}
 
 // Per-lane group parameters: zs = (1024 + z, 1024 + z), ss = (s, s) as packed fp16 pairs.
 // ZF (the zeros format) is a template parameter so the loads stay branch-free and can
@@ -123,13 +178,13 @@ struct W4Args {
 template <int ZF>
 __device__ __forceinline__ void group_params(const W4Args& p, int g, int n, uint32_t* zs,
                                              uint32_t* ss) {
-    const uint16_t s = __builtin_bit_cast(uint16_t, p.S[(int64_t)g * p.N + n]);
+    const uint16_t s = __builtin_bit_cast(uint16_t, p.S[s_index<ZF>(p, g, n)]);
     uint32_t z;
-    if constexpr (ZF == WMMA_ZEROS_PACKED) {
-        const uint32_t zw = (uint32_t)static_cast<const int32_t*>(p.Z)[(int64_t)g * (p.N / 8) + n / 8];
+    if constexpr (ZF != WMMA_ZEROS_U8) {
+        const uint32_t zw = (uint32_t)static_cast<const int32_t*>(p.Z)[z_index<ZF>(p, g, n)];
         z = (zw >> (4 * (n & 7))) & 0xFu;
     } else {
-        z = static_cast<const uint8_t*>(p.Z)[(int64_t)g * p.N + n] & 0xFu;
+        z = static_cast<const uint8_t*>(p.Z)[z_index<ZF>(p, g, n)] & 0xFu;
     }
     const uint32_t zh = 0x6400u | z;
     *zs = zh | (zh << 16);
@@ -141,17 +196,17 @@ __device__ __forceinline__ void group_params(const W4Args& p, int g, int n, uint
 template <int ZF>
 __device__ __forceinline__ void group_load(const W4Args& p, int g, int n, uint32_t* sraw,
                                            uint32_t* zraw) {
-    *sraw = __builtin_bit_cast(uint16_t, p.S[(int64_t)g * p.N + n]);
-    if constexpr (ZF == WMMA_ZEROS_PACKED)
-        *zraw = (uint32_t)static_cast<const int32_t*>(p.Z)[(int64_t)g * (p.N / 8) + n / 8];
+    *sraw = __builtin_bit_cast(uint16_t, p.S[s_index<ZF>(p, g, n)]);
+    if constexpr (ZF != WMMA_ZEROS_U8)
+        *zraw = (uint32_t)static_cast<const int32_t*>(p.Z)[z_index<ZF>(p, g, n)];
     else
-        *zraw = static_cast<const uint8_t*>(p.Z)[(int64_t)g * p.N + n];
+        *zraw = static_cast<const uint8_t*>(p.Z)[z_index<ZF>(p, g, n)];
 }
 template <int ZF>
 __device__ __forceinline__ void group_decode(uint32_t sraw, uint32_t zraw, int n, uint32_t* zs,
                                              uint32_t* ss) {
     uint32_t z;
-    if constexpr (ZF == WMMA_ZEROS_PACKED)
+    if constexpr (ZF != WMMA_ZEROS_U8)
         z = (zraw >> (4 * (n & 7))) & 0xFu;
     else
         z = zraw & 0xFu;
@@ -387,7 +442,7 @@ w4a16_decode_kernel(W4Args p) {
             }
         }
         uint32_t z;
-        if constexpr (ZF == WMMA_ZEROS_PACKED)
+        if constexpr (ZF != WMMA_ZEROS_U8)
             z = (R.z[u] >> (4 * (n & 7))) & 0xFu;
         else
             z = R.z[u] & 0xFu;
@@ -545,11 +600,11 @@ w4a16_decode_mfma_kernel(W4Args p) {
         for (int m = 0; m < MM; ++m)
             R.a[m] = *reinterpret_cast<const u32x4*>(p.A + (int64_t)m * p.lda + ka);
         const int g = ppl >> p.pp_shift;  // G = 128 << pp_shift
-        R.s = __builtin_bit_cast(uint16_t, p.S[(int64_t)g * p.N + n]);
-        if constexpr (ZF == WMMA_ZEROS_PACKED)
-            R.z = (uint32_t)static_cast<const int32_t*>(p.Z)[(int64_t)g * (p.N / 8) + n / 8];
+        R.s = __builtin_bit_cast(uint16_t, p.S[s_index<ZF>(p, g, n)]);
+        if constexpr (ZF != WMMA_ZEROS_U8)
+            R.z = (uint32_t)static_cast<const int32_t*>(p.Z)[z_index<ZF>(p, g, n)];
         else
-            R.z = static_cast<const uint8_t*>(p.Z)[(int64_t)g * p.N + n];
+            R.z = static_cast<const uint8_t*>(p.Z)[z_index<ZF>(p, g, n)];
 #pragma unroll
         for (int u = 0; u < DM_U; ++u) {
             const int pp = min(wave + DM_NW * (DM_U * r + u), KP - 1);
@@ -597,7 +652,7 @@ w4a16_decode_mfma_kernel(W4Args p) {
         uint32_t rs = R.s, rz = R.z;
         asm volatile("" : "+v"(rs), "+v"(rz));  // no work on them hoisted up to their load
         uint32_t z;
-        if constexpr (ZF == WMMA_ZEROS_PACKED)
+        if constexpr (ZF != WMMA_ZEROS_U8)
             z = (rz >> (4 * (n & 7))) & 0xFu;
         else
             z = rz & 0xFu;
@@ -739,11 +794,11 @@ w4a16_skinny_kernel(W4Args p) {
 #pragma unroll
         for (int sc = 0; sc < 2; ++sc) {
             const int n = 32 * nt + 16 * sc + col;
-            sraw[sc] = __builtin_bit_cast(uint16_t, p.S[(int64_t)g * p.N + n]);
-            if constexpr (ZF == WMMA_ZEROS_PACKED)
-                zraw[sc] = (uint32_t)static_cast<const int32_t*>(p.Z)[(int64_t)g * (p.N / 8) + n / 8];
+            sraw[sc] = __builtin_bit_cast(uint16_t, p.S[s_index<ZF>(p, g, n)]);
+            if constexpr (ZF != WMMA_ZEROS_U8)
+                zraw[sc] = (uint32_t)static_cast<const int32_t*>(p.Z)[z_index<ZF>(p, g, n)];
             else
-                zraw[sc] = static_cast<const uint8_t*>(p.Z)[(int64_t)g * p.N + n];
+                zraw[sc] = static_cast<const uint8_t*>(p.Z)[z_index<ZF>(p, g, n)];
         }
     }
     // Activations and weights, pair-step by pair-step (clamped: every load is issued).
@@ -769,7 +824,7 @@ w4a16_skinny_kernel(W4Args p) {
 #pragma unroll
     for (int sc = 0; sc < 2; ++sc) {
         uint32_t z;
-        if constexpr (ZF == WMMA_ZEROS_PACKED)
+        if constexpr (ZF != WMMA_ZEROS_U8)
             z = (zraw[sc] >> (4 * ((32 * nt + 16 * sc + col) & 7))) & 0xFu;
         else
             z = zraw[sc] & 0xFu;
@@ -929,11 +984,15 @@ __device__ __forceinline__ void w4g_issue(const W4Args& p, const W4GLane& L,
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) {
         R.w[j] = buf_load16(rw, (L.w_off[j] + k * 1024u) | dead);
-        R.s[j] = buf_load2(rs, (L.s_off[j] + g * (uint32_t)p.N * 2u) | dead);
-        if constexpr (ZF == WMMA_ZEROS_PACKED)
-            R.z[j] = buf_load4(rz, (L.z_off[j] + g * (uint32_t)(p.N / 8) * 4u) | dead);
+        // byte strides from group g to g + 1
+        const uint32_t s_gs = ZF == WMMA_ZEROS_SLICED ? 32u : (uint32_t)p.N * 2u;
+        const uint32_t z_gs = ZF == WMMA_ZEROS_SLICED ? 8u
+                              : ZF == WMMA_ZEROS_PACKED ? (uint32_t)(p.N / 8) * 4u : (uint32_t)p.N;
+        R.s[j] = buf_load2(rs, (L.s_off[j] + g * s_gs) | dead);
+        if constexpr (ZF != WMMA_ZEROS_U8)
+            R.z[j] = buf_load4(rz, (L.z_off[j] + g * z_gs) | dead);
         else
-            R.z[j] = buf_load1(rz, (L.z_off[j] + g * (uint32_t)p.N) | dead);
+            R.z[j] = buf_load1(rz, (L.z_off[j] + g * z_gs) | dead);
     }
 }
 
@@ -957,7 +1016,7 @@ __device__ __forceinline__ void w4g_stage(const W4Args& p, const W4GLane& L,
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) {
         uint32_t z;
-        if constexpr (ZF == WMMA_ZEROS_PACKED)
+        if constexpr (ZF != WMMA_ZEROS_U8)
             z = (R.z[j] >> (4 * (lane & 7))) & 0xFu;  // column % 8 == lane % 8
         else
             z = R.z[j] & 0xFu;
@@ -1031,9 +1090,10 @@ w4a16_gemm_kernel(W4Args p) {
         const bool ok = n < p.N;
         const int ntile = n >> 5;
         L.w_off[j] = ok ? (uint32_t)(((int64_t)ntile * KC * 64 + lane) * 16) : kOobOffset;
-        L.s_off[j] = ok ? (uint32_t)n * 2u : kOobOffset;
-        if constexpr (ZF == WMMA_ZEROS_PACKED)
-            L.z_off[j] = ok ? (uint32_t)(n >> 3) * 4u : kOobOffset;
+        // scale / zero byte offsets at group 0
+        L.s_off[j] = ok ? (uint32_t)(s_index<ZF>(p, 0, n) * 2) : kOobOffset;
+        if constexpr (ZF != WMMA_ZEROS_U8)
+            L.z_off[j] = ok ? (uint32_t)(z_index<ZF>(p, 0, n) * 4) : kOobOffset;
         else
             L.z_off[j] = ok ? (uint32_t)n : kOobOffset;
     }
@@ -1291,6 +1351,21 @@ hipError_t launch_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q,
     return hipGetLastError();
 }
 
+hipError_t launch_int4_params_slice(const void* scales, const void* zeros, int zeros_format,
+                                    int KG, int N, void* scales_out, int32_t* zeros_out,
+                                    hipStream_t stream) {
+    const int64_t total = (int64_t)(N / 16) * KG;
+    const auto* s = static_cast<const uint16_t*>(scales);
+    auto* so = static_cast<uint16_t*>(scales_out);
+    if (zeros_format == WMMA_ZEROS_PACKED)
+        hipLaunchKernelGGL(int4_params_slice_kernel<WMMA_ZEROS_PACKED>, dim3(grid_for(total, 256)),
+                           dim3(256), 0, stream, s, zeros, KG, N, so, zeros_out);
+    else
+        hipLaunchKernelGGL(int4_params_slice_kernel<WMMA_ZEROS_U8>, dim3(grid_for(total, 256)),
+                           dim3(256), 0, stream, s, zeros, KG, N, so, zeros_out);
+    return hipGetLastError();
+}
+
 // Host-only: choose the kernel and K split.
 //   decode-mfma  M <= 4, G = 128 * 2^j, K % 128 == 0, the staged activations fit LDS and
 //                the 16-column slices give at least half a workgroup per CU.
@@ -1465,9 +1540,11 @@ hipError_t launch_w4a16(const W4A16Launch& w, hipStream_t stream) {
     a.ws = static_cast<float*>(w.workspace);
     a.split = w.plan.split;
     a.kc_per_split = w.plan.k_per_split / 64;
+    a.kg = w.K / w.G;
     a.pp_shift = 0;
     while (w.G >= 128 && (128 << (a.pp_shift + 1)) <= w.G) ++a.pp_shift;
     if (w.zeros_format == WMMA_ZEROS_PACKED) return launch_w4a16_zf<WMMA_ZEROS_PACKED>(a, w, stream);
+    if (w.zeros_format == WMMA_ZEROS_SLICED) return launch_w4a16_zf<WMMA_ZEROS_SLICED>(a, w, stream);
     return launch_w4a16_zf<WMMA_ZEROS_U8>(a, w, stream);
 }
 
