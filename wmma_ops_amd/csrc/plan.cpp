@@ -74,6 +74,46 @@ int make_plan(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* ou
         return WMMA_OK;
     }
 
+    if (M <= 128 && K >= 512) {
+        // Few rows: the GEMM streams B, and the chip is filled by choosing the tile and the
+        // K split together.  Estimated time = (workgroups on the busiest CU) x tile area /
+        // (split x tile efficiency x the fraction of the tile's rows that exist), with 15%
+        // per extra split for the partial sums.  Measured on MI355X at M = 64, 128 and
+        // N = 4096..14336, K = 4096, 14336: this picks the fastest of the 64x64, 128x64 and
+        // 128x128 tiles with splits 1, 2, 4 in every case (up to 22% over choosing the tile
+        // first and splitting only an under-filled chip; with a 10% split term it chose
+        // split 4 for M = 64, N = 11008, measured 17% slower than no split).
+        const int cands[] = {WMMA_TILE_64x64, WMMA_TILE_128x64, WMMA_TILE_128x128};
+        int best_cfg = WMMA_TILE_64x64, best_split = 1;
+        double best_cost = 1e300;
+        for (int cfg : cands) {
+            const TileShape& t = kTiles[cfg];
+            const int64_t tiles = (int64_t)ceil_div(M, t.bm) * ceil_div(N, t.bn);
+            const double eff = kTileEff[cfg] * std::min(1.0, (double)M / t.bm);
+            for (int sp : {1, 2, 4}) {
+                // a split needs K >= 256 per part and a GEMM big enough (>= 2^30
+                // multiply-adds) for the partial-sum pass to pay for itself
+                if (sp > 1 && (K / sp < 256 || (int64_t)M * N * K < (int64_t(1) << 30))) break;
+                const int64_t w = tiles * sp;
+                const double cost = (double)ceil_div64(w, num_cus) * t.bm * t.bn / (sp * eff) *
+                                    (1.0 + 0.15 * (sp - 1));
+                if (cost < best_cost * 0.999) {
+                    best_cost = cost;
+                    best_cfg = cfg;
+                    best_split = sp;
+                }
+            }
+        }
+        const TileShape& t = kTiles[best_cfg];
+        p.kernel = WMMA_KERNEL_TILED;
+        p.tile_cfg = best_cfg;
+        p.tile_m = t.bm;
+        p.tile_n = t.bn;
+        finish_split(M, N, K, ceil_div(M, t.bm) * ceil_div(N, t.bn), best_split, &p);
+        *out = p;
+        return WMMA_OK;
+    }
+
     // Tiled MFMA kernel: rank tiles by estimated time = waves of workgroups x tile area
     // / tile efficiency.  A wave of workgroups is num_cus of them (one per CU).
     const int order[] = {WMMA_TILE_256x256, WMMA_TILE_256x128, WMMA_TILE_128x128,
