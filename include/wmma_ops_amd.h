@@ -95,6 +95,22 @@ int wmma_gemm_f16f32(const void* A, int64_t lda, const void* B, int64_t ldb,
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Explicit plans.  wmma_gemm_plan_custom builds the plan of one kernel (WMMA_KERNEL_*),
+ * tile (WMMA_TILE_*, ignored by the skinny kernel) and K split for a shape, completed as
+ * the planner completes its own; wmma_gemm_f16f32_plan runs wmma_gemm_f16f32 with such a
+ * plan (it must describe this M, N, K; workspace: plan->workspace_bytes).  They replace the
+ * reference's tuned dispatch (autotune.py:131-283 emits select_tuned_tile): the autotuner
+ * (wmma_ops_amd/autotune.py) times plans through them, and its table of measured winners
+ * is compiled into the planner.
+ */
+int wmma_gemm_plan_custom(int M, int N, int K, int kernel, int tile_cfg, int split_k,
+                          wmma_gemm_plan* out);
+int wmma_gemm_f16f32_plan(const void* A, int64_t lda, const void* B, int64_t ldb,
+                          const float* C_in, int64_t ldc_in, float* C_out, int64_t ldc, int M,
+                          int N, int K, float alpha, float beta, const wmma_gemm_plan* plan,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * INT4 weights.  The reference has no INT4 code; the layout is this library's own.
  * "GPTQ layout": qweight is int32 [K/8, N]; weight q[k][n] (0..15) sits in bits
  * 4*(k%8) .. 4*(k%8)+3 of qweight[k/8][n].  K % 64 == 0 and N % 32 == 0 are required.

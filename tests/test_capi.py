@@ -40,6 +40,9 @@ def lib():
     L.wmma_int4_prepack.argtypes = [vp, i32, i32, vp, vp]
     L.wmma_int4_unpack.argtypes = [vp, i32, i32, vp, vp]
     L.wmma_int4_prepack_params.argtypes = [vp, vp, i32, i32, i32, i32, vp, vp, vp]
+    L.wmma_gemm_plan_custom.argtypes = [i32, i32, i32, i32, i32, i32, ctypes.POINTER(Plan)]
+    L.wmma_gemm_f16f32_plan.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, f32, f32,
+                                        ctypes.POINTER(Plan), vp, sz, vp]
     L.wmma_w4a16_gemm.argtypes = [vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, vp, i64, vp, sz, vp]
     L.wmma_flash_attn_fwd.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, i32, vp]
     L.wmma_flash_attn_fwd_gqa.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, vp]
@@ -179,6 +182,52 @@ def test_int4_validation_codes(lib):
     assert w(A=FAKE + 2) == MISALIGNED
     assert w(lda=100) == INVALID
     assert w(M=0) == OK
+
+
+TUNED = os.path.join(ROOT, "wmma_ops_amd", "csrc", "tuned_table.inc")
+
+
+def tuned_entries():
+    pat = re.compile(r"\{(-?\d+), (-?\d+), (-?\d+), WMMA_KERNEL_(TILED|SKINNY), (-?\d+), (\d+)\}")
+    out = []
+    for m in pat.finditer(open(TUNED).read()):
+        M, N, K = int(m.group(1)), int(m.group(2)), int(m.group(3))
+        if M >= 0:
+            out.append((M, N, K, 1 if m.group(4) == "SKINNY" else 0, int(m.group(5)), int(m.group(6))))
+    return out
+
+
+def test_tuned_table_drives_the_planner(lib):
+    # every autotuned shape gets exactly its measured plan on a 256-CU device, and the
+    # heuristics elsewhere (another CU count, or an explicit tile)
+    entries = tuned_entries()
+    assert entries, "the autotuned table is empty"
+    for M, N, K, kernel, tile, split in entries:
+        p = Plan()
+        assert lib.wmma_gemm_plan_make(M, N, K, -1, 256, ctypes.byref(p)) == OK
+        assert (p.kernel, p.split_k) == (kernel, split)
+        if kernel == 0:
+            assert p.tile_cfg == tile
+        q = Plan()
+        assert lib.wmma_gemm_plan_custom(M, N, K, kernel, tile, split, ctypes.byref(q)) == OK
+        assert (q.k_per_split, q.grid, q.workspace_bytes) == (p.k_per_split, p.grid, p.workspace_bytes)
+
+
+def test_plan_custom_validation(lib):
+    p = Plan()
+    assert lib.wmma_gemm_plan_custom(64, 64, 4096, 0, 3, 4, ctypes.byref(p)) == OK
+    assert (p.kernel, p.tile_cfg, p.split_k, p.k_per_split) == (0, 3, 4, 1024)
+    assert p.workspace_bytes == 4 * 64 * 64 * 4
+    assert lib.wmma_gemm_plan_custom(64, 64, 4096, 0, 6, 1, ctypes.byref(p)) == INVALID   # no such tile
+    assert lib.wmma_gemm_plan_custom(17, 64, 4096, 1, -1, 2, ctypes.byref(p)) == INVALID  # skinny: M <= 16
+    assert lib.wmma_gemm_plan_custom(16, 64, 128, 1, -1, 4, ctypes.byref(p)) == INVALID   # K < 64 per split
+    assert lib.wmma_gemm_plan_custom(16, 64, 4096, 2, 0, 1, ctypes.byref(p)) == INVALID   # no such kernel
+    assert lib.wmma_gemm_plan_custom(16, 64, 4096, 0, 0, 33, ctypes.byref(p)) == INVALID  # split > 32
+    # a plan made for another shape is rejected before anything is launched
+    assert lib.wmma_gemm_plan_custom(64, 64, 4096, 0, 0, 2, ctypes.byref(p)) == OK
+    assert lib.wmma_gemm_f16f32_plan(FAKE, 2048, FAKE, 64, None, 64, FAKE, 64, 64, 64, 2048, 1.0, 0.0,
+                                     ctypes.byref(p), FAKE, 1 << 20, None) == INVALID
+    assert b"plan does not describe this shape" in lib.wmma_last_error()
 
 
 def test_prepack_params_validation_codes(lib):

@@ -150,6 +150,33 @@ def test_skinny_split_k_any_workspace(wo, M, N, K):
     _check(Ci, og.gemm_ref(A, B, 2.0, 0.5, Cin))
 
 
+# Explicit plans (the autotuner's entry point): every kernel, tile and split gives the
+# oracle's result within tolerance, including the epilogue.
+@pytest.mark.parametrize("kernel,tile,split", [(0, t, s) for t in range(6) for s in (1, 3, 8)] +
+                         [(1, -1, s) for s in (1, 5, 32)])
+def test_gemm_explicit_plans(wo, kernel, tile, split):
+    import ctypes
+    from tests.test_capi import Plan
+    report("gemm_plan", kernel=kernel, tile=tile, split=split)
+    lib = _capi()
+    lib.wmma_gemm_plan_custom.argtypes = [ctypes.c_int] * 6 + [ctypes.POINTER(Plan)]
+    vp, i64, i32, f32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    lib.wmma_gemm_f16f32_plan.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, f32, f32,
+                                          ctypes.POINTER(Plan), vp, sz, vp]
+    M, N, K = (13, 200, 4096) if kernel == 1 else (300, 264, 2560)
+    A, B = _inputs(M, N, K, 5 + tile + split)
+    Cin = torch.randn(M, N, generator=torch.Generator().manual_seed(6))
+    p = Plan()
+    assert lib.wmma_gemm_plan_custom(M, N, K, kernel, tile, split, ctypes.byref(p)) == 0
+    ws = torch.empty(max(p.workspace_bytes, 1), dtype=torch.uint8, device="cuda")
+    Ad, Bd, C = A.cuda(), B.cuda(), Cin.cuda()
+    rc = lib.wmma_gemm_f16f32_plan(Ad.data_ptr(), K, Bd.data_ptr(), N, C.data_ptr(), N, C.data_ptr(), N,
+                                   M, N, K, 2.0, 0.5, ctypes.byref(p), ws.data_ptr(), p.workspace_bytes,
+                                   torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    _check(C, og.gemm_ref(A, B, 2.0, 0.5, Cin))
+
+
 def test_skinny_epilogue_in_place(wo):
     A, B = _inputs(16, 4096, 4096, 11, bstd=0.02)
     C = torch.randn(16, 4096, generator=torch.Generator().manual_seed(12))

@@ -95,10 +95,12 @@ size_t wmma_gemm_workspace_size(int M, int N, int K, int tile_cfg) {
     return p.workspace_bytes;
 }
 
-int wmma_gemm_f16f32(const void* A, int64_t lda, const void* B, int64_t ldb, const float* C_in,
-                     int64_t ldc_in, float* C_out, int64_t ldc, int M, int N, int K, float alpha,
-                     float beta, int tile_cfg, void* workspace, size_t workspace_bytes,
-                     void* stream) {
+// Shared checks and launch of wmma_gemm_f16f32 / wmma_gemm_f16f32_plan.  `plan` is NULL
+// for the planner's own plan (tile_cfg), else an explicit plan for exactly this shape.
+static int gemm_run(const void* A, int64_t lda, const void* B, int64_t ldb, const float* C_in,
+                    int64_t ldc_in, float* C_out, int64_t ldc, int M, int N, int K, float alpha,
+                    float beta, int tile_cfg, const wmma_gemm_plan* explicit_plan,
+                    void* workspace, size_t workspace_bytes, void* stream) {
     if (M < 0 || N < 0 || K < 0) return fail(WMMA_ERR_INVALID_ARG, "negative GEMM dimension");
     if (tile_cfg < WMMA_TILE_AUTO || tile_cfg >= WMMA_TILE_COUNT)
         return fail(WMMA_ERR_INVALID_ARG,
@@ -120,8 +122,19 @@ int wmma_gemm_f16f32(const void* A, int64_t lda, const void* B, int64_t ldb, con
             return fail(WMMA_ERR_UNSUPPORTED, "leading dimension too large for 32-bit offsets");
     }
     wmma_gemm_plan plan{};
-    int rc = make_plan(M, N, K, tile_cfg, current_cus(), &plan);
-    if (rc != WMMA_OK) return fail(rc, "planner rejected the shape");
+    if (explicit_plan) {
+        // Rebuild the plan from its choices for this shape: a plan made for another shape,
+        // or edited by hand, is rejected rather than launched.
+        int rc = make_custom_plan(M, N, K, explicit_plan->kernel, explicit_plan->tile_cfg,
+                                  explicit_plan->split_k, &plan);
+        if (rc != WMMA_OK || plan.k_per_split != explicit_plan->k_per_split ||
+            plan.split_k != explicit_plan->split_k || plan.workspace_bytes != explicit_plan->workspace_bytes)
+            return fail(WMMA_ERR_INVALID_ARG, "plan does not describe this shape (make it with "
+                                              "wmma_gemm_plan_custom or wmma_gemm_plan_make)");
+    } else {
+        int rc = make_plan(M, N, K, tile_cfg, current_cus(), &plan);
+        if (rc != WMMA_OK) return fail(rc, "planner rejected the shape");
+    }
     if (plan.workspace_bytes > 0) {
         if (!workspace)
             return fail(WMMA_ERR_WORKSPACE, "split-K needs a workspace of %zu bytes",
@@ -151,6 +164,33 @@ int wmma_gemm_f16f32(const void* A, int64_t lda, const void* B, int64_t ldb, con
             aligned16(A) && aligned16(B);
     g.plan = plan;
     return hip_status(launch_gemm(g, static_cast<hipStream_t>(stream)), "gemm launch");
+}
+
+int wmma_gemm_f16f32(const void* A, int64_t lda, const void* B, int64_t ldb, const float* C_in,
+                     int64_t ldc_in, float* C_out, int64_t ldc, int M, int N, int K, float alpha,
+                     float beta, int tile_cfg, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+    return gemm_run(A, lda, B, ldb, C_in, ldc_in, C_out, ldc, M, N, K, alpha, beta, tile_cfg,
+                    nullptr, workspace, workspace_bytes, stream);
+}
+
+int wmma_gemm_plan_custom(int M, int N, int K, int kernel, int tile_cfg, int split_k,
+                          wmma_gemm_plan* out) {
+    if (!out) return fail(WMMA_ERR_INVALID_ARG, "NULL plan");
+    if (make_custom_plan(M, N, K, kernel, tile_cfg, split_k, out) != WMMA_OK)
+        return fail(WMMA_ERR_INVALID_ARG,
+                    "no such plan: kernel %d, tile %d, split %d for M=%d N=%d K=%d", kernel,
+                    tile_cfg, split_k, M, N, K);
+    return ok();
+}
+
+int wmma_gemm_f16f32_plan(const void* A, int64_t lda, const void* B, int64_t ldb,
+                          const float* C_in, int64_t ldc_in, float* C_out, int64_t ldc, int M,
+                          int N, int K, float alpha, float beta, const wmma_gemm_plan* plan,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+    if (!plan) return fail(WMMA_ERR_INVALID_ARG, "NULL plan");
+    return gemm_run(A, lda, B, ldb, C_in, ldc_in, C_out, ldc, M, N, K, alpha, beta,
+                    WMMA_TILE_AUTO, plan, workspace, workspace_bytes, stream);
 }
 
 // ------------------------------------------------------------------------------ INT4 --

@@ -25,11 +25,55 @@ static void finish_split(int M, int N, int K, int tiles, int split, wmma_gemm_pl
     p->workspace_bytes = split > 1 ? (size_t)split * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
+// The autotuned table: exact shapes measured on a 256-CU MI355X.
+#include "tuned_table.inc"
+
+const TunedPlan* tuned_plans(int* count) {
+    *count = (int)(sizeof(kTunedPlans) / sizeof(kTunedPlans[0]));
+    return kTunedPlans;
+}
+
+int make_custom_plan(int M, int N, int K, int kernel, int tile_cfg, int split,
+                     wmma_gemm_plan* out) {
+    if (!out || M < 0 || N < 0 || K < 0 || split < 1 || split > kMaxSplitK)
+        return WMMA_ERR_INVALID_ARG;
+    wmma_gemm_plan p{};
+    int tiles;
+    if (kernel == WMMA_KERNEL_SKINNY) {
+        if (M > kSkinnyMaxM) return WMMA_ERR_INVALID_ARG;
+        p.kernel = WMMA_KERNEL_SKINNY;
+        p.tile_cfg = -1;
+        p.tile_m = kSkinnyMaxM;
+        p.tile_n = kSkinnyBlockN;
+        tiles = ceil_div(std::max(N, 1), kSkinnyBlockN);
+    } else if (kernel == WMMA_KERNEL_TILED) {
+        if (tile_cfg < 0 || tile_cfg >= WMMA_TILE_COUNT) return WMMA_ERR_INVALID_ARG;
+        const TileShape& t = kTiles[tile_cfg];
+        p.kernel = WMMA_KERNEL_TILED;
+        p.tile_cfg = tile_cfg;
+        p.tile_m = t.bm;
+        p.tile_n = t.bn;
+        tiles = ceil_div(std::max(M, 1), t.bm) * ceil_div(std::max(N, 1), t.bn);
+    } else {
+        return WMMA_ERR_INVALID_ARG;
+    }
+    if (split > 1 && K < split * kBlockK) return WMMA_ERR_INVALID_ARG;
+    finish_split(M, N, K, tiles, split, &p);
+    *out = p;
+    return WMMA_OK;
+}
+
 int make_plan(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* out) {
     if (!out || M < 0 || N < 0 || K < 0) return WMMA_ERR_INVALID_ARG;
     if (tile_cfg < WMMA_TILE_AUTO || tile_cfg >= WMMA_TILE_COUNT) return WMMA_ERR_INVALID_ARG;
     if (num_cus <= 0) num_cus = 256;
     wmma_gemm_plan p{};
+
+    if (tile_cfg == WMMA_TILE_AUTO && num_cus == 256) {
+        for (const TunedPlan& e : kTunedPlans)
+            if (e.M == M && e.N == N && e.K == K)
+                return make_custom_plan(M, N, K, e.kernel, e.tile_cfg, e.split, out);
+    }
 
     if (tile_cfg != WMMA_TILE_AUTO) {
         // Explicit tile (matmul_tiled): exactly that tile, no split.
