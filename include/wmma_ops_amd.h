@@ -174,6 +174,23 @@ int wmma_w4a16_gemm(const void* A, int64_t lda, const int32_t* packed, const voi
                     const void* zeros, int zeros_format, int M, int N, int K, int group_size,
                     float* Y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same with an fp16 Y (each fp32 result rounded once to fp16; split-K partials stay
+ * fp32).  No reference counterpart: the fp16-output option of the W4A16 path. */
+int wmma_w4a16_gemm_f16out(const void* A, int64_t lda, const int32_t* packed,
+                           const void* scales, const void* zeros, int zeros_format, int M, int N,
+                           int K, int group_size, void* Y, int64_t ldy, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/*
+ * AutoAWQ checkpoint tensors to this library's inputs, bit-exact: qweight_awq int32
+ * [K, N/8] and qzeros_awq int32 [K/G, N/8], eight columns per word in AutoAWQ's nibble
+ * order (column 8c + {0,2,4,6,1,3,5,7}[i] in nibble i) -> qweight int32 [K/8, N] (GPTQ
+ * layout, for wmma_int4_prepack) and zeros int32 [K/G, N/8] (WMMA_ZEROS_PACKED).  AWQ's
+ * scales fp16 [K/G, N] are already this library's layout.  No reference counterpart.
+ */
+int wmma_int4_from_awq(const int32_t* qweight_awq, const int32_t* qzeros_awq, int K, int N,
+                       int group_size, int32_t* qweight, int32_t* zeros, void* stream);
+
 /*
  * Flash-attention forward.  Q [B,H,Sq,D], K and V [B,H,Sk,D], O [B,H,Sq,D]; fp16,
  * contiguous.  O = softmax(scale * Q K^T (+ causal mask: key j <= query i, aligned to

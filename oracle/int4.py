@@ -54,6 +54,41 @@ def pack_zeros(z: np.ndarray) -> np.ndarray:
     return out.view(np.int32)
 
 
+# AutoAWQ (GEMM checkpoint format; AutoAWQ 0.2.x, not installed here) packs eight columns
+# per int32 along N: column 8c + AWQ_ORDER[i] in nibble i, for qweight [K, N/8] and qzeros
+# [K/G, N/8] alike (its packing code's AWQ_ORDER / AWQ_REVERSE_ORDER).  Restated from that
+# published order; no AutoAWQ fixture exists here, so the adapter's parity is unpinned by
+# an AutoAWQ run and pinned only by this restatement and round trips.
+AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)
+
+
+def pack_awq(q: np.ndarray) -> np.ndarray:
+    """uint8 [R, N] (0..15) -> int32 [R, N/8] in AutoAWQ's nibble order."""
+    q = np.asarray(q, dtype=np.uint32)
+    R, N = q.shape
+    assert N % 8 == 0
+    q = q.reshape(R, N // 8, 8)
+    out = np.zeros((R, N // 8), dtype=np.uint32)
+    for i, col in enumerate(AWQ_ORDER):
+        out |= (q[:, :, col] & 0xF) << np.uint32(4 * i)
+    return out.view(np.int32)
+
+
+def unpack_awq(w: np.ndarray) -> np.ndarray:
+    """Inverse of pack_awq: int32 [R, N/8] -> uint8 [R, N]."""
+    w = np.asarray(w).view(np.uint32)
+    R, C = w.shape
+    out = np.zeros((R, C, 8), dtype=np.uint8)
+    for i, col in enumerate(AWQ_ORDER):
+        out[:, :, col] = (w >> np.uint32(4 * i)) & 0xF
+    return out.reshape(R, C * 8)
+
+
+def awq_to_gptq(qweight_awq: np.ndarray, qzeros_awq: np.ndarray):
+    """AutoAWQ qweight/qzeros -> (GPTQ-layout qweight [K/8, N], packed zeros [K/G, N/8])."""
+    return pack_gptq(unpack_awq(qweight_awq)), pack_zeros(unpack_awq(qzeros_awq))
+
+
 def slice_params(s: np.ndarray, z: np.ndarray):
     """Slice-major group parameters (this library's WMMA_ZEROS_SLICED layout):
     scales fp16 [K/G, N] -> [N/16, K/G, 16]; uint8 zeros [K/G, N] -> int32 [N/16, K/G, 2]

@@ -41,6 +41,8 @@ def lib():
     L.wmma_int4_unpack.argtypes = [vp, i32, i32, vp, vp]
     L.wmma_int4_prepack_params.argtypes = [vp, vp, i32, i32, i32, i32, vp, vp, vp]
     L.wmma_gemm_plan_custom.argtypes = [i32, i32, i32, i32, i32, i32, ctypes.POINTER(Plan)]
+    L.wmma_int4_from_awq.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp]
+    L.wmma_w4a16_gemm_f16out.argtypes = [vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, vp, i64, vp, sz, vp]
     L.wmma_gemm_f16f32_plan.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, f32, f32,
                                         ctypes.POINTER(Plan), vp, sz, vp]
     L.wmma_w4a16_gemm.argtypes = [vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, vp, i64, vp, sz, vp]
@@ -228,6 +230,18 @@ def test_plan_custom_validation(lib):
     assert lib.wmma_gemm_f16f32_plan(FAKE, 2048, FAKE, 64, None, 64, FAKE, 64, 64, 64, 2048, 1.0, 0.0,
                                      ctypes.byref(p), FAKE, 1 << 20, None) == INVALID
     assert b"plan does not describe this shape" in lib.wmma_last_error()
+
+
+def test_awq_and_f16out_validation_codes(lib):
+    a = lambda **kw: lib.wmma_int4_from_awq(kw.get("q", FAKE), FAKE, kw.get("K", 256), kw.get("N", 64),
+                                            kw.get("G", 64), FAKE, FAKE, None)
+    assert a(K=100) == INVALID             # K % 8
+    assert a(G=96) == INVALID              # group size must divide K
+    assert a(q=None) == INVALID
+    assert a(q=FAKE + 2) == MISALIGNED
+    w = lambda Y: lib.wmma_w4a16_gemm_f16out(FAKE, 256, FAKE, FAKE, FAKE, 0, 1, 64, 256, 64, Y, 64,
+                                             None, 0, None)
+    assert w(FAKE + 1) == MISALIGNED       # fp16 Y must be 2-byte aligned
 
 
 def test_prepack_params_validation_codes(lib):

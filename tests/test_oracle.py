@@ -273,3 +273,22 @@ def test_slice_params_layout():
     # the packed-zeros words of a slice are the standard packed words, regrouped
     zp = oi.pack_zeros(z)
     assert np.array_equal(z_sl.reshape(N // 16, ng, 2).transpose(1, 0, 2).reshape(ng, N // 8), zp)
+
+
+def test_awq_pack_round_trip_and_order():
+    rng = np.random.default_rng(11)
+    q = rng.integers(0, 16, (32, 64), dtype=np.uint8)
+    w = oi.pack_awq(q)
+    assert w.shape == (32, 8) and w.dtype == np.int32
+    assert np.array_equal(oi.unpack_awq(w), q)
+    # a single nonzero column lands in the nibble AutoAWQ's order assigns it
+    for col in range(8):
+        one = np.zeros((1, 8), dtype=np.uint8)
+        one[0, col] = 0xF
+        nib = oi.AWQ_ORDER.index(col)
+        assert int(oi.pack_awq(one).view(np.uint32)[0, 0]) == 0xF << (4 * nib)
+    # the order is a permutation, and converting to the GPTQ layout keeps every value
+    assert sorted(oi.AWQ_ORDER) == list(range(8))
+    z = rng.integers(0, 16, (4, 64), dtype=np.uint8)
+    qg, zp = oi.awq_to_gptq(oi.pack_awq(np.repeat(q, 1, axis=0)), oi.pack_awq(z))
+    assert np.array_equal(oi.unpack_gptq(qg), q) and np.array_equal(oi.unpack_zeros(zp), z)

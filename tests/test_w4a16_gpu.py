@@ -181,6 +181,34 @@ def test_w4a16_sliced_params_same_bits(wo, M, K, N, G):
     assert og.max_rel_err(Ys, oi.w4a16_ref(A, q, s, z, G)) <= 1e-3
 
 
+# AutoAWQ import: bit-exact conversion to the GPTQ layout and packed zeros, and the same
+# product as the GPTQ-layout path.
+@pytest.mark.parametrize("K,N,G", [(256, 64, 64), (4096, 1024, 128)])
+def test_int4_from_awq_bit_exact(wo, K, N, G):
+    rng = np.random.default_rng(K + N)
+    q = rng.integers(0, 16, (K, N), dtype=np.uint8)
+    z = rng.integers(0, 16, (K // G, N), dtype=np.uint8)
+    qw, qz = wo.int4_from_awq(torch.from_numpy(oi.pack_awq(q)).cuda(), torch.from_numpy(oi.pack_awq(z)).cuda())
+    assert np.array_equal(qw.cpu().numpy(), oi.pack_gptq(q))
+    assert np.array_equal(qz.cpu().numpy(), oi.pack_zeros(z))
+
+
+# fp16 output: every kernel (decode, skinny, GEMM; with and without a K split) rounds its
+# fp32 result once, so the fp16 output equals the fp32 output converted.
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 16, 33, 300])
+@pytest.mark.parametrize("K,N,G", [(4096, 1024, 128), (1024, 352, 64)])
+def test_w4a16_fp16_output(wo, M, K, N, G):
+    report("w4a16_f16out", M=M, K=K, N=N, G=G)
+    A, q, s, z = oi.make_inputs(M, K, N, G, seed=M + K + N)
+    pk = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
+    args = (A.cuda(), pk, torch.from_numpy(s).cuda(), torch.from_numpy(oi.pack_zeros(z)).cuda(), G)
+    Y32 = wo.matmul_int4(*args)
+    Y16 = wo.matmul_int4(*args, out_dtype=torch.float16)
+    assert Y16.dtype == torch.float16 and Y16.shape == Y32.shape
+    assert torch.equal(Y16, Y32.half())
+    assert torch.equal(wo.matmul_int4(*args, out_dtype=torch.float32), Y32)
+
+
 def test_w4a16_zero_when_q_equals_z(wo):
     K, N, G = 256, 64, 128
     q = np.full((K, N), 9, dtype=np.uint8)

@@ -279,9 +279,10 @@ int wmma_w4a16_plan_make(int M, int N, int K, int group_size, int num_cus, wmma_
     return ok();
 }
 
-int wmma_w4a16_gemm(const void* A, int64_t lda, const int32_t* packed, const void* scales,
-                    const void* zeros, int zeros_format, int M, int N, int K, int group_size,
-                    float* Y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
+static int w4a16_run(const void* A, int64_t lda, const int32_t* packed, const void* scales,
+                     const void* zeros, int zeros_format, int M, int N, int K, int group_size,
+                     void* Y, int64_t ldy, bool y_half, void* workspace, size_t workspace_bytes,
+                     void* stream) {
     if (M < 0) return fail(WMMA_ERR_INVALID_ARG, "M must be non-negative");
     if (int rc = check_int4_shape(K, N)) return rc;
     if (group_size <= 0 || group_size % 32 != 0 || K % group_size != 0)
@@ -321,10 +322,45 @@ int wmma_w4a16_gemm(const void* A, int64_t lda, const int32_t* packed, const voi
     w.N = N;
     w.K = K;
     w.G = group_size;
-    w.Y = Y;
+    w.Y = static_cast<float*>(Y);
+    w.y_half = y_half;
     w.ldy = ldy;
     w.workspace = workspace;
     return hip_status(launch_w4a16(w, static_cast<hipStream_t>(stream)), "w4a16 launch");
+}
+
+int wmma_w4a16_gemm(const void* A, int64_t lda, const int32_t* packed, const void* scales,
+                    const void* zeros, int zeros_format, int M, int N, int K, int group_size,
+                    float* Y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
+    return w4a16_run(A, lda, packed, scales, zeros, zeros_format, M, N, K, group_size, Y, ldy,
+                     false, workspace, workspace_bytes, stream);
+}
+
+int wmma_w4a16_gemm_f16out(const void* A, int64_t lda, const int32_t* packed,
+                           const void* scales, const void* zeros, int zeros_format, int M, int N,
+                           int K, int group_size, void* Y, int64_t ldy, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+    if (Y && (reinterpret_cast<uintptr_t>(Y) & 1u) != 0)
+        return fail(WMMA_ERR_MISALIGNED, "fp16 Y must be 2-byte aligned");
+    return w4a16_run(A, lda, packed, scales, zeros, zeros_format, M, N, K, group_size, Y, ldy,
+                     true, workspace, workspace_bytes, stream);
+}
+
+int wmma_int4_from_awq(const int32_t* qweight_awq, const int32_t* qzeros_awq, int K, int N,
+                       int group_size, int32_t* qweight, int32_t* zeros, void* stream) {
+    if (K <= 0 || N <= 0 || K % 8 != 0 || N % 8 != 0)
+        return fail(WMMA_ERR_INVALID_ARG, "K and N must be positive multiples of 8");
+    if (group_size <= 0 || K % group_size != 0)
+        return fail(WMMA_ERR_INVALID_ARG, "group_size (%d) must divide K (%d)", group_size, K);
+    if (!qweight_awq || !qzeros_awq || !qweight || !zeros)
+        return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
+    for (const void* ptr : {(const void*)qweight_awq, (const void*)qzeros_awq, (const void*)qweight,
+                            (const void*)zeros})
+        if ((reinterpret_cast<uintptr_t>(ptr) & 3u) != 0)
+            return fail(WMMA_ERR_MISALIGNED, "int32 tensors must be 4-byte aligned");
+    return hip_status(launch_int4_from_awq(qweight_awq, qzeros_awq, K, N, K / group_size, qweight,
+                                           zeros, static_cast<hipStream_t>(stream)),
+                      "awq conversion launch");
 }
 
 // ----------------------------------------------------------------------------- flash --

@@ -33,6 +33,11 @@ hipError_t launch_int4_unprepack(const int32_t* packed, int K, int N, int32_t* q
 hipError_t launch_int4_params_slice(const void* scales, const void* zeros, int zeros_format,
                                     int KG, int N, void* scales_out, int32_t* zeros_out,
                                     hipStream_t stream);
+// AutoAWQ tensors (qweight [K][N/8], qzeros [KG][N/8], nibbles in AWQ order) to this
+// library's GPTQ-layout qweight [K/8][N] and packed zeros [KG][N/8].
+hipError_t launch_int4_from_awq(const int32_t* qweight_awq, const int32_t* qzeros_awq, int K,
+                                int N, int KG, int32_t* qweight, int32_t* zeros,
+                                hipStream_t stream);
 hipError_t launch_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q,
                               hipStream_t stream);
 
@@ -61,10 +66,11 @@ struct W4A16Launch {
     const void* zeros;
     int zeros_format;
     int M, N, K, G;
-    float* Y;
+    float* Y;          // fp32 [M][ldy], or fp16 when y_half
     int64_t ldy;
     void* workspace;
     W4A16Plan plan;
+    bool y_half = false;
 };
 hipError_t launch_w4a16(const W4A16Launch& w, hipStream_t stream);
 // Planner for the W4A16 kernels (host-only).  `aligned`: scales 8-byte aligned and, for

@@ -241,6 +241,30 @@ torch::Tensor unpack_int4(torch::Tensor qweight) {
     return out;
 }
 
+// int4_from_awq(qweight [K, N/8] int32, qzeros [K/G, N/8] int32) -- AutoAWQ checkpoint
+// tensors -> (qweight [K/8, N] GPTQ layout, zeros [K/G, N/8] packed), bit-exact.
+std::vector<torch::Tensor> int4_from_awq(torch::Tensor qweight, torch::Tensor qzeros) {
+    TORCH_CHECK(qweight.is_cuda() && qzeros.is_cuda(), "Inputs must be CUDA tensors");
+    TORCH_CHECK(qweight.device() == qzeros.device(), "Inputs must be on same device");
+    TORCH_CHECK(qweight.dtype() == torch::kInt32 && qweight.dim() == 2,
+                "AWQ qweight must be int32 [K, N/8]");
+    TORCH_CHECK(qzeros.dtype() == torch::kInt32 && qzeros.dim() == 2 &&
+                    qzeros.size(1) == qweight.size(1),
+                "AWQ qzeros must be int32 [K/group_size, N/8]");
+    const int64_t K = qweight.size(0), N = qweight.size(1) * 8, ng = qzeros.size(0);
+    TORCH_CHECK(ng > 0 && K % ng == 0 && K % 8 == 0, "qzeros rows must divide K (a multiple of 8)");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(qweight.device());
+    qweight = qweight.contiguous();
+    qzeros = qzeros.contiguous();
+    auto qo = torch::empty({K / 8, N}, qweight.options());
+    auto zo = torch::empty({ng, N / 8}, qweight.options());
+    int rc = wmma_int4_from_awq(qweight.data_ptr<int32_t>(), qzeros.data_ptr<int32_t>(), (int)K,
+                                (int)N, (int)(K / ng), qo.data_ptr<int32_t>(),
+                                zo.data_ptr<int32_t>(), current_stream(qweight));
+    check_status(rc, "wmma_int4_from_awq");
+    return {qo, zo};
+}
+
 // prepack_int4_params(scales[K/G, N] fp16, zeros[K/G, N/8] int32 or [K/G, N] uint8)
 //   -> (scales [N/16, K/G, 16] fp16, zeros [N/16, K/G, 2] int32): the slice-major layout
 //   matmul_int4 also accepts (a 16-column slice's parameters contiguous).
@@ -279,7 +303,12 @@ std::vector<torch::Tensor> prepack_int4_params(torch::Tensor scales, torch::Tens
 //             zeros[K/G, N/8] int32 packed or [K/G, N] uint8, group_size=128) -> fp32 [M, N];
 // or scales and zeros as returned by prepack_int4_params.
 torch::Tensor matmul_int4(torch::Tensor A, torch::Tensor packed, torch::Tensor scales,
-                          torch::Tensor zeros, int64_t group_size) {
+                          torch::Tensor zeros, int64_t group_size,
+                          c10::optional<at::ScalarType> out_dtype) {
+    const bool half_out = out_dtype.has_value() && *out_dtype == torch::kFloat16;
+    TORCH_CHECK(!out_dtype.has_value() || *out_dtype == torch::kFloat16 ||
+                    *out_dtype == torch::kFloat32,
+                "out_dtype must be float32 or float16");
     TORCH_CHECK(A.is_cuda() && packed.is_cuda() && scales.is_cuda() && zeros.is_cuda(),
                 "Inputs must be CUDA tensors");
     TORCH_CHECK(A.device() == packed.device() && A.device() == scales.device() &&
@@ -321,10 +350,19 @@ torch::Tensor matmul_int4(torch::Tensor A, torch::Tensor packed, torch::Tensor s
     zeros = zeros.contiguous();
     check_aligned(A, "A must be 16-byte aligned");
     const int M = (int)A.size(0);
-    auto Y = torch::empty({A.size(0), N}, torch::dtype(torch::kFloat32).device(A.device()));
+    auto Y = torch::empty({A.size(0), N},
+                          torch::dtype(half_out ? torch::kFloat16 : torch::kFloat32).device(A.device()));
     const size_t ws_bytes = wmma_w4a16_workspace_size(M, (int)N, (int)K, (int)group_size);
     torch::Tensor ws = workspace_for(ws_bytes, A);
-    int rc = wmma_w4a16_gemm(A.data_ptr(), A.stride(0), packed.data_ptr<int32_t>(),
+    int rc;
+    if (half_out)
+        rc = wmma_w4a16_gemm_f16out(A.data_ptr(), A.stride(0), packed.data_ptr<int32_t>(),
+                                    scales.data_ptr(), zeros.data_ptr(), zfmt, M, (int)N, (int)K,
+                                    (int)group_size, Y.data_ptr(), Y.stride(0),
+                                    ws.defined() ? ws.data_ptr() : nullptr, ws_bytes,
+                                    current_stream(A));
+    else
+        rc = wmma_w4a16_gemm(A.data_ptr(), A.stride(0), packed.data_ptr<int32_t>(),
                              scales.data_ptr(), zeros.data_ptr(), zfmt, M, (int)N, (int)K,
                              (int)group_size, Y.data_ptr<float>(), Y.stride(0),
                              ws.defined() ? ws.data_ptr() : nullptr, ws_bytes, current_stream(A));
@@ -375,9 +413,13 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("prepack_int4_params", &prepack_int4_params,
           "scales/zeros -> slice-major layout accepted by matmul_int4", py::arg("scales"),
           py::arg("zeros"));
-    m.def("matmul_int4", &matmul_int4, "W4A16 dequant GEMM: fp16 A @ int4 W -> fp32",
+    m.def("matmul_int4", &matmul_int4,
+          "W4A16 dequant GEMM: fp16 A @ int4 W -> fp32 (or fp16 with out_dtype=torch.float16)",
           py::arg("A"), py::arg("packed"), py::arg("scales"), py::arg("zeros"),
-          py::arg("group_size") = 128);
+          py::arg("group_size") = 128, py::arg("out_dtype") = py::none());
+    m.def("int4_from_awq", &int4_from_awq,
+          "AutoAWQ qweight [K,N/8] / qzeros [K/G,N/8] -> GPTQ-layout qweight and packed zeros",
+          py::arg("qweight"), py::arg("qzeros"));
     m.def("w4a16_plan", &w4a16_plan, "Planner decision for a W4A16 shape", py::arg("M"),
           py::arg("N"), py::arg("K"), py::arg("group_size") = 128, py::arg("num_cus") = 256);
     m.def("gemm_plan", &gemm_plan, "Planner decision for a GEMM shape", py::arg("M"), py::arg("N"),

@@ -100,6 +100,39 @@ int4_unpack_kernel(const int32_t* __restrict__ qw, int K, int N, uint8_t* __rest
     }
 }
 
+// AutoAWQ (GEMM format) to this library's GPTQ layout.  AutoAWQ packs eight columns per
+// int32 along N, column 8c + kAwqOrder[i] in nibble i (kAwqOrder = {0, 2, 4, 6, 1, 3, 5, 7},
+// its AWQ_ORDER), for qweight [K][N/8] and qzeros [K/G][N/8] alike; so column 8c + j sits
+// in nibble kAwqPos[j] = {0, 4, 1, 5, 2, 6, 3, 7}[j] (its AWQ_REVERSE_ORDER).  One thread
+// per output word: qweight words gather 8 rows of one column, zero words permute nibbles.
+__constant__ int kAwqPos[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+
+__global__ void __launch_bounds__(256)
+int4_from_awq_kernel(const int32_t* __restrict__ qw, const int32_t* __restrict__ qz, int K, int N,
+                     int KG, int32_t* __restrict__ qw_out, int32_t* __restrict__ qz_out) {
+    const int64_t nw = (int64_t)(K / 8) * N, nz = (int64_t)KG * (N / 8);
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < nw + nz;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        if (t < nw) {  // GPTQ word (k8, n): nibble j = q[8 k8 + j][n]
+            const int64_t k8 = t / N;
+            const int n = (int)(t % N);
+            const int sh = 4 * kAwqPos[n & 7];
+            uint32_t word = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                word |= (((uint32_t)qw[(8 * k8 + j) * (N / 8) + n / 8] >> sh) & 0xFu) << (4 * j);
+            qw_out[t] = (int32_t)word;
+        } else {       // packed zero word: nibble j = z[g][8c + j]
+            const int64_t u = t - nw;
+            const uint32_t src = (uint32_t)qz[u];
+            uint32_t word = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) word |= ((src >> (4 * kAwqPos[j])) & 0xFu) << (4 * j);
+            qz_out[u] = (int32_t)word;
+        }
+    }
+}
+
 // Group parameters to the slice-major layout (WMMA_ZEROS_SLICED): one thread per
 // (16-column slice, group) writes the slice's 16 scales and its two zero words.
 template <int ZF>
@@ -145,7 +178,17 @@ struct W4Args {
     int kc_per_split;     // 64-deep chunks per split
     int pp_shift;         // decode-MFMA kernel: log2(G / 128)
     int kg;               // K / G (groups)
+    int y_half;           // Y is fp16 (each fp32 result rounded once), else fp32
 };
+
+// Final store of one result: fp32, or fp16 rounded once from the fp32 sum.  Split-K
+// partials stay fp32 in the workspace; only the final value is converted.
+__device__ __forceinline__ void store_y(const W4Args& p, int64_t idx, float v) {
+    if (p.y_half)
+        reinterpret_cast<f16*>(p.Y)[idx] = (f16)v;
+    else
+        p.Y[idx] = v;
+}
 
 // Element index of scale s[g][n], and of the zeros element (int32 word of eight nibbles,
 // nibble n % 8; or byte) holding z[g][n], per zeros format ZF:
@@ -300,7 +343,7 @@ w4a16_gemv_kernel(W4Args p) {
             if (p.split > 1)
                 p.ws[((int64_t)blockIdx.y * M + m) * p.N + col] = v;
             else
-                p.Y[(int64_t)m * p.ldy + col] = v;
+                store_y(p, (int64_t)m * p.ldy + col, v);
         }
     }
 }
@@ -490,7 +533,7 @@ w4a16_decode_kernel(W4Args p) {
         float v = red[0][m][c];
 #pragma unroll
         for (int w = 1; w < DV_NW; ++w) v += red[w][m][c];
-        p.Y[(int64_t)m * p.ldy + 32 * nt + 16 * sc + c] = v;
+        store_y(p, (int64_t)m * p.ldy + 32 * nt + 16 * sc + c, v);
     }
 }
 
@@ -741,7 +784,7 @@ w4a16_decode_mfma_kernel(W4Args p) {
         float v = red[0][m][c];
 #pragma unroll
         for (int w = 1; w < DM_NW; ++w) v += red[w][m][c];
-        p.Y[(int64_t)m * p.ldy + 32 * nt + 16 * sc + c] = v;
+        store_y(p, (int64_t)m * p.ldy + 32 * nt + 16 * sc + c, v);
     }
 }
 
@@ -890,7 +933,7 @@ w4a16_skinny_kernel(W4Args p) {
         if (partial)
             p.ws[((int64_t)blockIdx.y * M + m) * p.N + n] = acc;
         else
-            p.Y[(int64_t)m * p.ldy + n] = acc;
+            store_y(p, (int64_t)m * p.ldy + n, acc);
     }
 }
 
@@ -1149,7 +1192,12 @@ w4a16_gemm_kernel(W4Args p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = row0 + 32 * i + 8 * (r >> 2) + (r & 3), col = col0 + 32 * j;
-                if (full || (row < p.M && col < p.N)) out[(int64_t)row * ldo + col] = acc[i][j][r];
+                if (full || (row < p.M && col < p.N)) {
+                    if (partial)
+                        out[(int64_t)row * ldo + col] = acc[i][j][r];
+                    else
+                        store_y(p, (int64_t)row * ldo + col, acc[i][j][r]);
+                }
             }
 }
 
@@ -1286,7 +1334,7 @@ w4a16_mfma_kernel(W4Args p) {
                 if (partial)
                     p.ws[((int64_t)blockIdx.y * p.M + m) * p.N + n] = acc[j][i][r];
                 else
-                    p.Y[(int64_t)m * p.ldy + n] = acc[j][i][r];
+                    store_y(p, (int64_t)m * p.ldy + n, acc[j][i][r]);
             }
         }
     }
@@ -1294,7 +1342,7 @@ w4a16_mfma_kernel(W4Args p) {
 
 template <int W>
 __global__ void __launch_bounds__(256)
-w4a16_reduce_kernel(const float* ws, int split, float* Y, int64_t ldy, int M, int N) {
+w4a16_reduce_kernel(const float* ws, int split, float* Y, int64_t ldy, int M, int N, int y_half) {
     const int64_t total = (int64_t)M * N;
     const int nv = (N + W - 1) / W;
     for (int row = blockIdx.y; row < M; row += gridDim.y) {
@@ -1303,7 +1351,12 @@ w4a16_reduce_kernel(const float* ws, int split, float* Y, int64_t ldy, int M, in
             float v[W];
             splitk_sum<W>(ws + (int64_t)row * N + col, total, split, v);
 #pragma unroll
-            for (int e = 0; e < W; ++e) Y[(int64_t)row * ldy + col + e] = v[e];
+            for (int e = 0; e < W; ++e) {
+                if (y_half)
+                    reinterpret_cast<f16*>(Y)[(int64_t)row * ldy + col + e] = (f16)v[e];
+                else
+                    Y[(int64_t)row * ldy + col + e] = v[e];
+            }
         }
     }
 }
@@ -1348,6 +1401,15 @@ hipError_t launch_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q,
     const int64_t total = (int64_t)(K / 8) * N;
     hipLaunchKernelGGL(int4_unpack_kernel, dim3(grid_for(total, 256)), dim3(256), 0, stream,
                        qweight, K, N, q);
+    return hipGetLastError();
+}
+
+hipError_t launch_int4_from_awq(const int32_t* qweight_awq, const int32_t* qzeros_awq, int K,
+                                int N, int KG, int32_t* qweight, int32_t* zeros,
+                                hipStream_t stream) {
+    const int64_t total = (int64_t)(K / 8) * N + (int64_t)KG * (N / 8);
+    hipLaunchKernelGGL(int4_from_awq_kernel, dim3(grid_for(total, 256)), dim3(256), 0, stream,
+                       qweight_awq, qzeros_awq, K, N, KG, qweight, zeros);
     return hipGetLastError();
 }
 
@@ -1514,10 +1576,10 @@ hipError_t launch_w4a16_zf(const W4Args& a, const W4A16Launch& w, hipStream_t st
     const float* ws = static_cast<const float*>(w.workspace);
     if (vec4)
         hipLaunchKernelGGL(w4a16_reduce_kernel<4>, grid, dim3(256), 0, stream, ws, pl.split, w.Y,
-                           w.ldy, w.M, w.N);
+                           w.ldy, w.M, w.N, w.y_half ? 1 : 0);
     else
         hipLaunchKernelGGL(w4a16_reduce_kernel<1>, grid, dim3(256), 0, stream, ws, pl.split, w.Y,
-                           w.ldy, w.M, w.N);
+                           w.ldy, w.M, w.N, w.y_half ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -1541,6 +1603,7 @@ hipError_t launch_w4a16(const W4A16Launch& w, hipStream_t stream) {
     a.split = w.plan.split;
     a.kc_per_split = w.plan.k_per_split / 64;
     a.kg = w.K / w.G;
+    a.y_half = w.y_half ? 1 : 0;
     a.pp_shift = 0;
     while (w.G >= 128 && (128 << (a.pp_shift + 1)) <= w.G) ++a.pp_shift;
     if (w.zeros_format == WMMA_ZEROS_PACKED) return launch_w4a16_zf<WMMA_ZEROS_PACKED>(a, w, stream);
