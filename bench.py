@@ -290,6 +290,30 @@ def fam_flash(wo):
                  frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4),
                  max_rel_err=float(f"{err:.3e}"))
         del Qd, Kd, Vd
+    # packed variable-length batch (flash_attention_varlen): six ragged sequences, 16384
+    # tokens, 32 query / 8 key-value heads; FLOPs counted per sequence
+    lens = [1024, 3072, 2048, 4096, 512, 5632]
+    Hkv = 8
+    cu = torch.tensor([0] + [sum(lens[:i + 1]) for i in range(len(lens))], dtype=torch.int32)
+    g = torch.Generator().manual_seed(42 + 4)
+    q = torch.randn(sum(lens), H, D, generator=g).half()
+    k = torch.randn(sum(lens), Hkv, D, generator=g).half()
+    v = torch.randn(sum(lens), Hkv, D, generator=g).half()
+    qd, kd, vd, cud = q.cuda(), k.cuda(), v.cuda(), cu.cuda()
+    for causal in (False, True):
+        run = lambda i: wo.flash_attention_varlen(qd, kd, vd, cud, cud, max(lens), max(lens), causal,
+                                                  1.0 / math.sqrt(D))
+        ms = time_batches(run, 10)
+        O = run(0)
+        a, e = cu[0].item(), cu[1].item()   # first sequence checked against the oracle
+        ref = oatt.sdpa_varlen_ref(q[a:e], k[a:e], v[a:e], cu[:2], cu[:2], causal)
+        err = og.max_rel_err(O[a:e].float(), ref)
+        fl = sum((4.0 * H * S_ * S_ * D) if not causal else 4.0 * H * D * S_ * (S_ + 1) / 2
+                 for S_ in lens)
+        line(family="flash", varlen=lens, H=H, Hkv=Hkv, D=D, causal=causal, us=round(ms * 1e3, 1),
+             TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
+             frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4),
+             max_rel_err=float(f"{err:.3e}"))
 
 
 def fam_copy(wo):

@@ -215,6 +215,21 @@ int wmma_flash_attn_fwd_gqa(const void* Q, const void* K, const void* V, void* O
                             int Hkv, int Sq, int Sk, int D, float scale, int causal,
                             void* stream);
 
+/*
+ * Variable-length (packed) batches: Q and O [total_q, H, D], K and V [total_k, Hkv, D]
+ * fp16; sequence b is rows cu_seqlens_q[b] .. cu_seqlens_q[b+1] of Q/O and
+ * cu_seqlens_k[b] .. cu_seqlens_k[b+1] of K/V (int32 [B+1], device memory, non-decreasing,
+ * lengths at most max_seqlen_q / max_seqlen_k).  Causal masking is top-left aligned per
+ * sequence, as in wmma_flash_attn_fwd; a query row of a sequence with no keys gets zeros.
+ * Offsets outside [0, total] are clamped, so inconsistent cu_seqlens give wrong rows, never
+ * an access outside the tensors.  No counterpart in the reference: the variable-length
+ * extension of its documented flash_attention (README.md:221-251).
+ */
+int wmma_flash_attn_varlen_fwd(const void* Q, const void* K, const void* V, void* O,
+                               const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int B,
+                               int H, int Hkv, int total_q, int total_k, int max_seqlen_q,
+                               int max_seqlen_k, int D, float scale, int causal, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

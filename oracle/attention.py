@@ -69,3 +69,21 @@ def make_inputs(B: int, H: int, S: int, D: int, seed: int, Sk: int | None = None
     K = torch.randn(B, Hkv, Sk, D, generator=g).half()
     V = torch.randn(B, Hkv, Sk, D, generator=g).half()
     return Q, K, V
+
+
+def sdpa_varlen_ref(q, k, v, cu_q, cu_k, causal: bool = False, scale: float = -1.0):
+    """Packed variable-length batches ([total, heads, D], sequence b in rows
+    cu[b] .. cu[b+1]): sdpa_ref per sequence, top-left causal alignment per sequence; a
+    query of a sequence with no keys gives zeros."""
+    cu_q = [int(x) for x in cu_q]
+    cu_k = [int(x) for x in cu_k]
+    out = torch.zeros(q.shape[0], q.shape[1], q.shape[2], dtype=torch.float32)
+    for b in range(len(cu_q) - 1):
+        qa, qe, ka, ke = cu_q[b], cu_q[b + 1], cu_k[b], cu_k[b + 1]
+        if qe <= qa or ke <= ka:
+            continue
+        Q = q[qa:qe].transpose(0, 1).unsqueeze(0)   # [1, H, Sq, D]
+        K = k[ka:ke].transpose(0, 1).unsqueeze(0)
+        V = v[ka:ke].transpose(0, 1).unsqueeze(0)
+        out[qa:qe] = sdpa_ref(Q, K, V, causal, scale)[0].transpose(0, 1)
+    return out

@@ -48,6 +48,7 @@ def lib():
     L.wmma_w4a16_gemm.argtypes = [vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, vp, i64, vp, sz, vp]
     L.wmma_flash_attn_fwd.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, i32, vp]
     L.wmma_flash_attn_fwd_gqa.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, vp]
+    L.wmma_flash_attn_varlen_fwd.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 8 + [f32, i32, vp]
     return L
 
 
@@ -270,6 +271,11 @@ def test_flash_validation_codes(lib):
     assert b"must divide" in lib.wmma_last_error()
     assert g(8, 0) == INVALID
     assert g(0, 0) == OK                           # no heads: nothing to do
+    v = lambda **kw: lib.wmma_flash_attn_varlen_fwd(FAKE, FAKE, FAKE, FAKE, kw.get("cu", FAKE), FAKE, 2,
+                                                    8, kw.get("Hkv", 2), 100, 100, 64, 64, 128, 0.1, 0, None)
+    assert v(Hkv=3) == INVALID
+    assert v(cu=None) == INVALID
+    assert v(cu=FAKE + 2) == MISALIGNED
 
 
 # ---------------------------------------------------------------- torch layer on CPU --

@@ -1,6 +1,8 @@
 """GPU parity of flash-attention forward against fp32 CPU SDPA (max rel err <= 1e-3)."""
 import math
 
+import numpy as np
+
 import pytest
 import torch
 
@@ -110,6 +112,42 @@ def test_flash_gqa_head_mapping(wo):
         assert torch.allclose(O[:, h].float(), torch.full((2, 200, D), want), atol=2e-3 * want), h
 
 
+# Variable-length packed batches ([total, heads, D] with cu_seqlens): ragged lengths
+# (including 1 and lengths that are not multiples of the 64-key tile or 256-query block),
+# an empty sequence, different query and key lengths, grouped-query heads, both head sizes.
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("H,Hkv,D", [(8, 8, 128), (8, 2, 64), (6, 3, 128)])
+def test_flash_varlen(wo, causal, H, Hkv, D):
+    lens_q = [300, 1, 0, 1000, 64, 257]
+    lens_k = [300, 1, 5, 1000, 77, 700]
+    report("flash_varlen", H=H, Hkv=Hkv, D=D, causal=causal)
+    cu_q = torch.tensor([0] + list(np.cumsum(lens_q)), dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(np.cumsum(lens_k)), dtype=torch.int32)
+    g = torch.Generator().manual_seed(H * 10 + D)
+    q = torch.randn(int(cu_q[-1]), H, D, generator=g).half()
+    k = torch.randn(int(cu_k[-1]), Hkv, D, generator=g).half()
+    v = torch.randn(int(cu_k[-1]), Hkv, D, generator=g).half()
+    O = wo.flash_attention_varlen(q.cuda(), k.cuda(), v.cuda(), cu_q.cuda(), cu_k.cuda(),
+                                  max(lens_q), max(lens_k), causal=causal)
+    ref = oatt.sdpa_varlen_ref(q, k, v, cu_q, cu_k, causal)
+    assert O.dtype == torch.float16 and O.shape == q.shape
+    assert torch.isfinite(O).all()
+    err = og.max_rel_err(O.float().cpu(), ref)
+    assert err <= TOL, err
+
+
+def test_flash_varlen_equals_dense(wo):
+    # equal lengths: the packed problem is the dense one, computed to the same bits
+    B, H, S, D = 3, 4, 333, 128
+    Q, K, V = oatt.make_inputs(B, H, S, D, seed=12)
+    pack = lambda X: X.transpose(1, 2).reshape(B * S, H, D).contiguous().cuda()
+    cu = torch.arange(0, (B + 1) * S, S, dtype=torch.int32).cuda()
+    for causal in (False, True):
+        dense = wo.flash_attention(Q.cuda(), K.cuda(), V.cuda(), causal=causal)
+        packed = wo.flash_attention_varlen(pack(Q), pack(K), pack(V), cu, cu, S, S, causal=causal)
+        assert torch.equal(packed, dense.transpose(1, 2).reshape(B * S, H, D))
+
+
 def test_flash_errors(wo):
     x = torch.zeros(1, 1, 8, 96, dtype=torch.half, device="cuda")
     with pytest.raises(RuntimeError, match="head_dim"):
@@ -121,3 +159,7 @@ def test_flash_errors(wo):
     kv = torch.zeros(1, 4, 8, 64, dtype=torch.half, device="cuda")
     with pytest.raises(RuntimeError, match="K/V heads must divide Q heads"):
         wo.flash_attention(q, kv, kv)
+    p = torch.zeros(8, 2, 64, dtype=torch.half, device="cuda")
+    cu = torch.tensor([0, 8], dtype=torch.int64, device="cuda")
+    with pytest.raises(RuntimeError, match="cu_seqlens must be int32"):
+        wo.flash_attention_varlen(p, p, p, cu, cu, 8, 8)

@@ -292,3 +292,21 @@ def test_awq_pack_round_trip_and_order():
     z = rng.integers(0, 16, (4, 64), dtype=np.uint8)
     qg, zp = oi.awq_to_gptq(oi.pack_awq(np.repeat(q, 1, axis=0)), oi.pack_awq(z))
     assert np.array_equal(oi.unpack_gptq(qg), q) and np.array_equal(oi.unpack_zeros(zp), z)
+
+
+def test_sdpa_varlen_ref_equals_dense_for_equal_lengths():
+    # equal-length packed sequences are the dense [B, H, S, D] problem, per sequence
+    B, H, Hkv, S, D = 3, 4, 2, 9, 16
+    Q, K, V = oatt.make_inputs(B, H, S, D, seed=21, Hkv=Hkv)
+    cu = torch.arange(0, (B + 1) * S, S, dtype=torch.int32)
+    pack = lambda X: X.transpose(1, 2).reshape(B * S, X.shape[1], D)
+    for causal in (False, True):
+        got = oatt.sdpa_varlen_ref(pack(Q), pack(K), pack(V), cu, cu, causal)
+        want = pack(oatt.sdpa_ref(Q, K, V, causal))
+        assert torch.allclose(got, want, atol=1e-6)
+    # an empty sequence contributes nothing; a sequence without keys gives zeros
+    cu_q = torch.tensor([0, 0, 5], dtype=torch.int32)
+    cu_k = torch.tensor([0, 3, 3], dtype=torch.int32)
+    q = torch.randn(5, 2, 8).half()
+    kv = torch.randn(3, 2, 8).half()
+    assert torch.count_nonzero(oatt.sdpa_varlen_ref(q, kv, kv, cu_q, cu_k)) == 0

@@ -38,6 +38,7 @@ gemm = _C.gemm
 gemm_inplace = _C.gemm_inplace
 gemm_adaptive = _C.gemm_adaptive
 flash_attention = _C.flash_attention
+flash_attention_varlen = _C.flash_attention_varlen
 prepack_int4 = _C.prepack_int4
 prepack_int4_params = _C.prepack_int4_params
 int4_from_awq = _C.int4_from_awq
@@ -62,6 +63,6 @@ TILE_CONFIGS = {0: (64, 64), 1: (128, 64), 2: (256, 64), 3: (128, 128), 4: (256,
 
 __all__ = [
     "matmul", "matmul_adaptive", "matmul_tiled", "gemm", "gemm_inplace", "gemm_adaptive",
-    "flash_attention", "prepack_int4", "prepack_int4_params", "int4_from_awq", "unprepack_int4", "unpack_int4", "matmul_int4",
+    "flash_attention", "flash_attention_varlen", "prepack_int4", "prepack_int4_params", "int4_from_awq", "unprepack_int4", "unpack_int4", "matmul_int4",
     "gemm_plan", "w4a16_plan", "TILE_CONFIGS", "LIBRARY_PATH", "HEADER_PATH", *_REFERENCE_VARIANTS,
 ]

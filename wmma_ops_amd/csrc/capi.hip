@@ -396,6 +396,48 @@ int wmma_flash_attn_fwd_gqa(const void* Q, const void* K, const void* V, void* O
     return hip_status(launch_flash_fwd(f, static_cast<hipStream_t>(stream)), "flash launch");
 }
 
+int wmma_flash_attn_varlen_fwd(const void* Q, const void* K, const void* V, void* O,
+                               const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int B,
+                               int H, int Hkv, int total_q, int total_k, int max_seqlen_q,
+                               int max_seqlen_k, int D, float scale, int causal, void* stream) {
+    if (B < 0 || H < 0 || total_q < 0 || total_k < 0 || max_seqlen_q < 0 || max_seqlen_k < 0)
+        return fail(WMMA_ERR_INVALID_ARG, "negative dimension");
+    if (D != 64 && D != 128) return fail(WMMA_ERR_UNSUPPORTED, "head_dim %d (supported: 64, 128)", D);
+    if (!(scale > 0.0f) || !std::isfinite(scale))
+        return fail(WMMA_ERR_INVALID_ARG, "scale must be positive and finite");
+    if (H > 0 && (Hkv <= 0 || H % Hkv != 0))
+        return fail(WMMA_ERR_INVALID_ARG, "key/value heads (%d) must divide query heads (%d)", Hkv, H);
+    if (B == 0 || H == 0 || total_q == 0 || max_seqlen_q == 0) return ok();
+    if (!Q || !K || !V || !O || !cu_seqlens_q || !cu_seqlens_k)
+        return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
+    if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O))
+        return fail(WMMA_ERR_MISALIGNED, "Q, K, V and O must be 16-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(cu_seqlens_q) & 3u) || (reinterpret_cast<uintptr_t>(cu_seqlens_k) & 3u))
+        return fail(WMMA_ERR_MISALIGNED, "cu_seqlens must be 4-byte aligned");
+    // 32-bit offsets inside one sequence of one head
+    if ((int64_t)max_seqlen_q * H * D * 2 > kMaxOffset || (int64_t)max_seqlen_k * Hkv * D * 2 > kMaxOffset)
+        return fail(WMMA_ERR_UNSUPPORTED, "sequence too long for 32-bit offsets");
+    if ((int64_t)B * H > 2147483647LL) return fail(WMMA_ERR_UNSUPPORTED, "too many heads");
+    FlashLaunch f{};
+    f.Q = Q;
+    f.K = K;
+    f.V = V;
+    f.O = O;
+    f.B = B;
+    f.H = H;
+    f.Hkv = Hkv;
+    f.Sq = max_seqlen_q;
+    f.Sk = max_seqlen_k;
+    f.D = D;
+    f.scale = scale;
+    f.causal = causal != 0;
+    f.cu_q = cu_seqlens_q;
+    f.cu_k = cu_seqlens_k;
+    f.total_q = total_q;
+    f.total_k = total_k;
+    return hip_status(launch_flash_fwd(f, static_cast<hipStream_t>(stream)), "flash launch");
+}
+
 int wmma_flash_attn_fwd(const void* Q, const void* K, const void* V, void* O, int B, int H,
                         int Sq, int Sk, int D, float scale, int causal, void* stream) {
     return wmma_flash_attn_fwd_gqa(Q, K, V, O, B, H, H, Sq, Sk, D, scale, causal, stream);

@@ -43,6 +43,14 @@ struct FlashArgs {
     int nqb;           // query blocks
     float scale_log2;  // scale * log2(e)
     int group;         // query heads per key/value head (1: multi-head attention)
+    // Variable length (cu_q != nullptr): Q/O packed [total_q][H][D], K/V [total_k][Hkv][D];
+    // sequence b spans rows cu_q[b] .. cu_q[b+1] (and cu_k likewise).  Sq/Sk then hold the
+    // longest lengths; every row index is clamped into [0, total) so inconsistent offsets
+    // cannot send a load or store outside the tensors.
+    const int* cu_q;
+    const int* cu_k;
+    int H, Hkv;
+    int total_q, total_k;
 };
 
 constexpr int FA_WAVES = 8;                 // waves per workgroup (two per SIMD)
@@ -296,16 +304,38 @@ flash_fwd_kernel(FlashArgs p) {
     const int qb_idx = CAUSAL ? (p.nqb - 1 - (int)blockIdx.y) : (int)blockIdx.y;
     const int q0 = qb_idx * FA_BQ;
     const int qw = q0 + wave * FA_WQ;
-    const int Sq = p.Sq, Sk = p.Sk;
     const float c = p.scale_log2;
 
-    // Grouped-query attention: query heads bh of one batch entry come in runs of `group`
-    // that share key/value head bh / group (heads are the inner index of both).
-    const int kvh = bh / p.group;
-    const f16* Qb = p.Q + (int64_t)bh * Sq * D;
-    const f16* Kb = p.K + (int64_t)kvh * Sk * D;
-    const f16* Vb = p.V + (int64_t)kvh * Sk * D;
-    f16* Ob = p.O + (int64_t)bh * Sq * D;
+    // Rows of this (batch, head): base offsets and row strides (elements).  Grouped-query
+    // attention: query heads of one batch entry come in runs of `group` that share one
+    // key/value head (heads are the inner index of both layouts).
+    int Sq, Sk, qs, ks;
+    int64_t q_base, k_base;
+    if (p.cu_q) {
+        const int b = bh / p.H, hq = bh % p.H;
+        const int qa = min(max(p.cu_q[b], 0), p.total_q);
+        const int qe = min(max(p.cu_q[b + 1], qa), p.total_q);
+        const int ka = min(max(p.cu_k[b], 0), p.total_k);
+        const int ke = min(max(p.cu_k[b + 1], ka), p.total_k);
+        Sq = min(qe - qa, p.Sq);
+        Sk = min(ke - ka, p.Sk);
+        qs = p.H * D;
+        ks = p.Hkv * D;
+        q_base = (int64_t)qa * qs + (int64_t)hq * D;
+        k_base = (int64_t)ka * ks + (int64_t)(hq / p.group) * D;
+    } else {
+        Sq = p.Sq;
+        Sk = p.Sk;
+        qs = D;
+        ks = D;
+        q_base = (int64_t)bh * Sq * D;
+        k_base = (int64_t)(bh / p.group) * Sk * D;
+    }
+    if (q0 >= Sq) return;  // a query block past this sequence (variable length): no work
+    const f16* Qb = p.Q + q_base;
+    const f16* Kb = p.K + k_base;
+    const f16* Vb = p.V + k_base;
+    f16* Ob = p.O + q_base;
 
     // Q fragments (B operand of S^T): query qw + 32 qb + lane%32, d = 16 ds + 8 h + 0..7.
     f16x8 qf[FA_NQB][C::NDS];
@@ -317,7 +347,7 @@ flash_fwd_kernel(FlashArgs p) {
 #pragma unroll
             for (int ds = 0; ds < C::NDS; ++ds)
                 qf[qb][ds] = as_f16x8(buf_load16(
-                    rs, q < Sq ? (uint32_t)(((int64_t)q * D + 16 * ds + 8 * h) * 2) : kOobOffset));
+                    rs, q < Sq ? (uint32_t)(((int64_t)q * qs + 16 * ds + 8 * h) * 2) : kOobOffset));
         }
     }
 
@@ -330,9 +360,9 @@ flash_fwd_kernel(FlashArgs p) {
         const int P = 64 * (wave * C::DMA + i) + lane;
         const int row = P / C::DCH, pc = P % C::DCH;
         L.k_row[i] = row;
-        L.k_off[i] = (uint32_t)((row * D + 8 * (pc ^ swz_k<D>(row))) * 2);
+        L.k_off[i] = (uint32_t)((row * ks + 8 * (pc ^ swz_k<D>(row))) * 2);
         L.v_row[i] = row;
-        L.v_off[i] = (uint32_t)((row * D + 8 * (pc ^ swz_v<D>(row))) * 2);
+        L.v_off[i] = (uint32_t)((row * ks + 8 * (pc ^ swz_v<D>(row))) * 2);
     }
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -357,8 +387,8 @@ flash_fwd_kernel(FlashArgs p) {
     const int T = (kv_end + FA_BKV - 1) / FA_BKV;
     // Tiles this wave needs (causal: keys <= its last query).
     const int Tw = CAUSAL ? min(T, (qw + FA_WQ - 1) / FA_BKV + 1) : T;
-    auto rk_of = [&](int t) { return make_rsrc(Kb + (int64_t)min(t, T - 1) * FA_BKV * D); };
-    auto rv_of = [&](int t) { return make_rsrc(Vb + (int64_t)min(t, T - 1) * FA_BKV * D); };
+    auto rk_of = [&](int t) { return make_rsrc(Kb + (int64_t)min(t, T - 1) * FA_BKV * ks); };
+    auto rv_of = [&](int t) { return make_rsrc(Vb + (int64_t)min(t, T - 1) * FA_BKV * ks); };
     auto kleft = [&](int t) { return t < T ? Sk - t * FA_BKV : 0; };
     // A tile needs masking if it reaches past Sk or (causal) past this wave's first query.
     auto masked = [&](int t) {
@@ -408,7 +438,7 @@ flash_fwd_kernel(FlashArgs p) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) v[e] = (f16)(O[db][qb][4 * g + e] * inv);
                     const int d = 32 * db + 8 * g + 4 * h;
-                    *reinterpret_cast<f16x4*>(Ob + (int64_t)q * D + d) = v;
+                    *reinterpret_cast<f16x4*>(Ob + (int64_t)q * qs + d) = v;
                 }
             }
         }
@@ -436,6 +466,12 @@ hipError_t launch_flash_fwd(const FlashLaunch& f, hipStream_t stream) {
     a.Sk = f.Sk;
     a.nqb = ceil_div(f.Sq, FA_BQ);
     a.group = f.H / f.Hkv;
+    a.cu_q = f.cu_q;
+    a.cu_k = f.cu_k;
+    a.H = f.H;
+    a.Hkv = f.Hkv;
+    a.total_q = f.total_q;
+    a.total_k = f.total_k;
     a.scale_log2 = f.scale * 1.4426950408889634f;
     const int BH = f.B * f.H;
     if (f.D == 128)

@@ -86,6 +86,11 @@ struct FlashLaunch {
     int Hkv;  // key/value heads (H % Hkv == 0; H for multi-head attention)
     float scale;
     bool causal;
+    // Variable length: packed Q/O [total_q][H][D], K/V [total_k][Hkv][D], sequence b in
+    // rows cu_q[b] .. cu_q[b+1] (cu_k likewise); Sq/Sk are then the longest lengths.
+    const int* cu_q = nullptr;
+    const int* cu_k = nullptr;
+    int total_q = 0, total_k = 0;
 };
 hipError_t launch_flash_fwd(const FlashLaunch& f, hipStream_t stream);
 

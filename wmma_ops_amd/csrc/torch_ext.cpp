@@ -196,6 +196,45 @@ torch::Tensor flash_attention(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
     return O;
 }
 
+// flash_attention_varlen(q [total_q, H, D], k/v [total_k, Hkv, D], cu_seqlens_q/k int32
+// [B+1], max_seqlen_q, max_seqlen_k, causal=False, scale=-1.0) -> fp16 [total_q, H, D]
+torch::Tensor flash_attention_varlen(torch::Tensor q, torch::Tensor k, torch::Tensor v,
+                                     torch::Tensor cu_q, torch::Tensor cu_k, int64_t max_q,
+                                     int64_t max_k, bool causal, double scale) {
+    TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda() && cu_q.is_cuda() && cu_k.is_cuda(),
+                "Inputs must be CUDA tensors");
+    TORCH_CHECK(q.device() == k.device() && q.device() == v.device() && q.device() == cu_q.device() &&
+                    q.device() == cu_k.device(),
+                "Inputs must be on same device");
+    TORCH_CHECK(q.dtype() == torch::kFloat16 && k.dtype() == torch::kFloat16 &&
+                    v.dtype() == torch::kFloat16,
+                "Inputs must be float16");
+    TORCH_CHECK(q.dim() == 3 && k.dim() == 3 && v.dim() == 3, "Inputs must be 3D [total, heads, D]");
+    TORCH_CHECK(k.sizes() == v.sizes(), "K and V must have the same shape");
+    TORCH_CHECK(q.size(2) == k.size(2), "Q and K must agree in head_dim");
+    TORCH_CHECK(k.size(1) > 0 && q.size(1) % k.size(1) == 0, "K/V heads must divide Q heads");
+    TORCH_CHECK(cu_q.dtype() == torch::kInt32 && cu_k.dtype() == torch::kInt32 && cu_q.dim() == 1 &&
+                    cu_q.sizes() == cu_k.sizes() && cu_q.size(0) >= 1,
+                "cu_seqlens must be int32 [B+1], equal for Q and K");
+    const int64_t D = q.size(2);
+    TORCH_CHECK(D == 64 || D == 128, "head_dim must be 64 or 128");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+    q = q.contiguous();
+    k = k.contiguous();
+    v = v.contiguous();
+    cu_q = cu_q.contiguous();
+    cu_k = cu_k.contiguous();
+    const float sc = scale > 0.0 ? (float)scale : (float)(1.0 / std::sqrt((double)D));
+    auto O = torch::empty_like(q);
+    int rc = wmma_flash_attn_varlen_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(), cu_q.data_ptr<int32_t>(),
+        cu_k.data_ptr<int32_t>(), (int)(cu_q.size(0) - 1), (int)q.size(1), (int)k.size(1),
+        (int)q.size(0), (int)k.size(0), (int)max_q, (int)max_k, (int)D, sc, causal ? 1 : 0,
+        current_stream(q));
+    check_status(rc, "wmma_flash_attn_varlen_fwd");
+    return O;
+}
+
 void check_qweight(const torch::Tensor& q) {
     TORCH_CHECK(q.is_cuda(), "qweight must be a CUDA tensor");
     TORCH_CHECK(q.dtype() == torch::kInt32, "qweight must be int32");
@@ -407,6 +446,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("flash_attention", &flash_attention, "Flash-attention forward (fp16 in/out, fp32 softmax)",
           py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("causal") = false,
           py::arg("scale") = -1.0);
+    m.def("flash_attention_varlen", &flash_attention_varlen,
+          "Flash-attention forward on packed variable-length sequences", py::arg("q"), py::arg("k"),
+          py::arg("v"), py::arg("cu_seqlens_q"), py::arg("cu_seqlens_k"), py::arg("max_seqlen_q"),
+          py::arg("max_seqlen_k"), py::arg("causal") = false, py::arg("scale") = -1.0);
     m.def("prepack_int4", &prepack_int4, "GPTQ int4 qweight [K/8,N] -> MFMA layout", py::arg("qweight"));
     m.def("unprepack_int4", &unprepack_int4, "Inverse of prepack_int4", py::arg("packed"));
     m.def("unpack_int4", &unpack_int4, "GPTQ int4 qweight [K/8,N] -> uint8 [K,N]", py::arg("qweight"));
