@@ -230,6 +230,60 @@ int wmma_flash_attn_varlen_fwd(const void* Q, const void* K, const void* V, void
                                int H, int Hkv, int total_q, int total_k, int max_seqlen_q,
                                int max_seqlen_k, int D, float scale, int causal, void* stream);
 
+/*
+ * Forward for training: wmma_flash_attn_fwd_gqa that also writes lse [B,H,Sq] fp32, the
+ * natural-log log-sum-exp of each row of scale * Q K^T over its unmasked keys (+inf for a
+ * row with none), which wmma_flash_attn_bwd consumes.  lse may be NULL (no output).  No
+ * counterpart in the reference, whose documented flash_attention (README.md:221-251) is
+ * forward-only; this and the entry points below are its training extension.
+ */
+int wmma_flash_attn_fwd_lse(const void* Q, const void* K, const void* V, void* O, float* lse,
+                            int B, int H, int Hkv, int Sq, int Sk, int D, float scale, int causal,
+                            void* stream);
+
+/* The variable-length forward with lse [H, total_q] (row r of head h at h * total_q + r). */
+int wmma_flash_attn_varlen_fwd_lse(const void* Q, const void* K, const void* V, void* O,
+                                   float* lse, const int32_t* cu_seqlens_q,
+                                   const int32_t* cu_seqlens_k, int B, int H, int Hkv,
+                                   int total_q, int total_k, int max_seqlen_q, int max_seqlen_k,
+                                   int D, float scale, int causal, void* stream);
+
+/*
+ * Bytes of fp32 workspace wmma_flash_attn_bwd needs: 2 * 4 * B * H * Sq (two row
+ * statistics per query row).  For the variable-length backward pass B = 1, Sq = total_q.
+ */
+size_t wmma_flash_attn_bwd_workspace_size(int B, int H, int Sq);
+
+/*
+ * Flash-attention backward.  Given dO [B,H,Sq,D] and the forward's Q, K, V, O and lse
+ * (from wmma_flash_attn_fwd_lse with the same scale and causal flag), writes dQ [B,H,Sq,D],
+ * dK and dV [B,Hkv,Sk,D], fp16, the gradients of sum(O * dO): with P = softmax(scale Q K^T
+ * + mask), dV = P^T dO, dS = P o (dO V^T - rowsum(dO o O)), dQ = scale dS K,
+ * dK = scale dS^T Q; with Hkv < H, dK and dV of a key/value head are summed over the query
+ * heads that read it.  FP32 accumulation throughout; deterministic (no atomics; the same
+ * inputs give the same bits).  Sq == 0 gives dK = dV = 0.  workspace: at least
+ * wmma_flash_attn_bwd_workspace_size(B, H, Sq) bytes, 4-byte aligned, overwritten.
+ * Two kernels on `stream`.  No counterpart in the reference (its flash_attention,
+ * README.md:221-251, is forward-only).
+ */
+int wmma_flash_attn_bwd(const void* dO, const void* Q, const void* K, const void* V, const void* O,
+                        const float* lse, void* dQ, void* dK, void* dV, void* workspace,
+                        size_t workspace_bytes, int B, int H, int Hkv, int Sq, int Sk, int D,
+                        float scale, int causal, void* stream);
+
+/*
+ * The variable-length backward pass: dO, dQ as Q [total_q, H, D]; dK, dV as K [total_k,
+ * Hkv, D]; lse [H, total_q] from wmma_flash_attn_varlen_fwd_lse; workspace of
+ * wmma_flash_attn_bwd_workspace_size(1, H, total_q) bytes.  A sequence with no keys gets
+ * dQ = 0, one with no queries dK = dV = 0; rows outside every sequence are not written.
+ */
+int wmma_flash_attn_varlen_bwd(const void* dO, const void* Q, const void* K, const void* V,
+                               const void* O, const float* lse, void* dQ, void* dK, void* dV,
+                               const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                               void* workspace, size_t workspace_bytes, int B, int H, int Hkv,
+                               int total_q, int total_k, int max_seqlen_q, int max_seqlen_k,
+                               int D, float scale, int causal, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

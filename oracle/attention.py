@@ -87,3 +87,77 @@ def sdpa_varlen_ref(q, k, v, cu_q, cu_k, causal: bool = False, scale: float = -1
         V = v[ka:ke].transpose(0, 1).unsqueeze(0)
         out[qa:qe] = sdpa_ref(Q, K, V, causal, scale)[0].transpose(0, 1)
     return out
+
+
+# ------------------------------------------------------------------------ training path --
+# No reference counterpart: the reference's flash_attention is forward-only
+# (README.md:221-251).  These restate the mathematics of its training extension -- the
+# log-sum-exp a backward pass needs and the gradients of sum(O * dO) -- through the library
+# routines (torch.logsumexp, torch autograd of scaled_dot_product_attention); the tests pin
+# them against float64 finite differences and closed forms.
+
+def lse_ref(Q, K, causal: bool = False, scale: float = -1.0) -> torch.Tensor:
+    """Natural-log log-sum-exp of each row of scale * Q K^T over its unmasked keys, fp32
+    [B, H, Sq]; +inf for a row with no key (the value the kernels store there)."""
+    sc = resolve_scale(Q.shape[-1], scale)
+    Qf = Q.detach().cpu().float()
+    Kf = expand_kv(K.detach().cpu().float(), Q.shape[1])
+    S = torch.matmul(Qf, Kf.transpose(-1, -2).contiguous()) * sc
+    if causal:
+        sq, sk = S.shape[-2], S.shape[-1]
+        S = S.masked_fill(~torch.ones(sq, sk, dtype=torch.bool).tril(), float("-inf"))
+    out = torch.logsumexp(S, dim=-1)
+    return torch.where(torch.isneginf(out), torch.full_like(out, float("inf")), out)
+
+
+def sdpa_bwd_ref(Q, K, V, dO, causal: bool = False, scale: float = -1.0):
+    """(dQ, dK, dV), fp32 on the CPU: torch autograd of sdpa_ref's FP32 attention for the
+    upstream gradient dO.  With fewer K/V heads than Q heads the K/V gradients are summed
+    over the query heads that share them (autograd through expand_kv)."""
+    sc = resolve_scale(Q.shape[-1], scale)
+    H = Q.shape[1]
+    q = Q.detach().cpu().float().requires_grad_()
+    k = K.detach().cpu().float().requires_grad_()
+    v = V.detach().cpu().float().requires_grad_()
+    with torch.enable_grad():
+        out = F.scaled_dot_product_attention(q, expand_kv(k, H), expand_kv(v, H),
+                                             is_causal=causal, scale=sc)
+        out.backward(dO.detach().cpu().float())
+    return q.grad, k.grad, v.grad
+
+
+def sdpa_varlen_bwd_ref(q, k, v, dO, cu_q, cu_k, causal: bool = False, scale: float = -1.0):
+    """Gradients of sdpa_varlen_ref, per sequence (zero for rows of a sequence with no keys
+    or no queries, and for rows outside every sequence)."""
+    cu_q = [int(x) for x in cu_q]
+    cu_k = [int(x) for x in cu_k]
+    dq = torch.zeros(q.shape, dtype=torch.float32)
+    dk = torch.zeros(k.shape, dtype=torch.float32)
+    dv = torch.zeros(v.shape, dtype=torch.float32)
+    for b in range(len(cu_q) - 1):
+        qa, qe, ka, ke = cu_q[b], cu_q[b + 1], cu_k[b], cu_k[b + 1]
+        if qe <= qa or ke <= ka:
+            continue
+        t = lambda X, a, e: X[a:e].transpose(0, 1).unsqueeze(0)
+        gq, gk, gv = sdpa_bwd_ref(t(q, qa, qe), t(k, ka, ke), t(v, ka, ke), t(dO, qa, qe),
+                                  causal, scale)
+        dq[qa:qe] = gq[0].transpose(0, 1)
+        dk[ka:ke] = gk[0].transpose(0, 1)
+        dv[ka:ke] = gv[0].transpose(0, 1)
+    return dq, dk, dv
+
+
+def lse_varlen_ref(q, k, cu_q, cu_k, causal: bool = False, scale: float = -1.0) -> torch.Tensor:
+    """lse_ref per sequence in the packed layout [H, total_q] (+inf for a sequence with no
+    keys)."""
+    cu_q = [int(x) for x in cu_q]
+    cu_k = [int(x) for x in cu_k]
+    out = torch.full((q.shape[1], q.shape[0]), float("inf"), dtype=torch.float32)
+    for b in range(len(cu_q) - 1):
+        qa, qe, ka, ke = cu_q[b], cu_q[b + 1], cu_k[b], cu_k[b + 1]
+        if qe <= qa or ke <= ka:
+            continue
+        Q = q[qa:qe].transpose(0, 1).unsqueeze(0)
+        K = k[ka:ke].transpose(0, 1).unsqueeze(0)
+        out[:, qa:qe] = lse_ref(Q, K, causal, scale)[0]
+    return out

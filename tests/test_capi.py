@@ -49,6 +49,12 @@ def lib():
     L.wmma_flash_attn_fwd.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, i32, vp]
     L.wmma_flash_attn_fwd_gqa.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, vp]
     L.wmma_flash_attn_varlen_fwd.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 8 + [f32, i32, vp]
+    L.wmma_flash_attn_fwd_lse.argtypes = [vp, vp, vp, vp, vp] + [i32] * 6 + [f32, i32, vp]
+    L.wmma_flash_attn_varlen_fwd_lse.argtypes = [vp] * 7 + [i32] * 8 + [f32, i32, vp]
+    L.wmma_flash_attn_bwd_workspace_size.argtypes = [i32, i32, i32]
+    L.wmma_flash_attn_bwd_workspace_size.restype = sz
+    L.wmma_flash_attn_bwd.argtypes = [vp] * 10 + [sz] + [i32] * 6 + [f32, i32, vp]
+    L.wmma_flash_attn_varlen_bwd.argtypes = [vp] * 12 + [sz] + [i32] * 8 + [f32, i32, vp]
     return L
 
 
@@ -278,6 +284,45 @@ def test_flash_validation_codes(lib):
     assert v(cu=FAKE + 2) == MISALIGNED
 
 
+def test_flash_training_validation_codes(lib):
+    # forward with log-sum-exp
+    f = lambda **kw: lib.wmma_flash_attn_fwd_lse(FAKE, FAKE, FAKE, FAKE, kw.get("lse", FAKE), 1, 4, 2,
+                                                 128, 128, kw.get("D", 128), 0.1, 0, None)
+    assert f(D=96) == UNSUPPORTED
+    assert f(lse=FAKE + 2) == MISALIGNED
+    # workspace: two fp32 statistics per query row
+    assert lib.wmma_flash_attn_bwd_workspace_size(4, 32, 4096) == 2 * 4 * 4 * 32 * 4096
+    assert lib.wmma_flash_attn_bwd_workspace_size(0, 32, 4096) == 0
+    need = lib.wmma_flash_attn_bwd_workspace_size(1, 4, 128)
+
+    def bwd(**kw):
+        ptr = lambda k: kw.get(k, FAKE)
+        return lib.wmma_flash_attn_bwd(ptr("dO"), FAKE, FAKE, FAKE, ptr("O"), ptr("lse"), ptr("dQ"), FAKE,
+                                       FAKE, ptr("ws"), kw.get("wsb", need), 1, 4, kw.get("Hkv", 2),
+                                       kw.get("Sq", 128), kw.get("Sk", 128), kw.get("D", 128),
+                                       kw.get("scale", 0.1), 0, None)
+    assert bwd(D=32) == UNSUPPORTED
+    assert bwd(Hkv=3) == INVALID
+    assert bwd(scale=-1.0) == INVALID
+    assert bwd(dO=None) == INVALID
+    assert bwd(lse=None) == INVALID
+    assert bwd(dQ=FAKE + 8) == MISALIGNED
+    assert bwd(lse=FAKE + 1) == MISALIGNED
+    assert bwd(ws=None) == WORKSPACE
+    assert bwd(wsb=need - 4) == WORKSPACE
+    assert b"needed" in lib.wmma_last_error()
+    assert bwd(Sk=0) == INVALID                   # queries without keys
+    assert bwd(Sq=0, Sk=0) == OK                  # nothing to do
+    # variable length
+    vb = lambda **kw: lib.wmma_flash_attn_varlen_bwd(
+        FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, kw.get("cu", FAKE), FAKE, FAKE,
+        kw.get("wsb", 2 * 4 * 8 * 100), 2, 8, kw.get("Hkv", 2), 100, 100, 64, 64, 128, 0.1, 0, None)
+    assert vb(Hkv=3) == INVALID
+    assert vb(cu=None) == INVALID
+    assert vb(cu=FAKE + 2) == MISALIGNED
+    assert vb(wsb=16) == WORKSPACE
+
+
 # ---------------------------------------------------------------- torch layer on CPU --
 def test_torch_extension_reference_errors(wo):
     A = torch.zeros(4, 8, dtype=torch.float16)
@@ -293,7 +338,9 @@ def test_torch_extension_reference_errors(wo):
                            torch.zeros(1, 1, 4, 64, dtype=torch.float16),
                            torch.zeros(1, 1, 4, 64, dtype=torch.float16))
     for name in ["matmul", "matmul_adaptive", "matmul_tiled", "gemm", "gemm_inplace", "gemm_adaptive",
-                 "flash_attention", "prepack_int4", "matmul_int4", "unpack_int4",
+                 "flash_attention", "flash_attention_forward", "flash_attention_backward",
+                 "flash_attention_varlen_forward", "flash_attention_varlen_backward",
+                 "prepack_int4", "matmul_int4", "unpack_int4",
                  "matmul_kunroll", "matmul_hilbert", "matmul_opt", "matmul_pingpong"]:
         assert callable(getattr(wo, name))
 

@@ -310,3 +310,98 @@ def test_sdpa_varlen_ref_equals_dense_for_equal_lengths():
     q = torch.randn(5, 2, 8).half()
     kv = torch.randn(3, 2, 8).half()
     assert torch.count_nonzero(oatt.sdpa_varlen_ref(q, kv, kv, cu_q, cu_k)) == 0
+
+
+# ------------------------------------------------------------------ attention training --
+def _lse_naive_f64(Q, K, causal, scale=-1.0):
+    Q = np.asarray(Q, dtype=np.float64)
+    K = oatt.expand_kv(np.asarray(K, dtype=np.float64), Q.shape[1])
+    S = np.einsum("...qd,...kd->...qk", Q, K) * oatt.resolve_scale(Q.shape[-1], scale)
+    if causal:
+        S = np.where(np.tril(np.ones(S.shape[-2:], dtype=bool)), S, -np.inf)
+    m = S.max(axis=-1, keepdims=True)
+    return (m + np.log(np.exp(S - m).sum(axis=-1, keepdims=True)))[..., 0]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("Sq,Sk,H,Hkv", [(7, 7, 2, 2), (5, 9, 4, 2), (9, 5, 3, 1)])
+def test_lse_ref_matches_naive_f64(causal, Sq, Sk, H, Hkv):
+    Q, K, _ = oatt.make_inputs(2, H, Sq, 16, seed=Sq + 3 * Sk, Sk=Sk, Hkv=Hkv)
+    got = oatt.lse_ref(Q, K, causal).double().numpy()
+    assert np.allclose(got, _lse_naive_f64(Q.numpy(), K.numpy(), causal), atol=2e-6)
+
+
+def _fd_grads(Q, K, V, dO, causal, eps=1e-6):
+    """Central finite differences of f = sum(attention_naive_f64(Q, K, V) * dO), float64."""
+    arrs = [np.asarray(X, dtype=np.float64).copy() for X in (Q, K, V)]
+    dO = np.asarray(dO, dtype=np.float64)
+    f = lambda: float((oatt.attention_naive_f64(*arrs, causal) * dO).sum())
+    grads = []
+    for X in arrs:
+        g = np.zeros_like(X)
+        for idx in np.ndindex(X.shape):
+            x0 = X[idx]
+            X[idx] = x0 + eps
+            fp = f()
+            X[idx] = x0 - eps
+            fm = f()
+            X[idx] = x0
+            g[idx] = (fp - fm) / (2 * eps)
+        grads.append(g)
+    return grads
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("H,Hkv,Sq,Sk", [(2, 2, 5, 5), (4, 2, 4, 6), (2, 1, 6, 3)])
+def test_sdpa_bwd_ref_matches_finite_differences(causal, H, Hkv, Sq, Sk):
+    # Gradients pinned by float64 finite differences of the explicit forward -- a route that
+    # shares nothing with autograd or with the dS = P (dP - Delta) closed form.
+    D = 4
+    Q, K, V = oatt.make_inputs(1, H, Sq, D, seed=H * 31 + Sq, Sk=Sk, Hkv=Hkv)
+    dO = torch.randn(1, H, Sq, D, generator=torch.Generator().manual_seed(7)).half()
+    want = _fd_grads(Q.numpy(), K.numpy(), V.numpy(), dO.numpy(), causal)
+    got = oatt.sdpa_bwd_ref(Q, K, V, dO, causal)
+    for g, w in zip(got, want):
+        assert g.shape == w.shape
+        assert np.allclose(g.double().numpy(), w, atol=2e-5 * max(1.0, np.abs(w).max()))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_sdpa_bwd_closed_forms(causal):
+    # softmax rows sum to 1 -> the dV rows sum to the dO rows; softmax is invariant to a
+    # per-row shift of the scores -> the dS rows sum to 0, so the dK rows sum to 0 and dQ
+    # vanishes when every key is the same vector.
+    B, H, Hkv, S, D = 2, 4, 2, 24, 16
+    Q, K, V = oatt.make_inputs(B, H, S, D, seed=5, Hkv=Hkv)
+    dO = torch.randn(B, H, S, D, generator=torch.Generator().manual_seed(8)).half()
+    dQ, dK, dV = oatt.sdpa_bwd_ref(Q, K, V, dO, causal)
+    dO_group = dO.float().view(B, Hkv, H // Hkv, S, D).sum(dim=(2, 3))
+    assert torch.allclose(dV.sum(dim=2), dO_group, atol=1e-4)
+    assert torch.allclose(dK.sum(dim=2), torch.zeros(B, Hkv, D), atol=1e-4)
+    Kc = K[:, :, :1].expand_as(K).contiguous()
+    dQc, _, _ = oatt.sdpa_bwd_ref(Q, Kc, V, dO, causal)
+    assert dQc.abs().max() < 1e-5
+
+
+def test_sdpa_varlen_bwd_ref_equals_dense():
+    B, H, Hkv, S, D = 3, 4, 2, 9, 16
+    Q, K, V = oatt.make_inputs(B, H, S, D, seed=22, Hkv=Hkv)
+    dO = torch.randn(B, H, S, D, generator=torch.Generator().manual_seed(9)).half()
+    cu = torch.arange(0, (B + 1) * S, S, dtype=torch.int32)
+    pack = lambda X: X.transpose(1, 2).reshape(B * S, X.shape[1], D)
+    for causal in (False, True):
+        got = oatt.sdpa_varlen_bwd_ref(pack(Q), pack(K), pack(V), pack(dO), cu, cu, causal)
+        want = oatt.sdpa_bwd_ref(Q, K, V, dO, causal)
+        for g, w in zip(got, want):
+            assert torch.allclose(g, pack(w), atol=1e-6)
+        lse = oatt.lse_varlen_ref(pack(Q), pack(K), cu, cu, causal)
+        assert torch.allclose(lse, oatt.lse_ref(Q, K, causal).permute(1, 0, 2).reshape(H, B * S))
+    # a sequence without keys: +inf log-sum-exp and zero gradients
+    cu_q = torch.tensor([0, 4, 6], dtype=torch.int32)
+    cu_k = torch.tensor([0, 0, 3], dtype=torch.int32)
+    q, dOq = torch.randn(6, 2, 8).half(), torch.randn(6, 2, 8).half()
+    kv = torch.randn(3, 2, 8).half()
+    lse = oatt.lse_varlen_ref(q, kv, cu_q, cu_k)
+    assert torch.isinf(lse[:, :4]).all() and torch.isfinite(lse[:, 4:]).all()
+    dq, _, _ = oatt.sdpa_varlen_bwd_ref(q, kv, kv, dOq, cu_q, cu_k)
+    assert torch.count_nonzero(dq[:4]) == 0 and torch.count_nonzero(dq[4:]) > 0

@@ -7,7 +7,7 @@ wmma_gemm.hip:2120-2157)::
     C = wmma_ops.matmul(A, B)                        # fp16 x fp16 -> fp32
     C = wmma_ops.gemm(A, B, alpha=2.0, beta=0.5, C=C0)
     wmma_ops.gemm_inplace(A, B, C, 2.0, 0.5)
-    O = wmma_ops.flash_attention(Q, K, V, causal=True)
+    O = wmma_ops.flash_attention(Q, K, V, causal=True)   # differentiable (fused backward)
     P = wmma_ops.prepack_int4(qweight); Y = wmma_ops.matmul_int4(A, P, scales, zeros, 128)
 
 Every function runs the HIP kernels in ``libwmma_ops_amd.so`` through the C++ extension
@@ -37,8 +37,72 @@ matmul_tiled = _C.matmul_tiled
 gemm = _C.gemm
 gemm_inplace = _C.gemm_inplace
 gemm_adaptive = _C.gemm_adaptive
-flash_attention = _C.flash_attention
-flash_attention_varlen = _C.flash_attention_varlen
+flash_attention_forward = _C.flash_attention_forward
+flash_attention_backward = _C.flash_attention_backward
+flash_attention_varlen_forward = _C.flash_attention_varlen_forward
+flash_attention_varlen_backward = _C.flash_attention_varlen_backward
+
+
+class FlashAttentionFunction(_torch.autograd.Function):
+    """Autograd node of flash_attention: the forward keeps O and the log-sum-exp, the
+    backward runs the fused dQ and dK/dV kernels."""
+
+    @staticmethod
+    def forward(ctx, Q, K, V, causal=False, scale=-1.0):
+        O, lse = _C.flash_attention_forward(Q, K, V, causal, scale)
+        ctx.save_for_backward(Q, K, V, O, lse)
+        ctx.causal, ctx.scale = causal, scale
+        return O
+
+    @staticmethod
+    def backward(ctx, dO):
+        Q, K, V, O, lse = ctx.saved_tensors
+        dQ, dK, dV = _C.flash_attention_backward(dO, Q, K, V, O, lse, ctx.causal, ctx.scale)
+        return dQ, dK, dV, None, None
+
+
+class FlashAttentionVarlenFunction(_torch.autograd.Function):
+    """Autograd node of flash_attention_varlen."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, cu_q, cu_k, max_q, max_k, causal=False, scale=-1.0):
+        O, lse = _C.flash_attention_varlen_forward(q, k, v, cu_q, cu_k, max_q, max_k, causal, scale)
+        ctx.save_for_backward(q, k, v, O, lse, cu_q, cu_k)
+        ctx.args = (max_q, max_k, causal, scale)
+        return O
+
+    @staticmethod
+    def backward(ctx, dO):
+        q, k, v, O, lse, cu_q, cu_k = ctx.saved_tensors
+        max_q, max_k, causal, scale = ctx.args
+        dq, dk, dv = _C.flash_attention_varlen_backward(dO, q, k, v, O, lse, cu_q, cu_k, max_q,
+                                                        max_k, causal, scale)
+        return dq, dk, dv, None, None, None, None, None, None
+
+
+def _needs_grad(*ts) -> bool:
+    return _torch.is_grad_enabled() and any(t.requires_grad for t in ts)
+
+
+def flash_attention(Q, K, V, causal: bool = False, scale: float = -1.0):
+    """flash_attention(Q, K, V, causal=False, scale=-1.0) (the reference's README.md:221-251):
+    fp16 [B,H,Sq,D] attention output.  Differentiable when an input requires grad (the
+    reference's op is forward-only; inference calls take the plain forward kernel)."""
+    if _needs_grad(Q, K, V):
+        return FlashAttentionFunction.apply(Q, K, V, causal, scale)
+    return _C.flash_attention(Q, K, V, causal, scale)
+
+
+def flash_attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                           causal: bool = False, scale: float = -1.0):
+    """Packed variable-length attention ([total, heads, D] with int32 cu_seqlens [B+1]);
+    differentiable in q, k, v."""
+    if _needs_grad(q, k, v):
+        return FlashAttentionVarlenFunction.apply(q, k, v, cu_seqlens_q, cu_seqlens_k,
+                                                  max_seqlen_q, max_seqlen_k, causal, scale)
+    return _C.flash_attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                                     max_seqlen_k, causal, scale)
+
 prepack_int4 = _C.prepack_int4
 prepack_int4_params = _C.prepack_int4_params
 int4_from_awq = _C.int4_from_awq
@@ -63,6 +127,8 @@ TILE_CONFIGS = {0: (64, 64), 1: (128, 64), 2: (256, 64), 3: (128, 128), 4: (256,
 
 __all__ = [
     "matmul", "matmul_adaptive", "matmul_tiled", "gemm", "gemm_inplace", "gemm_adaptive",
-    "flash_attention", "flash_attention_varlen", "prepack_int4", "prepack_int4_params", "int4_from_awq", "unprepack_int4", "unpack_int4", "matmul_int4",
+    "flash_attention", "flash_attention_varlen", "flash_attention_forward",
+    "flash_attention_backward", "flash_attention_varlen_forward", "flash_attention_varlen_backward",
+    "FlashAttentionFunction", "FlashAttentionVarlenFunction", "prepack_int4", "prepack_int4_params", "int4_from_awq", "unprepack_int4", "unpack_int4", "matmul_int4",
     "gemm_plan", "w4a16_plan", "TILE_CONFIGS", "LIBRARY_PATH", "HEADER_PATH", *_REFERENCE_VARIANTS,
 ]

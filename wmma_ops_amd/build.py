@@ -28,7 +28,7 @@ ARCH = "gfx950"
 LIB_NAME = "libwmma_ops_amd.so"
 EXT_NAME = "_C" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so")
 
-HIP_SOURCES = ["capi.hip", "gemm.hip", "w4a16.hip", "flash_fwd.hip"]
+HIP_SOURCES = ["capi.hip", "gemm.hip", "w4a16.hip", "flash_fwd.hip", "flash_bwd.hip"]
 HOST_SOURCES = ["plan.cpp"]
 
 HIP_FLAGS = [

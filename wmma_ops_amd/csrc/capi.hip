@@ -364,22 +364,52 @@ int wmma_int4_from_awq(const int32_t* qweight_awq, const int32_t* qzeros_awq, in
 }
 
 // ----------------------------------------------------------------------------- flash --
-int wmma_flash_attn_fwd_gqa(const void* Q, const void* K, const void* V, void* O, int B, int H,
-                            int Hkv, int Sq, int Sk, int D, float scale, int causal, void* stream) {
+namespace {
+
+// Shape checks shared by the dense forward and backward entry points.
+int flash_dense_check(int B, int H, int Hkv, int Sq, int Sk, int D, float scale) {
     if (B < 0 || H < 0 || Sq < 0 || Sk < 0) return fail(WMMA_ERR_INVALID_ARG, "negative dimension");
     if (D != 64 && D != 128) return fail(WMMA_ERR_UNSUPPORTED, "head_dim %d (supported: 64, 128)", D);
     if (!(scale > 0.0f) || !std::isfinite(scale))
         return fail(WMMA_ERR_INVALID_ARG, "scale must be positive and finite");
     if (H > 0 && (Hkv <= 0 || H % Hkv != 0))
         return fail(WMMA_ERR_INVALID_ARG, "key/value heads (%d) must divide query heads (%d)", Hkv, H);
+    if ((int64_t)Sq * D * 2 > kMaxOffset || (int64_t)Sk * D * 2 > kMaxOffset)
+        return fail(WMMA_ERR_UNSUPPORTED, "sequence too long for 32-bit offsets");
+    if ((int64_t)B * H > 2147483647LL) return fail(WMMA_ERR_UNSUPPORTED, "too many heads");
+    return WMMA_OK;
+}
+
+int flash_varlen_check(int B, int H, int Hkv, int total_q, int total_k, int max_q, int max_k,
+                       int D, float scale) {
+    if (B < 0 || H < 0 || total_q < 0 || total_k < 0 || max_q < 0 || max_k < 0)
+        return fail(WMMA_ERR_INVALID_ARG, "negative dimension");
+    if (D != 64 && D != 128) return fail(WMMA_ERR_UNSUPPORTED, "head_dim %d (supported: 64, 128)", D);
+    if (!(scale > 0.0f) || !std::isfinite(scale))
+        return fail(WMMA_ERR_INVALID_ARG, "scale must be positive and finite");
+    if (H > 0 && (Hkv <= 0 || H % Hkv != 0))
+        return fail(WMMA_ERR_INVALID_ARG, "key/value heads (%d) must divide query heads (%d)", Hkv, H);
+    // 32-bit offsets inside one sequence of one head
+    if ((int64_t)max_q * H * D * 2 > kMaxOffset || (int64_t)max_k * Hkv * D * 2 > kMaxOffset)
+        return fail(WMMA_ERR_UNSUPPORTED, "sequence too long for 32-bit offsets");
+    if ((int64_t)B * H > 2147483647LL) return fail(WMMA_ERR_UNSUPPORTED, "too many heads");
+    return WMMA_OK;
+}
+
+bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+}  // namespace
+
+int wmma_flash_attn_fwd_lse(const void* Q, const void* K, const void* V, void* O, float* lse,
+                            int B, int H, int Hkv, int Sq, int Sk, int D, float scale, int causal,
+                            void* stream) {
+    if (int rc = flash_dense_check(B, H, Hkv, Sq, Sk, D, scale)) return rc;
     if (B == 0 || H == 0 || Sq == 0) return ok();
     if (Sk == 0) return fail(WMMA_ERR_INVALID_ARG, "Sk must be positive when Sq > 0");
     if (!Q || !K || !V || !O) return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
     if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O))
         return fail(WMMA_ERR_MISALIGNED, "Q, K, V and O must be 16-byte aligned");
-    if ((int64_t)Sq * D * 2 > kMaxOffset || (int64_t)Sk * D * 2 > kMaxOffset)
-        return fail(WMMA_ERR_UNSUPPORTED, "sequence too long for 32-bit offsets");
-    if ((int64_t)B * H > 2147483647LL) return fail(WMMA_ERR_UNSUPPORTED, "too many heads");
+    if (lse && !aligned4(lse)) return fail(WMMA_ERR_MISALIGNED, "lse must be 4-byte aligned");
     FlashLaunch f{};
     f.Q = Q;
     f.K = K;
@@ -393,31 +423,30 @@ int wmma_flash_attn_fwd_gqa(const void* Q, const void* K, const void* V, void* O
     f.D = D;
     f.scale = scale;
     f.causal = causal != 0;
+    f.lse = lse;
     return hip_status(launch_flash_fwd(f, static_cast<hipStream_t>(stream)), "flash launch");
 }
 
-int wmma_flash_attn_varlen_fwd(const void* Q, const void* K, const void* V, void* O,
-                               const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int B,
-                               int H, int Hkv, int total_q, int total_k, int max_seqlen_q,
-                               int max_seqlen_k, int D, float scale, int causal, void* stream) {
-    if (B < 0 || H < 0 || total_q < 0 || total_k < 0 || max_seqlen_q < 0 || max_seqlen_k < 0)
-        return fail(WMMA_ERR_INVALID_ARG, "negative dimension");
-    if (D != 64 && D != 128) return fail(WMMA_ERR_UNSUPPORTED, "head_dim %d (supported: 64, 128)", D);
-    if (!(scale > 0.0f) || !std::isfinite(scale))
-        return fail(WMMA_ERR_INVALID_ARG, "scale must be positive and finite");
-    if (H > 0 && (Hkv <= 0 || H % Hkv != 0))
-        return fail(WMMA_ERR_INVALID_ARG, "key/value heads (%d) must divide query heads (%d)", Hkv, H);
+int wmma_flash_attn_fwd_gqa(const void* Q, const void* K, const void* V, void* O, int B, int H,
+                            int Hkv, int Sq, int Sk, int D, float scale, int causal, void* stream) {
+    return wmma_flash_attn_fwd_lse(Q, K, V, O, nullptr, B, H, Hkv, Sq, Sk, D, scale, causal, stream);
+}
+
+int wmma_flash_attn_varlen_fwd_lse(const void* Q, const void* K, const void* V, void* O,
+                                   float* lse, const int32_t* cu_seqlens_q,
+                                   const int32_t* cu_seqlens_k, int B, int H, int Hkv,
+                                   int total_q, int total_k, int max_seqlen_q, int max_seqlen_k,
+                                   int D, float scale, int causal, void* stream) {
+    if (int rc = flash_varlen_check(B, H, Hkv, total_q, total_k, max_seqlen_q, max_seqlen_k, D, scale))
+        return rc;
     if (B == 0 || H == 0 || total_q == 0 || max_seqlen_q == 0) return ok();
     if (!Q || !K || !V || !O || !cu_seqlens_q || !cu_seqlens_k)
         return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
     if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O))
         return fail(WMMA_ERR_MISALIGNED, "Q, K, V and O must be 16-byte aligned");
-    if ((reinterpret_cast<uintptr_t>(cu_seqlens_q) & 3u) || (reinterpret_cast<uintptr_t>(cu_seqlens_k) & 3u))
+    if (!aligned4(cu_seqlens_q) || !aligned4(cu_seqlens_k))
         return fail(WMMA_ERR_MISALIGNED, "cu_seqlens must be 4-byte aligned");
-    // 32-bit offsets inside one sequence of one head
-    if ((int64_t)max_seqlen_q * H * D * 2 > kMaxOffset || (int64_t)max_seqlen_k * Hkv * D * 2 > kMaxOffset)
-        return fail(WMMA_ERR_UNSUPPORTED, "sequence too long for 32-bit offsets");
-    if ((int64_t)B * H > 2147483647LL) return fail(WMMA_ERR_UNSUPPORTED, "too many heads");
+    if (lse && !aligned4(lse)) return fail(WMMA_ERR_MISALIGNED, "lse must be 4-byte aligned");
     FlashLaunch f{};
     f.Q = Q;
     f.K = K;
@@ -435,12 +464,116 @@ int wmma_flash_attn_varlen_fwd(const void* Q, const void* K, const void* V, void
     f.cu_k = cu_seqlens_k;
     f.total_q = total_q;
     f.total_k = total_k;
+    f.lse = lse;
     return hip_status(launch_flash_fwd(f, static_cast<hipStream_t>(stream)), "flash launch");
+}
+
+int wmma_flash_attn_varlen_fwd(const void* Q, const void* K, const void* V, void* O,
+                               const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int B,
+                               int H, int Hkv, int total_q, int total_k, int max_seqlen_q,
+                               int max_seqlen_k, int D, float scale, int causal, void* stream) {
+    return wmma_flash_attn_varlen_fwd_lse(Q, K, V, O, nullptr, cu_seqlens_q, cu_seqlens_k, B, H,
+                                          Hkv, total_q, total_k, max_seqlen_q, max_seqlen_k, D,
+                                          scale, causal, stream);
 }
 
 int wmma_flash_attn_fwd(const void* Q, const void* K, const void* V, void* O, int B, int H,
                         int Sq, int Sk, int D, float scale, int causal, void* stream) {
     return wmma_flash_attn_fwd_gqa(Q, K, V, O, B, H, H, Sq, Sk, D, scale, causal, stream);
+}
+
+size_t wmma_flash_attn_bwd_workspace_size(int B, int H, int Sq) {
+    if (B <= 0 || H <= 0 || Sq <= 0) return 0;
+    return (size_t)2 * sizeof(float) * (size_t)B * (size_t)H * (size_t)Sq;
+}
+
+namespace {
+int flash_bwd_run(FlashBwdLaunch& f, void* workspace, size_t workspace_bytes, void* stream) {
+    // Query-side tensors are read only when there are query rows, key-side ones only when
+    // there are key rows (either side may be empty).
+    const int64_t rows = flash_bwd_workspace_rows(f);
+    const bool has_q = rows > 0, has_k = f.cu_k ? f.total_k > 0 : (int64_t)f.B * f.Hkv * f.Sk > 0;
+    if ((has_q && (!f.dO || !f.Q || !f.O || !f.lse || !f.dQ)) || (has_k && (!f.K || !f.V || !f.dK || !f.dV)))
+        return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
+    if (!aligned16(f.dO) || !aligned16(f.Q) || !aligned16(f.K) || !aligned16(f.V) ||
+        !aligned16(f.O) || !aligned16(f.dQ) || !aligned16(f.dK) || !aligned16(f.dV))
+        return fail(WMMA_ERR_MISALIGNED, "dO, Q, K, V, O, dQ, dK and dV must be 16-byte aligned");
+    if (!aligned4(f.lse)) return fail(WMMA_ERR_MISALIGNED, "lse must be 4-byte aligned");
+    const size_t need = (size_t)2 * sizeof(float) * (size_t)rows;
+    if (need > 0) {
+        if (!workspace) return fail(WMMA_ERR_WORKSPACE, "NULL workspace");
+        if (!aligned4(workspace)) return fail(WMMA_ERR_MISALIGNED, "workspace must be 4-byte aligned");
+        if (workspace_bytes < need)
+            return fail(WMMA_ERR_WORKSPACE, "workspace of %zu bytes, %zu needed", workspace_bytes, need);
+    }
+    f.ws = static_cast<float*>(workspace);
+    return hip_status(launch_flash_bwd(f, static_cast<hipStream_t>(stream)), "flash backward launch");
+}
+}  // namespace
+
+int wmma_flash_attn_bwd(const void* dO, const void* Q, const void* K, const void* V, const void* O,
+                        const float* lse, void* dQ, void* dK, void* dV, void* workspace,
+                        size_t workspace_bytes, int B, int H, int Hkv, int Sq, int Sk, int D,
+                        float scale, int causal, void* stream) {
+    if (int rc = flash_dense_check(B, H, Hkv, Sq, Sk, D, scale)) return rc;
+    if (B == 0 || H == 0 || (Sq == 0 && Sk == 0)) return ok();
+    if (Sk == 0) return fail(WMMA_ERR_INVALID_ARG, "Sk must be positive when Sq > 0");
+    FlashBwdLaunch f{};
+    f.Q = Q;
+    f.K = K;
+    f.V = V;
+    f.O = O;
+    f.dO = dO;
+    f.lse = lse;
+    f.dQ = dQ;
+    f.dK = dK;
+    f.dV = dV;
+    f.B = B;
+    f.H = H;
+    f.Hkv = Hkv;
+    f.Sq = Sq;
+    f.Sk = Sk;
+    f.D = D;
+    f.scale = scale;
+    f.causal = causal != 0;
+    return flash_bwd_run(f, workspace, workspace_bytes, stream);
+}
+
+int wmma_flash_attn_varlen_bwd(const void* dO, const void* Q, const void* K, const void* V,
+                               const void* O, const float* lse, void* dQ, void* dK, void* dV,
+                               const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                               void* workspace, size_t workspace_bytes, int B, int H, int Hkv,
+                               int total_q, int total_k, int max_seqlen_q, int max_seqlen_k,
+                               int D, float scale, int causal, void* stream) {
+    if (int rc = flash_varlen_check(B, H, Hkv, total_q, total_k, max_seqlen_q, max_seqlen_k, D, scale))
+        return rc;
+    if (B == 0 || H == 0 || (total_q == 0 && total_k == 0)) return ok();
+    if (!cu_seqlens_q || !cu_seqlens_k) return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
+    if (!aligned4(cu_seqlens_q) || !aligned4(cu_seqlens_k))
+        return fail(WMMA_ERR_MISALIGNED, "cu_seqlens must be 4-byte aligned");
+    FlashBwdLaunch f{};
+    f.Q = Q;
+    f.K = K;
+    f.V = V;
+    f.O = O;
+    f.dO = dO;
+    f.lse = lse;
+    f.dQ = dQ;
+    f.dK = dK;
+    f.dV = dV;
+    f.B = B;
+    f.H = H;
+    f.Hkv = Hkv;
+    f.Sq = max_seqlen_q;
+    f.Sk = max_seqlen_k;
+    f.D = D;
+    f.scale = scale;
+    f.causal = causal != 0;
+    f.cu_q = cu_seqlens_q;
+    f.cu_k = cu_seqlens_k;
+    f.total_q = total_q;
+    f.total_k = total_k;
+    return flash_bwd_run(f, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

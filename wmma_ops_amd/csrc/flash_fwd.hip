@@ -51,6 +51,9 @@ struct FlashArgs {
     const int* cu_k;
     int H, Hkv;
     int total_q, total_k;
+    // Optional per-row log-sum-exp of the scaled scores (natural log; +inf for a row with
+    // no key): [B*H][Sq] dense, [H][total_q] variable length.
+    float* lse;
 };
 
 constexpr int FA_WAVES = 8;                 // waves per workgroup (two per SIMD)
@@ -310,7 +313,7 @@ flash_fwd_kernel(FlashArgs p) {
     // attention: query heads of one batch entry come in runs of `group` that share one
     // key/value head (heads are the inner index of both layouts).
     int Sq, Sk, qs, ks;
-    int64_t q_base, k_base;
+    int64_t q_base, k_base, lse_base;
     if (p.cu_q) {
         const int b = bh / p.H, hq = bh % p.H;
         const int qa = min(max(p.cu_q[b], 0), p.total_q);
@@ -323,6 +326,7 @@ flash_fwd_kernel(FlashArgs p) {
         ks = p.Hkv * D;
         q_base = (int64_t)qa * qs + (int64_t)hq * D;
         k_base = (int64_t)ka * ks + (int64_t)(hq / p.group) * D;
+        lse_base = (int64_t)hq * p.total_q + qa;
     } else {
         Sq = p.Sq;
         Sk = p.Sk;
@@ -330,6 +334,7 @@ flash_fwd_kernel(FlashArgs p) {
         ks = D;
         q_base = (int64_t)bh * Sq * D;
         k_base = (int64_t)(bh / p.group) * Sk * D;
+        lse_base = (int64_t)bh * Sq;
     }
     if (q0 >= Sq) return;  // a query block past this sequence (variable length): no work
     const f16* Qb = p.Q + q_base;
@@ -429,6 +434,12 @@ flash_fwd_kernel(FlashArgs p) {
         const int q = qrow0 + 32 * qb;
         const float l_tot = l_run[qb] + __shfl_xor(l_run[qb], 32);
         const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        // log-sum-exp: m_run is the running max of the base-2 scaled scores, l_tot the sum
+        // of exp2(score - m_run), so ln(sum exp) = (m_run + log2 l_tot) * ln 2.
+        if (p.lse && h == 0 && q < Sq)
+            p.lse[lse_base + q] = l_tot > 0.0f
+                                      ? (m_run[qb] + __builtin_amdgcn_logf(l_tot)) * 0.6931471805599453f
+                                      : __builtin_huge_valf();
         if (q < Sq) {
 #pragma unroll
             for (int db = 0; db < C::NDB; ++db) {
@@ -472,6 +483,7 @@ hipError_t launch_flash_fwd(const FlashLaunch& f, hipStream_t stream) {
     a.Hkv = f.Hkv;
     a.total_q = f.total_q;
     a.total_k = f.total_k;
+    a.lse = f.lse;
     a.scale_log2 = f.scale * 1.4426950408889634f;
     const int BH = f.B * f.H;
     if (f.D == 128)

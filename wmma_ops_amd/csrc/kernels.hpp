@@ -91,7 +91,33 @@ struct FlashLaunch {
     const int* cu_q = nullptr;
     const int* cu_k = nullptr;
     int total_q = 0, total_k = 0;
+    // Optional log-sum-exp output (fp32, natural log): [B*H][Sq], or [H][total_q] for
+    // variable length.
+    float* lse = nullptr;
 };
 hipError_t launch_flash_fwd(const FlashLaunch& f, hipStream_t stream);
+
+// Flash-attention backward: dQ, dK, dV (fp16, the layouts of Q, K, V) from dO, Q, K, V, O
+// and the forward's log-sum-exp.  ws: fp32 workspace of 2 * flash_bwd_workspace_rows().
+struct FlashBwdLaunch {
+    const void* Q;
+    const void* K;
+    const void* V;
+    const void* O;
+    const void* dO;
+    const float* lse;
+    void* dQ;
+    void* dK;
+    void* dV;
+    float* ws;
+    int B, H, Hkv, Sq, Sk, D;
+    float scale;
+    bool causal;
+    const int* cu_q = nullptr;
+    const int* cu_k = nullptr;
+    int total_q = 0, total_k = 0;
+};
+int64_t flash_bwd_workspace_rows(const FlashBwdLaunch& f);
+hipError_t launch_flash_bwd(const FlashBwdLaunch& f, hipStream_t stream);
 
 }  // namespace wmma_amd

@@ -8,7 +8,8 @@
 // the reference a device guard is taken, so the launch goes to the tensors' device.
 //
 // Additions the reference lacks: flash_attention (documented at README.md:221-251 but
-// never bound), the INT4 entry points (prepack_int4, unpack_int4, unprepack_int4,
+// never bound) and its training entry points (forward with log-sum-exp, backward), the INT4
+// entry points (prepack_int4, unpack_int4, unprepack_int4,
 // matmul_int4), and the split-K workspace, which is taken from the caching allocator.
 #include <torch/extension.h>
 
@@ -162,12 +163,9 @@ void gemm_inplace(torch::Tensor A, torch::Tensor B, torch::Tensor C, double alph
     run_gemm(A, B, C, C, alpha, beta, WMMA_TILE_AUTO);
 }
 
-// flash_attention(Q, K, V, causal=False, scale=-1.0) (README.md:221-251): Q [B,H,Sq,D],
-// K/V [B,Hkv,Sk,D] fp16 with Hkv dividing H (Hkv < H: grouped-query attention, query head h
-// reads key/value head h / (H/Hkv)); scale <= 0 selects 1/sqrt(D).  Returns fp16
-// [B,H,Sq,D].
-torch::Tensor flash_attention(torch::Tensor Q, torch::Tensor K, torch::Tensor V, bool causal,
-                              double scale) {
+// Checks of the dense attention inputs Q [B,H,Sq,D], K/V [B,Hkv,Sk,D] (flash_attention and
+// its training entry points).
+void check_flash_dense(const torch::Tensor& Q, const torch::Tensor& K, const torch::Tensor& V) {
     TORCH_CHECK(Q.is_cuda() && K.is_cuda() && V.is_cuda(), "Inputs must be CUDA tensors");
     TORCH_CHECK(Q.device() == K.device() && Q.device() == V.device(),
                 "Inputs must be on same device");
@@ -180,27 +178,12 @@ torch::Tensor flash_attention(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
                 "Q and K must agree in batch and head_dim");
     TORCH_CHECK(K.size(1) > 0 && Q.size(1) % K.size(1) == 0,
                 "K/V heads must divide Q heads");
-    const int64_t D = Q.size(3);
-    TORCH_CHECK(D == 64 || D == 128, "head_dim must be 64 or 128");
-    const c10::hip::HIPGuardMasqueradingAsCUDA guard(Q.device());
-    Q = Q.contiguous();
-    K = K.contiguous();
-    V = V.contiguous();
-    const float sc = scale > 0.0 ? (float)scale : (float)(1.0 / std::sqrt((double)D));
-    auto O = torch::empty_like(Q);
-    int rc = wmma_flash_attn_fwd_gqa(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(),
-                                     (int)Q.size(0), (int)Q.size(1), (int)K.size(1),
-                                     (int)Q.size(2), (int)K.size(2), (int)D, sc, causal ? 1 : 0,
-                                     current_stream(Q));
-    check_status(rc, "wmma_flash_attn_fwd_gqa");
-    return O;
+    TORCH_CHECK(Q.size(3) == 64 || Q.size(3) == 128, "head_dim must be 64 or 128");
 }
 
-// flash_attention_varlen(q [total_q, H, D], k/v [total_k, Hkv, D], cu_seqlens_q/k int32
-// [B+1], max_seqlen_q, max_seqlen_k, causal=False, scale=-1.0) -> fp16 [total_q, H, D]
-torch::Tensor flash_attention_varlen(torch::Tensor q, torch::Tensor k, torch::Tensor v,
-                                     torch::Tensor cu_q, torch::Tensor cu_k, int64_t max_q,
-                                     int64_t max_k, bool causal, double scale) {
+// Checks of the packed inputs q [total_q,H,D], k/v [total_k,Hkv,D], cu_seqlens int32 [B+1].
+void check_flash_varlen(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
+                        const torch::Tensor& cu_q, const torch::Tensor& cu_k) {
     TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda() && cu_q.is_cuda() && cu_k.is_cuda(),
                 "Inputs must be CUDA tensors");
     TORCH_CHECK(q.device() == k.device() && q.device() == v.device() && q.device() == cu_q.device() &&
@@ -216,23 +199,180 @@ torch::Tensor flash_attention_varlen(torch::Tensor q, torch::Tensor k, torch::Te
     TORCH_CHECK(cu_q.dtype() == torch::kInt32 && cu_k.dtype() == torch::kInt32 && cu_q.dim() == 1 &&
                     cu_q.sizes() == cu_k.sizes() && cu_q.size(0) >= 1,
                 "cu_seqlens must be int32 [B+1], equal for Q and K");
+    TORCH_CHECK(q.size(2) == 64 || q.size(2) == 128, "head_dim must be 64 or 128");
+}
+
+// Gradient-side checks: dO and O have Q's shape (fp16, same device), lse is fp32 of the
+// given shape.
+void check_flash_grad_inputs(const torch::Tensor& Q, const torch::Tensor& dO, const torch::Tensor& O,
+                             const torch::Tensor& lse, at::IntArrayRef lse_shape) {
+    TORCH_CHECK(dO.is_cuda() && O.is_cuda() && lse.is_cuda(), "Inputs must be CUDA tensors");
+    TORCH_CHECK(dO.device() == Q.device() && O.device() == Q.device() && lse.device() == Q.device(),
+                "Inputs must be on same device");
+    TORCH_CHECK(dO.dtype() == torch::kFloat16 && O.dtype() == torch::kFloat16,
+                "dO and O must be float16");
+    TORCH_CHECK(dO.sizes() == Q.sizes() && O.sizes() == Q.sizes(), "dO and O must have Q's shape");
+    TORCH_CHECK(lse.dtype() == torch::kFloat32 && lse.sizes() == lse_shape,
+                "lse must be float32 ", lse_shape);
+}
+
+float flash_scale(double scale, int64_t D) {
+    return scale > 0.0 ? (float)scale : (float)(1.0 / std::sqrt((double)D));
+}
+
+// Runs the dense forward; lse_out (fp32 [B,H,Sq]) may be undefined (no log-sum-exp).
+torch::Tensor flash_dense_fwd(torch::Tensor Q, torch::Tensor K, torch::Tensor V, bool causal,
+                              double scale, torch::Tensor* lse_out) {
+    check_flash_dense(Q, K, V);
+    const int64_t D = Q.size(3);
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(Q.device());
+    Q = Q.contiguous();
+    K = K.contiguous();
+    V = V.contiguous();
+    auto O = torch::empty_like(Q);
+    float* lse = nullptr;
+    if (lse_out) {
+        *lse_out = torch::empty({Q.size(0), Q.size(1), Q.size(2)}, Q.options().dtype(torch::kFloat32));
+        lse = lse_out->data_ptr<float>();
+    }
+    int rc = wmma_flash_attn_fwd_lse(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(), lse,
+                                     (int)Q.size(0), (int)Q.size(1), (int)K.size(1),
+                                     (int)Q.size(2), (int)K.size(2), (int)D, flash_scale(scale, D),
+                                     causal ? 1 : 0, current_stream(Q));
+    check_status(rc, "wmma_flash_attn_fwd_lse");
+    return O;
+}
+
+// flash_attention(Q, K, V, causal=False, scale=-1.0) (README.md:221-251): Q [B,H,Sq,D],
+// K/V [B,Hkv,Sk,D] fp16 with Hkv dividing H (Hkv < H: grouped-query attention, query head h
+// reads key/value head h / (H/Hkv)); scale <= 0 selects 1/sqrt(D).  Returns fp16
+// [B,H,Sq,D].
+torch::Tensor flash_attention(torch::Tensor Q, torch::Tensor K, torch::Tensor V, bool causal,
+                              double scale) {
+    return flash_dense_fwd(Q, K, V, causal, scale, nullptr);
+}
+
+// flash_attention_forward(Q, K, V, causal=False, scale=-1.0) -> (O, lse): the forward for
+// training, with lse fp32 [B,H,Sq] (natural-log log-sum-exp of each scaled score row).
+std::tuple<torch::Tensor, torch::Tensor> flash_attention_forward(torch::Tensor Q, torch::Tensor K,
+                                                                 torch::Tensor V, bool causal,
+                                                                 double scale) {
+    torch::Tensor lse;
+    auto O = flash_dense_fwd(Q, K, V, causal, scale, &lse);
+    return {O, lse};
+}
+
+// flash_attention_backward(dO, Q, K, V, O, lse, causal=False, scale=-1.0) -> (dQ, dK, dV),
+// fp16 with the shapes of Q, K, V; O and lse from flash_attention_forward with the same
+// causal flag and scale.
+std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> flash_attention_backward(
+    torch::Tensor dO, torch::Tensor Q, torch::Tensor K, torch::Tensor V, torch::Tensor O,
+    torch::Tensor lse, bool causal, double scale) {
+    check_flash_dense(Q, K, V);
+    check_flash_grad_inputs(Q, dO, O, lse, {Q.size(0), Q.size(1), Q.size(2)});
+    const int64_t B = Q.size(0), H = Q.size(1), Sq = Q.size(2), D = Q.size(3);
+    TORCH_CHECK(Sq == 0 || K.size(2) > 0, "K must have keys when Q has queries");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(Q.device());
+    Q = Q.contiguous();
+    K = K.contiguous();
+    V = V.contiguous();
+    O = O.contiguous();
+    dO = dO.contiguous();
+    lse = lse.contiguous();
+    auto dQ = torch::empty_like(Q);
+    auto dK = torch::empty_like(K);
+    auto dV = torch::empty_like(V);
+    const size_t ws_bytes = wmma_flash_attn_bwd_workspace_size((int)B, (int)H, (int)Sq);
+    auto ws = torch::empty({(int64_t)(ws_bytes / 4)}, Q.options().dtype(torch::kFloat32));
+    int rc = wmma_flash_attn_bwd(dO.data_ptr(), Q.data_ptr(), K.data_ptr(), V.data_ptr(),
+                                 O.data_ptr(), lse.data_ptr<float>(), dQ.data_ptr(), dK.data_ptr(),
+                                 dV.data_ptr(), ws.data_ptr(), ws_bytes, (int)B, (int)H,
+                                 (int)K.size(1), (int)Sq, (int)K.size(2), (int)D,
+                                 flash_scale(scale, D), causal ? 1 : 0, current_stream(Q));
+    check_status(rc, "wmma_flash_attn_bwd");
+    return {dQ, dK, dV};
+}
+
+torch::Tensor flash_varlen_fwd(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor cu_q,
+                               torch::Tensor cu_k, int64_t max_q, int64_t max_k, bool causal,
+                               double scale, torch::Tensor* lse_out) {
+    check_flash_varlen(q, k, v, cu_q, cu_k);
     const int64_t D = q.size(2);
-    TORCH_CHECK(D == 64 || D == 128, "head_dim must be 64 or 128");
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     q = q.contiguous();
     k = k.contiguous();
     v = v.contiguous();
     cu_q = cu_q.contiguous();
     cu_k = cu_k.contiguous();
-    const float sc = scale > 0.0 ? (float)scale : (float)(1.0 / std::sqrt((double)D));
     auto O = torch::empty_like(q);
-    int rc = wmma_flash_attn_varlen_fwd(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(), cu_q.data_ptr<int32_t>(),
+    float* lse = nullptr;
+    if (lse_out) {
+        *lse_out = torch::empty({q.size(1), q.size(0)}, q.options().dtype(torch::kFloat32));
+        lse = lse_out->data_ptr<float>();
+    }
+    int rc = wmma_flash_attn_varlen_fwd_lse(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(), lse, cu_q.data_ptr<int32_t>(),
         cu_k.data_ptr<int32_t>(), (int)(cu_q.size(0) - 1), (int)q.size(1), (int)k.size(1),
-        (int)q.size(0), (int)k.size(0), (int)max_q, (int)max_k, (int)D, sc, causal ? 1 : 0,
-        current_stream(q));
-    check_status(rc, "wmma_flash_attn_varlen_fwd");
+        (int)q.size(0), (int)k.size(0), (int)max_q, (int)max_k, (int)D, flash_scale(scale, D),
+        causal ? 1 : 0, current_stream(q));
+    check_status(rc, "wmma_flash_attn_varlen_fwd_lse");
     return O;
+}
+
+// flash_attention_varlen(q [total_q, H, D], k/v [total_k, Hkv, D], cu_seqlens_q/k int32
+// [B+1], max_seqlen_q, max_seqlen_k, causal=False, scale=-1.0) -> fp16 [total_q, H, D]
+torch::Tensor flash_attention_varlen(torch::Tensor q, torch::Tensor k, torch::Tensor v,
+                                     torch::Tensor cu_q, torch::Tensor cu_k, int64_t max_q,
+                                     int64_t max_k, bool causal, double scale) {
+    return flash_varlen_fwd(q, k, v, cu_q, cu_k, max_q, max_k, causal, scale, nullptr);
+}
+
+// flash_attention_varlen_forward(...) -> (O, lse fp32 [H, total_q])
+std::tuple<torch::Tensor, torch::Tensor> flash_attention_varlen_forward(
+    torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor cu_q, torch::Tensor cu_k,
+    int64_t max_q, int64_t max_k, bool causal, double scale) {
+    torch::Tensor lse;
+    auto O = flash_varlen_fwd(q, k, v, cu_q, cu_k, max_q, max_k, causal, scale, &lse);
+    return {O, lse};
+}
+
+// flash_attention_varlen_backward(dO, q, k, v, O, lse, cu_seqlens_q, cu_seqlens_k,
+// max_seqlen_q, max_seqlen_k, causal=False, scale=-1.0) -> (dq, dk, dv)
+std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> flash_attention_varlen_backward(
+    torch::Tensor dO, torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor O,
+    torch::Tensor lse, torch::Tensor cu_q, torch::Tensor cu_k, int64_t max_q, int64_t max_k,
+    bool causal, double scale) {
+    check_flash_varlen(q, k, v, cu_q, cu_k);
+    check_flash_grad_inputs(q, dO, O, lse, {q.size(1), q.size(0)});
+    const int64_t H = q.size(1), D = q.size(2);
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+    q = q.contiguous();
+    k = k.contiguous();
+    v = v.contiguous();
+    O = O.contiguous();
+    dO = dO.contiguous();
+    lse = lse.contiguous();
+    cu_q = cu_q.contiguous();
+    cu_k = cu_k.contiguous();
+    auto dq = torch::empty_like(q);
+    auto dk = torch::empty_like(k);
+    auto dv = torch::empty_like(v);
+    // rows outside every sequence are not written by the kernels: start from zeros
+    if (q.numel()) dq.zero_();
+    if (k.numel()) {
+        dk.zero_();
+        dv.zero_();
+    }
+    const size_t ws_bytes = wmma_flash_attn_bwd_workspace_size(1, (int)H, (int)q.size(0));
+    auto ws = torch::empty({(int64_t)(ws_bytes / 4)}, q.options().dtype(torch::kFloat32));
+    int rc = wmma_flash_attn_varlen_bwd(
+        dO.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(),
+        lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+        cu_q.data_ptr<int32_t>(), cu_k.data_ptr<int32_t>(), ws.data_ptr(), ws_bytes,
+        (int)(cu_q.size(0) - 1), (int)H, (int)k.size(1), (int)q.size(0), (int)k.size(0),
+        (int)max_q, (int)max_k, (int)D, flash_scale(scale, D), causal ? 1 : 0, current_stream(q));
+    check_status(rc, "wmma_flash_attn_varlen_bwd");
+    return {dq, dk, dv};
 }
 
 void check_qweight(const torch::Tensor& q) {
@@ -450,6 +590,23 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "Flash-attention forward on packed variable-length sequences", py::arg("q"), py::arg("k"),
           py::arg("v"), py::arg("cu_seqlens_q"), py::arg("cu_seqlens_k"), py::arg("max_seqlen_q"),
           py::arg("max_seqlen_k"), py::arg("causal") = false, py::arg("scale") = -1.0);
+    m.def("flash_attention_forward", &flash_attention_forward,
+          "Flash-attention forward for training: returns (O, lse fp32 [B, H, Sq])", py::arg("Q"),
+          py::arg("K"), py::arg("V"), py::arg("causal") = false, py::arg("scale") = -1.0);
+    m.def("flash_attention_backward", &flash_attention_backward,
+          "Flash-attention backward: (dQ, dK, dV) from dO, Q, K, V, O and lse", py::arg("dO"),
+          py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("O"), py::arg("lse"),
+          py::arg("causal") = false, py::arg("scale") = -1.0);
+    m.def("flash_attention_varlen_forward", &flash_attention_varlen_forward,
+          "Variable-length forward for training: returns (O, lse fp32 [H, total_q])", py::arg("q"),
+          py::arg("k"), py::arg("v"), py::arg("cu_seqlens_q"), py::arg("cu_seqlens_k"),
+          py::arg("max_seqlen_q"), py::arg("max_seqlen_k"), py::arg("causal") = false,
+          py::arg("scale") = -1.0);
+    m.def("flash_attention_varlen_backward", &flash_attention_varlen_backward,
+          "Variable-length backward: (dq, dk, dv)", py::arg("dO"), py::arg("q"), py::arg("k"),
+          py::arg("v"), py::arg("O"), py::arg("lse"), py::arg("cu_seqlens_q"),
+          py::arg("cu_seqlens_k"), py::arg("max_seqlen_q"), py::arg("max_seqlen_k"),
+          py::arg("causal") = false, py::arg("scale") = -1.0);
     m.def("prepack_int4", &prepack_int4, "GPTQ int4 qweight [K/8,N] -> MFMA layout", py::arg("qweight"));
     m.def("unprepack_int4", &unprepack_int4, "Inverse of prepack_int4", py::arg("packed"));
     m.def("unpack_int4", &unpack_int4, "GPTQ int4 qweight [K/8,N] -> uint8 [K,N]", py::arg("qweight"));
