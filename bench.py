@@ -23,7 +23,8 @@ Workload families (--workload):
   epilogue   configs[1]: C = 2.0*A@B + 0.5*C, out-of-place and in-place, 1024^3/4096^3
   skinny     configs[2]: M in {1,16,64,128} x N in {4096,11008,14336}, K=4096; K=14336,N=4096
   w4a16      configs[3]: M in {1,16,128,2048} x N in {4096,14336}, K=4096, G=128
-  flash      configs[4]: [4,32,4096,128], causal and non-causal; and with 8 K/V heads (GQA)
+  flash      configs[4]: [4,32,4096,128], causal and non-causal, forward and backward; with
+             8 K/V heads (GQA); a packed variable-length batch
   copy       a plain 256 MiB device copy (calibrates the rocprofv3 byte counters)
 HBM-bound cases rotate their inputs over more than 512 MB (twice the 256 MB MALL) so the
 bytes really come from HBM; microsecond-scale kernels are replayed from a HIP graph.
@@ -289,6 +290,22 @@ def fam_flash(wo):
                  TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
                  frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4),
                  max_rel_err=float(f"{err:.3e}"))
+            # backward pass (dQ, dK, dV from dO): FLOPs counted as 2.5x the forward's (the five
+            # matrix products of the gradient; the kernels also recompute S and dP once more)
+            sc = 1.0 / math.sqrt(D)
+            O, lse = wo.flash_attention_forward(Qd, Kd, Vd, causal, sc)
+            dO = torch.randn(B, H, S, D, generator=torch.Generator().manual_seed(77)).half()
+            dOd = dO.cuda()
+            msb = time_batches(lambda i: wo.flash_attention_backward(dOd, Qd, Kd, Vd, O, lse, causal, sc), 5)
+            grads = wo.flash_attention_backward(dOd, Qd, Kd, Vd, O, lse, causal, sc)
+            ref = oatt.sdpa_bwd_ref(Q[0:1, 0:g], Kt[0:1, 0:1], V[0:1, 0:1], dO[0:1, 0:g], causal, sc)
+            errb = max(og.max_rel_err(x[0:1, 0:y.shape[1]].float(), y) for x, y in zip(grads, ref))
+            flb = 2.5 * fl
+            line(family="flash_bwd", B=B, H=H, Hkv=Hkv, S=S, D=D, causal=causal,
+                 us=round(msb * 1e3, 1), TFLOPS=round(flb / (msb * 1e-3) / 1e12, 1),
+                 frac_mfma_peak=round(flb / (msb * 1e-3) / PEAK_FP16_FLOPS, 4),
+                 max_rel_err=float(f"{errb:.3e}"))
+            del O, lse, dOd, grads
         del Qd, Kd, Vd
     # packed variable-length batch (flash_attention_varlen): six ragged sequences, 16384
     # tokens, 32 query / 8 key-value heads; FLOPs counted per sequence

@@ -32,6 +32,8 @@
 //    only tiles crossing the diagonal are masked.  Heaviest workgroups are dispatched first.
 //  * Query rows past the end of a sequence load as zeros (dO = 0, Delta = 0), so they add
 //    nothing to dK, dV without a mask; key rows past the end are never stored.
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 #include "plan.hpp"
@@ -42,9 +44,17 @@ namespace {
 
 constexpr int FB_WAVES_Q = 8;             // dQ kernel: waves per workgroup (two per SIMD)
 constexpr int FB_WAVES_KV = 4;            // dK/dV kernel: one wave per SIMD (see below)
-constexpr int FB_ROWS = 32;               // queries (dQ) or keys (dK/dV) per wave
-constexpr int FB_BLOCK_Q = FB_WAVES_Q * FB_ROWS;    // queries owned by a dQ workgroup
-constexpr int FB_BLOCK_KV = FB_WAVES_KV * FB_ROWS;  // keys owned by a dK/dV workgroup
+constexpr int FB_ROWS = 32;               // queries per dQ wave
+constexpr int FB_BLOCK_Q = FB_WAVES_Q * FB_ROWS;  // queries owned by a dQ workgroup
+// dK/dV wave: KB 32-key blocks (each LDS read of Q or dO feeds KB matrix instructions).  Two
+// for D = 64; for D = 128 the resident K, V, dK and dV of two blocks (384 registers) leave
+// too few for the rest and the kernel spills.
+template <int D>
+struct FbKv {
+    static constexpr int KB = D == 64 ? 2 : 1;
+    static constexpr int ROWS = 32 * KB;              // keys per wave
+    static constexpr int BLOCK = FB_WAVES_KV * ROWS;  // keys per workgroup
+};
 constexpr int FB_T = 64;                  // rows per streamed tile
 constexpr int FB_NS = 4;                  // LDS ring depth
 constexpr float kNegInfB = -__builtin_huge_valf();
@@ -309,7 +319,8 @@ __device__ __forceinline__ void fb_store_rows(f16* base, int stride, int row, in
 
 // ---------------------------------------------------------------------------- dQ kernel --
 // One tile (64 keys) of the dQ kernel: barrier, DMA of tile t+3, then two 32-key blocks of
-// S^T, dP^T, dS^T and dQ^T += K^T dS^T.
+// S^T, dP^T, dS^T and dQ^T += K^T dS^T.  masked: the tile reaches past Sk or (causal) past
+// this wave's first query.
 template <int D, bool CAUSAL>
 __device__ __forceinline__ void fb_dq_iter(const WMMA_LDS unsigned char* __restrict__ cur,
                                            WMMA_LDS unsigned char* __restrict__ dst,
@@ -331,16 +342,23 @@ __device__ __forceinline__ void fb_dq_iter(const WMMA_LDS unsigned char* __restr
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
         // S^T, dP^T: lane%32 = query, element r = key 32 kb + 8 (r/4) + 4 h + r%4.
-        const f32x16 S = fb_rows_x_frag<D>(cur, L, kb, qf, f32x16{});
+        f32x16 S = fb_rows_x_frag<D>(cur, L, kb, qf, f32x16{});
         const f32x16 dP = fb_rows_x_frag<D>(cur + C::TILE, L, kb, dof, f32x16{});
-        // Keys at row offset 8 (r/4) + r%4 >= lim are masked (past Sk or, causal, past
-        // this lane's query).
-        const int lim = (CAUSAL ? min(Sk, qrow + 1) : Sk) - (kv0 + 32 * kb + 4 * L.h);
+        // On masked tiles only: S = -inf for keys at row offset 8 (r/4) + r%4 >= lim (past
+        // Sk or, causal, past this lane's query).  The empty asm keeps this a real
+        // (wave-uniform) branch instead of selects executed on every tile (two waves per
+        // SIMD hide the split scheduling region; peeling the masked tiles into a loop of
+        // their own, as the dK/dV kernel does, measured no faster here).
+        if (masked) {
+            asm volatile("" ::: "memory");
+            const int lim = (CAUSAL ? min(Sk, qrow + 1) : Sk) - (kv0 + 32 * kb + 4 * L.h);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) S[r] = 8 * (r >> 2) + (r & 3) < lim ? S[r] : kNegInfB;
+        }
         f16x8 dS[2];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(S[r], c, -lse2));
-            if (masked) pv = 8 * (r >> 2) + (r & 3) < lim ? pv : 0.0f;
+            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(S[r], c, -lse2));
             dS[r >> 3][r & 7] = (f16)(pv * (dP[r] - delta));
         }
 #pragma unroll
@@ -434,18 +452,56 @@ flash_bwd_dq_kernel(BwdArgs p) {
 }
 
 // ------------------------------------------------------------------------- dK/dV kernel --
-// One tile (64 queries of one query head) of the dK/dV kernel.
-template <int D, bool CAUSAL>
+// acc[kb] += A B_kb^T over all d steps for KB register fragment sets: each row-wise LDS read
+// of A (32 rows of block `rb`) feeds KB matrix instructions.
+template <int D, int W, int KB>
+__device__ __forceinline__ void fb_rows_x_frags(const WMMA_LDS unsigned char* tile,
+                                                const FbLane<D, W>& L, int rb,
+                                                const f16x8 (&f)[KB][FbDim<D>::NDS],
+                                                f32x16 (&acc)[KB]) {
+    const WMMA_LDS unsigned char* base = tile + rb * 32 * FbDim<D>::RB + L.row_addr;
+#pragma unroll
+    for (int ds = 0; ds < FbDim<D>::NDS; ++ds) {
+        const int c = (2 * ds + L.h) ^ L.row_sw;
+        const f16x8 a = as_f16x8(*(const WMMA_LDS u32x4*)(base + (c << 4)));
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) acc[kb] = mfma32(a, f[kb][ds], acc[kb]);
+    }
+}
+
+// acc[kb][db] += T^T B_kb over the 16-row step `step` of tile T: each transposing read feeds
+// KB matrix instructions.
+template <int D, int W, int KB>
+__device__ __forceinline__ void fb_tr_x_multi(const WMMA_LDS unsigned char* tile,
+                                              const FbLane<D, W>& L, int step, const f16x8 (&b)[KB],
+                                              f32x16 (&acc)[KB][FbDim<D>::NDB]) {
+    const int off = 16 * step * FbDim<D>::RB;
+#pragma unroll
+    for (int db = 0; db < FbDim<D>::NDB; ++db) {
+        const f16x4 lo = lds_read_tr16(tile + fb_tr_addr<D, W>(L, db, false) + off);
+        const f16x4 hi = lds_read_tr16(tile + fb_tr_addr<D, W>(L, db, true) + off);
+        const f16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) acc[kb][db] = mfma32(a, b[kb], acc[kb][db]);
+    }
+}
+
+// One tile (64 queries of one query head) of the dK/dV kernel; the wave owns KB 32-key
+// blocks starting at key `key0` (this lane: key0 + 32 kb + lane%32).  MASK (causal tiles
+// that cross the workgroup's diagonal): zero P where key > query.  A compile-time choice: the
+// diagonal tiles run in a loop of their own, so the main loop body is one branch-free block
+// the scheduler can interleave across its two query blocks.
+template <int D, bool MASK>
 __device__ __forceinline__ void fb_kv_iter(const WMMA_LDS unsigned char* __restrict__ cur,
                                            WMMA_LDS unsigned char* __restrict__ dst,
                                            const FbLane<D, FB_WAVES_KV>& L, int wave,
                                            __amdgpu_buffer_rsrc_t rq, __amdgpu_buffer_rsrc_t rdo,
                                            __amdgpu_buffer_rsrc_t rst, int qleft_dma,
-                                           const f16x8 (&kf)[FbCfg<D, FB_WAVES_KV>::NDS],
-                                           const f16x8 (&vf)[FbCfg<D, FB_WAVES_KV>::NDS],
-                                           f32x16 (&dk)[FbCfg<D, FB_WAVES_KV>::NDB],
-                                           f32x16 (&dv)[FbCfg<D, FB_WAVES_KV>::NDB], float c, int q0,
-                                           int key, bool live, bool masked) {
+                                           const f16x8 (&kf)[FbKv<D>::KB][FbDim<D>::NDS],
+                                           const f16x8 (&vf)[FbKv<D>::KB][FbDim<D>::NDS],
+                                           f32x16 (&dk)[FbKv<D>::KB][FbDim<D>::NDB],
+                                           f32x16 (&dv)[FbKv<D>::KB][FbDim<D>::NDB], float c, int q0,
+                                           int key0) {
     using C = FbCfg<D, FB_WAVES_KV>;
     __builtin_amdgcn_s_waitcnt(0xC07F);
     wait_vmcnt<(FB_NS - 2) * C::PER_STAGE_KV>();
@@ -458,47 +514,66 @@ __device__ __forceinline__ void fb_kv_iter(const WMMA_LDS unsigned char* __restr
         lds_dma4(rst, wave < 2 && lane < qleft_dma ? (uint32_t)(4 * lane) : kOobOffset,
                  dst + 2 * C::TILE + wave * C::STAT);
     }
-    if (!live) return;
+    // No early exit for tiles wholly before this wave's keys: they take the masked path
+    // (all of P is zero).  A skip would give the loop two paths that the register allocator
+    // joins by moving the dK/dV accumulators between register files.
     const WMMA_LDS unsigned char* st = cur + 2 * C::TILE;
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
         // Accumulators start at -L/scale and -Delta of their query rows 32 qb + 8 g + 4 h + 0..3:
         // S = Q K^T - L/scale, dP = dO V^T - Delta, lane%32 = key, element r = query
         // 32 qb + 8 (r/4) + 4 h + r%4.
-        f32x16 S;
+        f32x16 S[FbKv<D>::KB];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const f32x4 l4 = *(const WMMA_LDS f32x4*)(st + 4 * (32 * qb + 8 * g + 4 * L.h));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) S[4 * g + e] = l4[e];
-        }
-        S = fb_rows_x_frag<D>(cur, L, qb, kf, S);
-        // P = exp2(c S) (in place); causal: zero where key > query, i.e. where the row
-        // offset 8 (r/4) + r%4 is below `lim`.
-        const int lim = key - (q0 + 32 * qb + 4 * L.h);
-        f16x8 P[2];
+            for (int kb = 0; kb < FbKv<D>::KB; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            float pv = __builtin_amdgcn_exp2f(S[r] * c);
-            if (CAUSAL && masked) pv = 8 * (r >> 2) + (r & 3) >= lim ? pv : 0.0f;
-            S[r] = pv;
-            P[r >> 3][r & 7] = (f16)pv;
+                for (int e = 0; e < 4; ++e) S[kb][4 * g + e] = l4[e];
         }
-        f32x16 dP;
+        // Diagonal tiles: S starts at -inf (and stays there) where key > query, i.e. where
+        // the row offset 8 (r/4) + r%4 is below `lim` (a no-op for waves whose keys all
+        // precede the tile's queries).
+        if (MASK) {
+#pragma unroll
+            for (int kb = 0; kb < FbKv<D>::KB; ++kb) {
+                const int lim = key0 + 32 * kb - (q0 + 32 * qb + 4 * L.h);
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    S[kb][r] = 8 * (r >> 2) + (r & 3) >= lim ? S[kb][r] : kNegInfB;
+            }
+        }
+        fb_rows_x_frags<D, FB_WAVES_KV, FbKv<D>::KB>(cur, L, qb, kf, S);
+        // P = exp2(c S) (in place)
+        f16x8 P[2][FbKv<D>::KB];
+#pragma unroll
+        for (int kb = 0; kb < FbKv<D>::KB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float pv = __builtin_amdgcn_exp2f(S[kb][r] * c);
+                S[kb][r] = pv;
+                P[r >> 3][kb][r & 7] = (f16)pv;
+            }
+        f32x16 dP[FbKv<D>::KB];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const f32x4 d4 = *(const WMMA_LDS f32x4*)(st + C::STAT + 4 * (32 * qb + 8 * g + 4 * L.h));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) dP[4 * g + e] = d4[e];
-        }
-        dP = fb_rows_x_frag<D>(cur + C::TILE, L, qb, vf, dP);
-        f16x8 dS[2];
+            for (int kb = 0; kb < FbKv<D>::KB; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) dS[r >> 3][r & 7] = (f16)(S[r] * dP[r]);
+                for (int e = 0; e < 4; ++e) dP[kb][4 * g + e] = d4[e];
+        }
+        fb_rows_x_frags<D, FB_WAVES_KV, FbKv<D>::KB>(cur + C::TILE, L, qb, vf, dP);
+        f16x8 dS[2][FbKv<D>::KB];
+#pragma unroll
+        for (int kb = 0; kb < FbKv<D>::KB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) dS[r >> 3][kb][r & 7] = (f16)(S[kb][r] * dP[kb][r]);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-            fb_tr_x<D>(cur + C::TILE, L, 2 * qb + hh, P[hh], dv);
-            fb_tr_x<D>(cur, L, 2 * qb + hh, dS[hh], dk);
+            fb_tr_x_multi<D, FB_WAVES_KV, FbKv<D>::KB>(cur + C::TILE, L, 2 * qb + hh, P[hh], dv);
+            fb_tr_x_multi<D, FB_WAVES_KV, FbKv<D>::KB>(cur, L, 2 * qb + hh, dS[hh], dk);
         }
     }
 }
@@ -516,16 +591,18 @@ flash_bwd_dkdv_kernel(BwdArgs p) {
     const int h = lane >> 5, c32 = lane & 31;
     const int bkv = blockIdx.x;
     const int b = bkv / p.Hkv, j = bkv % p.Hkv;
-    const int k0 = (int)blockIdx.y * FB_BLOCK_KV;  // causal: lower key blocks are heavier, and first
-    const int kw = k0 + wave * FB_ROWS;
+    const int k0 = (int)blockIdx.y * FbKv<D>::BLOCK;  // causal: lower key blocks are heavier, and first
+    const int kw = k0 + wave * FbKv<D>::ROWS;
     const SeqGeo G0 = seq_geo<D>(p, b, j * p.group);
     if (k0 >= G0.Sk) return;
     const int Sq = G0.Sq, Sk = G0.Sk;
-    const int key = kw + c32;
 
-    f16x8 kf[C::NDS], vf[C::NDS];
-    fb_load_frag<D>(p.K + G0.k_base, G0.ks, key, Sk, h, kf);
-    fb_load_frag<D>(p.V + G0.k_base, G0.ks, key, Sk, h, vf);
+    f16x8 kf[FbKv<D>::KB][C::NDS], vf[FbKv<D>::KB][C::NDS];
+#pragma unroll
+    for (int kb = 0; kb < FbKv<D>::KB; ++kb) {
+        fb_load_frag<D>(p.K + G0.k_base, G0.ks, kw + 32 * kb + c32, Sk, h, kf[kb]);
+        fb_load_frag<D>(p.V + G0.k_base, G0.ks, kw + 32 * kb + c32, Sk, h, vf[kb]);
+    }
 
     FbLane<D, FB_WAVES_KV> L;
     fb_lane_init<D>(L, wave, lane, G0.qs);
@@ -548,12 +625,14 @@ flash_bwd_dkdv_kernel(BwdArgs p) {
     };
     auto qleft = [&](int u, int t) { return u < U ? Sq - t * FB_T : 0; };
 
-    f32x16 dk[C::NDB], dv[C::NDB];
+    f32x16 dk[FbKv<D>::KB][C::NDB], dv[FbKv<D>::KB][C::NDB];
 #pragma unroll
-    for (int db = 0; db < C::NDB; ++db) {
-        dk[db] = f32x16{};
-        dv[db] = f32x16{};
-    }
+    for (int kb = 0; kb < FbKv<D>::KB; ++kb)
+#pragma unroll
+        for (int db = 0; db < C::NDB; ++db) {
+            dk[kb][db] = f32x16{};
+            dv[kb][db] = f32x16{};
+        }
     const float c = p.c;
 
     if (U > 0) {
@@ -570,31 +649,39 @@ flash_bwd_dkdv_kernel(BwdArgs p) {
         };
 #pragma unroll
         for (int s = 0; s < FB_NS - 1; ++s) issue(lds + s * C::STAGE_KV, s);
-        for (int u = 0; u < U; ++u) {
+        auto step = [&](auto mask_tag, int u) {
             const int uf = u + FB_NS - 1;
             int gi, t, gf, tf;
             tile_of(u, gi, t);
             tile_of(uf, gf, tf);
-            const int q0 = t * FB_T;
             const int64_t qoff = G0.q_base + gf * qh + (int64_t)tf * FB_T * G0.qs;
-            const bool live = !CAUSAL || q0 + FB_T - 1 >= kw;
-            const bool masked = CAUSAL && q0 < kw + FB_ROWS - 1;
-            fb_kv_iter<D, CAUSAL>(lds + (u % FB_NS) * C::STAGE_KV, lds + (uf % FB_NS) * C::STAGE_KV,
-                                  L, wave, make_rsrc(p.Q + qoff), make_rsrc(p.dO + qoff),
-                                  make_rsrc(st_src + G0.r_base + gf * rh + (int64_t)tf * FB_T),
-                                  qleft(uf, tf), kf, vf, dk, dv, c, q0, key, live, masked);
+            fb_kv_iter<D, decltype(mask_tag)::value>(
+                lds + (u % FB_NS) * C::STAGE_KV, lds + (uf % FB_NS) * C::STAGE_KV, L, wave,
+                make_rsrc(p.Q + qoff), make_rsrc(p.dO + qoff),
+                make_rsrc(st_src + G0.r_base + gf * rh + (int64_t)tf * FB_T), qleft(uf, tf), kf, vf,
+                dk, dv, c, t * FB_T, kw + c32);
+        };
+        // Causal: the first BLOCK/64 tiles of each query head hold queries below the
+        // workgroup's last key (k0 is a multiple of the tile, so exactly these).
+        const int nmask = CAUSAL ? min(nT, FbKv<D>::BLOCK / FB_T) : 0;
+        for (int gi = 0, u = 0; gi < p.group; ++gi) {
+            for (const int e = u + nmask; u < e; ++u) step(std::true_type{}, u);
+            for (const int e = (gi + 1) * nT; u < e; ++u) step(std::false_type{}, u);
         }
         wait_vmcnt<0>();
     }
-    fb_store_rows<D>(p.dK + G0.k_base, G0.ks, key, Sk, h, dk, p.scale);
-    fb_store_rows<D>(p.dV + G0.k_base, G0.ks, key, Sk, h, dv, 1.0f);
+#pragma unroll
+    for (int kb = 0; kb < FbKv<D>::KB; ++kb) {
+        fb_store_rows<D>(p.dK + G0.k_base, G0.ks, kw + 32 * kb + c32, Sk, h, dk[kb], p.scale);
+        fb_store_rows<D>(p.dV + G0.k_base, G0.ks, kw + 32 * kb + c32, Sk, h, dv[kb], 1.0f);
+    }
 }
 
 template <int D>
 void launch_bwd_d(const BwdArgs& a, int B, bool causal, hipStream_t stream) {
     const dim3 bq(FB_WAVES_Q * kWave), bk(FB_WAVES_KV * kWave);
     const dim3 gq(B * a.H, a.nqb);
-    const dim3 gk(B * a.Hkv, ceil_div(a.Sk, FB_BLOCK_KV));
+    const dim3 gk(B * a.Hkv, ceil_div(a.Sk, FbKv<D>::BLOCK));
     // The dQ kernel writes the row statistics the dK/dV kernel reads: same stream, in order.
     // An empty side (no query or no key rows) launches nothing for it; with no query rows
     // the dK/dV kernel still runs and stores zeros.
