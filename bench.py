@@ -307,6 +307,19 @@ def fam_flash(wo):
                  max_rel_err=float(f"{errb:.3e}"))
             del O, lse, dOd, grads
         del Qd, Kd, Vd
+    # CPU baseline: fp32 SDPA on the host cores (forward, and forward + autograd backward)
+    # over a bounded sample of (batch, head) slices of the same workload
+    threads = cpu_threads()
+    Q, Kt, V = oatt.make_inputs(1, 2, S, D, seed=42 + 4)
+    dO = torch.randn(1, 2, S, D, generator=torch.Generator().manual_seed(77)).half()
+    for causal in (False, True):
+        t, n = cpu_time(lambda: oatt.sdpa_ref(Q, Kt, V, causal), 3.0, 10)
+        tb, nb = cpu_time(lambda: oatt.sdpa_bwd_ref(Q, Kt, V, dO, causal), 3.0, 10)
+        fl = 4.0 * 2 * S * S * D if not causal else 4.0 * 2 * D * S * (S + 1) / 2
+        line(family="flash_cpu", S=S, D=D, causal=causal, cores=threads, cpu_model=cpu_model(),
+             fwd_TFLOPS=round(fl / t / 1e12, 4), bwd_TFLOPS=round(2.5 * fl / tb / 1e12, 4),
+             sample=f"2 heads of [1,2,{S},{D}]: sdpa_ref {n} calls, median {t * 1e3:.0f} ms; "
+                    f"sdpa_bwd_ref {nb} calls, median {tb * 1e3:.0f} ms")
     # packed variable-length batch (flash_attention_varlen): six ragged sequences, 16384
     # tokens, 32 query / 8 key-value heads; FLOPs counted per sequence
     lens = [1024, 3072, 2048, 4096, 512, 5632]
@@ -380,31 +393,71 @@ def gemm_bench(wo, steps, warmup):
     return ms_step, ms_kernel, err
 
 
-def cpu_baseline(seconds):
-    """The oracle's fp32 torch.matmul on host cores, on a bounded sample of 4096^3 calls."""
-    import torch
+def cpu_model() -> str:
+    """The host CPU's model name (what lscpu prints), read from /proc/cpuinfo."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    from oracle import gemm as og
+
+def cpu_threads() -> int:
+    """Host threads for the CPU baselines: the process's CPUs, at most 16 (the GPU box's
+    share of one GPU)."""
+    import torch
 
     threads = min(16, len(os.sched_getaffinity(0)))
     torch.set_num_threads(threads)
-    g = torch.Generator().manual_seed(42 + 1)
-    A = torch.randn(M, K, generator=g).half()
-    B = torch.randn(K, N, generator=g).half()
-    og.gemm_ref(A, B)  # warm-up
+    return threads
+
+
+def cpu_time(fn, seconds, max_calls=50):
+    """Median wall time (s) of fn() after one warm-up, over at least 3 calls and about
+    `seconds` of work."""
+    fn()
     times = []
     t_end = time.perf_counter() + seconds
     while time.perf_counter() < t_end or len(times) < 3:
         t0 = time.perf_counter()
-        og.gemm_ref(A, B)
+        fn()
         times.append(time.perf_counter() - t0)
-        if len(times) >= 50:
+        if len(times) >= max_calls:
             break
-    t = statistics.median(times)
-    return {"value": round(2.0 * M * N * K / t / 1e12, 4), "unit": "TFLOPS", "cores": threads,
-            "kind": "port",
-            "sample": f"{len(times)} calls of torch.matmul(A.float(), B.float()) at 4096^3 "
-                      f"(oracle.gemm.gemm_ref), median {t * 1e3:.1f} ms"}
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline(seconds):
+    """The oracle on host cores, bounded samples of the headline workloads: fp32
+    torch.matmul at 4096^3, and the W4A16 M = 1 decode (GPTQ unpack, fp16((q - z) * s)
+    dequantisation and matmul, N = 14336)."""
+    import torch
+
+    from oracle import gemm as og
+    from oracle import int4 as oi
+
+    threads = cpu_threads()
+    g = torch.Generator().manual_seed(42 + 1)
+    A = torch.randn(M, K, generator=g).half()
+    B = torch.randn(K, N, generator=g).half()
+    t, n = cpu_time(lambda: og.gemm_ref(A, B), seconds)
+    out = {"value": round(2.0 * M * N * K / t / 1e12, 4), "unit": "TFLOPS", "cores": threads,
+           "kind": "port",
+           "sample": f"{n} calls of torch.matmul(A.float(), B.float()) at 4096^3 "
+                     f"(oracle.gemm.gemm_ref), median {t * 1e3:.1f} ms",
+           "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count()}
+    # W4A16 decode: the time includes unpacking the packed GPTQ words and the dequantisation
+    Aq, q, sc, z = oi.make_inputs(1, 4096, 14336, 128, seed=42 + 3)
+    qw = oi.pack_gptq(q)
+    nbytes = 4096 * 14336 // 2 + (4096 // 128) * 14336 * 2 + (4096 // 128) * 14336 // 2 + 2 * 4096 + 4 * 14336
+    tw, nw = cpu_time(lambda: oi.w4a16_ref(Aq, oi.unpack_gptq(qw), sc, z, 128), seconds / 4, 10)
+    out["w4a16_m1"] = {"value": round(nbytes / tw / 1e9, 3), "unit": "GB/s", "cores": threads,
+                       "sample": f"{nw} calls of unpack_gptq + dequant + matmul at M=1, N=14336, "
+                                 f"K=4096, G=128 (oracle.int4), median {tw * 1e3:.1f} ms"}
+    return out
 
 
 def headline(wo, args):
