@@ -63,11 +63,16 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--workload", choices=sorted(FAMILIES), help="one config family")
     ap.add_argument("--suite", action="store_true", help="every config family")
+    ap.add_argument("--quick", action="store_true",
+                    help="with --workload/--suite: two calls per case, no settle phase and no "
+                         "graph capture -- for rocprofv3 counter passes; its times are not "
+                         "the benchmark")
     return ap.parse_args()
 
 
 # ---------------------------------------------------------------------------- timing --
 SETTLE_MS = 100.0  # sustained load before any timing: the GPU's clock ramps up over ~50 ms
+QUICK = False      # --quick: few launches per case (counter collection), see parse()
 
 
 def settle(fn, ms=SETTLE_MS):
@@ -75,6 +80,8 @@ def settle(fn, ms=SETTLE_MS):
     that follow see the clock a sustained workload runs at, not the idle one."""
     import torch
 
+    if QUICK:
+        return
     spent, i = 0.0, 0
     while spent < ms:
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -92,6 +99,8 @@ def time_batches(fn, calls, batches=5):
     in ms.  fn(i) runs call i (so inputs can rotate)."""
     import torch
 
+    if QUICK:
+        calls, batches = min(calls, 2), 1
     settle(fn)
     torch.cuda.synchronize()
     out = []
@@ -111,6 +120,8 @@ def time_graph(fn, copies, batches=5):
     replayed `batches` times (median); returns (ms, outputs of the captured calls)."""
     import torch
 
+    if QUICK:  # no capture: counter passes see plain launches
+        return time_batches(fn, 2), [fn(0)]
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
@@ -309,17 +320,18 @@ def fam_flash(wo):
         del Qd, Kd, Vd
     # CPU baseline: fp32 SDPA on the host cores (forward, and forward + autograd backward)
     # over a bounded sample of (batch, head) slices of the same workload
-    threads = cpu_threads()
-    Q, Kt, V = oatt.make_inputs(1, 2, S, D, seed=42 + 4)
-    dO = torch.randn(1, 2, S, D, generator=torch.Generator().manual_seed(77)).half()
-    for causal in (False, True):
-        t, n = cpu_time(lambda: oatt.sdpa_ref(Q, Kt, V, causal), 3.0, 10)
-        tb, nb = cpu_time(lambda: oatt.sdpa_bwd_ref(Q, Kt, V, dO, causal), 3.0, 10)
-        fl = 4.0 * 2 * S * S * D if not causal else 4.0 * 2 * D * S * (S + 1) / 2
-        line(family="flash_cpu", S=S, D=D, causal=causal, cores=threads, cpu_model=cpu_model(),
-             fwd_TFLOPS=round(fl / t / 1e12, 4), bwd_TFLOPS=round(2.5 * fl / tb / 1e12, 4),
-             sample=f"2 heads of [1,2,{S},{D}]: sdpa_ref {n} calls, median {t * 1e3:.0f} ms; "
-                    f"sdpa_bwd_ref {nb} calls, median {tb * 1e3:.0f} ms")
+    if not QUICK:
+        threads = cpu_threads()
+        Q, Kt, V = oatt.make_inputs(1, 2, S, D, seed=42 + 4)
+        dO = torch.randn(1, 2, S, D, generator=torch.Generator().manual_seed(77)).half()
+        for causal in (False, True):
+            t, n = cpu_time(lambda: oatt.sdpa_ref(Q, Kt, V, causal), 3.0, 10)
+            tb, nb = cpu_time(lambda: oatt.sdpa_bwd_ref(Q, Kt, V, dO, causal), 3.0, 10)
+            fl = 4.0 * 2 * S * S * D if not causal else 4.0 * 2 * D * S * (S + 1) / 2
+            line(family="flash_cpu", S=S, D=D, causal=causal, cores=threads, cpu_model=cpu_model(),
+                 fwd_TFLOPS=round(fl / t / 1e12, 4), bwd_TFLOPS=round(2.5 * fl / tb / 1e12, 4),
+                 sample=f"2 heads of [1,2,{S},{D}]: sdpa_ref {n} calls, median {t * 1e3:.0f} ms; "
+                        f"sdpa_bwd_ref {nb} calls, median {tb * 1e3:.0f} ms")
     # packed variable-length batch (flash_attention_varlen): six ragged sequences, 16384
     # tokens, 32 query / 8 key-value heads; FLOPs counted per sequence
     lens = [1024, 3072, 2048, 4096, 512, 5632]
@@ -512,6 +524,8 @@ def main():
     import wmma_ops_amd as wo
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    global QUICK
+    QUICK = args.quick and bool(args.suite or args.workload)
     if args.suite:
         for name in ("gemm", "epilogue", "skinny", "w4a16", "flash"):
             FAMILIES[name](wo)
