@@ -163,3 +163,25 @@ def test_flash_errors(wo):
     cu = torch.tensor([0, 8], dtype=torch.int64, device="cuda")
     with pytest.raises(RuntimeError, match="cu_seqlens must be int32"):
         wo.flash_attention_varlen(p, p, p, cu, cu, 8, 8)
+
+
+# More work items (batch*head x 256-query blocks) than CUs, so several waves of workgroups
+# share each CU: ragged lengths, Sq != Sk, grouped-query heads, and query blocks with fewer
+# key tiles than the 4-deep ring (Sk = 100: two key tiles).
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,H,Hkv,Sq,Sk,D", [(2, 64, 64, 1000, 1000, 128), (4, 64, 16, 700, 300, 64),
+                                             (1, 300, 300, 256, 100, 128), (8, 40, 8, 513, 513, 64)])
+def test_flash_many_items(wo, causal, B, H, Hkv, Sq, Sk, D):
+    report("flash_many_items", B=B, H=H, Hkv=Hkv, Sq=Sq, Sk=Sk, D=D, causal=causal)
+    Q, K, V = oatt.make_inputs(B, H, Sq, D, seed=B * H + Sq + Sk, Sk=Sk, Hkv=Hkv)
+    O, lse = wo.flash_attention_forward(Q.cuda(), K.cuda(), V.cuda(), causal)
+    assert torch.isfinite(O).all()
+    g = H // Hkv
+    for b, h in [(0, 0), (B - 1, H - 1), (B // 2, H // 2), (0, H - 1)]:
+        j = h // g
+        ref = oatt.sdpa_ref(Q[b:b + 1, h:h + 1], K[b:b + 1, j:j + 1], V[b:b + 1, j:j + 1], causal)
+        _check(O[b:b + 1, h:h + 1], ref)
+        lref = oatt.lse_ref(Q[b:b + 1, h:h + 1], K[b:b + 1, j:j + 1], causal)
+        assert torch.allclose(lse[b:b + 1, h:h + 1].cpu(), lref, atol=1e-4, rtol=1e-5)
+    # the inference entry point computes the same bits
+    assert torch.equal(O, wo.flash_attention(Q.cuda(), K.cuda(), V.cuda(), causal))
