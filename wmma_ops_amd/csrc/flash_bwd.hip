@@ -14,8 +14,9 @@
 //    K^T read by the transposing ds_read_b64_tr_b16.  It also computes Delta from its own
 //    dO and O fragments and writes Delta and L / scale (the log-sum-exp in raw-score units)
 //    to the workspace for the second kernel.
-//  * dK/dV kernel: a workgroup owns 256 keys of one (batch, key/value head), 8 waves x 32
-//    keys, with the wave's K and V fragments in registers and dK^T, dV^T accumulated in
+//  * dK/dV kernel: a workgroup owns the keys of one (batch, key/value head) -- 4 waves, one
+//    per SIMD with the whole 512-register file, x 64 keys for D = 64 and x 32 keys for
+//    D = 128 -- with the wave's K and V fragments in registers and dK^T, dV^T accumulated in
 //    registers.  It streams 64-query tiles of Q, dO and the two row statistics through the
 //    LDS ring -- for grouped-query attention, the tiles of every query head of the group in
 //    turn, which makes dK and dV the sum over the group without a second pass.  Per 32-query
