@@ -334,6 +334,31 @@ gemm_mfma_kernel(GemmArgs p) {
                     const int row = row0 + i * 32 + 8 * (r >> 2) + (r & 3);
                     out[(int64_t)row * ldo + col0 + j * 32] = alpha * acc[i][j][r];
                 }
+    } else if (full_tile) {
+        // beta * C_in on a full tile: the C_in reads of 32x32 block b+1 are issued before
+        // the stores of block b, so the reads stream instead of waiting one block at a time.
+        // In place (C_in == C_out) this is still exact: every element is read by the lane
+        // that writes it, and the blocks' addresses are disjoint.
+        const float beta = p.beta;
+        const float* cin = p.Cin + (int64_t)row0 * p.ldcin + col0;
+        float* o = out + (int64_t)row0 * ldo + col0;
+        constexpr int NB = FM * FN;
+        float cv[2][16];
+        auto load_c = [&](int b, float* c) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                c[r] = cin[(int64_t)((b / FN) * 32 + 8 * (r >> 2) + (r & 3)) * p.ldcin + (b % FN) * 32];
+        };
+        load_c(0, cv[0]);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            if (b + 1 < NB) load_c(b + 1, cv[(b + 1) & 1]);
+            const int i = b / FN, j = b % FN;
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                o[(int64_t)(i * 32 + 8 * (r >> 2) + (r & 3)) * ldo + j * 32] =
+                    alpha * acc[i][j][r] + beta * cv[b & 1][r];
+        }
     } else {
         const float beta = p.beta;
 #pragma unroll
