@@ -113,6 +113,31 @@ def _capi():
     return lib
 
 
+
+# Row strides of C_in and C_out larger than N and different from each other: the epilogue
+# reads C_in at its own stride, writes only the N columns of each output row, and leaves
+# the padding of both buffers alone (512x512 takes full 256x256 tiles, 300x264 ragged ones).
+@pytest.mark.parametrize("M,N,K,tile", [(512, 512, 1024, 5), (300, 264, 640, -1)])
+def test_gemm_strided_c(wo, M, N, K, tile):
+    report("gemm_strided_c", M=M, N=N, K=K, tile=tile)
+    lib = _capi()
+    A, B = _inputs(M, N, K, 31 + M)
+    ldcin, ldc = N + 40, N + 72
+    g = torch.Generator().manual_seed(32)
+    Cin = torch.randn(M, ldcin, generator=g)
+    Cout = torch.full((M, ldc), 7.0)
+    Ad, Bd, Cid, Cod = A.cuda(), B.cuda(), Cin.cuda(), Cout.cuda()
+    nws = lib.wmma_gemm_workspace_size(M, N, K, tile)
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda")
+    rc = lib.wmma_gemm_f16f32(Ad.data_ptr(), K, Bd.data_ptr(), N, Cid.data_ptr(), ldcin,
+                              Cod.data_ptr(), ldc, M, N, K, 2.0, 0.5, tile, ws.data_ptr(), nws,
+                              torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    out = Cod.cpu()
+    _check(out[:, :N].contiguous(), og.gemm_ref(A, B, 2.0, 0.5, Cin[:, :N].contiguous()))
+    assert torch.equal(out[:, N:], Cout[:, N:])
+    assert torch.equal(Cid.cpu(), Cin)
+
 # Split-K partials go through a caller workspace whose contents are arbitrary: a workspace
 # of random bytes, the same workspace again and re-randomised must all give the same bits
 # (fixed summation order), within tolerance of the oracle, and so must the in-place
