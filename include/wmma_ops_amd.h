@@ -148,7 +148,7 @@ size_t wmma_w4a16_workspace_size(int M, int N, int K, int group_size);
 #define WMMA_W4_KERNEL_DECODE 1       /* M <= 4, other group sizes: VALU dot products      */
 #define WMMA_W4_KERNEL_GEMV_SPLIT 2   /* M <= 4, narrow N: 32 columns per workgroup, split-K */
 #define WMMA_W4_KERNEL_MFMA 3         /* other shapes: tiled MFMA kernel                     */
-#define WMMA_W4_KERNEL_SKINNY 4       /* 4 < M <= 32: 32 columns per workgroup, matrix pipe */
+#define WMMA_W4_KERNEL_SKINNY 4       /* 4 < M <= 32: 32/64 columns per workgroup, matrix pipe */
 #define WMMA_W4_KERNEL_GEMM 5         /* M > 32: LDS-DMA MFMA GEMM                           */
 
 typedef struct wmma_w4a16_plan {

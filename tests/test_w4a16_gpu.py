@@ -72,12 +72,17 @@ def test_w4a16_group_sizes_and_u8_zeros(wo, M, K, N, G):
 # The 4 < M <= 32 matrix-pipe kernel: one and two 16-row blocks, K split over workgroups
 # (N=1024, N=352; and N=4096 for M > 16), a ragged last split (K=4224: 33 pair-steps), G=256,
 # a tile count that is not a multiple of the XCD count (N=352), lda > K, both zero formats.
+# N=8192 (M <= 16, with a 2-way K split) and N=12288 (all M) take two 32-column tiles per
+# workgroup on a 256-CU device.
 @pytest.mark.parametrize("M", [5, 8, 16, 17, 31, 32])
-@pytest.mark.parametrize("K,N,G", [(4096, 4096, 128), (4224, 1024, 128), (1536, 352, 256)])
+@pytest.mark.parametrize("K,N,G", [(4096, 4096, 128), (4224, 1024, 128), (1536, 352, 256),
+                                   (8192, 8192, 128), (4096, 12288, 256)])
 def test_w4a16_skinny(wo, M, K, N, G):
     plan = wo.w4a16_plan(M, N, K, G)
     report("w4a16_skinny", M=M, K=K, N=N, G=G, plan=plan)
     assert plan[0] == 4
+    if N == 8192 and M <= 16:
+        assert plan[1] == 2
     A, q, s, z = oi.make_inputs(M, K, N, G, seed=7 * M + K + N)
     ref = oi.w4a16_ref(A, q, s, z, G)
     pk = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
@@ -168,7 +173,8 @@ def test_prepack_params_bit_exact(wo):
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 16, 17, 32, 33, 128, 300])
-@pytest.mark.parametrize("K,N,G", [(4096, 1024, 128), (1024, 352, 64), (2048, 160, 256), (512, 96, 32)])
+@pytest.mark.parametrize("K,N,G", [(4096, 1024, 128), (1024, 352, 64), (2048, 160, 256), (512, 96, 32),
+                                   (2048, 12288, 128)])
 def test_w4a16_sliced_params_same_bits(wo, M, K, N, G):
     report("w4a16_sliced", M=M, K=K, N=N, G=G)
     A, q, s, z = oi.make_inputs(M, K, N, G, seed=M * 7 + N + G)

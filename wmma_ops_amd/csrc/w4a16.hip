@@ -813,30 +813,35 @@ void launch_decode_mfma(const W4Args& a, int M, dim3 grid, dim3 block, size_t ld
 //    range is split over blockIdx.y (SK_NW * SK_U pair-steps per split) and the partials
 //    go to the workspace for w4a16_reduce_kernel.
 // The B operand is the decode kernel's: W = fp16((q - z) s) rounded once per weight.
-// D layout per 16-row block b and half sc: lane l holds column 32*nt + 16*sc + l%16 and
-// rows 16*b + 4*(l/16) + r.
+//  * NT = 2 puts two adjacent 32-column tiles in one workgroup: every activation fragment
+//    feeds four MFMAs and the activation bytes a CU reads per weight byte halve (at
+//    M = 16 they are twice the weight bytes of a one-tile workgroup).
+// D layout per 16-row block b and 16-column half sc (0 .. 2*NT-1): lane l holds column
+// 32*NT*wg + 16*sc + l%16 and rows 16*b + 4*(l/16) + r.
 constexpr int SK_NW = 8;
 
-template <int ZF, int MB, int U>
+template <int ZF, int MB, int U, int NT>
 __global__ void __launch_bounds__(SK_NW * kWave)
 w4a16_skinny_kernel(W4Args p) {
-    __shared__ float red[SK_NW][MB * 16][33];
+    constexpr int NH = 2 * NT;  // 16-column halves per workgroup
+    __shared__ float red[SK_NW][MB * 16][32 * NT + 1];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nt = xcd_remap(blockIdx.x, gridDim.x);
+    const int wg = xcd_remap(blockIdx.x, gridDim.x);
+    const int n0 = 32 * NT * wg;  // first column of the workgroup
     const int col = lane & 15, sub = lane >> 4, dc = sub >> 1, h = sub & 1;
     const int K = p.K, M = p.M, KC = K / 64, KP = KC / 2;
     const int kp0 = blockIdx.y * (SK_NW * U);
 
-    // Group parameters: lane l fetches pair-step min(l/16, U-1) of this wave for both
-    // 16-column halves; a lane shuffle later hands each lane its own.
-    uint32_t sraw[2], zraw[2];
+    // Group parameters: lane l fetches pair-step min(l/16, U-1) of this wave for every
+    // 16-column half; a lane shuffle later hands each lane its own.
+    uint32_t sraw[NH], zraw[NH];
     {
         const int ppl = min(kp0 + wave + SK_NW * min(sub, U - 1), KP - 1);
         const int g = ppl >> p.pp_shift;  // G = 128 << pp_shift
 #pragma unroll
-        for (int sc = 0; sc < 2; ++sc) {
-            const int n = 32 * nt + 16 * sc + col;
+        for (int sc = 0; sc < NH; ++sc) {
+            const int n = n0 + 16 * sc + col;
             sraw[sc] = __builtin_bit_cast(uint16_t, p.S[s_index<ZF>(p, g, n)]);
             if constexpr (ZF != WMMA_ZEROS_U8)
                 zraw[sc] = (uint32_t)static_cast<const int32_t*>(p.Z)[z_index<ZF>(p, g, n)];
@@ -845,8 +850,8 @@ w4a16_skinny_kernel(W4Args p) {
         }
     }
     // Activations and weights, pair-step by pair-step (clamped: every load is issued).
-    u32x4 av[U][MB][4], wv[U][2];
-    const u32x4* wbase = p.W + (int64_t)nt * KC * 64 + 32 * h + col;
+    u32x4 av[U][MB][4], wv[U][NH];
+    const u32x4* wbase = p.W + (int64_t)NT * wg * KC * 64 + 32 * h + col;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int pp = min(kp0 + wave + SK_NW * u, KP - 1);
@@ -858,31 +863,35 @@ w4a16_skinny_kernel(W4Args p) {
             for (int q = 0; q < 4; ++q) av[u][b][q] = *reinterpret_cast<const u32x4*>(ap + 8 * q);
         }
 #pragma unroll
-        for (int sc = 0; sc < 2; ++sc)
-            wv[u][sc] = __builtin_nontemporal_load(wbase + 16 * sc + (int64_t)(2 * pp + dc) * 64);
+        for (int sc = 0; sc < NH; ++sc)
+            wv[u][sc] = __builtin_nontemporal_load(wbase + (int64_t)(sc >> 1) * KC * 64 + 16 * (sc & 1) +
+                                                   (int64_t)(2 * pp + dc) * 64);
     }
 
-    asm volatile("" : "+v"(sraw[0]), "+v"(sraw[1]), "+v"(zraw[0]), "+v"(zraw[1]));
-    int sz[2];
 #pragma unroll
-    for (int sc = 0; sc < 2; ++sc) {
+    for (int sc = 0; sc < NH; ++sc) asm volatile("" : "+v"(sraw[sc]), "+v"(zraw[sc]));
+    int sz[NH];
+#pragma unroll
+    for (int sc = 0; sc < NH; ++sc) {
         uint32_t z;
         if constexpr (ZF != WMMA_ZEROS_U8)
-            z = (zraw[sc] >> (4 * ((32 * nt + 16 * sc + col) & 7))) & 0xFu;
+            z = (zraw[sc] >> (4 * ((n0 + 16 * sc + col) & 7))) & 0xFu;
         else
             z = zraw[sc] & 0xFu;
         sz[sc] = (int)(sraw[sc] | (z << 16));
     }
     uint32_t magic = 0x64006400u;
     asm volatile("" : "+v"(magic));
-    f32x4 d[MB][2];
+    f32x4 d[MB][NH];
 #pragma unroll
-    for (int b = 0; b < MB; ++b) d[b][0] = d[b][1] = f32x4{};
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int sc = 0; sc < NH; ++sc) d[b][sc] = f32x4{};
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        uint32_t v[2];
+        uint32_t v[NH];
 #pragma unroll
-        for (int sc = 0; sc < 2; ++sc) v[sc] = (uint32_t)__shfl(sz[sc], 16 * u + col);
+        for (int sc = 0; sc < NH; ++sc) v[sc] = (uint32_t)__shfl(sz[sc], 16 * u + col);
         if (kp0 + wave + SK_NW * u < KP) {  // uniform
             f16x8 a[MB][4];
 #pragma unroll
@@ -897,7 +906,7 @@ w4a16_skinny_kernel(W4Args p) {
                     }
                 }
 #pragma unroll
-            for (int sc = 0; sc < 2; ++sc) {
+            for (int sc = 0; sc < NH; ++sc) {
                 const uint32_t zz = v[sc] >> 16, s = v[sc] & 0xFFFFu;
                 const uint32_t z1 = 0x6400u | zz, z16 = 0x6400u | (zz << 4);
                 const f16x2 zs1 = as_h2(z1 | (z1 << 16)), zs16 = as_h2(z16 | (z16 << 16));
@@ -919,17 +928,17 @@ w4a16_skinny_kernel(W4Args p) {
 #pragma unroll
     for (int b = 0; b < MB; ++b)
 #pragma unroll
-        for (int sc = 0; sc < 2; ++sc)
+        for (int sc = 0; sc < NH; ++sc)
 #pragma unroll
             for (int r = 0; r < 4; ++r) red[wave][16 * b + 4 * sub + r][16 * sc + col] = d[b][sc][r];
     __syncthreads();
     const bool partial = gridDim.y > 1;
-    for (int i = tid; i < M * 32; i += SK_NW * kWave) {
-        const int m = i >> 5, c = i & 31;
+    for (int i = tid; i < M * 32 * NT; i += SK_NW * kWave) {
+        const int m = i / (32 * NT), c = i % (32 * NT);
         float acc = red[0][m][c];
 #pragma unroll
         for (int w = 1; w < SK_NW; ++w) acc += red[w][m][c];
-        const int n = 32 * nt + c;
+        const int n = n0 + c;
         if (partial)
             p.ws[((int64_t)blockIdx.y * M + m) * p.N + n] = acc;
         else
@@ -950,15 +959,15 @@ int skinny_u(int M, int N, int K, int num_cus) {
     return 1;
 }
 
-template <int ZF, int MB>
+template <int ZF, int MB, int NT>
 void launch_skinny_mb(const W4Args& a, int U, dim3 grid, hipStream_t stream) {
     const dim3 block(SK_NW * kWave);
     if (U == 4)
-        hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, (MB == 1 ? 4 : 2)>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, (MB == 1 ? 4 : 2), NT>), grid, block, 0, stream, a);
     else if (U == 2)
-        hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, 2>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, 2, NT>), grid, block, 0, stream, a);
     else
-        hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, 1>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, 1, NT>), grid, block, 0, stream, a);
 }
 
 // ------------------------------------------------------ W4A16 GEMM (M > 32), LDS-DMA --
@@ -1434,7 +1443,7 @@ hipError_t launch_int4_params_slice(const void* scales, const void* zeros, int z
 //   decode       M <= 4 with the same slice condition, other group sizes.
 //   gemv-split   other M <= 4 shapes: one workgroup per 32 columns, K split (plus a reduce
 //                pass) only when fewer than 2*CUs workgroups would exist.
-//   skinny       4 < M <= 32 with G = 128 * 2^j: 32 columns per workgroup, K split (plus
+//   skinny       4 < M <= 32 with G = 128 * 2^j: 32 or 64 columns per workgroup, K split (plus
 //                a reduce pass) only when the tiles alone give under half a workgroup per CU.
 //   gemm         M > 32: LDS-DMA MFMA GEMM (256x256 tiles from 512 rows, else 128x128),
 //                K split (plus a reduce pass) only when the tiles cannot fill the chip.
@@ -1456,7 +1465,14 @@ W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
         return pl;
     }
     if (M > DM_MAXM && M <= 32 && K % 128 == 0 && G % 128 == 0 && ((G / 128) & (G / 128 - 1)) == 0) {
-        const int u = skinny_u(M, N, K, num_cus);
+        // Two tiles per workgroup when the pairs alone still give half a workgroup per CU
+        // (M <= 16) or 3/4 of one (M > 16, where each workgroup carries twice the MFMA work).
+        // Measured at K = 4096: M = 16 11.8 -> 10.2-10.7 us at N = 14336 and 11.6 -> 10.0 at
+        // N = 11008; M = 24, 32 gain at N = 14336 only; at N = 4096 pairs need a K split
+        // and lose (5.9 -> 7.9 us at M = 8).
+        const int tiles = N / 32;
+        pl.big = tiles % 2 == 0 && (M <= 16 ? tiles >= num_cus : 2 * tiles >= 3 * num_cus);
+        const int u = skinny_u(M, pl.big ? N / 2 : N, K, num_cus);
         pl.kind = W4_SKINNY;
         pl.k_per_split = SK_NW * u * 128;
         pl.split = ceil_div(K, pl.k_per_split);
@@ -1549,11 +1565,18 @@ hipError_t launch_w4a16_zf(const W4Args& a, const W4A16Launch& w, hipStream_t st
         launch_w4g<ZF>(a, big ? 0 : 1, grid, stream);
     } else if (pl.kind == W4_SKINNY) {
         const int U = pl.k_per_split / (SK_NW * 128);
-        const dim3 grid(ntiles, pl.split);
-        if (w.M <= 16)
-            launch_skinny_mb<ZF, 1>(a, U, grid, stream);
-        else
-            launch_skinny_mb<ZF, 2>(a, U, grid, stream);
+        const dim3 grid(pl.big ? ntiles / 2 : ntiles, pl.split);
+        if (pl.big) {
+            if (w.M <= 16)
+                launch_skinny_mb<ZF, 1, 2>(a, U, grid, stream);
+            else
+                launch_skinny_mb<ZF, 2, 2>(a, U, grid, stream);
+        } else {
+            if (w.M <= 16)
+                launch_skinny_mb<ZF, 1, 1>(a, U, grid, stream);
+            else
+                launch_skinny_mb<ZF, 2, 1>(a, U, grid, stream);
+        }
     } else if (pl.kind == W4_GEMV_SPLIT) {
         hipLaunchKernelGGL((w4a16_gemv_kernel<ZF>), dim3(ntiles, pl.split), dim3(GV_NW * kWave), 0,
                            stream, a);
