@@ -146,6 +146,10 @@ def test_w4a16_plan_make(lib):
     k, s, kps, ws = plan(16, 2048, 4096)               # skinny, 64 tiles: K split
     assert (k, s, kps) == (4, 2, 2048) and ws == 2 * 16 * 2048 * 4
     assert plan(128, 14336, 4096)[:2] == (5, 2)        # 112 tiles of 128x128: split 2
+    assert plan(128, 4096, 4096)[:2] == (5, 4)         # 32 tiles: split capped at 4 ...
+    assert plan(64, 4096, 4096)[:2] == (5, 8)          # ... and at 8 for M <= 64
+    # skinny with two 32-column tiles per workgroup (256 pairs) and a 2-way K split
+    assert plan(16, 8192, 8192) == (4, 2, 4096, 2 * 16 * 8192 * 4)
     assert plan(2048, 4096, 4096)[:2] == (5, 1)        # 512 tiles of 128x128, no split
     assert plan(1024, 14336, 4096)[:2] == (5, 1)       # 224 tiles of 256x256
     assert plan(32, 14336, 4096)[0] == 4
