@@ -168,6 +168,18 @@ int wmma_w4a16_plan_make(int M, int N, int K, int group_size, int num_cus, wmma_
  * (dequantised value rounded once to fp16).  packed: output of wmma_int4_prepack.
  * scales: fp16 [K/G, N] (or [N/16][K/G][16] with WMMA_ZEROS_SLICED).  zeros: per
  * zeros_format.  G = group_size, G % 32 == 0, K % G == 0.
+ * Arithmetic by path (wmma_w4a16_plan_make reports the path of a shape).  The tiled
+ * kernels (WMMA_W4_KERNEL_SKINNY, _GEMM, _MFMA, _GEMV_SPLIT) and the decode kernel at
+ * M = 3, 4 form each weight exactly as written above before its fp32-accumulated product.
+ * Two decode paths form no per-weight fp16 value: WMMA_W4_KERNEL_DECODE_MFMA at M <= 2
+ * and WMMA_W4_KERNEL_DECODE (M <= 4).  For each 128-deep (resp. 32-deep) K run inside a
+ * group they accumulate the exact products a * (1024 + q) (a * (64 + q) at k % 8 in
+ * {2,3,6,7}) and the activation sums in fp32 and add s * (D - P - z Q) once per run: the
+ * same value up to fp32 rounding and the omitted fp16 rounding of each dequantised weight
+ * (measured max relative error 2.2e-4 at K = 4096).  The bits of a row therefore depend
+ * on the path M selects: row 0 of an M = 2 call can differ in the last bits from row 0 of
+ * an M = 3 call (not batch-invariant across that boundary).  Every path is deterministic
+ * (no atomics; a K split is summed in a fixed order).
  * No reference counterpart (BASELINE-defined W4A16 path).
  */
 int wmma_w4a16_gemm(const void* A, int64_t lda, const int32_t* packed, const void* scales,
@@ -190,6 +202,33 @@ int wmma_w4a16_gemm_f16out(const void* A, int64_t lda, const int32_t* packed,
  */
 int wmma_int4_from_awq(const int32_t* qweight_awq, const int32_t* qzeros_awq, int K, int N,
                        int group_size, int32_t* qweight, int32_t* zeros, void* stream);
+
+/*
+ * GPTQ checkpoint zero points to this library's packed zeros (WMMA_ZEROS_PACKED), bit-exact.
+ * qzeros int32 [K/G, N/8] holds z[g][n] in nibble n%8 of word [g][n/8] -- the layout of
+ * WMMA_ZEROS_PACKED -- but AutoGPTQ's "gptq" checkpoint format (WMMA_GPTQ_V1) packs z - 1
+ * there and dequantises with (stored + 1); GPTQModel's "gptq_v2" format (WMMA_GPTQ_V2)
+ * stores z.  zeros[g][n] = stored + 1 (v1) or stored (v2).  A v1 stored nibble of 15 means
+ * z = 16 (the result of packing z = 0 as z - 1), which a 4-bit zero point cannot hold: its
+ * nibble becomes 0 and *overflow, when overflow != NULL (device int32), is set to 1; the
+ * call never clears *overflow, so the caller zeroes it first and checks it after.  GPTQ's
+ * qweight [K/8, N] and scales [K/G, N] are this library's layout already.  No reference
+ * counterpart.
+ */
+#define WMMA_GPTQ_V1 1
+#define WMMA_GPTQ_V2 2
+int wmma_int4_from_gptq_zeros(const int32_t* qzeros, int K, int N, int group_size,
+                              int zero_format, int32_t* zeros, int32_t* overflow, void* stream);
+
+/*
+ * Act-order GPTQ checkpoints (desc_act, a g_idx that is not k / G): row k of the quantised
+ * weights belongs to group g_idx[k].  With perm = a stable sort of the rows by g_idx (G rows
+ * per group), qweight_out row k = qweight row perm[k] (GPTQ layout, int32 [K/8, N]; perm
+ * int32 [K], entries clamped into [0, K)), so that the groups are contiguous again and
+ * Y = A[:, perm] @ W_out equals A @ W.  No reference counterpart.
+ */
+int wmma_int4_permute_rows(const int32_t* qweight, const int32_t* perm, int K, int N,
+                           int32_t* qweight_out, void* stream);
 
 /*
  * Flash-attention forward.  Q [B,H,Sq,D], K and V [B,H,Sk,D], O [B,H,Sq,D]; fp16,

@@ -89,6 +89,48 @@ def awq_to_gptq(qweight_awq: np.ndarray, qzeros_awq: np.ndarray):
     return pack_gptq(unpack_awq(qweight_awq)), pack_zeros(unpack_awq(qzeros_awq))
 
 
+# GPTQ checkpoints.  AutoGPTQ's "gptq" format (v1; AutoGPTQ 0.7.x, not installed here) keeps
+# qweight [K/8, N] (q[k][n] in nibble k%8 of word [k//8][n]) and scales [K/G, N] in this
+# library's layout, but its packing code subtracts 1 from each zero point before packing it
+# into qzeros [K/G, N/8] (nibble n%8 of word [g][n//8]) and its dequantisation adds the 1
+# back: W[k][n] = (q[k][n] - (stored + 1)) * s.  GPTQModel's "gptq_v2" stores z itself.
+# Act-order (desc_act) checkpoints carry g_idx [K], the group of each row.  Restated from
+# that published packing and dequantisation; no GPTQ fixture exists here, so the adapter's
+# parity with a GPTQ run is unpinned and rests on these restatements and closed forms.
+def pack_gptq_v1_zeros(z: np.ndarray) -> np.ndarray:
+    """uint8 zero points z [K/G, N] (1..16) -> v1 qzeros int32 [K/G, N/8] holding z - 1."""
+    z = np.asarray(z, dtype=np.int32)
+    assert z.min() >= 1 and z.max() <= 16, "v1 stores z - 1 in four bits"
+    return pack_zeros((z - 1).astype(np.uint8))
+
+
+def gptq_dequant(qweight: np.ndarray, qzeros: np.ndarray, scales: np.ndarray, g_idx,
+                 v1: bool = True) -> np.ndarray:
+    """GPTQ dequantisation W [K, N] fp16: fp16((q[k][n] - z[g_idx[k]][n]) * s[g_idx[k]][n]),
+    z = stored nibble + 1 (v1) or stored nibble (v2); g_idx None means k // G."""
+    q = unpack_gptq(qweight).astype(np.int32)
+    K, N = q.shape
+    z = unpack_zeros(qzeros).astype(np.int32) + (1 if v1 else 0)
+    G = K // z.shape[0]
+    g = np.arange(K) // G if g_idx is None else np.asarray(g_idx, dtype=np.int64)
+    return (q - z[g, :]).astype(np.float16) * np.asarray(scales, dtype=np.float16)[g, :]
+
+
+def gptq_w4a16_ref(A: torch.Tensor, qweight, qzeros, scales, g_idx, v1: bool = True) -> torch.Tensor:
+    """Y = A.float() @ gptq_dequant(...).float(), fp32 on the CPU."""
+    W = torch.from_numpy(gptq_dequant(qweight, qzeros, scales, g_idx, v1).astype(np.float32))
+    return torch.matmul(A.detach().cpu().float(), W)
+
+
+def act_order_g_idx(K: int, G: int, seed: int) -> np.ndarray:
+    """A desc_act g_idx: rows visited in a random order, the i-th visited row in group i // G
+    (how GPTQ assigns groups when it quantises columns by decreasing Hessian diagonal)."""
+    order = np.random.default_rng(seed).permutation(K)
+    g_idx = np.empty(K, dtype=np.int32)
+    g_idx[order] = np.arange(K) // G
+    return g_idx
+
+
 def slice_params(s: np.ndarray, z: np.ndarray):
     """Slice-major group parameters (this library's WMMA_ZEROS_SLICED layout):
     scales fp16 [K/G, N] -> [N/16, K/G, 16]; uint8 zeros [K/G, N] -> int32 [N/16, K/G, 2]
@@ -123,7 +165,7 @@ def _permute_word_nibbles(w: np.ndarray, inverse: bool = False) -> np.ndarray:
 
 
 def prepack(qweight: np.ndarray) -> np.ndarray:
-    """GPTQ qweight [K/8, N] -> prepacked int32, returned with shape [K/8, N]."""
+    """GPTQ qweight [K/8, N] -> prepacked int32 [N/32, K/64, 64, 4]."""
     w = np.asarray(qweight).view(np.uint32)
     kg, N = w.shape
     K = kg * 8
@@ -133,15 +175,15 @@ def prepack(qweight: np.ndarray) -> np.ndarray:
     t = w.reshape(KC, 2, 4, NT, 32)            # [kc, h, word, nt, c]
     t = t.transpose(3, 0, 1, 4, 2)             # [nt, kc, h, c, word]
     t = _permute_word_nibbles(t)
-    return np.ascontiguousarray(t).reshape(kg, N).view(np.int32)
+    return np.ascontiguousarray(t).reshape(NT, KC, 64, 4).view(np.int32)
 
 
 def unprepack(packed: np.ndarray) -> np.ndarray:
-    """Inverse of prepack."""
+    """Inverse of prepack: int32 [N/32, K/64, 64, 4] -> GPTQ qweight [K/8, N]."""
     p = np.asarray(packed).view(np.uint32)
-    kg, N = p.shape
-    K = kg * 8
-    KC, NT = K // 64, N // 32
+    NT, KC = p.shape[0], p.shape[1]
+    assert p.shape == (NT, KC, 64, 4)
+    kg, N = KC * 8, NT * 32
     t = p.reshape(NT, KC, 2, 32, 4)            # [nt, kc, h, c, word]
     t = _permute_word_nibbles(t, inverse=True)
     t = t.transpose(1, 2, 4, 0, 3)             # [kc, h, word, nt, c]

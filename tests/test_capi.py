@@ -42,6 +42,8 @@ def lib():
     L.wmma_int4_prepack_params.argtypes = [vp, vp, i32, i32, i32, i32, vp, vp, vp]
     L.wmma_gemm_plan_custom.argtypes = [i32, i32, i32, i32, i32, i32, ctypes.POINTER(Plan)]
     L.wmma_int4_from_awq.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp]
+    L.wmma_int4_from_gptq_zeros.argtypes = [vp, i32, i32, i32, i32, vp, vp, vp]
+    L.wmma_int4_permute_rows.argtypes = [vp, vp, i32, i32, vp, vp]
     L.wmma_w4a16_gemm_f16out.argtypes = [vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, vp, i64, vp, sz, vp]
     L.wmma_gemm_f16f32_plan.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, f32, f32,
                                         ctypes.POINTER(Plan), vp, sz, vp]
@@ -351,3 +353,43 @@ def test_torch_extension_reference_errors(wo):
 
 def test_torch_plan_binding(wo):
     assert wo.gemm_plan(4096, 4096, 4096) == [0, 5, 256, 256, 1, 4096, 256, 0]
+
+
+def test_import_name_of_the_reference():
+    # The reference's module is `wmma_ops` (setup.py:18-21); `import wmma_ops` gives this
+    # library, the same module object as wmma_ops_amd.
+    import wmma_ops
+    import wmma_ops_amd
+    assert wmma_ops is wmma_ops_amd
+    for name in ["matmul", "matmul_adaptive", "matmul_tiled", "gemm", "gemm_inplace",
+                 "gemm_adaptive", "flash_attention", "matmul_asmOpt", "matmul_xor_optimized"]:
+        assert callable(getattr(wmma_ops, name))
+    with pytest.raises(RuntimeError, match="Inputs must be CUDA tensors"):
+        wmma_ops.matmul_adaptive(torch.zeros(4, 8, dtype=torch.float16),
+                                 torch.zeros(8, 4, dtype=torch.float16))
+
+
+def test_gptq_entry_points_validate(lib):
+    FAKE = 1 << 20
+    # zeros: bad format, N not a multiple of 8, group size not dividing K, misalignment
+    assert lib.wmma_int4_from_gptq_zeros(FAKE, 256, 64, 64, 3, FAKE, None, None) == INVALID
+    assert lib.wmma_int4_from_gptq_zeros(FAKE, 256, 60, 64, 1, FAKE, None, None) == INVALID
+    assert lib.wmma_int4_from_gptq_zeros(FAKE, 256, 64, 96, 1, FAKE, None, None) == INVALID
+    assert lib.wmma_int4_from_gptq_zeros(FAKE + 2, 256, 64, 64, 2, FAKE, None, None) == MISALIGNED
+    assert lib.wmma_int4_from_gptq_zeros(None, 256, 64, 64, 1, FAKE, None, None) == INVALID
+    # row permutation: K not a multiple of 8, in place, NULL perm
+    assert lib.wmma_int4_permute_rows(FAKE, FAKE * 2, 100, 64, FAKE * 3, None) == INVALID
+    assert lib.wmma_int4_permute_rows(FAKE, FAKE * 2, 128, 64, FAKE, None) == INVALID
+    assert lib.wmma_int4_permute_rows(FAKE, None, 128, 64, FAKE * 3, None) == INVALID
+
+
+def test_w4a16_offset_limits(lib):
+    # 32-bit buffer offsets: the whole-A bound applies per 256-row tile, so a long prefill is
+    # accepted up to the launch (nothing here reaches the GPU: the pointers below are
+    # checked for NULL only after the shape checks, and this call fails on the K bound);
+    # K so large that one workgroup's weight columns pass 2^31 bytes is rejected.
+    FAKE = 1 << 20
+    K = 1 << 24
+    rc = lib.wmma_w4a16_gemm(FAKE, K, FAKE, FAKE, FAKE, 0, 4, 64, K, 128, FAKE, 64, None, 0, None)
+    assert rc == UNSUPPORTED
+    assert b"weight offsets" in lib.wmma_last_error()

@@ -37,6 +37,24 @@ def test_flash_baseline_config(wo, causal):
         _check(O[b:b + 1, h:h + 1], ref)
 
 
+# The same configuration checked on every one of its 128 (batch, head) slices against the
+# fp32 CPU reference, eight heads per CPU call; the error is the global max-relative metric.
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_baseline_config_all_heads(wo, causal):
+    B, H, S, D = 4, 32, 4096, 128
+    report("flash_all_heads", B=B, H=H, S=S, D=D, causal=causal)
+    Q, K, V = oatt.make_inputs(B, H, S, D, seed=42 + 4)
+    O = wo.flash_attention(Q.cuda(), K.cuda(), V.cuda(), causal=causal,
+                           scale=1.0 / math.sqrt(D)).cpu().float()
+    worst, peak = 0.0, 0.0
+    for b in range(B):
+        for h in range(0, H, 8):
+            ref = oatt.sdpa_ref(Q[b:b + 1, h:h + 8], K[b:b + 1, h:h + 8], V[b:b + 1, h:h + 8], causal)
+            worst = max(worst, (O[b:b + 1, h:h + 8] - ref).abs().max().item())
+            peak = max(peak, ref.abs().max().item())
+    assert worst / peak <= TOL, f"max rel err {worst / peak:.3e}"
+
+
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("B,H,Sq,Sk,D", [(2, 8, 512, 512, 64), (1, 4, 77, 77, 128), (2, 2, 200, 200, 64),
                                          (1, 3, 100, 300, 128), (1, 2, 300, 100, 64), (1, 1, 1, 1, 128),

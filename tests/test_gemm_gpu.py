@@ -39,6 +39,24 @@ def test_known_answer_fragment(wo):
         assert torch.equal(wo.matmul_tiled(A.cuda(), B.cuda(), cfg).cpu(), C)
 
 
+# The reference's own correctness cases: the seven seeded shapes of its fragment-loading
+# test (test_fragment_loading.py:67-75, seed 42, fp32 torch.matmul reference) and the
+# small-K shapes of its patch test (test_rocwmma_patch.py:58-106), through every entry
+# point: matmul, matmul_adaptive, the asmOpt alias it calls, and every matmul_tiled tile.
+@pytest.mark.parametrize("M,N,K", [(512, 512, 64), (512, 512, 128), (1024, 1024, 256),
+                                   (2048, 2048, 512), (4096, 4096, 1024), (2048, 1024, 512),
+                                   (1024, 2048, 512), (2048, 2048, 128)])
+def test_reference_test_shapes(wo, M, N, K):
+    report("reference_shapes", M=M, N=N, K=K, plan=wo.gemm_plan(M, N, K))
+    A, B = _inputs(M, N, K, 42)
+    ref = og.gemm_ref(A, B)
+    Ad, Bd = A.cuda(), B.cuda()
+    for fn in (wo.matmul, wo.matmul_adaptive, wo.matmul_asmOpt):
+        _check(fn(Ad, Bd), ref)
+    for cfg in range(6):
+        _check(wo.matmul_tiled(Ad, Bd, cfg), ref)
+
+
 # configs[0] and configs[1] of the task: square and rectangular shapes
 @pytest.mark.parametrize("M,N,K", [(512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048),
                                    (4096, 4096, 4096), (4096, 4096, 2048)])
@@ -51,7 +69,8 @@ def test_matmul_baseline_shapes(wo, M, N, K):
     _check(wo.matmul_adaptive(Ad, Bd), ref)
 
 
-@pytest.mark.parametrize("M,N,K", [(1024, 1024, 1024), (4096, 4096, 4096)])
+@pytest.mark.parametrize("M,N,K", [(1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096),
+                                   (4096, 4096, 2048)])
 def test_gemm_epilogue_out_of_place_and_in_place(wo, M, N, K):
     # C = 2.0*A*B + 0.5*C with C fp32 N(0,1), out-of-place and in-place.
     report("gemm_epilogue", M=M, N=N, K=K)
@@ -277,3 +296,24 @@ def test_integer_data_exact(wo):
         A = torch.randint(-2, 3, (M, K), generator=g).half()
         B = torch.randint(-2, 3, (K, N), generator=g).half()
         assert torch.equal(wo.matmul(A.cuda(), B.cuda()).cpu(), og.gemm_ref(A, B)), (M, N, K)
+
+
+def test_reference_alignment_texts(wo):
+    # The reference's texts (wmma_gemm.hip:1443-1446, 1483-1486 say "... for vectorized
+    # loads"; matmul_adaptive, gemm and gemm_adaptive, :1207-1210 and :1920-1923, do not),
+    # reached through the reference's own module name.
+    import wmma_ops
+    buf = torch.zeros(64 * 64 + 8, dtype=torch.half, device="cuda")
+    A = buf[1:1 + 64 * 64].view(64, 64)   # contiguous, 2 bytes past a 16-byte boundary
+    B = torch.zeros(64, 64, dtype=torch.half, device="cuda")
+    assert A.is_contiguous() and A.data_ptr() % 16 == 2
+    for fn in (wmma_ops.matmul, lambda a, b: wmma_ops.matmul_tiled(a, b, 0)):
+        with pytest.raises(RuntimeError, match="A must be 16-byte aligned for vectorized loads"):
+            fn(A, B)
+    for fn in (wmma_ops.matmul_adaptive, wmma_ops.gemm, wmma_ops.gemm_adaptive):
+        with pytest.raises(RuntimeError) as e:
+            fn(A, B)
+        assert "A must be 16-byte aligned" in str(e.value) and "vectorized" not in str(e.value)
+    # and the reference's module name runs the HIP GEMM
+    Ah, Bh = _inputs(256, 128, 192, 4)
+    _check(wmma_ops.matmul(Ah.cuda(), Bh.cuda()), og.gemm_ref(Ah, Bh))

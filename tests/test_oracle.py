@@ -134,9 +134,9 @@ def test_prepack_bijection_and_c_restatement(K, N):
     q = _rand_q(K, N, K + N)
     qw = oi.pack_gptq(q)
     pk = oi.prepack(qw)
-    assert pk.shape == qw.shape and pk.dtype == np.int32
+    assert pk.shape == (N // 32, K // 64, 64, 4) and pk.dtype == np.int32
     assert np.array_equal(oi.unprepack(pk), qw)
-    assert np.array_equal(cref.prepack(qw), pk)           # independent C restatement
+    assert np.array_equal(cref.prepack(qw).reshape(pk.shape), pk)  # independent C restatement
     # same multiset of nibbles
     nib = lambda a: np.sort(np.concatenate([(a.view(np.uint32) >> (4 * j)) & 0xF for j in range(8)], axis=None))
     assert np.array_equal(nib(pk), nib(qw))
@@ -194,7 +194,7 @@ def test_golden_int4_fixture():
     d = np.load(path)
     q, s, z = d["q"], d["scales"], d["zeros_u8"]
     assert np.array_equal(oi.pack_gptq(q), d["qweight"])
-    assert np.array_equal(oi.prepack(d["qweight"]), d["packed"])
+    assert np.array_equal(oi.prepack(d["qweight"]).reshape(d["packed"].shape), d["packed"])
     assert np.array_equal(oi.pack_zeros(z), d["zeros_packed"])
     assert np.array_equal(oi.dequant(q, s, z, 64).view(np.uint16), d["w_fp16_bits"])
     A = torch.from_numpy(d["A"])
@@ -405,3 +405,46 @@ def test_sdpa_varlen_bwd_ref_equals_dense():
     assert torch.isinf(lse[:, :4]).all() and torch.isfinite(lse[:, 4:]).all()
     dq, _, _ = oatt.sdpa_varlen_bwd_ref(q, kv, kv, dOq, cu_q, cu_k)
     assert torch.count_nonzero(dq[:4]) == 0 and torch.count_nonzero(dq[4:]) > 0
+
+
+# GPTQ checkpoint restatement: v1 zero offset and act-order g_idx, pinned by closed forms
+# and by the native dequantisation (which it must reproduce when the layouts agree).
+def test_gptq_v1_zero_offset_closed_forms():
+    K, N, G = 256, 64, 64
+    rng = np.random.default_rng(21)
+    q = rng.integers(0, 16, (K, N), dtype=np.uint8)
+    z = rng.integers(1, 16, (K // G, N), dtype=np.uint8)
+    s = rng.uniform(0.001, 0.02, (K // G, N)).astype(np.float16)
+    qz1 = oi.pack_gptq_v1_zeros(z)
+    assert np.array_equal(oi.unpack_zeros(qz1), z - 1)                 # stored z - 1
+    w1 = oi.gptq_dequant(oi.pack_gptq(q), qz1, s, None, v1=True)
+    w2 = oi.gptq_dequant(oi.pack_gptq(q), oi.pack_zeros(z), s, None, v1=False)
+    native = oi.dequant(q, s, z, G)
+    assert np.array_equal(w1.view(np.uint16), native.view(np.uint16))
+    assert np.array_equal(w2.view(np.uint16), native.view(np.uint16))
+    # q == z (v1 storing z - 1) gives exactly zero; a plain layout g_idx equals none
+    zq = np.repeat(z, G, axis=0)
+    assert not np.any(oi.gptq_dequant(oi.pack_gptq(zq), qz1, s, None, v1=True))
+    plain = np.arange(K) // G
+    assert np.array_equal(oi.gptq_dequant(oi.pack_gptq(q), qz1, s, plain).view(np.uint16),
+                          w1.view(np.uint16))
+
+
+def test_gptq_act_order_rows_follow_g_idx():
+    # Build an act-order checkpoint by scattering the rows of a plain one: row k of the
+    # checkpoint is row rank[k] of the plain layout, where rank sorts the rows by group.
+    K, N, G = 256, 32, 32
+    rng = np.random.default_rng(22)
+    q = rng.integers(0, 16, (K, N), dtype=np.uint8)
+    z = rng.integers(1, 16, (K // G, N), dtype=np.uint8)
+    s = rng.uniform(0.001, 0.02, (K // G, N)).astype(np.float16)
+    g_idx = oi.act_order_g_idx(K, G, 5)
+    assert np.array_equal(np.bincount(g_idx), np.full(K // G, G))
+    perm = np.argsort(g_idx, kind="stable")           # sorted position -> checkpoint row
+    rank = np.empty(K, dtype=np.int64)
+    rank[perm] = np.arange(K)                          # checkpoint row -> sorted position
+    assert np.array_equal(g_idx[perm], np.arange(K) // G)
+    q_ckpt = q[rank]
+    w = oi.gptq_dequant(oi.pack_gptq(q_ckpt), oi.pack_gptq_v1_zeros(z), s, g_idx)
+    native = oi.dequant(q, s, z, G)
+    assert np.array_equal(w[perm].view(np.uint16), native.view(np.uint16))

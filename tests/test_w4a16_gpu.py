@@ -17,12 +17,14 @@ GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "int4_k256_n64_g64.np
 def test_golden_fixture_bit_exact(wo):
     d = np.load(GOLDEN)
     qw = torch.from_numpy(d["qweight"]).cuda()
-    assert np.array_equal(wo.prepack_int4(qw).cpu().numpy(), d["packed"])
+    K, N = d["q"].shape
+    packed = d["packed"].reshape(N // 32, K // 64, 64, 4)  # the fixture stores it flat
+    assert np.array_equal(wo.prepack_int4(qw).cpu().numpy(), packed)
     assert np.array_equal(wo.unpack_int4(qw).cpu().numpy(), d["q"])
-    assert np.array_equal(wo.unprepack_int4(torch.from_numpy(d["packed"]).cuda()).cpu().numpy(),
+    assert np.array_equal(wo.unprepack_int4(torch.from_numpy(packed).cuda()).cpu().numpy(),
                           d["qweight"])
     A = torch.from_numpy(d["A"])
-    Y = wo.matmul_int4(A.cuda(), torch.from_numpy(d["packed"]).cuda(),
+    Y = wo.matmul_int4(A.cuda(), torch.from_numpy(packed).cuda(),
                        torch.from_numpy(d["scales"]).cuda(), torch.from_numpy(d["zeros_packed"]).cuda(), 64)
     assert og.max_rel_err(Y, torch.from_numpy(d["Y"])) <= 1e-3
 
@@ -240,7 +242,7 @@ def test_w4a16_integer_weights_exact(wo):
 
 
 def test_w4a16_errors(wo):
-    pk = torch.zeros(8, 64, dtype=torch.int32, device="cuda")
+    pk = torch.zeros(2, 1, 64, 4, dtype=torch.int32, device="cuda")  # prepacked K=64, N=64
     A = torch.zeros(1, 64, dtype=torch.half, device="cuda")
     s = torch.zeros(1, 64, dtype=torch.half, device="cuda")
     z = torch.zeros(1, 8, dtype=torch.int32, device="cuda")
@@ -253,3 +255,96 @@ def test_w4a16_errors(wo):
         wo.matmul_int4(A, pk, s3, z, 64)
     with pytest.raises(RuntimeError, match="must be a multiple of 64"):
         wo.prepack_int4(torch.zeros(3, 64, dtype=torch.int32, device="cuda"))
+    # a GPTQ qweight [K/8, N] where prepacked weights belong is rejected, not read as garbage
+    with pytest.raises(RuntimeError, match="output of prepack_int4"):
+        wo.matmul_int4(A, torch.zeros(8, 64, dtype=torch.int32, device="cuda"), s, z, 64)
+    with pytest.raises(RuntimeError, match="output of prepack_int4"):
+        wo.unprepack_int4(torch.zeros(8, 64, dtype=torch.int32, device="cuda"))
+
+
+# Tiny-magnitude activations: the decode kernel pre-scales a quarter of the activations by
+# 1/16 in fp16, which is inexact for fp16-subnormal |a| < 2^-10; the error stays far inside
+# the bound (a relative error against max|Y|).
+@pytest.mark.parametrize("M", [1, 2, 16])
+def test_w4a16_tiny_activations(wo, M):
+    K, N, G = 4096, 4096, 128
+    report("w4a16_tiny", M=M)
+    A, q, s, z = oi.make_inputs(M, K, N, G, seed=31 + M)
+    A = (A.float() * 1e-4).half()
+    ref = oi.w4a16_ref(A, q, s, z, G)
+    pk = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
+    Y = wo.matmul_int4(A.cuda(), pk, torch.from_numpy(s).cuda(), torch.from_numpy(oi.pack_zeros(z)).cuda(), G)
+    assert og.max_rel_err(Y, ref) <= 1e-3
+
+
+# GPTQ checkpoints (int4_from_gptq).  v1 stores z - 1: the adapter's zeros equal the packed
+# true zeros bit for bit, and v2 passes them through.
+@pytest.mark.parametrize("K,N,G", [(256, 64, 64), (4096, 1024, 128)])
+def test_int4_from_gptq_zeros_bit_exact(wo, K, N, G):
+    rng = np.random.default_rng(K + 3 * N)
+    q = rng.integers(0, 16, (K, N), dtype=np.uint8)
+    z = rng.integers(1, 16, (K // G, N), dtype=np.uint8)
+    qw = torch.from_numpy(oi.pack_gptq(q)).cuda()
+    qw1, zo1, perm1 = wo.int4_from_gptq(qw, torch.from_numpy(oi.pack_gptq_v1_zeros(z)).cuda())
+    assert perm1 is None and torch.equal(qw1, qw)
+    assert np.array_equal(zo1.cpu().numpy(), oi.pack_zeros(z))
+    z2 = rng.integers(0, 16, (K // G, N), dtype=np.uint8)
+    _, zo2, _ = wo.int4_from_gptq(qw, torch.from_numpy(oi.pack_zeros(z2)).cuda(), zero_format="v2")
+    assert np.array_equal(zo2.cpu().numpy(), oi.pack_zeros(z2))
+
+
+def test_int4_from_gptq_v1_q_equals_z_is_zero(wo):
+    # q == z in every group: with v1 zeros stored as z - 1 every product term is exactly 0
+    K, N, G = 1024, 256, 128
+    rng = np.random.default_rng(9)
+    z = rng.integers(1, 16, (K // G, N), dtype=np.uint8)
+    q = np.repeat(z, G, axis=0)
+    s = rng.uniform(0.001, 0.02, (K // G, N)).astype(np.float16)
+    qw, zo, _ = wo.int4_from_gptq(torch.from_numpy(oi.pack_gptq(q)).cuda(),
+                                  torch.from_numpy(oi.pack_gptq_v1_zeros(z)).cuda())
+    pk = wo.prepack_int4(qw)
+    for M in (1, 5, 40):
+        A = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).half().cuda()
+        assert torch.count_nonzero(wo.matmul_int4(A, pk, torch.from_numpy(s).cuda(), zo, G)) == 0
+
+
+@pytest.mark.parametrize("M", [1, 16, 128])
+def test_int4_from_gptq_g_idx(wo, M):
+    K, N, G = 4096, 1024, 128
+    report("gptq_g_idx", M=M, K=K, N=N, G=G)
+    A, q, s, z = oi.make_inputs(M, K, N, G, seed=40 + M)
+    z = np.maximum(z, 1)  # v1 zero points are 1..16
+    qw = torch.from_numpy(oi.pack_gptq(q)).cuda()
+    qz = torch.from_numpy(oi.pack_gptq_v1_zeros(z)).cuda()
+    sd = torch.from_numpy(s).cuda()
+    # a plain g_idx (k // G) is the plain layout: no permutation, the same bits
+    plain = torch.arange(K, dtype=torch.int32, device="cuda") // G
+    qw0, zo0, perm0 = wo.int4_from_gptq(qw, qz)
+    qwp, zop, permp = wo.int4_from_gptq(qw, qz, plain)
+    assert perm0 is None and permp is None and torch.equal(qw0, qwp) and torch.equal(zo0, zop)
+    Y0 = wo.matmul_int4(A.cuda(), wo.prepack_int4(qw0), sd, zo0, G)
+    assert og.max_rel_err(Y0, oi.gptq_w4a16_ref(A, oi.pack_gptq(q), oi.pack_gptq_v1_zeros(z), s, None)) <= 1e-3
+    # act order: rows regrouped by a stable sort, A's columns gathered by perm
+    g_idx = oi.act_order_g_idx(K, G, seed=M)
+    qwa, zoa, perma = wo.int4_from_gptq(qw, qz, torch.from_numpy(g_idx).cuda())
+    assert perma is not None and perma.dtype == torch.int64
+    assert np.array_equal(perma.cpu().numpy(), np.argsort(g_idx, kind="stable"))
+    assert np.array_equal(wo.unpack_int4(qwa).cpu().numpy(), q[perma.cpu().numpy()])
+    Ya = wo.matmul_int4(A.cuda(), wo.prepack_int4(qwa), sd, zoa, G, perm=perma)
+    ref = oi.gptq_w4a16_ref(A, oi.pack_gptq(q), oi.pack_gptq_v1_zeros(z), s, g_idx)
+    assert og.max_rel_err(Ya, ref) <= 1e-3
+
+
+def test_int4_from_gptq_errors(wo):
+    K, N, G = 256, 64, 64
+    qw = torch.zeros(K // 8, N, dtype=torch.int32, device="cuda")
+    bad = torch.from_numpy(oi.pack_zeros(np.full((K // G, N), 15, dtype=np.uint8))).cuda()
+    with pytest.raises(RuntimeError, match="zero point 16"):
+        wo.int4_from_gptq(qw, bad)                     # v1 nibble 15 = zero point 16
+    wo.int4_from_gptq(qw, bad, zero_format="v2")       # as stored in v2: fine
+    qz = torch.zeros(K // G, N // 8, dtype=torch.int32, device="cuda")
+    uneven = torch.zeros(K, dtype=torch.int32, device="cuda")  # every row in group 0
+    with pytest.raises(RuntimeError, match="exactly group_size rows"):
+        wo.int4_from_gptq(qw, qz, uneven)
+    with pytest.raises(RuntimeError, match="zero_format"):
+        wo.int4_from_gptq(qw, qz, zero_format="v3")

@@ -96,7 +96,14 @@ def flash_attention(Q, K, V, causal: bool = False, scale: float = -1.0):
 def flash_attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
                            causal: bool = False, scale: float = -1.0):
     """Packed variable-length attention ([total, heads, D] with int32 cu_seqlens [B+1]);
-    differentiable in q, k, v."""
+    differentiable in q, k, v.
+
+    max_seqlen_q / max_seqlen_k must be at least the longest sequence in cu_seqlens_q /
+    cu_seqlens_k: each sequence is processed up to that many rows only, so rows of a longer
+    sequence past it are never written (the output and, for training, the log-sum-exp keep
+    whatever their allocation held there) and no error is raised.  Offsets outside the
+    packed tensors are clamped, so inconsistent cu_seqlens give wrong rows, never an access
+    outside the tensors."""
     if _needs_grad(q, k, v):
         return FlashAttentionVarlenFunction.apply(q, k, v, cu_seqlens_q, cu_seqlens_k,
                                                   max_seqlen_q, max_seqlen_k, causal, scale)
@@ -106,6 +113,7 @@ def flash_attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
 prepack_int4 = _C.prepack_int4
 prepack_int4_params = _C.prepack_int4_params
 int4_from_awq = _C.int4_from_awq
+int4_from_gptq = _C.int4_from_gptq
 unprepack_int4 = _C.unprepack_int4
 unpack_int4 = _C.unpack_int4
 matmul_int4 = _C.matmul_int4
@@ -129,6 +137,6 @@ __all__ = [
     "matmul", "matmul_adaptive", "matmul_tiled", "gemm", "gemm_inplace", "gemm_adaptive",
     "flash_attention", "flash_attention_varlen", "flash_attention_forward",
     "flash_attention_backward", "flash_attention_varlen_forward", "flash_attention_varlen_backward",
-    "FlashAttentionFunction", "FlashAttentionVarlenFunction", "prepack_int4", "prepack_int4_params", "int4_from_awq", "unprepack_int4", "unpack_int4", "matmul_int4",
+    "FlashAttentionFunction", "FlashAttentionVarlenFunction", "prepack_int4", "prepack_int4_params", "int4_from_awq", "int4_from_gptq", "unprepack_int4", "unpack_int4", "matmul_int4",
     "gemm_plan", "w4a16_plan", "TILE_CONFIGS", "LIBRARY_PATH", "HEADER_PATH", *_REFERENCE_VARIANTS,
 ]

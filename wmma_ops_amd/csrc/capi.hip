@@ -302,8 +302,15 @@ static int w4a16_run(const void* A, int64_t lda, const int32_t* packed, const vo
         return fail(WMMA_ERR_MISALIGNED, "scales must be 2-byte aligned");
     if (zeros_format != WMMA_ZEROS_U8 && (reinterpret_cast<uintptr_t>(zeros) & 3u) != 0)
         return fail(WMMA_ERR_MISALIGNED, "packed zeros must be 4-byte aligned");
-    if ((int64_t)M * lda * 2 > kMaxOffset)
-        return fail(WMMA_ERR_UNSUPPORTED, "activation matrix too large for 32-bit offsets");
+    // 32-bit buffer offsets: the tiled kernels address A from their first row (at most 256
+    // rows), the LDS-DMA GEMM its weights from its first 32-column tile (at most 8 tiles of
+    // K * 16 bytes), and every kernel the group parameters from their start.
+    if ((int64_t)std::min(M, 256) * lda * 2 > kMaxOffset)
+        return fail(WMMA_ERR_UNSUPPORTED, "activation rows too long for 32-bit offsets");
+    if ((int64_t)8 * K * 16 > kMaxOffset)
+        return fail(WMMA_ERR_UNSUPPORTED, "K (%d) too large for 32-bit weight offsets", K);
+    if ((int64_t)(K / group_size) * N * 2 > kMaxOffset)
+        return fail(WMMA_ERR_UNSUPPORTED, "group parameters too large for 32-bit offsets");
     W4A16Launch w{};
     const bool aligned = (reinterpret_cast<uintptr_t>(scales) & 7u) == 0 &&
                          (zeros_format != WMMA_ZEROS_U8 ||
@@ -361,6 +368,38 @@ int wmma_int4_from_awq(const int32_t* qweight_awq, const int32_t* qzeros_awq, in
     return hip_status(launch_int4_from_awq(qweight_awq, qzeros_awq, K, N, K / group_size, qweight,
                                            zeros, static_cast<hipStream_t>(stream)),
                       "awq conversion launch");
+}
+
+int wmma_int4_from_gptq_zeros(const int32_t* qzeros, int K, int N, int group_size,
+                              int zero_format, int32_t* zeros, int32_t* overflow, void* stream) {
+    if (K <= 0 || N <= 0 || N % 8 != 0)
+        return fail(WMMA_ERR_INVALID_ARG, "K must be positive and N a positive multiple of 8");
+    if (group_size <= 0 || K % group_size != 0)
+        return fail(WMMA_ERR_INVALID_ARG, "group_size (%d) must divide K (%d)", group_size, K);
+    if (zero_format != WMMA_GPTQ_V1 && zero_format != WMMA_GPTQ_V2)
+        return fail(WMMA_ERR_INVALID_ARG, "unknown GPTQ zero format %d", zero_format);
+    if (!qzeros || !zeros) return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
+    for (const void* ptr : {(const void*)qzeros, (const void*)zeros, (const void*)overflow})
+        if ((reinterpret_cast<uintptr_t>(ptr) & 3u) != 0)
+            return fail(WMMA_ERR_MISALIGNED, "int32 tensors must be 4-byte aligned");
+    return hip_status(launch_int4_gptq_zeros(qzeros, K / group_size, N,
+                                             zero_format == WMMA_GPTQ_V1 ? 1 : 0, zeros, overflow,
+                                             static_cast<hipStream_t>(stream)),
+                      "gptq zeros launch");
+}
+
+int wmma_int4_permute_rows(const int32_t* qweight, const int32_t* perm, int K, int N,
+                           int32_t* qweight_out, void* stream) {
+    if (K <= 0 || N <= 0 || K % 8 != 0)
+        return fail(WMMA_ERR_INVALID_ARG, "K must be a positive multiple of 8 and N positive");
+    if (!qweight || !perm || !qweight_out) return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
+    if (qweight == qweight_out) return fail(WMMA_ERR_INVALID_ARG, "the permutation cannot run in place");
+    for (const void* ptr : {(const void*)qweight, (const void*)perm, (const void*)qweight_out})
+        if ((reinterpret_cast<uintptr_t>(ptr) & 3u) != 0)
+            return fail(WMMA_ERR_MISALIGNED, "int32 tensors must be 4-byte aligned");
+    return hip_status(launch_int4_permute_rows(qweight, perm, K, N, qweight_out,
+                                               static_cast<hipStream_t>(stream)),
+                      "row permutation launch");
 }
 
 // ----------------------------------------------------------------------------- flash --

@@ -40,6 +40,13 @@ hipError_t launch_int4_from_awq(const int32_t* qweight_awq, const int32_t* qzero
                                 hipStream_t stream);
 hipError_t launch_int4_unpack(const int32_t* qweight, int K, int N, uint8_t* q,
                               hipStream_t stream);
+// GPTQ checkpoint zero points (packed [KG][N/8]) + add (1 for AutoGPTQ's v1 format, 0 for
+// v2) per nibble; *overflow (may be NULL) set to 1 where a nibble would exceed 15.
+hipError_t launch_int4_gptq_zeros(const int32_t* qzeros, int KG, int N, int add, int32_t* zeros,
+                                  int32_t* overflow, hipStream_t stream);
+// GPTQ-layout weights with rows permuted: output row k = input row perm[k].
+hipError_t launch_int4_permute_rows(const int32_t* qweight, const int32_t* perm, int K, int N,
+                                    int32_t* out, hipStream_t stream);
 
 // W4A16 kernel families.
 enum W4A16Kind {

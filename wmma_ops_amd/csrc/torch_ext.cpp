@@ -69,13 +69,19 @@ void run_gemm(const torch::Tensor& A, const torch::Tensor& B, const torch::Tenso
     check_status(rc, "wmma_gemm_f16f32");
 }
 
-torch::Tensor matmul_impl(torch::Tensor A, torch::Tensor B, int tile_cfg, bool same_device) {
+// `vec_text`: the reference's matmul and matmul_tiled say "... aligned for vectorized loads"
+// (wmma_gemm.hip:1443-1446, 1483-1486), its matmul_adaptive just "... aligned"
+// (wmma_gemm.hip:1207-1210).
+torch::Tensor matmul_impl(torch::Tensor A, torch::Tensor B, int tile_cfg, bool same_device,
+                          bool vec_text) {
     check_ab(A, B, same_device);
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(A.device());
     A = A.contiguous();
     B = B.contiguous();
-    check_aligned(A, "A must be 16-byte aligned for vectorized loads");
-    check_aligned(B, "B must be 16-byte aligned for vectorized loads");
+    check_aligned(A, vec_text ? "A must be 16-byte aligned for vectorized loads"
+                              : "A must be 16-byte aligned");
+    check_aligned(B, vec_text ? "B must be 16-byte aligned for vectorized loads"
+                              : "B must be 16-byte aligned");
     auto C = torch::empty({A.size(0), B.size(1)}, torch::dtype(torch::kFloat32).device(A.device()));
     run_gemm(A, B, torch::Tensor(), C, 1.0, 0.0, tile_cfg);
     return C;
@@ -83,12 +89,12 @@ torch::Tensor matmul_impl(torch::Tensor A, torch::Tensor B, int tile_cfg, bool s
 
 // matmul (wmma_gemm.hip:1432-1470).  The tile is chosen by the planner.
 torch::Tensor matmul(torch::Tensor A, torch::Tensor B) {
-    return matmul_impl(A, B, WMMA_TILE_AUTO, true);
+    return matmul_impl(A, B, WMMA_TILE_AUTO, true, true);
 }
 
 // matmul_adaptive (wmma_gemm.hip:1197-1263).
 torch::Tensor matmul_adaptive(torch::Tensor A, torch::Tensor B) {
-    return matmul_impl(A, B, WMMA_TILE_AUTO, true);
+    return matmul_impl(A, B, WMMA_TILE_AUTO, true, false);
 }
 
 // matmul_tiled (wmma_gemm.hip:1473-1528): like the reference, no same-device check.
@@ -101,7 +107,7 @@ torch::Tensor matmul_tiled(torch::Tensor A, torch::Tensor B, int64_t tile_config
     TORCH_CHECK(tile_config >= 0 && tile_config < WMMA_TILE_COUNT,
                 "Invalid tile_config: 0=64x64, 1=128x64, 2=256x64, 3=128x128, 4=256x128, "
                 "5=256x256");
-    return matmul_impl(A, B, (int)tile_config, false);
+    return matmul_impl(A, B, (int)tile_config, false, true);
 }
 
 // gemm / gemm_adaptive (wmma_gemm.hip:1891-1945, 1997-2078): C is read only when
@@ -381,28 +387,42 @@ void check_qweight(const torch::Tensor& q) {
     TORCH_CHECK(q.dim() == 2, "qweight must be 2D [K/8, N]");
 }
 
-// prepack_int4(qweight[K/8, N] int32, GPTQ order) -> prepacked int32 [N/32, K/64, 64, 4]
-// (returned flattened as [K/8, N] so it has the same element count and dtype).
+// The prepacked weights are int32 [N/32, K/64, 64, 4] (include/wmma_ops_amd.h): a shape of
+// their own, so a GPTQ qweight [K/8, N] passed where prepacked weights belong is rejected
+// instead of being read as garbage.
+void check_packed(const torch::Tensor& pk) {
+    TORCH_CHECK(pk.is_cuda(), "packed must be a CUDA tensor");
+    TORCH_CHECK(pk.dtype() == torch::kInt32 && pk.dim() == 4 && pk.size(2) == 64 &&
+                    pk.size(3) == 4,
+                "packed must be the int32 [N/32, K/64, 64, 4] output of prepack_int4 (a GPTQ "
+                "qweight [K/8, N] must go through prepack_int4 first)");
+}
+
+// prepack_int4(qweight[K/8, N] int32, GPTQ order) -> prepacked int32 [N/32, K/64, 64, 4].
 torch::Tensor prepack_int4(torch::Tensor qweight) {
     check_qweight(qweight);
+    const int64_t K = qweight.size(0) * 8, N = qweight.size(1);
+    TORCH_CHECK(K > 0 && N > 0, "K and N must be positive");
+    TORCH_CHECK(K % 64 == 0, "K (", K, ") must be a multiple of 64");
+    TORCH_CHECK(N % 32 == 0, "N (", N, ") must be a multiple of 32");
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(qweight.device());
     qweight = qweight.contiguous();
-    const int K = (int)qweight.size(0) * 8, N = (int)qweight.size(1);
-    auto out = torch::empty_like(qweight);
-    check_status(wmma_int4_prepack(qweight.data_ptr<int32_t>(), K, N, out.data_ptr<int32_t>(),
-                                   current_stream(qweight)),
+    auto out = torch::empty({N / 32, K / 64, 64, 4}, qweight.options());
+    check_status(wmma_int4_prepack(qweight.data_ptr<int32_t>(), (int)K, (int)N,
+                                   out.data_ptr<int32_t>(), current_stream(qweight)),
                  "wmma_int4_prepack");
     return out;
 }
 
+// unprepack_int4(packed [N/32, K/64, 64, 4]) -> GPTQ qweight int32 [K/8, N].
 torch::Tensor unprepack_int4(torch::Tensor packed) {
-    check_qweight(packed);
+    check_packed(packed);
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(packed.device());
     packed = packed.contiguous();
-    const int K = (int)packed.size(0) * 8, N = (int)packed.size(1);
-    auto out = torch::empty_like(packed);
-    check_status(wmma_int4_unprepack(packed.data_ptr<int32_t>(), K, N, out.data_ptr<int32_t>(),
-                                     current_stream(packed)),
+    const int64_t K = packed.size(1) * 64, N = packed.size(0) * 32;
+    auto out = torch::empty({K / 8, N}, packed.options());
+    check_status(wmma_int4_unprepack(packed.data_ptr<int32_t>(), (int)K, (int)N,
+                                     out.data_ptr<int32_t>(), current_stream(packed)),
                  "wmma_int4_unprepack");
     return out;
 }
@@ -444,6 +464,68 @@ std::vector<torch::Tensor> int4_from_awq(torch::Tensor qweight, torch::Tensor qz
     return {qo, zo};
 }
 
+// int4_from_gptq(qweight [K/8, N] int32, qzeros [K/G, N/8] int32, g_idx=None,
+//                zero_format="v1") -> (qweight [K/8, N], zeros [K/G, N/8], perm or None).
+// GPTQ checkpoints keep qweight and scales in this library's layout; the zero points need
+// +1 per nibble in AutoGPTQ's v1 format ("v2": as stored).  g_idx (int32 [K], row -> group)
+// equal to k / G, or None, is the plain layout (perm None).  Any other g_idx (act-order /
+// desc_act) must give every group exactly G rows: the rows are then sorted by group (a
+// stable sort) and perm (int64 [K]) is returned; pass it to matmul_int4 (perm=...), which
+// multiplies A[:, perm].  One-time conversion: it synchronises to check the v1 zero range
+// and the g_idx group sizes.
+std::vector<c10::optional<torch::Tensor>> int4_from_gptq(torch::Tensor qweight, torch::Tensor qzeros,
+                                                         c10::optional<torch::Tensor> g_idx,
+                                                         const std::string& zero_format) {
+    TORCH_CHECK(qweight.is_cuda() && qzeros.is_cuda(), "Inputs must be CUDA tensors");
+    TORCH_CHECK(qweight.device() == qzeros.device(), "Inputs must be on same device");
+    check_qweight(qweight);
+    TORCH_CHECK(qzeros.dtype() == torch::kInt32 && qzeros.dim() == 2 &&
+                    qzeros.size(1) * 8 == qweight.size(1),
+                "GPTQ qzeros must be int32 [K/group_size, N/8]");
+    TORCH_CHECK(zero_format == "v1" || zero_format == "v2", "zero_format must be \"v1\" or \"v2\"");
+    const int64_t K = qweight.size(0) * 8, N = qweight.size(1), ng = qzeros.size(0);
+    TORCH_CHECK(ng > 0 && K % ng == 0, "qzeros rows must divide K");
+    const int64_t G = K / ng;
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(qweight.device());
+    qweight = qweight.contiguous();
+    qzeros = qzeros.contiguous();
+    auto zo = torch::empty_like(qzeros);
+    auto overflow = torch::zeros({1}, qzeros.options());
+    int rc = wmma_int4_from_gptq_zeros(qzeros.data_ptr<int32_t>(), (int)K, (int)N, (int)G,
+                                       zero_format == "v1" ? WMMA_GPTQ_V1 : WMMA_GPTQ_V2,
+                                       zo.data_ptr<int32_t>(), overflow.data_ptr<int32_t>(),
+                                       current_stream(qweight));
+    check_status(rc, "wmma_int4_from_gptq_zeros");
+    TORCH_CHECK(overflow.item<int32_t>() == 0,
+                "GPTQ v1 qzeros hold a stored nibble 15 (zero point 16), which a 4-bit zero "
+                "point cannot represent");
+    c10::optional<torch::Tensor> perm;
+    torch::Tensor qo = qweight;
+    if (g_idx.has_value() && g_idx->defined()) {
+        torch::Tensor gi = *g_idx;
+        TORCH_CHECK(gi.device() == qweight.device(), "g_idx must be on the device of qweight");
+        TORCH_CHECK(gi.dim() == 1 && gi.size(0) == K &&
+                        (gi.dtype() == torch::kInt32 || gi.dtype() == torch::kInt64),
+                    "g_idx must be an int32 or int64 vector of K entries");
+        gi = gi.to(torch::kInt64);
+        auto plain = torch::arange(K, gi.options()).floor_divide(G);
+        if (!torch::equal(gi, plain)) {
+            TORCH_CHECK(gi.min().item<int64_t>() >= 0 && gi.max().item<int64_t>() < ng,
+                        "g_idx entries must lie in [0, K/group_size)");
+            TORCH_CHECK(torch::equal(torch::bincount(gi, {}, ng), torch::full({ng}, G, gi.options())),
+                        "act-order g_idx must assign exactly group_size rows to every group");
+            auto p = std::get<1>(torch::sort(gi, c10::optional<bool>(true), /*dim=*/0, /*descending=*/false));
+            auto p32 = p.to(torch::kInt32);
+            qo = torch::empty_like(qweight);
+            rc = wmma_int4_permute_rows(qweight.data_ptr<int32_t>(), p32.data_ptr<int32_t>(), (int)K,
+                                        (int)N, qo.data_ptr<int32_t>(), current_stream(qweight));
+            check_status(rc, "wmma_int4_permute_rows");
+            perm = p;
+        }
+    }
+    return {qo, zo, perm};
+}
+
 // prepack_int4_params(scales[K/G, N] fp16, zeros[K/G, N/8] int32 or [K/G, N] uint8)
 //   -> (scales [N/16, K/G, 16] fp16, zeros [N/16, K/G, 2] int32): the slice-major layout
 //   matmul_int4 also accepts (a 16-column slice's parameters contiguous).
@@ -483,7 +565,8 @@ std::vector<torch::Tensor> prepack_int4_params(torch::Tensor scales, torch::Tens
 // or scales and zeros as returned by prepack_int4_params.
 torch::Tensor matmul_int4(torch::Tensor A, torch::Tensor packed, torch::Tensor scales,
                           torch::Tensor zeros, int64_t group_size,
-                          c10::optional<at::ScalarType> out_dtype) {
+                          c10::optional<at::ScalarType> out_dtype,
+                          c10::optional<torch::Tensor> perm) {
     const bool half_out = out_dtype.has_value() && *out_dtype == torch::kFloat16;
     TORCH_CHECK(!out_dtype.has_value() || *out_dtype == torch::kFloat16 ||
                     *out_dtype == torch::kFloat32,
@@ -495,8 +578,8 @@ torch::Tensor matmul_int4(torch::Tensor A, torch::Tensor packed, torch::Tensor s
                 "Inputs must be on same device");
     TORCH_CHECK(A.dtype() == torch::kFloat16, "A must be float16");
     TORCH_CHECK(A.dim() == 2, "A must be 2D");
-    check_qweight(packed);
-    const int64_t K = packed.size(0) * 8, N = packed.size(1);
+    check_packed(packed);
+    const int64_t K = packed.size(1) * 64, N = packed.size(0) * 32;
     TORCH_CHECK(A.size(1) == K, "Inner dimensions must match");
     TORCH_CHECK(group_size > 0 && K % group_size == 0, "group_size must divide K");
     const int64_t ng = K / group_size;
@@ -523,6 +606,12 @@ torch::Tensor matmul_int4(torch::Tensor A, torch::Tensor packed, torch::Tensor s
         zfmt = WMMA_ZEROS_U8;
     }
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(A.device());
+    if (perm.has_value() && perm->defined()) {  // act-order weights from int4_from_gptq
+        TORCH_CHECK(perm->device() == A.device() && perm->dim() == 1 && perm->size(0) == K &&
+                        perm->dtype() == torch::kInt64,
+                    "perm must be the int64 [K] permutation returned by int4_from_gptq");
+        A = A.index_select(1, *perm);
+    }
     A = A.contiguous();
     packed = packed.contiguous();
     scales = scales.contiguous();
@@ -616,7 +705,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("matmul_int4", &matmul_int4,
           "W4A16 dequant GEMM: fp16 A @ int4 W -> fp32 (or fp16 with out_dtype=torch.float16)",
           py::arg("A"), py::arg("packed"), py::arg("scales"), py::arg("zeros"),
-          py::arg("group_size") = 128, py::arg("out_dtype") = py::none());
+          py::arg("group_size") = 128, py::arg("out_dtype") = py::none(),
+          py::arg("perm") = py::none());
+    m.def("int4_from_gptq", &int4_from_gptq,
+          "GPTQ qweight [K/8,N] / qzeros [K/G,N/8] (+ g_idx) -> (qweight, packed zeros, perm or None)",
+          py::arg("qweight"), py::arg("qzeros"), py::arg("g_idx") = py::none(),
+          py::arg("zero_format") = "v1");
     m.def("int4_from_awq", &int4_from_awq,
           "AutoAWQ qweight [K,N/8] / qzeros [K/G,N/8] -> GPTQ-layout qweight and packed zeros",
           py::arg("qweight"), py::arg("qzeros"));

@@ -133,6 +133,53 @@ int4_from_awq_kernel(const int32_t* __restrict__ qw, const int32_t* __restrict__
     }
 }
 
+// GPTQ checkpoint zero points to this library's packed zeros.  AutoGPTQ's "gptq" (v1)
+// format packs z - 1 into the nibbles of qzeros [K/G][N/8] (nibble n%8 of word n/8, the
+// layout of WMMA_ZEROS_PACKED) and dequantises with stored + 1; its "gptq_v2" format (and
+// this library) stores z itself.  add = 1 (v1) or 0 (v2) is added to every nibble; a v1
+// nibble of 15 stands for z = 16, which four bits cannot hold: such a word sets *overflow
+// to 1 (a plain store of the same value from every writer, never cleared here).
+__global__ void __launch_bounds__(256)
+int4_gptq_zeros_kernel(const int32_t* __restrict__ qz, int64_t words, uint32_t add,
+                       int32_t* __restrict__ out, int32_t* __restrict__ overflow) {
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < words;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const uint32_t src = (uint32_t)qz[t];
+        uint32_t word = 0;
+        bool over = false;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t z = ((src >> (4 * j)) & 0xFu) + add;
+            over |= z > 15u;
+            word |= (z & 0xFu) << (4 * j);
+        }
+        out[t] = (int32_t)word;
+        if (over && overflow) *overflow = 1;
+    }
+}
+
+// Row permutation of GPTQ-layout weights (act-order checkpoints): output row k is input row
+// perm[k] (perm entries clamped into [0, K)).  One thread per output word (8 rows of one
+// column), coalesced along n.
+__global__ void __launch_bounds__(256)
+int4_permute_rows_kernel(const int32_t* __restrict__ qw, const int32_t* __restrict__ perm, int K,
+                         int N, int32_t* __restrict__ out) {
+    const int64_t total = (int64_t)(K / 8) * N;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t k8 = t / N;
+        const int n = (int)(t % N);
+        uint32_t word = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int src = min(max(perm[8 * k8 + j], 0), K - 1);
+            const uint32_t v = (uint32_t)qw[(int64_t)(src >> 3) * N + n];
+            word |= ((v >> (4 * (src & 7))) & 0xFu) << (4 * j);
+        }
+        out[t] = (int32_t)word;
+    }
+}
+
 // Group parameters to the slice-major layout (WMMA_ZEROS_SLICED): one thread per
 // (16-column slice, group) writes the slice's 16 scales and its two zero words.
 template <int ZF>
@@ -558,19 +605,20 @@ w4a16_decode_kernel(W4Args p) {
 //
 // The multiply-accumulate runs on v_mfma_f32_16x16x32_f16, with the scale and zero point
 // applied to each pair-step's partial sum rather than to every weight:
-//   A operand (lane l: row l%16 = activation row m, K quarter l/16): the activations a',
-//     where a' = a at offsets {0,1,4,5} and a/16 at {2,3,6,7} of every 8 values;
+//   A operand (lane l: row l%16 = activation row m, K quarter l/16): the activations a,
+//     unchanged;
 //   B operand (lane l: column l%16 = slice column n, same K quarter): the raw nibbles of
 //     one prepacked word as fp16.  (w & 0x000F000F) | 0x6400.. is the exact fp16 pair
-//     (1024 + q0, 1024 + q1); the pairs at offsets {2,3,6,7} come out of
-//     (w & 0x00F000F0) | 0x6400.. as 1024 + 16 q, which the a/16 of the A operand turns
-//     back into 64 + q.  One shift and four v_and_or per 8 weights.
+//     (1024 + q0, 1024 + q1) (ulp 1 at 1024); the nibbles at offsets {2,3,6,7} sit four
+//     bits higher, and (w & 0x00F000F0) | 0x5400.. reads them as 64 + q (ulp 1/16 at 64).
+//     One shift and four v_and_or per 8 weights.
 //   Per pair-step t (128 values of K, inside one group g):
-//     sum_k a_k (q_k - z) s = s (D_t - 1024 P_t - z Q_t),
-//     D_t = sum a' B (four MFMAs into a fresh accumulator), P_t = sum a', Q_t = sum a.
+//     sum_k a_k (q_k - z) s = s (D_t - P_t - z Q_t),
+//     D_t = sum a B (four MFMAs into a fresh accumulator), P_t = 1024 sum_{0,1,4,5} a +
+//     64 sum_{2,3,6,7} a, Q_t = sum a.
 //   The lane that loaded pair-step t's activation chunk sums its 8 values (v_dot2 against
 //   ones), a 16-lane DPP reduction gives P_t and Q_t for the whole pair-step, and that same
-//   lane holds s and z of (t, its column), so it adds s (1024 P_t + z Q_t) to a private
+//   lane holds s and z of (t, its column), so it adds s (P_t + z Q_t) to a private
 //   correction that is reduced once at the end.  The products are exact and the sums are
 //   fp32, so the result differs from the fp16-rounded dequantised weights of the definition
 //   by at most their rounding (2^-11 of each weight).
@@ -655,8 +703,8 @@ w4a16_decode_mfma_kernel(W4Args p) {
         }
     };
 
-    uint32_t magic = 0x64006400u;
-    asm volatile("" : "+v"(magic));  // keep the constant in a VGPR: one v_and_or per pair
+    uint32_t magic = 0x64006400u, magic_hi = 0x54005400u;
+    asm volatile("" : "+v"(magic), "+v"(magic_hi));  // constants in VGPRs: one v_and_or per pair
     // DEFER: scale and zero applied per pair-step (fewer VALU operations for one or two
     // rows; from three rows on the per-row sums cost as much as they save).
     constexpr bool DEFER = MM <= 2;
@@ -683,14 +731,8 @@ w4a16_decode_mfma_kernel(W4Args p) {
                 P[m] = row16_sum(__builtin_fmaf(e2, 64.0f, e1 * 1024.0f));
                 Q[m] = row16_sum(e1 + e2);
             }
-            // stage a' (this lane's chunk of row m)
-            f16x8 a = as_f16x8(R.a[m]);
-#pragma unroll
-            for (int e = 2; e < 8; e += 4) {
-                a[e] = a[e] * (f16)0.0625f;
-                a[e + 1] = a[e + 1] * (f16)0.0625f;
-            }
-            *reinterpret_cast<u32x4*>(buf + m * DM_ROW + 128 * sub + 8 * col) = as_u32x4(a);
+            // stage this lane's chunk of row m
+            *reinterpret_cast<u32x4*>(buf + m * DM_ROW + 128 * sub + 8 * col) = R.a[m];
         }
         uint32_t rs = R.s, rz = R.z;
         asm volatile("" : "+v"(rs), "+v"(rz));  // no work on them hoisted up to their load
@@ -714,23 +756,23 @@ w4a16_decode_mfma_kernel(W4Args p) {
             const int pp = wave + DM_NW * (DM_U * r + u);
             if (pp < KP) {
                 const uint32_t zz = v >> 16, s = v & 0xFFFFu;
-                const uint32_t z1 = 0x6400u | zz, z16 = 0x6400u | (zz << 4);
-                const f16x2 zs1 = as_h2(z1 | (z1 << 16)), zs16 = as_h2(z16 | (z16 << 16));
+                const uint32_t z1 = 0x6400u | zz, zhi = 0x5400u | (zz << 4);
+                const f16x2 zs1 = as_h2(z1 | (z1 << 16)), zshi = as_h2(zhi | (zhi << 16));
                 const f16x2 ss = as_h2(s | (s << 16));
                 f32x4 acc = DEFER ? f32x4{} : d;
 #pragma unroll
                 for (int w = 0; w < 4; ++w) {
                     const uint32_t x = R.w[u][w], x8 = x >> 8;
                     u32x4 bv;
-                    bv[0] = (x & 0x000F000Fu) | magic;
-                    bv[1] = (x & 0x00F000F0u) | magic;
+                    bv[0] = (x & 0x000F000Fu) | magic;       // 1024 + q
+                    bv[1] = (x & 0x00F000F0u) | magic_hi;    // 64 + q
                     bv[2] = (x8 & 0x000F000Fu) | magic;
-                    bv[3] = (x8 & 0x00F000F0u) | magic;
-                    if constexpr (!DEFER) {  // W = fp16((q - z) s), 16 W at {2,3,6,7}
+                    bv[3] = (x8 & 0x00F000F0u) | magic_hi;
+                    if constexpr (!DEFER) {  // W = fp16((q - z) s)
                         bv[0] = as_u32((as_h2(bv[0]) - zs1) * ss);
-                        bv[1] = as_u32((as_h2(bv[1]) - zs16) * ss);
+                        bv[1] = as_u32((as_h2(bv[1]) - zshi) * ss);
                         bv[2] = as_u32((as_h2(bv[2]) - zs1) * ss);
-                        bv[3] = as_u32((as_h2(bv[3]) - zs16) * ss);
+                        bv[3] = as_u32((as_h2(bv[3]) - zshi) * ss);
                     }
                     const f16x8 av = as_f16x8(*reinterpret_cast<const u32x4*>(arow + 128 * u + 8 * w));
                     acc = mfma16(av, as_f16x8(bv), acc);
@@ -807,12 +849,12 @@ void launch_decode_mfma(const W4Args& a, int M, dim3 grid, dim3 block, size_t ld
 //    activation fragment feeds two MFMAs;
 //  * the activations come straight from L2 into registers in the MFMA A-operand layout --
 //    lane l: row 16*b + l%16 (clamped to M-1; those rows are never stored), K quarter l/16,
-//    i.e. 64 contiguous bytes per lane per pair-step -- then a' = a with offsets {2,3,6,7}
-//    of every 8 scaled by 1/16 (two v_pk_mul) to cancel the 16x of those weight pairs;
+//    i.e. 64 contiguous bytes per lane per pair-step;
 //  * SK_U pair-steps per wave; when the 32-column tiles alone cannot fill the chip the K
 //    range is split over blockIdx.y (SK_NW * SK_U pair-steps per split) and the partials
 //    go to the workspace for w4a16_reduce_kernel.
-// The B operand is the decode kernel's: W = fp16((q - z) s) rounded once per weight.
+// The B operand is the decode kernel's nibble encoding (1024 + q, and 64 + q at offsets
+// {2,3,6,7}) less the same encoding of z, times s: W = fp16((q - z) s), one rounding.
 //  * NT = 2 puts two adjacent 32-column tiles in one workgroup: every activation fragment
 //    feeds four MFMAs and the activation bytes a CU reads per weight byte halve (at
 //    M = 16 they are twice the weight bytes of a one-tile workgroup).
@@ -880,8 +922,8 @@ w4a16_skinny_kernel(W4Args p) {
             z = zraw[sc] & 0xFu;
         sz[sc] = (int)(sraw[sc] | (z << 16));
     }
-    uint32_t magic = 0x64006400u;
-    asm volatile("" : "+v"(magic));
+    uint32_t magic = 0x64006400u, magic_hi = 0x54005400u;
+    asm volatile("" : "+v"(magic), "+v"(magic_hi));
     f32x4 d[MB][NH];
 #pragma unroll
     for (int b = 0; b < MB; ++b)
@@ -897,28 +939,21 @@ w4a16_skinny_kernel(W4Args p) {
 #pragma unroll
             for (int b = 0; b < MB; ++b)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    a[b][q] = as_f16x8(av[u][b][q]);
-#pragma unroll
-                    for (int e = 2; e < 8; e += 4) {
-                        a[b][q][e] = a[b][q][e] * (f16)0.0625f;
-                        a[b][q][e + 1] = a[b][q][e + 1] * (f16)0.0625f;
-                    }
-                }
+                for (int q = 0; q < 4; ++q) a[b][q] = as_f16x8(av[u][b][q]);
 #pragma unroll
             for (int sc = 0; sc < NH; ++sc) {
                 const uint32_t zz = v[sc] >> 16, s = v[sc] & 0xFFFFu;
-                const uint32_t z1 = 0x6400u | zz, z16 = 0x6400u | (zz << 4);
-                const f16x2 zs1 = as_h2(z1 | (z1 << 16)), zs16 = as_h2(z16 | (z16 << 16));
+                const uint32_t z1 = 0x6400u | zz, zhi = 0x5400u | (zz << 4);
+                const f16x2 zs1 = as_h2(z1 | (z1 << 16)), zshi = as_h2(zhi | (zhi << 16));
                 const f16x2 ss = as_h2(s | (s << 16));
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const uint32_t x = wv[u][sc][q], x8 = x >> 8;
                     u32x4 bv;
                     bv[0] = as_u32((as_h2((x & 0x000F000Fu) | magic) - zs1) * ss);
-                    bv[1] = as_u32((as_h2((x & 0x00F000F0u) | magic) - zs16) * ss);
+                    bv[1] = as_u32((as_h2((x & 0x00F000F0u) | magic_hi) - zshi) * ss);
                     bv[2] = as_u32((as_h2((x8 & 0x000F000Fu) | magic) - zs1) * ss);
-                    bv[3] = as_u32((as_h2((x8 & 0x00F000F0u) | magic) - zs16) * ss);
+                    bv[3] = as_u32((as_h2((x8 & 0x00F000F0u) | magic_hi) - zshi) * ss);
 #pragma unroll
                     for (int b = 0; b < MB; ++b) d[b][sc] = mfma16(a[b][q], as_f16x8(bv), d[b][sc]);
                 }
@@ -1136,11 +1171,13 @@ w4a16_gemm_kernel(W4Args p) {
         L.a_addr[i] = r * 128;
         L.a_sw[i] = swz8(r);
     }
+    // The weight resource starts at the workgroup's first 32-column tile, so weight offsets
+    // stay below (BN / 32) * K * 16 bytes whatever the size of the whole matrix.
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
         const int n = n0 + wn * TN + 32 * j + (lane & 31);
         const bool ok = n < p.N;
-        const int ntile = n >> 5;
+        const int ntile = (n >> 5) - (n0 >> 5);
         L.w_off[j] = ok ? (uint32_t)(((int64_t)ntile * KC * 64 + lane) * 16) : kOobOffset;
         // scale / zero byte offsets at group 0
         L.s_off[j] = ok ? (uint32_t)(s_index<ZF>(p, 0, n) * 2) : kOobOffset;
@@ -1150,7 +1187,7 @@ w4a16_gemm_kernel(W4Args p) {
             L.z_off[j] = ok ? (uint32_t)n : kOobOffset;
     }
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A + (int64_t)m0 * p.lda);
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W + (int64_t)(n0 >> 5) * KC * 64);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.S);
     const __amdgpu_buffer_rsrc_t rz = make_rsrc(p.Z);
 
@@ -1419,6 +1456,22 @@ hipError_t launch_int4_from_awq(const int32_t* qweight_awq, const int32_t* qzero
     const int64_t total = (int64_t)(K / 8) * N + (int64_t)KG * (N / 8);
     hipLaunchKernelGGL(int4_from_awq_kernel, dim3(grid_for(total, 256)), dim3(256), 0, stream,
                        qweight_awq, qzeros_awq, K, N, KG, qweight, zeros);
+    return hipGetLastError();
+}
+
+hipError_t launch_int4_gptq_zeros(const int32_t* qzeros, int KG, int N, int add, int32_t* zeros,
+                                  int32_t* overflow, hipStream_t stream) {
+    const int64_t words = (int64_t)KG * (N / 8);
+    hipLaunchKernelGGL(int4_gptq_zeros_kernel, dim3(grid_for(words, 256)), dim3(256), 0, stream,
+                       qzeros, words, (uint32_t)add, zeros, overflow);
+    return hipGetLastError();
+}
+
+hipError_t launch_int4_permute_rows(const int32_t* qweight, const int32_t* perm, int K, int N,
+                                    int32_t* out, hipStream_t stream) {
+    const int64_t total = (int64_t)(K / 8) * N;
+    hipLaunchKernelGGL(int4_permute_rows_kernel, dim3(grid_for(total, 256)), dim3(256), 0, stream,
+                       qweight, perm, K, N, out);
     return hipGetLastError();
 }
 
