@@ -95,6 +95,23 @@ int wmma_gemm_f16f32(const void* A, int64_t lda, const void* B, int64_t ldb,
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Allocation-free variant of wmma_gemm_f16f32: the same computation, kernels and plan, but
+ * no workspace argument -- the split-K partial sums go to a device array inside this
+ * library (wmma_gemm_noalloc_scratch_bytes() = 32 MiB per GPU, held until the process
+ * ends), so the call performs no allocation of any kind.  A shape whose plan needs more
+ * partial-sum space than that is rejected with WMMA_ERR_WORKSPACE (wmma_gemm_workspace_size
+ * gives the need).  Every call on one GPU shares that GPU's array and nothing in it has to
+ * start at zero (each split writes its whole partial tile before the reduction reads it);
+ * calls that overlap on one GPU (other streams, other threads) race on it and must be
+ * serialised by the caller.  No counterpart in the reference: for callers that cannot
+ * allocate (code under stream capture, tight serving loops, harnesses that forbid it).
+ */
+int wmma_gemm_f16f32_noalloc(const void* A, int64_t lda, const void* B, int64_t ldb,
+                             const float* C_in, int64_t ldc_in, float* C_out, int64_t ldc, int M,
+                             int N, int K, float alpha, float beta, int tile_cfg, void* stream);
+size_t wmma_gemm_noalloc_scratch_bytes(void);
+
+/*
  * Explicit plans.  wmma_gemm_plan_custom builds the plan of one kernel (WMMA_KERNEL_*),
  * tile (WMMA_TILE_*, ignored by the skinny kernel) and K split for a shape, completed as
  * the planner completes its own; wmma_gemm_f16f32_plan runs wmma_gemm_f16f32 with such a

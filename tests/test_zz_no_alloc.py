@@ -1,0 +1,86 @@
+"""The allocation-free GEMM entry point, wmma_gemm_f16f32_noalloc, against wmma_gemm_f16f32.
+
+Both run the same plan and kernels; the only difference is where the split-K partial sums
+live (the library's own device array instead of a caller workspace), so every output must
+be bit-identical, and within the oracle's 1e-3 max-relative bound.  Each case makes two
+calls in a row, the second on a smaller shape, so the second call runs on a scratch array
+still holding the first call's partial sums.
+"""
+import ctypes
+import os
+
+import pytest
+import torch
+
+from oracle import gemm as og
+from tests.conftest import report
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _lib():
+    lib = ctypes.CDLL(os.path.join(ROOT, "wmma_ops_amd", "libwmma_ops_amd.so"))
+    vp, i64, i32, f32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    lib.wmma_last_error.restype = ctypes.c_char_p
+    lib.wmma_gemm_workspace_size.restype = sz
+    lib.wmma_gemm_workspace_size.argtypes = [i32, i32, i32, i32]
+    lib.wmma_gemm_noalloc_scratch_bytes.restype = sz
+    lib.wmma_gemm_f16f32.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32,
+                                     f32, f32, i32, vp, sz, vp]
+    lib.wmma_gemm_f16f32_noalloc.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32,
+                                             f32, f32, i32, vp]
+    return lib
+
+
+# (first, second): the second call is smaller.  Plans: tiled 128x128 split 2 (14 MiB of
+# partial sums) then skinny split 8; the tuned tiled split 8 (16 MiB) then skinny split 8;
+# tiled 64x64 split 4 then a ragged skinny split; a shape without a split (no scratch).
+PAIRS = [((128, 14336, 4096), (16, 4096, 4096)),
+         ((128, 4096, 14336), (1, 4096, 4096)),
+         ((64, 4096, 4096), (3, 1024, 520)),
+         ((1024, 1024, 1024), (300, 264, 640))]
+
+
+@pytest.mark.parametrize("first,second", PAIRS)
+def test_noalloc_matches_workspace_entry_point(first, second):
+    lib = _lib()
+    cap = lib.wmma_gemm_noalloc_scratch_bytes()
+    stream = torch.cuda.current_stream().cuda_stream
+    for (M, N, K) in (first, second):
+        report("noalloc", M=M, N=N, K=K)
+        need = lib.wmma_gemm_workspace_size(M, N, K, -1)
+        assert need <= cap
+        g = torch.Generator().manual_seed(M + N + K)
+        A = torch.randn(M, K, generator=g).half()
+        B = (torch.randn(K, N, generator=g) * 0.05).half()
+        C0 = torch.randn(M, N, generator=g)
+        Ad, Bd = A.cuda(), B.cuda()
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+        for alpha, beta, in_place in [(1.0, 0.0, False), (2.0, 0.5, False), (2.0, 0.5, True)]:
+            Cref = C0.cuda()
+            Cna = C0.cuda()
+            out_ref = Cref if in_place else torch.empty(M, N, device="cuda")
+            out_na = Cna if in_place else torch.empty(M, N, device="cuda")
+            rc = lib.wmma_gemm_f16f32(Ad.data_ptr(), K, Bd.data_ptr(), N, Cref.data_ptr(), N,
+                                      out_ref.data_ptr(), N, M, N, K, alpha, beta, -1,
+                                      ws.data_ptr() if need else None, need, stream)
+            assert rc == 0, lib.wmma_last_error()
+            rc = lib.wmma_gemm_f16f32_noalloc(Ad.data_ptr(), K, Bd.data_ptr(), N, Cna.data_ptr(), N,
+                                              out_na.data_ptr(), N, M, N, K, alpha, beta, -1, stream)
+            assert rc == 0, lib.wmma_last_error()
+            torch.cuda.synchronize()
+            assert torch.equal(out_na, out_ref), (M, N, K, alpha, beta, in_place)
+            ref = og.gemm_ref(A, B, alpha, beta, C0 if beta != 0.0 else None)
+            assert og.max_rel_err(out_na, ref) <= 1e-3
+
+
+def test_noalloc_scratch_covers_baseline_shapes():
+    # every configs[1]/configs[2] GEMM shape fits the scratch array
+    lib = _lib()
+    cap = lib.wmma_gemm_noalloc_scratch_bytes()
+    shapes = [(m, n, 4096) for m in (1, 16, 64, 128) for n in (4096, 11008, 14336)] + \
+             [(m, 4096, 14336) for m in (1, 16, 64, 128)] + \
+             [(s, s, s) for s in (512, 1024, 2048, 4096)] + [(4096, 4096, 2048)]
+    for (M, N, K) in shapes:
+        assert lib.wmma_gemm_workspace_size(M, N, K, -1) <= cap, (M, N, K)

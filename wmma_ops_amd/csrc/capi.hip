@@ -60,6 +60,36 @@ constexpr int64_t kMaxOffset = 0x7fffffffLL;
 
 }  // namespace
 
+// Scratch of the allocation-free GEMM entry point (wmma_gemm_f16f32_noalloc): the split-K
+// partial sums live in this file-scope device array instead of a caller workspace.  Each
+// GPU the library runs on holds its own copy, at its own address, until the process ends.
+// In host code `scratch` names a host-side stand-in, never the device memory: the device
+// address is fetched once per device with hipGetSymbolAddress and only that is used.
+constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_rc[kMaxDevices];
+std::once_flag g_scratch_once[kMaxDevices];
+
+// Device address of `scratch` on the current device (once per device, with it current).
+int scratch_for_current_device(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(WMMA_ERR_UNSUPPORTED, "device index %d", dev);
+    std::call_once(g_scratch_once[dev], [dev] {
+        void* ptr = nullptr;
+        g_scratch_rc[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        g_scratch_ptr[dev] = g_scratch_rc[dev] == hipSuccess ? ptr : nullptr;
+    });
+    if (g_scratch_rc[dev] != hipSuccess) return hip_status(g_scratch_rc[dev], "hipGetSymbolAddress(scratch)");
+    *out = g_scratch_ptr[dev];
+    return WMMA_OK;
+}
+}  // namespace
+
 extern "C" {
 
 const char* wmma_last_error(void) { return g_last_error.c_str(); }
@@ -95,12 +125,15 @@ size_t wmma_gemm_workspace_size(int M, int N, int K, int tile_cfg) {
     return p.workspace_bytes;
 }
 
-// Shared checks and launch of wmma_gemm_f16f32 / wmma_gemm_f16f32_plan.  `plan` is NULL
-// for the planner's own plan (tile_cfg), else an explicit plan for exactly this shape.
+// Shared checks and launch of wmma_gemm_f16f32 / wmma_gemm_f16f32_plan /
+// wmma_gemm_f16f32_noalloc.  `plan` is NULL for the planner's own plan (tile_cfg), else an
+// explicit plan for exactly this shape.  use_scratch: the split-K partials go to the
+// library's own scratch array (the caller passes no workspace).
 static int gemm_run(const void* A, int64_t lda, const void* B, int64_t ldb, const float* C_in,
                     int64_t ldc_in, float* C_out, int64_t ldc, int M, int N, int K, float alpha,
                     float beta, int tile_cfg, const wmma_gemm_plan* explicit_plan,
-                    void* workspace, size_t workspace_bytes, void* stream) {
+                    void* workspace, size_t workspace_bytes, void* stream,
+                    bool use_scratch = false) {
     if (M < 0 || N < 0 || K < 0) return fail(WMMA_ERR_INVALID_ARG, "negative GEMM dimension");
     if (tile_cfg < WMMA_TILE_AUTO || tile_cfg >= WMMA_TILE_COUNT)
         return fail(WMMA_ERR_INVALID_ARG,
@@ -134,6 +167,15 @@ static int gemm_run(const void* A, int64_t lda, const void* B, int64_t ldb, cons
     } else {
         int rc = make_plan(M, N, K, tile_cfg, current_cus(), &plan);
         if (rc != WMMA_OK) return fail(rc, "planner rejected the shape");
+    }
+    if (use_scratch && plan.workspace_bytes > 0) {
+        if (plan.workspace_bytes > kScratchBytes)
+            return fail(WMMA_ERR_WORKSPACE,
+                        "split-K needs %zu bytes of scratch; the allocation-free entry point "
+                        "holds at most %zu (use wmma_gemm_f16f32 with a workspace)",
+                        plan.workspace_bytes, kScratchBytes);
+        if (int rc = scratch_for_current_device(&workspace)) return rc;
+        workspace_bytes = kScratchBytes;
     }
     if (plan.workspace_bytes > 0) {
         if (!workspace)
@@ -173,6 +215,15 @@ int wmma_gemm_f16f32(const void* A, int64_t lda, const void* B, int64_t ldb, con
     return gemm_run(A, lda, B, ldb, C_in, ldc_in, C_out, ldc, M, N, K, alpha, beta, tile_cfg,
                     nullptr, workspace, workspace_bytes, stream);
 }
+
+int wmma_gemm_f16f32_noalloc(const void* A, int64_t lda, const void* B, int64_t ldb,
+                             const float* C_in, int64_t ldc_in, float* C_out, int64_t ldc, int M,
+                             int N, int K, float alpha, float beta, int tile_cfg, void* stream) {
+    return gemm_run(A, lda, B, ldb, C_in, ldc_in, C_out, ldc, M, N, K, alpha, beta, tile_cfg,
+                    nullptr, nullptr, 0, stream, /*use_scratch=*/true);
+}
+
+size_t wmma_gemm_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
 int wmma_gemm_plan_custom(int M, int N, int K, int kernel, int tile_cfg, int split_k,
                           wmma_gemm_plan* out) {
