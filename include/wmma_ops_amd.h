@@ -131,8 +131,10 @@ int wmma_gemm_f16f32_plan(const void* A, int64_t lda, const void* B, int64_t ldb
  * INT4 weights.  The reference has no INT4 code; the layout is this library's own.
  * "GPTQ layout": qweight is int32 [K/8, N]; weight q[k][n] (0..15) sits in bits
  * 4*(k%8) .. 4*(k%8)+3 of qweight[k/8][n].  K % 64 == 0 and N % 32 == 0 are required.
- * Prepacked layout: int32 [N/32][K/64][64 lanes][4]; lane l of block (nt, kc) holds
- * column n = 32*nt + l%32 and the four GPTQ words of k-groups 8*kc + 4*(l/32) + 0..3.
+ * Prepacked layout: int32 [N/16][K/64][32][4]; entry l of block kc of 16-column slice s
+ * holds column n = 16*s + l%16 and the four GPTQ words of k-groups 8*kc + 4*(l/16) + 0..3,
+ * each with its nibbles reordered to k-offsets {0,2,4,6,1,3,5,7}.  A slice's weights are
+ * one contiguous run over all of K.
  */
 int wmma_int4_prepack(const int32_t* qweight, int K, int N, int32_t* packed, void* stream);
 /* Inverse of wmma_int4_prepack (prepacked layout back to the GPTQ layout). */

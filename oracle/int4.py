@@ -6,8 +6,8 @@ are the task's W4A16 definition and this library's written layout specification
 
   GPTQ qweight  int32 [K/8, N]; q[k][n] = (qweight[k//8][n] >> 4*(k%8)) & 0xF
   packed zeros  int32 [K/G, N/8]; z[g][n] = (zeros[g][n//8] >> 4*(n%8)) & 0xF
-  prepacked     int32 [N/32][K/64][64][4]; block (nt, kc), lane l, word w holds the
-                GPTQ word of k-group kg = 8*kc + 4*(l//32) + w for column 32*nt + l%32,
+  prepacked     int32 [N/16][K/64][32][4]; slice s, block kc, entry l, word w holds the
+                GPTQ word of k-group kg = 8*kc + 4*(l//16) + w for column 16*s + l%16,
                 with its nibbles reordered: nibble p holds k-offset PERM[p]
   dequant       W[k][n] = fp16((q - z) * s), q - z exact, one rounding to fp16
   W4A16         Y = A.float() @ W.float()   (fp32 accumulate)
@@ -165,28 +165,28 @@ def _permute_word_nibbles(w: np.ndarray, inverse: bool = False) -> np.ndarray:
 
 
 def prepack(qweight: np.ndarray) -> np.ndarray:
-    """GPTQ qweight [K/8, N] -> prepacked int32 [N/32, K/64, 64, 4]."""
+    """GPTQ qweight [K/8, N] -> prepacked int32 [N/16, K/64, 32, 4]."""
     w = np.asarray(qweight).view(np.uint32)
     kg, N = w.shape
     K = kg * 8
     assert K % 64 == 0 and N % 32 == 0
-    KC, NT = K // 64, N // 32
-    # w[kg, n] with kg = 8*kc + 4*h + word, n = 32*nt + c  ->  out[nt, kc, 32*h + c, word]
-    t = w.reshape(KC, 2, 4, NT, 32)            # [kc, h, word, nt, c]
-    t = t.transpose(3, 0, 1, 4, 2)             # [nt, kc, h, c, word]
+    KC, NS = K // 64, N // 16
+    # w[kg, n] with kg = 8*kc + 4*h + word, n = 16*s + c  ->  out[s, kc, 16*h + c, word]
+    t = w.reshape(KC, 2, 4, NS, 16)            # [kc, h, word, s, c]
+    t = t.transpose(3, 0, 1, 4, 2)             # [s, kc, h, c, word]
     t = _permute_word_nibbles(t)
-    return np.ascontiguousarray(t).reshape(NT, KC, 64, 4).view(np.int32)
+    return np.ascontiguousarray(t).reshape(NS, KC, 32, 4).view(np.int32)
 
 
 def unprepack(packed: np.ndarray) -> np.ndarray:
-    """Inverse of prepack: int32 [N/32, K/64, 64, 4] -> GPTQ qweight [K/8, N]."""
+    """Inverse of prepack: int32 [N/16, K/64, 32, 4] -> GPTQ qweight [K/8, N]."""
     p = np.asarray(packed).view(np.uint32)
-    NT, KC = p.shape[0], p.shape[1]
-    assert p.shape == (NT, KC, 64, 4)
-    kg, N = KC * 8, NT * 32
-    t = p.reshape(NT, KC, 2, 32, 4)            # [nt, kc, h, c, word]
+    NS, KC = p.shape[0], p.shape[1]
+    assert p.shape == (NS, KC, 32, 4)
+    kg, N = KC * 8, NS * 16
+    t = p.reshape(NS, KC, 2, 16, 4)            # [s, kc, h, c, word]
     t = _permute_word_nibbles(t, inverse=True)
-    t = t.transpose(1, 2, 4, 0, 3)             # [kc, h, word, nt, c]
+    t = t.transpose(1, 2, 4, 0, 3)             # [kc, h, word, s, c]
     return np.ascontiguousarray(t).reshape(kg, N).view(np.int32)
 
 

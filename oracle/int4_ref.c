@@ -4,9 +4,9 @@
  * numpy restatement in oracle/int4.py so the two can check each other.
  *
  * GPTQ qweight int32 [K/8][N]: q[k][n] = (qweight[k/8][n] >> 4*(k%8)) & 15.
- * Prepacked int32 [N/32][K/64][64][4]: lane l, word w of block (nt, kc) is the GPTQ word of
- * k-group 8*kc + 4*(l/32) + w, column 32*nt + l%32, with nibble p holding k-offset
- * perm[p] = {0,2,4,6,1,3,5,7}[p].
+ * Prepacked int32 [N/16][K/64][32][4]: entry l, word w of block kc of 16-column slice s is
+ * the GPTQ word of k-group 8*kc + 4*(l/16) + w, column 16*s + l%16, with nibble p holding
+ * k-offset perm[p] = {0,2,4,6,1,3,5,7}[p].
  * dequant: fp16((q - z) * s) -- computed here from the fp16 bit pattern of s by exact
  * integer arithmetic and an explicit round-to-nearest-even to fp16.
  */
@@ -26,14 +26,14 @@ void oracle_int4_pack_gptq(const uint8_t* q, int K, int N, int32_t* qweight) {
 }
 
 void oracle_int4_prepack(const int32_t* qweight, int K, int N, int32_t* out) {
-    const int KC = K / 64, NT = N / 32;
+    const int KC = K / 64, NS = N / 16;
     size_t idx = 0;
-    for (int nt = 0; nt < NT; ++nt)
+    for (int s = 0; s < NS; ++s)
         for (int kc = 0; kc < KC; ++kc)
-            for (int l = 0; l < 64; ++l)
+            for (int l = 0; l < 32; ++l)
                 for (int w = 0; w < 4; ++w) {
-                    const int kg = 8 * kc + 4 * (l / 32) + w;
-                    const int n = 32 * nt + l % 32;
+                    const int kg = 8 * kc + 4 * (l / 16) + w;
+                    const int n = 16 * s + l % 16;
                     const uint32_t src = (uint32_t)qweight[(size_t)kg * N + n];
                     uint32_t dst = 0;
                     for (int p = 0; p < 8; ++p) dst |= ((src >> (4 * kPerm[p])) & 15u) << (4 * p);

@@ -134,7 +134,7 @@ def test_prepack_bijection_and_c_restatement(K, N):
     q = _rand_q(K, N, K + N)
     qw = oi.pack_gptq(q)
     pk = oi.prepack(qw)
-    assert pk.shape == (N // 32, K // 64, 64, 4) and pk.dtype == np.int32
+    assert pk.shape == (N // 16, K // 64, 32, 4) and pk.dtype == np.int32
     assert np.array_equal(oi.unprepack(pk), qw)
     assert np.array_equal(cref.prepack(qw).reshape(pk.shape), pk)  # independent C restatement
     # same multiset of nibbles
@@ -143,16 +143,16 @@ def test_prepack_bijection_and_c_restatement(K, N):
 
 
 def test_prepack_layout_spot_values():
-    # block (nt, kc), lane l, word w <- GPTQ word kg = 8*kc + 4*(l//32) + w, column 32*nt + l%32,
-    # nibble p holds k-offset PERM[p].
+    # slice s, block kc, entry l, word w <- GPTQ word kg = 8*kc + 4*(l//16) + w, column
+    # 16*s + l%16, nibble p holds k-offset PERM[p].
     K, N = 128, 64
     q = _rand_q(K, N, 11)
     qw = oi.pack_gptq(q)
-    pk = oi.prepack(qw).view(np.uint32).reshape(N // 32, K // 64, 64, 4)
-    for (nt, kc, l, w) in [(0, 0, 0, 0), (1, 1, 63, 3), (0, 1, 33, 2), (1, 0, 17, 1)]:
-        kg = 8 * kc + 4 * (l // 32) + w
-        n = 32 * nt + l % 32
-        word = int(pk[nt, kc, l, w])
+    pk = oi.prepack(qw).view(np.uint32).reshape(N // 16, K // 64, 32, 4)
+    for (sl, kc, l, w) in [(0, 0, 0, 0), (3, 1, 31, 3), (1, 1, 17, 2), (2, 0, 9, 1)]:
+        kg = 8 * kc + 4 * (l // 16) + w
+        n = 16 * sl + l % 16
+        word = int(pk[sl, kc, l, w])
         for p, koff in enumerate(oi.PERM):
             assert (word >> (4 * p)) & 0xF == q[8 * kg + koff, n]
 

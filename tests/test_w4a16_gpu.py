@@ -18,7 +18,8 @@ def test_golden_fixture_bit_exact(wo):
     d = np.load(GOLDEN)
     qw = torch.from_numpy(d["qweight"]).cuda()
     K, N = d["q"].shape
-    packed = d["packed"].reshape(N // 32, K // 64, 64, 4)  # the fixture stores it flat
+    packed = d["packed"]
+    assert packed.shape == (N // 16, K // 64, 32, 4)
     assert np.array_equal(wo.prepack_int4(qw).cpu().numpy(), packed)
     assert np.array_equal(wo.unpack_int4(qw).cpu().numpy(), d["q"])
     assert np.array_equal(wo.unprepack_int4(torch.from_numpy(packed).cuda()).cpu().numpy(),
@@ -242,7 +243,7 @@ def test_w4a16_integer_weights_exact(wo):
 
 
 def test_w4a16_errors(wo):
-    pk = torch.zeros(2, 1, 64, 4, dtype=torch.int32, device="cuda")  # prepacked K=64, N=64
+    pk = torch.zeros(4, 1, 32, 4, dtype=torch.int32, device="cuda")  # prepacked K=64, N=64
     A = torch.zeros(1, 64, dtype=torch.half, device="cuda")
     s = torch.zeros(1, 64, dtype=torch.half, device="cuda")
     z = torch.zeros(1, 8, dtype=torch.int32, device="cuda")

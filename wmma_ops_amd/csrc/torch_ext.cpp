@@ -387,18 +387,18 @@ void check_qweight(const torch::Tensor& q) {
     TORCH_CHECK(q.dim() == 2, "qweight must be 2D [K/8, N]");
 }
 
-// The prepacked weights are int32 [N/32, K/64, 64, 4] (include/wmma_ops_amd.h): a shape of
+// The prepacked weights are int32 [N/16, K/64, 32, 4] (include/wmma_ops_amd.h): a shape of
 // their own, so a GPTQ qweight [K/8, N] passed where prepacked weights belong is rejected
 // instead of being read as garbage.
 void check_packed(const torch::Tensor& pk) {
     TORCH_CHECK(pk.is_cuda(), "packed must be a CUDA tensor");
-    TORCH_CHECK(pk.dtype() == torch::kInt32 && pk.dim() == 4 && pk.size(2) == 64 &&
+    TORCH_CHECK(pk.dtype() == torch::kInt32 && pk.dim() == 4 && pk.size(2) == 32 &&
                     pk.size(3) == 4,
-                "packed must be the int32 [N/32, K/64, 64, 4] output of prepack_int4 (a GPTQ "
+                "packed must be the int32 [N/16, K/64, 32, 4] output of prepack_int4 (a GPTQ "
                 "qweight [K/8, N] must go through prepack_int4 first)");
 }
 
-// prepack_int4(qweight[K/8, N] int32, GPTQ order) -> prepacked int32 [N/32, K/64, 64, 4].
+// prepack_int4(qweight[K/8, N] int32, GPTQ order) -> prepacked int32 [N/16, K/64, 32, 4].
 torch::Tensor prepack_int4(torch::Tensor qweight) {
     check_qweight(qweight);
     const int64_t K = qweight.size(0) * 8, N = qweight.size(1);
@@ -407,19 +407,19 @@ torch::Tensor prepack_int4(torch::Tensor qweight) {
     TORCH_CHECK(N % 32 == 0, "N (", N, ") must be a multiple of 32");
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(qweight.device());
     qweight = qweight.contiguous();
-    auto out = torch::empty({N / 32, K / 64, 64, 4}, qweight.options());
+    auto out = torch::empty({N / 16, K / 64, 32, 4}, qweight.options());
     check_status(wmma_int4_prepack(qweight.data_ptr<int32_t>(), (int)K, (int)N,
                                    out.data_ptr<int32_t>(), current_stream(qweight)),
                  "wmma_int4_prepack");
     return out;
 }
 
-// unprepack_int4(packed [N/32, K/64, 64, 4]) -> GPTQ qweight int32 [K/8, N].
+// unprepack_int4(packed [N/16, K/64, 32, 4]) -> GPTQ qweight int32 [K/8, N].
 torch::Tensor unprepack_int4(torch::Tensor packed) {
     check_packed(packed);
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(packed.device());
     packed = packed.contiguous();
-    const int64_t K = packed.size(1) * 64, N = packed.size(0) * 32;
+    const int64_t K = packed.size(1) * 64, N = packed.size(0) * 16;
     auto out = torch::empty({K / 8, N}, packed.options());
     check_status(wmma_int4_unprepack(packed.data_ptr<int32_t>(), (int)K, (int)N,
                                      out.data_ptr<int32_t>(), current_stream(packed)),
@@ -579,7 +579,7 @@ torch::Tensor matmul_int4(torch::Tensor A, torch::Tensor packed, torch::Tensor s
     TORCH_CHECK(A.dtype() == torch::kFloat16, "A must be float16");
     TORCH_CHECK(A.dim() == 2, "A must be 2D");
     check_packed(packed);
-    const int64_t K = packed.size(1) * 64, N = packed.size(0) * 32;
+    const int64_t K = packed.size(1) * 64, N = packed.size(0) * 16;
     TORCH_CHECK(A.size(1) == K, "Inner dimensions must match");
     TORCH_CHECK(group_size > 0 && K % group_size == 0, "group_size must divide K");
     const int64_t ng = K / group_size;

@@ -6,14 +6,16 @@
 //
 // Layouts
 //   GPTQ qweight   int32 [K/8, N]: q[k][n] in bits 4*(k%8).. of qweight[k/8][n].
-//   prepacked      int32 [N/32][K/64][64 lanes][4 words]: lane l of block (nt, kc) holds
-//                  column n = 32*nt + l%32, words w = 0..3 for k-group
-//                  kg = 8*kc + 4*(l/32) + w (k = 8*kg .. 8*kg+7).  Inside a prepacked word
+//   prepacked      int32 [N/16][K/64][32][4 words]: entry (s, kc, l) of 16-column slice s
+//                  holds column n = 16*s + l%16, words w = 0..3 for k-group
+//                  kg = 8*kc + 4*(l/16) + w (k = 8*kg .. 8*kg+7).  Inside a prepacked word
 //                  nibble p holds k-offset kPerm[p] = {0,2,4,6,1,3,5,7}[p], so that
 //                  (word >> 4i) & 0x000F000F yields the pair (k 2i, k 2i+1) as two 16-bit
-//                  lanes.  One wave reading one block issues a single contiguous 1 KB load,
-//                  and each lane's 16 bytes are exactly the K-contiguous operand of four
-//                  32x32x16 MFMAs for its column.
+//                  lanes.  A slice's weights are one contiguous run over all of K (what a
+//                  decode workgroup streams); a 64-deep block of 32 columns is two 512-byte
+//                  runs, and each lane's 16 bytes are the K-contiguous operand of four
+//                  MFMAs for its column.  pk_index() below gives the 16-byte unit of
+//                  (column, 64-deep block, K half).
 //   scales         fp16 [K/G, N];  zeros int32 [K/G, N/8] (nibble n%8) or uint8 [K/G, N].
 //
 // Dequantisation in registers: (0x6400 | q) is the fp16 value 1024 + q, so
@@ -31,6 +33,11 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 __device__ __forceinline__ uint32_t as_u32(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
 
+// 16-byte unit of the prepacked weights holding column n, 64-deep block kc, K half h.
+__host__ __device__ __forceinline__ int64_t pk_index(int n, int kc, int h, int KC) {
+    return ((int64_t)(n >> 4) * KC + kc) * 32 + 16 * h + (n & 15);
+}
+
 // Nibble position -> k offset inside a prepacked word (and its inverse).
 __constant__ int kPermDev[8] = {0, 2, 4, 6, 1, 3, 5, 7};
 
@@ -40,15 +47,15 @@ __constant__ int kPermDev[8] = {0, 2, 4, 6, 1, 3, 5, 7};
 __global__ void __launch_bounds__(256)
 int4_prepack_kernel(const int32_t* __restrict__ qw, int K, int N, int32_t* __restrict__ out) {
     const int KC = K / 64;
-    const int64_t total = (int64_t)(N / 32) * KC * 64;
+    const int64_t total = (int64_t)(N / 16) * KC * 32;
     for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
          t += (int64_t)gridDim.x * blockDim.x) {
-        const int l = (int)(t & 63);
-        const int64_t blk = t >> 6;
+        const int l = (int)(t & 31);
+        const int64_t blk = t >> 5;
         const int kc = (int)(blk % KC);
-        const int nt = (int)(blk / KC);
-        const int n = 32 * nt + (l & 31);
-        const int kg0 = 8 * kc + 4 * (l >> 5);
+        const int sl = (int)(blk / KC);
+        const int n = 16 * sl + (l & 15);
+        const int kg0 = 8 * kc + 4 * (l >> 4);
         u32x4 v;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
@@ -66,15 +73,15 @@ int4_prepack_kernel(const int32_t* __restrict__ qw, int K, int N, int32_t* __res
 __global__ void __launch_bounds__(256)
 int4_unprepack_kernel(const int32_t* __restrict__ in, int K, int N, int32_t* __restrict__ qw) {
     const int KC = K / 64;
-    const int64_t total = (int64_t)(N / 32) * KC * 64;
+    const int64_t total = (int64_t)(N / 16) * KC * 32;
     for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
          t += (int64_t)gridDim.x * blockDim.x) {
-        const int l = (int)(t & 63);
-        const int64_t blk = t >> 6;
+        const int l = (int)(t & 31);
+        const int64_t blk = t >> 5;
         const int kc = (int)(blk % KC);
-        const int nt = (int)(blk / KC);
-        const int n = 32 * nt + (l & 31);
-        const int kg0 = 8 * kc + 4 * (l >> 5);
+        const int sl = (int)(blk / KC);
+        const int n = 16 * sl + (l & 15);
+        const int kg0 = 8 * kc + 4 * (l >> 4);
         const u32x4 v = reinterpret_cast<const u32x4*>(in)[t];
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
@@ -341,13 +348,13 @@ w4a16_gemv_kernel(W4Args p) {
 #pragma unroll
     for (int m = 0; m < GV_MAXM; ++m) acc[m] = 0.0f;
 
-    const u32x4* wbase = p.W + (int64_t)nt * KC * 64 + lane;
+    const u32x4* wbase = p.W + pk_index(n, 0, h, KC);
     for (int kcb = kc0 + wave; kcb < kc1; kcb += GV_NW * GV_UNROLL) {
         u32x4 wv[GV_UNROLL];
 #pragma unroll
         for (int u = 0; u < GV_UNROLL; ++u) {
             const int kc = kcb + u * GV_NW;
-            if (kc < kc1) wv[u] = __builtin_nontemporal_load(wbase + (int64_t)kc * 64);
+            if (kc < kc1) wv[u] = __builtin_nontemporal_load(wbase + (int64_t)kc * 32);
         }
 #pragma unroll
         for (int u = 0; u < GV_UNROLL; ++u) {
@@ -396,10 +403,10 @@ w4a16_gemv_kernel(W4Args p) {
 }
 
 // ------------------------------------------------------- decode (M <= GV_MAXM, no split) --
-// One workgroup owns a 16-column slice (half of a 32-column prepacked tile) and the whole
-// K range, so no cross-workgroup reduction is needed.  A wave load covers two consecutive
-// 64-deep chunks: lane l reads slice column l%16, chunk 2*pp + l/32, K half (l/16)%2 --
-// all 64 lanes active, 1 KB per instruction in 256-byte runs.  Each wave keeps DV_U loads
+// One workgroup owns a 16-column slice and the whole K range, so no cross-workgroup
+// reduction is needed.  A wave load covers two consecutive 64-deep chunks: lane l reads
+// slice column l%16, chunk 2*pp + l/32, K half (l/16)%2 -- all 64 lanes active, 1 KB of
+// the slice's contiguous weights per instruction.  Each wave keeps DV_U loads
 // of the next round in flight while it dequantises the current one.
 //
 // Arithmetic (VALU is the bottleneck of decode, not HBM): a prepacked word holds the
@@ -458,9 +465,9 @@ w4a16_decode_kernel(W4Args p) {
         }
     }
 
-    const u32x4* wcol = p.W + (int64_t)nt * KC * 64 + 32 * h + 16 * sc + col;
+    const u32x4* wcol = p.W + pk_index(n, 0, h, KC);
     auto load_one = [&](int pp, DecodeRound<MM>& R, int u) {
-        R.w[u] = __builtin_nontemporal_load(wcol + (int64_t)(2 * pp + dc) * 64);
+        R.w[u] = __builtin_nontemporal_load(wcol + (int64_t)(2 * pp + dc) * 32);
         group_load<ZF>(p, (64 * (2 * pp + dc) + 32 * h) / p.G, n, &R.s[u], &R.z[u]);
     };
     auto load_round = [&](int r, DecodeRound<MM>& R) {
@@ -585,11 +592,13 @@ w4a16_decode_kernel(W4Args p) {
 }
 
 // ---------------------------------------------- decode on the matrix pipe (M <= 4) --
-// One workgroup per 16-column slice (half of a 32-column prepacked tile) over the whole K
-// range, so no cross-workgroup reduction.  A wave load covers one 128-deep pair-step pp:
-// lane l reads slice column l%16, chunk 2*pp + l/32, K half (l/16)%2 -- 1 KB per
-// instruction in 256-byte runs.  Wave w owns pair-steps w + DM_NW * j; a round is DM_U of
-// them.
+// One workgroup per 16-column slice over the whole K range, so no cross-workgroup
+// reduction.  A wave load covers one 128-deep pair-step pp: lane l reads slice column
+// l%16, chunk 2*pp + l/32, K half (l/16)%2 -- 1 KB of the slice's contiguous weights per
+// instruction.  A round gives each wave DM_U consecutive pair-steps (wave w: pair-steps
+// DM_NW*DM_U*r + DM_U*w + u), so each wave streams 4 KB in one run: measured on MI355X
+// with the slice-contiguous layout, 7.5 -> 7.0 us at N = 14336 against pair-steps
+// interleaved across the waves.
 //
 // Every wave is self-contained until the final cross-wave sum: it loads the activations of
 // ITS pair-steps only (lane l: chunk l%16 of pair-step l/16 of the round, one 16-byte load
@@ -682,10 +691,13 @@ w4a16_decode_mfma_kernel(W4Args p) {
     // Staging buffers of this wave, each [MM][DM_ROW] halves.
     f16* sbuf = reinterpret_cast<f16*>(dm_smem) + (size_t)wave * dm_nbuf(ONE) * MM * DM_ROW;
 
-    const u32x4* wcol = p.W + (int64_t)nt * KC * 64 + 32 * h + 16 * sc + col;
+    const u32x4* wcol = p.W + pk_index(n, 0, h, KC);
+    // Pair-step u of round r for this wave: each wave streams DM_U consecutive pair-steps
+    // (4 KB of its slice's contiguous weights) per round.
+    auto pstep = [&](int r, int u) { return DM_NW * DM_U * r + DM_U * wave + u; };
     auto load_round = [&](int r, DecodeMRound<MM>& R) {
         // this lane's activation chunk / group parameters: pair-step `sub` of the round
-        const int ppl = min(wave + DM_NW * (DM_U * r + sub), KP - 1);
+        const int ppl = min(pstep(r, sub), KP - 1);
         const int ka = 128 * ppl + 8 * col;
 #pragma unroll
         for (int m = 0; m < MM; ++m)
@@ -698,8 +710,8 @@ w4a16_decode_mfma_kernel(W4Args p) {
             R.z = static_cast<const uint8_t*>(p.Z)[z_index<ZF>(p, g, n)];
 #pragma unroll
         for (int u = 0; u < DM_U; ++u) {
-            const int pp = min(wave + DM_NW * (DM_U * r + u), KP - 1);
-            R.w[u] = __builtin_nontemporal_load(wcol + (int64_t)(2 * pp + dc) * 64);
+            const int pp = min(pstep(r, u), KP - 1);
+            R.w[u] = __builtin_nontemporal_load(wcol + (int64_t)(2 * pp + dc) * 32);
         }
     };
 
@@ -716,7 +728,7 @@ w4a16_decode_mfma_kernel(W4Args p) {
     const f16x2 ones = {(f16)1.0f, (f16)1.0f};
     auto compute_round = [&](int r, const DecodeMRound<MM>& R, f16* buf) {
         // This lane's pair-step: its activation chunk, scale and zero.
-        const bool lane_live = wave + DM_NW * (DM_U * r + sub) < KP;
+        const bool lane_live = pstep(r, sub) < KP;
         float P[MM], Q[MM];
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
@@ -753,7 +765,7 @@ w4a16_decode_mfma_kernel(W4Args p) {
 #pragma unroll
         for (int u = 0; u < DM_U; ++u) {
             const uint32_t v = (uint32_t)__shfl(DEFER ? (int)rs : sz, 16 * u + col);
-            const int pp = wave + DM_NW * (DM_U * r + u);
+            const int pp = pstep(r, u);
             if (pp < KP) {
                 const uint32_t zz = v >> 16, s = v & 0xFFFFu;
                 const uint32_t z1 = 0x6400u | zz, zhi = 0x5400u | (zz << 4);
@@ -796,7 +808,7 @@ w4a16_decode_mfma_kernel(W4Args p) {
         // Round r+1 in flight while round r is computed; straight-line body (the loads
         // past the last round are clamped re-loads of it).  Staging buffers alternate, so
         // a wave's LDS writes for round r+1 never race its reads of round r.
-        const int rounds = (KP - wave + DM_NW * DM_U - 1) / (DM_NW * DM_U);
+        const int rounds = (KP - DM_U * wave + DM_NW * DM_U - 1) / (DM_NW * DM_U);
         DecodeMRound<MM> R0, R1;
         load_round(0, R0);
         load_round(1, R1);
@@ -893,7 +905,7 @@ w4a16_skinny_kernel(W4Args p) {
     }
     // Activations and weights, pair-step by pair-step (clamped: every load is issued).
     u32x4 av[U][MB][4], wv[U][NH];
-    const u32x4* wbase = p.W + (int64_t)NT * wg * KC * 64 + 32 * h + col;
+    const u32x4* wbase = p.W + pk_index(n0 + col, 0, h, KC);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int pp = min(kp0 + wave + SK_NW * u, KP - 1);
@@ -906,8 +918,7 @@ w4a16_skinny_kernel(W4Args p) {
         }
 #pragma unroll
         for (int sc = 0; sc < NH; ++sc)
-            wv[u][sc] = __builtin_nontemporal_load(wbase + (int64_t)(sc >> 1) * KC * 64 + 16 * (sc & 1) +
-                                                   (int64_t)(2 * pp + dc) * 64);
+            wv[u][sc] = __builtin_nontemporal_load(wbase + (int64_t)sc * KC * 32 + (int64_t)(2 * pp + dc) * 32);
     }
 
 #pragma unroll
@@ -1070,7 +1081,7 @@ __device__ __forceinline__ void w4g_issue(const W4Args& p, const W4GLane& L,
     const uint32_t g = (64u * k + 32u * (uint32_t)L.h) / (uint32_t)p.G;
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) {
-        R.w[j] = buf_load16(rw, (L.w_off[j] + k * 1024u) | dead);
+        R.w[j] = buf_load16(rw, (L.w_off[j] + k * 512u) | dead);
         // byte strides from group g to g + 1
         const uint32_t s_gs = ZF == WMMA_ZEROS_SLICED ? 32u : (uint32_t)p.N * 2u;
         const uint32_t z_gs = ZF == WMMA_ZEROS_SLICED ? 8u
@@ -1171,14 +1182,13 @@ w4a16_gemm_kernel(W4Args p) {
         L.a_addr[i] = r * 128;
         L.a_sw[i] = swz8(r);
     }
-    // The weight resource starts at the workgroup's first 32-column tile, so weight offsets
-    // stay below (BN / 32) * K * 16 bytes whatever the size of the whole matrix.
+    // The weight resource starts at the workgroup's first column, so weight offsets stay
+    // below (BN / 16) * K * 8 bytes whatever the size of the whole matrix.
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
         const int n = n0 + wn * TN + 32 * j + (lane & 31);
         const bool ok = n < p.N;
-        const int ntile = (n >> 5) - (n0 >> 5);
-        L.w_off[j] = ok ? (uint32_t)(((int64_t)ntile * KC * 64 + lane) * 16) : kOobOffset;
+        L.w_off[j] = ok ? (uint32_t)((pk_index(n, 0, L.h, KC) - pk_index(n0, 0, 0, KC)) * 16) : kOobOffset;
         // scale / zero byte offsets at group 0
         L.s_off[j] = ok ? (uint32_t)(s_index<ZF>(p, 0, n) * 2) : kOobOffset;
         if constexpr (ZF != WMMA_ZEROS_U8)
@@ -1187,7 +1197,7 @@ w4a16_gemm_kernel(W4Args p) {
             L.z_off[j] = ok ? (uint32_t)n : kOobOffset;
     }
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A + (int64_t)m0 * p.lda);
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W + (int64_t)(n0 >> 5) * KC * 64);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W + pk_index(n0, 0, 0, KC));
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.S);
     const __amdgpu_buffer_rsrc_t rz = make_rsrc(p.Z);
 
@@ -1333,7 +1343,7 @@ w4a16_mfma_kernel(W4Args p) {
         for (int j = 0; j < WNT; ++j) {
             const int nt = ntile0 + j;
             if (nt < ntiles) {
-                wv[j] = __builtin_nontemporal_load(p.W + ((int64_t)nt * KC + kc) * 64 + lane);
+                wv[j] = __builtin_nontemporal_load(p.W + pk_index(32 * nt + (lane & 31), kc, h, KC));
                 group_params<ZF>(p, (kc * 64 + 32 * h) / p.G, 32 * nt + (lane & 31), &zs[j], &ss[j]);
             } else {
                 wv[j] = u32x4{};
