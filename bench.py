@@ -26,6 +26,10 @@ Workload families (--workload):
   flash      configs[4]: [4,32,4096,128], causal and non-causal, forward and backward; with
              8 K/V heads (GQA); a packed variable-length batch
   copy       a plain 256 MiB device copy (calibrates the rocprofv3 byte counters)
+  mfma_ceiling  the matrix pipe's sustained rate with register operands and no memory
+             traffic (libwmma_calib.so): the ceiling the GEMM main loop is held against
+  read_floor a plain streaming read of the W4A16 M=1 weight sizes and of 1 GiB, graph
+             replayed over rotating buffers: the floor of the HBM-bound kernels
 HBM-bound cases rotate their inputs over more than 512 MB (twice the 256 MB MALL) so the
 bytes really come from HBM; microsecond-scale kernels are replayed from a HIP graph.
 
@@ -371,8 +375,81 @@ def fam_copy(wo):
          GBps_read_plus_write=round(2 * nbytes / (ms * 1e-3) / 1e9, 1))
 
 
+def calib_lib():
+    """The calibration kernels (include/wmma_calib.h): bench.py's measuring instruments."""
+    import ctypes
+
+    L = ctypes.CDLL(os.path.join(ROOT, "wmma_ops_amd", "libwmma_calib.so"))
+    vp, i32 = ctypes.c_void_p, ctypes.c_int
+    L.wmma_calib_mfma_ceiling.argtypes = [i32, i32, vp, vp, vp]
+    L.wmma_calib_mfma_ceiling_flops.argtypes = [i32, i32]
+    L.wmma_calib_mfma_ceiling_flops.restype = ctypes.c_double
+    L.wmma_calib_read_stream.argtypes = [vp, ctypes.c_size_t, i32, vp, vp]
+    return L
+
+
+def mfma_ceiling(calls=200, random_operands=True):
+    """Sustained rate (FLOP/s) of v_mfma_f32_32x32x16_f16 on register operands, 512
+    workgroups x 4 waves x 8 independent accumulators, ~1 ms launches back to back after
+    the settle phase: the matrix pipe's ceiling on this board, clock and power limits
+    included.  With random operands (fp16 N(0,1), as the GEMM's inputs) the operand bits
+    switch from one MFMA to the next; with constant operands they do not, and the board
+    draws less power."""
+    import torch
+
+    L = calib_lib()
+    wgs, iters = 512, 4000
+    sink = torch.zeros(wgs, device="cuda")
+    ops = None
+    if random_operands:
+        g = torch.Generator().manual_seed(42)
+        ops = torch.randn(wgs * 256 * 16 * 8, generator=g).half().cuda()
+    st = torch.cuda.current_stream().cuda_stream
+    run = lambda i: L.wmma_calib_mfma_ceiling(wgs, iters, ops.data_ptr() if ops is not None else None,
+                                              sink.data_ptr(), st)
+    assert run(0) == 0
+    ms = time_batches(run, calls if not QUICK else 2, batches=3)
+    return L.wmma_calib_mfma_ceiling_flops(wgs, iters) / (ms * 1e-3), ms
+
+
+def fam_mfma_ceiling(wo):
+    for rnd in (True, False):
+        fl, ms = mfma_ceiling(random_operands=rnd)
+        line(family="mfma_ceiling", operands="random N(0,1) fp16" if rnd else "constant",
+             TFLOPS=round(fl / 1e12, 1), frac_mfma_peak=round(fl / PEAK_FP16_FLOPS, 4),
+             us_per_launch=round(ms * 1e3, 1),
+             config="512 workgroups x 4 waves, each wave 4000 x 8 independent "
+                    "v_mfma_f32_32x32x16_f16 on register operands (no memory traffic)")
+
+
+def fam_read_floor(wo):
+    """Streaming reads of the W4A16 M=1 weight sizes (K=4096, N=4096 / 14336: 8 MiB, 28 MiB)
+    and of 1 GiB, buffers rotated over > 512 MB and replayed from a HIP graph, like the
+    W4A16 figures: the floor of an HBM-bound kernel reading that many bytes."""
+    import torch
+
+    L = calib_lib()
+    for nbytes in (4096 * 4096 // 2, 4096 * 14336 // 2, 1 << 30):
+        for loads in (4, 8):
+            cp = copies_for(nbytes)
+            bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(i & 255) for i in range(cp)]
+            sink = torch.zeros(nbytes // (8192 * loads) + 1, device="cuda")
+
+            def fn(i):
+                rc = L.wmma_calib_read_stream(bufs[i % cp].data_ptr(), nbytes, loads, sink.data_ptr(),
+                                              torch.cuda.current_stream().cuda_stream)
+                assert rc == 0
+
+            ms, _ = time_graph(fn, cp)
+            line(family="read_floor", bytes=nbytes, loads_per_wave=loads, us=round(ms * 1e3, 3),
+                 GBps=round(nbytes / (ms * 1e-3) / 1e9, 1),
+                 frac_hbm=round(nbytes / (ms * 1e-3) / PEAK_HBM_BPS, 4), rotation_copies=cp)
+            del bufs
+
+
 FAMILIES = {"gemm": fam_gemm, "epilogue": fam_epilogue, "skinny": fam_skinny,
-            "w4a16": fam_w4a16, "flash": fam_flash, "copy": fam_copy}
+            "w4a16": fam_w4a16, "flash": fam_flash, "copy": fam_copy,
+            "mfma_ceiling": fam_mfma_ceiling, "read_floor": fam_read_floor}
 
 
 # ------------------------------------------------------------------------ headline --
@@ -482,6 +559,7 @@ def headline(wo, args):
         with open(TRAFFIC_FILE) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
     plan = wo.gemm_plan(M, N, K)
+    ceiling, _ = mfma_ceiling(calls=100)
     out = {
         "metric": METRIC,
         "value": round(tflops, 2),
@@ -504,7 +582,14 @@ def headline(wo, args):
                      "peak": PEAK_FP16_FLOPS / 1e12, "unit": "TFLOP/s",
                      "frac": round(achieved * 1e12 / PEAK_FP16_FLOPS, 4), "traffic": traffic,
                      "kernel": "gemm_mfma_kernel<256,256,32,2,4,4> (BMxBNxBK, waves MxN, stages)",
-                     "kernel_us": round(ms_kernel * 1e3, 2)},
+                     "kernel_us": round(ms_kernel * 1e3, 2),
+                     # the matrix pipe's measured rate with register operands (no memory
+                     # traffic) on this board, from libwmma_calib.so, in the same run
+                     "ceiling": {"TFLOPS": round(ceiling / 1e12, 1),
+                                 "frac": round(achieved * 1e12 / ceiling, 4),
+                                 "what": "v_mfma_f32_32x32x16_f16 back to back, 512 workgroups "
+                                         "x 4 waves x 8 accumulators, random fp16 register "
+                                         "operands (bench.py --workload mfma_ceiling)"}},
     }
     if not args.no_w4a16:
         out["w4a16_m1"] = [w4a16_case(wo, 1, n) for n in (4096, 14336)]

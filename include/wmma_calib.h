@@ -1,0 +1,39 @@
+/*
+ * wmma_calib.h -- calibration kernels (libwmma_calib.so), used by bench.py to measure what
+ * the MI355X itself sustains: the matrix pipe's rate with no memory traffic, and a plain
+ * streaming read.  They are measuring instruments, not part of the wmma_ops path, and have
+ * no counterpart in the reference.  Return 0 on success, nonzero on a bad argument (1, 2)
+ * or a launch error (5).  Asynchronous on `stream` (a hipStream_t as void*).
+ */
+#ifndef WMMA_CALIB_H
+#define WMMA_CALIB_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* `workgroups` workgroups of 4 waves; every wave issues `iters` (even) x 8 independent
+ * v_mfma_f32_32x32x16_f16 on register operands, each MFMA of a round on a different pair
+ * of the lane's 8 A and 8 B fragments.  operands: device memory of workgroups * 256 * 16
+ * 16-byte fragments (random data makes the operand bits switch as in a GEMM), or NULL for
+ * constant operands.  sink: device float[workgroups] (never written in practice; it keeps
+ * the work observable). */
+int wmma_calib_mfma_ceiling(int workgroups, int iters, const void* operands, float* sink,
+                            void* stream);
+/* FLOPs one wmma_calib_mfma_ceiling launch performs (2 per multiply-add). */
+double wmma_calib_mfma_ceiling_flops(int workgroups, int iters);
+
+/* Reads `bytes` (a multiple of 16; src 16-byte aligned) once: workgroups of 8 waves, each
+ * wave `loads_per_wave` (2, 4 or 8) 1 KB nontemporal loads of one contiguous run.
+ * sink: device float[bytes / (8 KB * loads_per_wave) + 1]. */
+int wmma_calib_read_stream(const void* src, size_t bytes, int loads_per_wave, float* sink,
+                           void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WMMA_CALIB_H */

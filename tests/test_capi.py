@@ -60,8 +60,8 @@ def lib():
     return L
 
 
-def declared_functions():
-    text = open(HEADER).read()
+def declared_functions(header=HEADER):
+    text = open(header).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     names = re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*(wmma_[A-Za-z0-9_]+)\s*\(",
                        text, flags=re.M)
@@ -79,6 +79,26 @@ def test_library_exports_every_declared_symbol(lib):
     missing = [n for n in declared_functions() if not hasattr(lib, n)]
     assert not missing, missing
     assert lib.wmma_abi_version() == 1
+
+
+def test_calibration_library_exports_its_header():
+    # bench.py's measuring instruments (include/wmma_calib.h, libwmma_calib.so)
+    calib = ctypes.CDLL(os.path.join(ROOT, "wmma_ops_amd", "libwmma_calib.so"))
+    names = declared_functions(os.path.join(ROOT, "include", "wmma_calib.h"))
+    assert names == ["wmma_calib_mfma_ceiling", "wmma_calib_mfma_ceiling_flops",
+                     "wmma_calib_read_stream"], names
+    assert not [n for n in names if not hasattr(calib, n)]
+    calib.wmma_calib_mfma_ceiling_flops.restype = ctypes.c_double
+    assert calib.wmma_calib_mfma_ceiling_flops(512, 1000) == 512 * 4 * 8 * 1000 * 2.0 * 32 * 32 * 16
+    # argument checks return before any launch
+    calib.wmma_calib_read_stream.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                             ctypes.c_void_p, ctypes.c_void_p]
+    assert calib.wmma_calib_read_stream(None, 1024, 4, 0x10000, None) == 1
+    assert calib.wmma_calib_read_stream(0x10000, 1024, 3, 0x10000, None) == 2
+    calib.wmma_calib_mfma_ceiling.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                              ctypes.c_void_p, ctypes.c_void_p]
+    assert calib.wmma_calib_mfma_ceiling(512, 3, None, 0x10000, None) == 1    # odd iters
+    assert calib.wmma_calib_mfma_ceiling(512, 4, 0x10002, 0x10000, None) == 1  # misaligned
 
 
 # ---------------------------------------------------------------- GEMM validation --

@@ -5,6 +5,7 @@
 Outputs (inside the package directory, next to this file):
     libwmma_ops_amd.so                      HIP kernels + C-ABI (include/wmma_ops_amd.h)
     _C.cpython-*.so                         pybind/torch layer, links the library above
+    libwmma_calib.so                        calibration kernels (include/wmma_calib.h)
 
 Only hipcc (for *.hip, --offload-arch=gfx950) and the host C++ compiler are used; no
 JIT cache, so the built files travel with the source tree.
@@ -78,6 +79,21 @@ def build_library(verbose: bool = False) -> str:
     return lib
 
 
+CALIB_NAME = "libwmma_calib.so"
+
+
+def build_calib(verbose: bool = False) -> str:
+    """The calibration kernels (include/wmma_calib.h), a library of their own."""
+    os.makedirs(BUILD, exist_ok=True)
+    obj = os.path.join(BUILD, "calib.hip.o")
+    _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, "calib.hip"), "-o", obj], verbose)
+    lib = os.path.join(PKG, CALIB_NAME)
+    tmp = lib + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, obj], verbose)
+    os.replace(tmp, lib)
+    return lib
+
+
 def build_extension(verbose: bool = False) -> str:
     import torch
     from torch.utils import cpp_extension as ce
@@ -115,6 +131,7 @@ def build_extension(verbose: bool = False) -> str:
 def build(verbose: bool = False) -> None:
     build_library(verbose)
     build_extension(verbose)
+    build_calib(verbose)
 
 
 if __name__ == "__main__":

@@ -1,0 +1,123 @@
+// Calibration kernels: what the hardware itself sustains, for the roofline figures that the
+// benchmarks quote.  Not part of the wmma_ops path (no reference counterpart); built into a
+// library of their own (libwmma_calib.so, declared in include/wmma_calib.h).
+//
+//  * mfma_ceiling_kernel -- every wave issues v_mfma_f32_32x32x16_f16 back to back on eight
+//    independent accumulators from fp16 operands held in registers: no memory traffic, no
+//    LDS, no dependent chains.  Its rate is the matrix pipe's sustained throughput on this
+//    board (clock and power limits included), the ceiling a GEMM main loop can approach;
+//    with random operands the operand bits switch as in a GEMM on random data.
+//  * read_stream_kernel -- streams a buffer once with 16-byte nontemporal loads (each
+//    workgroup a contiguous run, each wave `loads` 1 KB loads in flight) and folds the
+//    words into one value per workgroup, the floor of an HBM-bound kernel that reads the
+//    same bytes with the same launch shape.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/wmma_calib.h"
+#include "common.hpp"
+
+using namespace wmma_amd;
+
+namespace {
+
+template <int ACC>
+__global__ void __launch_bounds__(256) mfma_ceiling_kernel(int iters, const u32x4* operands,
+                                                           float* sink) {
+    f32x16 acc[ACC];
+#pragma unroll
+    for (int i = 0; i < ACC; ++i) acc[i] = f32x16{};
+    // ACC A fragments and ACC B fragments per lane.  From `operands` (random data, so the
+    // operand bits toggle from one MFMA to the next as in a GEMM on random inputs), or, with
+    // operands == NULL, constants from the thread index.  The switching activity of the
+    // operands moves the power draw, and with it the clock, so the two differ.
+    f16x8 a[ACC], b[ACC];
+#pragma unroll
+    for (int i = 0; i < ACC; ++i) {
+        if (operands) {
+            const int64_t base = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 2 * ACC;
+            a[i] = as_f16x8(operands[base + i]);
+            b[i] = as_f16x8(operands[base + ACC + i]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                a[i][e] = (f16)(float)((threadIdx.x + i) & 7);
+                b[i][e] = (f16)(float)e;
+            }
+        }
+    }
+    for (int it = 0; it < iters; it += 2) {
+        // every MFMA of the pair of rounds takes a different (A, B) pair
+#pragma unroll
+        for (int i = 0; i < ACC; ++i) acc[i] = mfma32(a[i], b[(i + 1) % ACC], acc[i]);
+#pragma unroll
+        for (int i = 0; i < ACC; ++i) acc[i] = mfma32(a[(i + 3) % ACC], b[i], acc[i]);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ACC; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += acc[i][r];
+    if (s == 1234.5f) sink[blockIdx.x] = s;  // never true; keeps the work alive
+}
+
+template <int LOADS>
+__global__ void __launch_bounds__(512) read_stream_kernel(const u32x4* src, int64_t units,
+                                                          float* sink) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t per_wg = (int64_t)8 * LOADS * 64;  // 16-byte units per workgroup
+    const int64_t base = (int64_t)blockIdx.x * per_wg;
+    u32x4 w[LOADS];
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+        const int64_t i = base + (int64_t)(wave * LOADS + u) * 64 + lane;
+        w[u] = __builtin_nontemporal_load(src + (i < units ? i : units - 1));
+    }
+    uint32_t x = 0;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) x ^= w[u][0] ^ w[u][1] ^ w[u][2] ^ w[u][3];
+    // every lane's words feed the result (a per-wave reduction), so no load is dead
+    x ^= __shfl_xor(x, 1);
+    x ^= __shfl_xor(x, 2);
+    x ^= __shfl_xor(x, 4);
+    x ^= __shfl_xor(x, 8);
+    x ^= __shfl_xor(x, 16);
+    x ^= __shfl_xor(x, 32);
+    if (x == 0x9E3779B9u && lane == 0) sink[blockIdx.x] = (float)wave;
+}
+
+}  // namespace
+
+extern "C" {
+
+int wmma_calib_mfma_ceiling(int workgroups, int iters, const void* operands, float* sink,
+                            void* stream) {
+    if (workgroups <= 0 || iters <= 0 || iters % 2 != 0 || !sink) return 1;
+    if ((reinterpret_cast<uintptr_t>(operands) & 15u) != 0) return 1;
+    hipLaunchKernelGGL((mfma_ceiling_kernel<8>), dim3(workgroups), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), iters,
+                       static_cast<const u32x4*>(operands), sink);
+    return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+double wmma_calib_mfma_ceiling_flops(int workgroups, int iters) {
+    // 4 waves x 8 accumulators x iters MFMAs of 32 x 32 x 16 (2 FLOP per multiply-add)
+    return (double)workgroups * 4 * 8 * iters * (2.0 * 32 * 32 * 16);
+}
+
+int wmma_calib_read_stream(const void* src, size_t bytes, int loads_per_wave, float* sink,
+                           void* stream) {
+    if (!src || !sink || bytes < 16 || (reinterpret_cast<uintptr_t>(src) & 15u) != 0) return 1;
+    const int64_t units = (int64_t)(bytes / 16);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    auto grid = [&](int loads) { return (int)((units + 8 * loads * 64 - 1) / (8 * loads * 64)); };
+    switch (loads_per_wave) {
+        case 2: hipLaunchKernelGGL(read_stream_kernel<2>, dim3(grid(2)), dim3(512), 0, st, (const u32x4*)src, units, sink); break;
+        case 4: hipLaunchKernelGGL(read_stream_kernel<4>, dim3(grid(4)), dim3(512), 0, st, (const u32x4*)src, units, sink); break;
+        case 8: hipLaunchKernelGGL(read_stream_kernel<8>, dim3(grid(8)), dim3(512), 0, st, (const u32x4*)src, units, sink); break;
+        default: return 2;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+}  // extern "C"
