@@ -150,6 +150,46 @@ __device__ __forceinline__ void grouped_tile(int pid, int tiles_m, int tiles_n, 
     *tn = in / gsize;
 }
 
+// Shuffled epilogue of a BM x BN fp32 tile held in 32x32 MFMA accumulators: wave (wm, wn)
+// owns the TM x TN sub-tile at (wm*TM, wn*TN) as FM x FN blocks, lane l holding column l%32
+// and element r row 8*(r/4) + 4*(l/32) + r%4 of each block.  Written to global memory
+// directly, every store instruction writes two rows of 128 bytes; staged row-major in LDS
+// first (CH rows at a time, CH*BN*4 bytes of `lds`), every wave then writes whole 16-byte
+// vectors of contiguous row runs -- measured on MI355X, 3.8 -> 1.3 us for the 64 KB output
+// of a 128 x 128 tile.  emit(r, c, v) stores the four values of tile row r, columns c..c+3.
+// Every thread of the workgroup must call it (it synchronises); the caller's LDS use must be
+// complete except for the barrier this function starts with.
+template <int BM, int BN, int WM, int WN, int CH, class Emit>
+__device__ __forceinline__ void shuffle_epilogue(float* lds,
+                                                 const f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
+                                                 int wm, int wn, int lane, Emit&& emit) {
+    constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+    constexpr int NT = WM * WN * kWave, V = BN / 4;
+    static_assert(CH % 32 == 0 && BM % CH == 0, "chunks of whole 32-row blocks");
+    const int h = lane >> 5;
+#pragma unroll
+    for (int c = 0; c < BM / CH; ++c) {
+        __syncthreads();  // earlier readers of the LDS are done
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int rb = wm * TM + 32 * i - c * CH;  // block's first row in the chunk (uniform)
+            if (rb >= 0 && rb < CH) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        lds[(rb + 8 * (r >> 2) + 4 * h + (r & 3)) * BN + wn * TN + 32 * j + (lane & 31)] =
+                            acc[i][j][r];
+            }
+        }
+        __syncthreads();
+        for (int e = (int)threadIdx.x; e < CH * V; e += NT) {
+            const int lr = e / V, lv = e - lr * V;
+            emit(c * CH + lr, 4 * lv, *reinterpret_cast<const float4*>(lds + lr * BN + 4 * lv));
+        }
+    }
+}
+
 // Sum of split-K partials p[s * stride + 0 .. W-1] over s = 0, 1, ..., split-1, added in
 // that order (the fixed order every split-K path shares, so results do not depend on
 // scheduling).  The loads of eight splits are issued before any is waited on: a split-K

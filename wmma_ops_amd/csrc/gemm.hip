@@ -324,6 +324,35 @@ gemm_mfma_kernel(GemmArgs p) {
     const int h = lane >> 5;
     const int row0 = m0 + wm * TM + 4 * h, col0 = n0 + wn * TN + (lane & 31);
     const bool full_tile = m0 + BM <= M && n0 + BN <= N;
+    // Full tiles whose rows take 16-byte vectors (output, and C_in when it is read) go
+    // through the shuffled epilogue when the LDS ring holds the whole fp32 tile: every
+    // store then writes whole 16-byte pieces of contiguous row runs.  In place is still
+    // exact: each vector of C_in is read by the thread that then writes it.  Not for the
+    // 256 x 256 tile (two chunks): there the shuffle cost more than it saved (4096^3:
+    // 121-124 -> 126 us; its 64 MB of output is write-bandwidth bound either way).
+    constexpr bool kShuffle = NS * STAGE >= BM * BN * 4;
+    if constexpr (kShuffle) {
+        const bool vec_ok =
+            full_tile && ldo % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 15u) == 0 &&
+            (!use_c || (p.ldcin % 4 == 0 && (reinterpret_cast<uintptr_t>(p.Cin) & 15u) == 0));
+        if (vec_ok) {
+            const float beta = p.beta;
+            shuffle_epilogue<BM, BN, WM, WN, BM>(
+                reinterpret_cast<float*>(smem), acc, wm, wn, lane, [&](int r, int c, float4 v) {
+                    float4 o = make_float4(alpha * v.x, alpha * v.y, alpha * v.z, alpha * v.w);
+                    if (use_c) {
+                        const float4 ci = *reinterpret_cast<const float4*>(
+                            p.Cin + (int64_t)(m0 + r) * p.ldcin + n0 + c);
+                        o.x += beta * ci.x;
+                        o.y += beta * ci.y;
+                        o.z += beta * ci.z;
+                        o.w += beta * ci.w;
+                    }
+                    *reinterpret_cast<float4*>(out + (int64_t)(m0 + r) * ldo + n0 + c) = o;
+                });
+            return;
+        }
+    }
     if (full_tile && !use_c) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)

@@ -1110,15 +1110,22 @@ __device__ __forceinline__ void w4g_stage(const W4Args& p, const W4GLane& L,
                                           f32x16 (&acc)[C::FM][C::FN]) {
     w4g_issue<C, ZF>(p, L, ra, rw, rs, rz, kc_next, dst, Rn);
     if (!compute) return;
+    // This stage's register slot passes through an empty asm first: without it the
+    // compiler hoists the dequantisation of a slot up to where its loads were just issued
+    // (NS - 1 stages early) and waits there for them (vmcnt(1..2)), so every stage paid
+    // the full memory latency.  The caller's wait_vmcnt already covers these loads.
+    W4GSlot<C::FN> r = R;
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) asm volatile("" : "+v"(r.w[j]), "+v"(r.s[j]), "+v"(r.z[j]));
     f16x2 zs[C::FN], ss[C::FN];
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) {
         uint32_t z;
         if constexpr (ZF != WMMA_ZEROS_U8)
-            z = (R.z[j] >> (4 * (lane & 7))) & 0xFu;  // column % 8 == lane % 8
+            z = (r.z[j] >> (4 * (lane & 7))) & 0xFu;  // column % 8 == lane % 8
         else
-            z = R.z[j] & 0xFu;
-        const uint32_t zh = 0x6400u | z, sv = R.s[j] & 0xFFFFu;
+            z = r.z[j] & 0xFu;
+        const uint32_t zh = 0x6400u | z, sv = r.s[j] & 0xFFFFu;
         zs[j] = as_h2(zh | (zh << 16));
         ss[j] = as_h2(sv | (sv << 16));
     }
@@ -1127,7 +1134,7 @@ __device__ __forceinline__ void w4g_stage(const W4Args& p, const W4GLane& L,
         f16x8 b[C::FN];
 #pragma unroll
         for (int j = 0; j < C::FN; ++j) {
-            const uint32_t x = R.w[j][ks];
+            const uint32_t x = r.w[j][ks];
             u32x4 bv;
 #pragma unroll
             for (int q = 0; q < 4; ++q)
@@ -1218,18 +1225,33 @@ w4a16_gemm_kernel(W4Args p) {
         // Main loop, unrolled by NS so every register-ring slot is a static index.  Stage
         // t reads LDS slot t % NS and ring[t % NS]; it issues stage t + NS - 1 into LDS slot
         // (t - 1) % NS and ring[(t - 1) % NS], both free once this stage's barrier passed.
-        for (int t0 = 0; t0 < nk; t0 += NS) {
+        // The full ring turns run a body with no branch (every stage computes; issues past
+        // the end are out-of-range loads, not skipped ones), so the compiler's own vmcnt
+        // waits stay exact across the back edge; the last nk % NS stages follow.
+        const int full_turns = nk / NS;
+        for (int t0 = 0; t0 < full_turns * NS; t0 += NS) {
 #pragma unroll
             for (int q = 0; q < NS; ++q) {
-                const int t = t0 + q;
                 wait_vmcnt<(NS - 2) * C::PER>();
                 __builtin_amdgcn_s_barrier();
                 asm volatile("" ::: "memory");
-                const int tn_ = t + NS - 1;
+                const int tn_ = t0 + q + NS - 1;
                 w4g_stage<C, ZF>(p, L, ra, rw, rs, rz, lds + q * C::A_BYTES,
                                  lds + ((q + NS - 1) % NS) * C::A_BYTES,
                                  tn_ < nk ? kc0 + tn_ : -1, ring[q], ring[(q + NS - 1) % NS],
-                                 t < nk, lane, magic, acc);
+                                 true, lane, magic, acc);
+            }
+        }
+        const int t1 = full_turns * NS;
+#pragma unroll
+        for (int q = 0; q < NS - 1; ++q) {
+            if (t1 + q < nk) {  // uniform
+                wait_vmcnt<(NS - 2) * C::PER>();
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                w4g_stage<C, ZF>(p, L, ra, rw, rs, rz, lds + q * C::A_BYTES,
+                                 lds + ((q + NS - 1) % NS) * C::A_BYTES, -1, ring[q],
+                                 ring[(q + NS - 1) % NS], true, lane, magic, acc);
             }
         }
         wait_vmcnt<0>();
@@ -1241,6 +1263,28 @@ w4a16_gemm_kernel(W4Args p) {
     const int64_t ldo = partial ? (int64_t)p.N : p.ldy;
     const int row0 = m0 + wm * TM + 4 * L.h, col0 = n0 + wn * TN + (lane & 31);
     const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
+    // Full tiles whose rows take 16-byte (fp32) or 8-byte (fp16) vectors go through the
+    // shuffled epilogue; the A ring's LDS holds CH rows of the tile at a time.
+    const bool half = !partial && p.y_half;
+    const bool vec_ok = full && ldo % 4 == 0 &&
+                        (reinterpret_cast<uintptr_t>(out) & (half ? 7u : 15u)) == 0;
+    if (vec_ok) {
+        constexpr int LDS_ROWS = NS * C::A_BYTES / (BN * 4);
+        constexpr int CH = LDS_ROWS >= BM ? BM : (LDS_ROWS >= 128 ? 128 : (LDS_ROWS >= 64 ? 64 : 32));
+        static_assert(CH * BN * 4 <= NS * C::A_BYTES, "shuffle chunk exceeds the LDS ring");
+        shuffle_epilogue<BM, BN, WM, WN, CH>(
+            reinterpret_cast<float*>(smem), acc, wm, wn, lane, [&](int r, int c, float4 v) {
+                const int64_t idx = (int64_t)(m0 + r) * ldo + n0 + c;
+                if (half) {
+                    typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+                    f16x4_t hv = {(f16)v.x, (f16)v.y, (f16)v.z, (f16)v.w};
+                    *reinterpret_cast<f16x4_t*>(reinterpret_cast<f16*>(p.Y) + idx) = hv;
+                } else {
+                    *reinterpret_cast<float4*>(out + idx) = v;
+                }
+            });
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
