@@ -291,7 +291,10 @@ def test_prepack_params_validation_codes(lib):
 def test_flash_validation_codes(lib):
     f = lambda **kw: lib.wmma_flash_attn_fwd(FAKE, FAKE, FAKE, kw.get("O", FAKE), 1, 1, kw.get("S", 128),
                                              kw.get("S", 128), kw.get("D", 128), kw.get("scale", 0.1), 0, None)
-    assert f(D=96) == UNSUPPORTED
+    # head dims: multiples of 8 from 8 to 128 (the torch layer pads other sizes)
+    for D in (0, 4, 100, 136, 256):
+        assert f(D=D) == UNSUPPORTED, D
+    assert b"multiples of 8" in lib.wmma_last_error()
     assert f(scale=0.0) == INVALID
     assert f(scale=float("nan")) == INVALID
     assert f(O=None) == INVALID
@@ -314,7 +317,8 @@ def test_flash_training_validation_codes(lib):
     # forward with log-sum-exp
     f = lambda **kw: lib.wmma_flash_attn_fwd_lse(FAKE, FAKE, FAKE, FAKE, kw.get("lse", FAKE), 1, 4, 2,
                                                  128, 128, kw.get("D", 128), 0.1, 0, None)
-    assert f(D=96) == UNSUPPORTED
+    for D in (4, 100, 136):
+        assert f(D=D) == UNSUPPORTED, D
     assert f(lse=FAKE + 2) == MISALIGNED
     # workspace: two fp32 statistics per query row
     assert lib.wmma_flash_attn_bwd_workspace_size(4, 32, 4096) == 2 * 4 * 4 * 32 * 4096
@@ -327,7 +331,7 @@ def test_flash_training_validation_codes(lib):
                                        FAKE, ptr("ws"), kw.get("wsb", need), 1, 4, kw.get("Hkv", 2),
                                        kw.get("Sq", 128), kw.get("Sk", 128), kw.get("D", 128),
                                        kw.get("scale", 0.1), 0, None)
-    assert bwd(D=32) == UNSUPPORTED
+    assert bwd(D=36) == UNSUPPORTED
     assert bwd(Hkv=3) == INVALID
     assert bwd(scale=-1.0) == INVALID
     assert bwd(dO=None) == INVALID

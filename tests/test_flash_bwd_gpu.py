@@ -66,6 +66,21 @@ def test_flash_bwd_shapes(wo, causal, B, H, Sq, Sk, D):
     print(f"[err] dQ {errs[0]:.2e} dK {errs[1]:.2e} dV {errs[2]:.2e}", flush=True)
 
 
+# Head dims other than 64 and 128 (see the forward's head-dim test): the dQ and dK/dV
+# kernels load the missing d columns as zeros and do not store them; grouped-query heads.
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("D", [16, 32, 48, 80, 96, 112, 33, 100])
+def test_flash_bwd_head_dims(wo, causal, D):
+    B, H, Hkv, Sq, Sk = 1, 4, 2, 300, 200
+    report("flash_bwd_head_dim", B=B, H=H, Hkv=Hkv, Sq=Sq, Sk=Sk, D=D, causal=causal)
+    Q, K, V = oatt.make_inputs(B, H, Sq, D, seed=900 + D, Sk=Sk, Hkv=Hkv)
+    dO = _dout((B, H, Sq, D), D)
+    O, lse = wo.flash_attention_forward(Q.cuda(), K.cuda(), V.cuda(), causal)
+    got = wo.flash_attention_backward(dO.cuda(), Q.cuda(), K.cuda(), V.cuda(), O, lse, causal)
+    errs = _grads_close(got, oatt.sdpa_bwd_ref(Q, K, V, dO, causal))
+    print(f"[err] D {D} dQ {errs[0]:.2e} dK {errs[1]:.2e} dV {errs[2]:.2e}", flush=True)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("Sq,D", [(1, 64), (77, 128)])
 def test_flash_bwd_single_key(wo, causal, Sq, D):
@@ -123,7 +138,7 @@ def test_flash_bwd_baseline_config(wo, causal):
 # Ragged packed sequences: lengths 1, 0, not multiples of the tiles, different query and
 # key lengths, a sequence with no keys (dQ = 0) and one with no queries (dK = dV = 0).
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("H,Hkv,D", [(4, 4, 128), (8, 2, 64)])
+@pytest.mark.parametrize("H,Hkv,D", [(4, 4, 128), (8, 2, 64), (4, 2, 80), (4, 4, 36)])
 def test_flash_bwd_varlen(wo, causal, H, Hkv, D):
     lens_q = [300, 1, 0, 700, 64, 5]
     lens_k = [300, 1, 9, 700, 77, 0]

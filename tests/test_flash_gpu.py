@@ -66,6 +66,36 @@ def test_flash_shapes(wo, causal, B, H, Sq, Sk, D):
     _check(O, oatt.sdpa_ref(Q, K, V, causal))
 
 
+# Head dims other than the kernels' 64 and 128: multiples of 8 run on the D = 64 or D = 128
+# kernel with the missing d columns loaded as zeros and not stored; other sizes are
+# zero-padded to a multiple of 8 by the torch layer.  Default scale 1/sqrt(D) of the
+# caller's D throughout.  Ragged Sq != Sk, both masks, grouped-query heads.
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("D", [8, 16, 24, 32, 40, 48, 56, 72, 80, 96, 104, 112, 120, 1, 33, 100, 127])
+def test_flash_head_dims(wo, causal, D):
+    B, H, Hkv, Sq, Sk = 2, 4, 2, 200, 333
+    report("flash_head_dim", B=B, H=H, Hkv=Hkv, Sq=Sq, Sk=Sk, D=D, causal=causal)
+    Q, K, V = oatt.make_inputs(B, H, Sq, D, seed=500 + D, Sk=Sk, Hkv=Hkv)
+    O, lse = wo.flash_attention_forward(Q.cuda(), K.cuda(), V.cuda(), causal)
+    _check(O, oatt.sdpa_ref(Q, K, V, causal))
+    ref_lse = oatt.lse_ref(Q, K, causal)
+    assert torch.allclose(lse.cpu(), ref_lse, atol=1e-4, rtol=1e-5), (lse.cpu() - ref_lse).abs().max()
+    assert torch.equal(O, wo.flash_attention(Q.cuda(), K.cuda(), V.cuda(), causal=causal))
+
+
+# The padded head dims leave the rows past D untouched: a head-dim-80 problem computes the
+# same bits as the same problem zero-padded to 128 by the caller, cut back to 80 columns.
+def test_flash_head_dim_equals_padded(wo):
+    B, H, S, D = 2, 3, 300, 80
+    Q, K, V = oatt.make_inputs(B, H, S, D, seed=77)
+    pad = lambda X: torch.nn.functional.pad(X, (0, 128 - D)).cuda()
+    for causal in (False, True):
+        O = wo.flash_attention(Q.cuda(), K.cuda(), V.cuda(), causal=causal)
+        Op = wo.flash_attention(pad(Q), pad(K), pad(V), causal=causal, scale=1.0 / math.sqrt(D))
+        assert torch.equal(O, Op[..., :D])
+        assert torch.count_nonzero(Op[..., D:]) == 0
+
+
 def test_flash_custom_scale(wo):
     Q, K, V = oatt.make_inputs(2, 4, 256, 64, seed=3)
     O = wo.flash_attention(Q.cuda(), K.cuda(), V.cuda(), False, 0.1)
@@ -134,7 +164,8 @@ def test_flash_gqa_head_mapping(wo):
 # (including 1 and lengths that are not multiples of the 64-key tile or 256-query block),
 # an empty sequence, different query and key lengths, grouped-query heads, both head sizes.
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("H,Hkv,D", [(8, 8, 128), (8, 2, 64), (6, 3, 128)])
+@pytest.mark.parametrize("H,Hkv,D", [(8, 8, 128), (8, 2, 64), (6, 3, 128), (4, 2, 80), (6, 6, 40),
+                                     (4, 1, 100)])
 def test_flash_varlen(wo, causal, H, Hkv, D):
     lens_q = [300, 1, 0, 1000, 64, 257]
     lens_k = [300, 1, 5, 1000, 77, 700]
@@ -167,9 +198,10 @@ def test_flash_varlen_equals_dense(wo):
 
 
 def test_flash_errors(wo):
-    x = torch.zeros(1, 1, 8, 96, dtype=torch.half, device="cuda")
-    with pytest.raises(RuntimeError, match="head_dim"):
-        wo.flash_attention(x, x, x)
+    for D in (136, 256):
+        x = torch.zeros(1, 1, 8, D, dtype=torch.half, device="cuda")
+        with pytest.raises(RuntimeError, match="head_dim must be between 1 and 128"):
+            wo.flash_attention(x, x, x)
     y = torch.zeros(1, 1, 8, 64, dtype=torch.float32, device="cuda")
     with pytest.raises(RuntimeError, match="float16"):
         wo.flash_attention(y, y, y)

@@ -456,10 +456,17 @@ int wmma_int4_permute_rows(const int32_t* qweight, const int32_t* perm, int K, i
 // ----------------------------------------------------------------------------- flash --
 namespace {
 
+// Head dims the kernels take: multiples of 8 (16-byte rows) from 8 to 128.
+int flash_head_dim_check(int D) {
+    if (D < 8 || D > 128 || D % 8 != 0)
+        return fail(WMMA_ERR_UNSUPPORTED, "head_dim %d (supported: multiples of 8 from 8 to 128)", D);
+    return WMMA_OK;
+}
+
 // Shape checks shared by the dense forward and backward entry points.
 int flash_dense_check(int B, int H, int Hkv, int Sq, int Sk, int D, float scale) {
     if (B < 0 || H < 0 || Sq < 0 || Sk < 0) return fail(WMMA_ERR_INVALID_ARG, "negative dimension");
-    if (D != 64 && D != 128) return fail(WMMA_ERR_UNSUPPORTED, "head_dim %d (supported: 64, 128)", D);
+    if (int rc = flash_head_dim_check(D)) return rc;
     if (!(scale > 0.0f) || !std::isfinite(scale))
         return fail(WMMA_ERR_INVALID_ARG, "scale must be positive and finite");
     if (H > 0 && (Hkv <= 0 || H % Hkv != 0))
@@ -474,7 +481,7 @@ int flash_varlen_check(int B, int H, int Hkv, int total_q, int total_k, int max_
                        int D, float scale) {
     if (B < 0 || H < 0 || total_q < 0 || total_k < 0 || max_q < 0 || max_k < 0)
         return fail(WMMA_ERR_INVALID_ARG, "negative dimension");
-    if (D != 64 && D != 128) return fail(WMMA_ERR_UNSUPPORTED, "head_dim %d (supported: 64, 128)", D);
+    if (int rc = flash_head_dim_check(D)) return rc;
     if (!(scale > 0.0f) || !std::isfinite(scale))
         return fail(WMMA_ERR_INVALID_ARG, "scale must be positive and finite");
     if (H > 0 && (Hkv <= 0 || H % Hkv != 0))

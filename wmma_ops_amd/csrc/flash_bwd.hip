@@ -33,6 +33,8 @@
 //    only tiles crossing the diagonal are masked.  Heaviest workgroups are dispatched first.
 //  * Query rows past the end of a sequence load as zeros (dO = 0, Delta = 0), so they add
 //    nothing to dK, dV without a mask; key rows past the end are never stored.
+//  * Head dims: as in the forward, any multiple of 8 up to 128 runs on the D = 64 or D = 128
+//    kernels with the d columns past the head dim loaded as zeros and never stored.
 #include <type_traits>
 
 #include "common.hpp"
@@ -142,6 +144,8 @@ struct BwdArgs {
     float c;           // scale * log2(e)
     float scale;
     int group;         // query heads per key/value head
+    int dr;            // head dim of the tensors: a multiple of 8, at most the kernel's D
+                       // (d columns dr .. D-1 load as zeros and are not stored)
     const int* cu_q;   // variable length (nullptr: dense), as in the forward
     const int* cu_k;
     int H, Hkv;
@@ -164,18 +168,18 @@ __device__ __forceinline__ SeqGeo seq_geo(const BwdArgs& p, int b, int hq) {
         const int ke = min(max(p.cu_k[b + 1], ka), p.total_k);
         g.Sq = min(qe - qa, p.Sq);
         g.Sk = min(ke - ka, p.Sk);
-        g.qs = p.H * D;
-        g.ks = p.Hkv * D;
-        g.q_base = (int64_t)qa * g.qs + (int64_t)hq * D;
-        g.k_base = (int64_t)ka * g.ks + (int64_t)(hq / p.group) * D;
+        g.qs = p.H * p.dr;
+        g.ks = p.Hkv * p.dr;
+        g.q_base = (int64_t)qa * g.qs + (int64_t)hq * p.dr;
+        g.k_base = (int64_t)ka * g.ks + (int64_t)(hq / p.group) * p.dr;
         g.r_base = (int64_t)hq * p.total_q + qa;
     } else {
         g.Sq = p.Sq;
         g.Sk = p.Sk;
-        g.qs = D;
-        g.ks = D;
-        g.q_base = ((int64_t)b * p.H + hq) * p.Sq * D;
-        g.k_base = ((int64_t)b * p.Hkv + hq / p.group) * p.Sk * D;
+        g.qs = p.dr;
+        g.ks = p.dr;
+        g.q_base = ((int64_t)b * p.H + hq) * p.Sq * p.dr;
+        g.k_base = ((int64_t)b * p.Hkv + hq / p.group) * p.Sk * p.dr;
         g.r_base = ((int64_t)b * p.H + hq) * p.Sq;
     }
     return g;
@@ -193,8 +197,11 @@ struct FbLane {
     int h;                            // lane / 32
 };
 
+// stride: row stride of the streamed tensor (elements); dr: its head dim.  LDS chunk pc of a
+// row receives global chunk pc ^ swizzle; chunks at d >= dr load zeros.
 template <int D, int W>
-__device__ __forceinline__ void fb_lane_init(FbLane<D, W>& L, int wave, int lane, int stride) {
+__device__ __forceinline__ void fb_lane_init(FbLane<D, W>& L, int wave, int lane, int stride,
+                                             int dr) {
     using C = FbCfg<D, W>;
     L.h = lane >> 5;
     L.dma_dst = wave * (C::DMA * 1024);
@@ -202,8 +209,9 @@ __device__ __forceinline__ void fb_lane_init(FbLane<D, W>& L, int wave, int lane
     for (int i = 0; i < C::DMA; ++i) {
         const int P = 64 * (wave * C::DMA + i) + lane;
         const int row = P / C::DCH, pc = P % C::DCH;
+        const int gc = pc ^ swz2<D>(row);
         L.dma_row[i] = row;
-        L.dma_off[i] = (uint32_t)((row * stride + 8 * (pc ^ swz2<D>(row))) * 2);
+        L.dma_off[i] = 8 * gc < dr ? (uint32_t)((row * stride + 8 * gc) * 2) : kOobOffset;
     }
     L.row_addr = (lane & 31) * C::RB;
     L.row_sw = swz2<D>(lane & 31);
@@ -290,21 +298,24 @@ __device__ __forceinline__ void fb_tr_x(const WMMA_LDS unsigned char* tile, cons
     }
 }
 
-// Register fragments of one row per lane: row `row` (valid if < n), d = 16 ds + 8 h + 0..7.
+// Register fragments of one row per lane: row `row` (valid if < n), d = 16 ds + 8 h + 0..7
+// (zeros for d >= dr).
 template <int D>
-__device__ __forceinline__ void fb_load_frag(const f16* base, int stride, int row, int n, int h,
-                                             f16x8 (&f)[FbDim<D>::NDS]) {
+__device__ __forceinline__ void fb_load_frag(const f16* base, int stride, int dr, int row, int n,
+                                             int h, f16x8 (&f)[FbDim<D>::NDS]) {
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(base);
 #pragma unroll
     for (int ds = 0; ds < FbDim<D>::NDS; ++ds)
         f[ds] = as_f16x8(buf_load16(
-            rs, row < n ? (uint32_t)(((int64_t)row * stride + 16 * ds + 8 * h) * 2) : kOobOffset));
+            rs, row < n && 16 * ds + 8 * h < dr
+                    ? (uint32_t)(((int64_t)row * stride + 16 * ds + 8 * h) * 2)
+                    : kOobOffset));
 }
 
 // Store a transposed accumulator (lane%32 = row, element r = d 32 db + 8 (r/4) + 4 h + r%4)
-// as fp16 rows of the output, scaled by s.
+// as fp16 rows of the output, scaled by s; columns d >= dr are not stored.
 template <int D>
-__device__ __forceinline__ void fb_store_rows(f16* base, int stride, int row, int n, int h,
+__device__ __forceinline__ void fb_store_rows(f16* base, int stride, int dr, int row, int n, int h,
                                               const f32x16 (&acc)[FbDim<D>::NDB], float s) {
     if (row >= n) return;
 #pragma unroll
@@ -314,7 +325,8 @@ __device__ __forceinline__ void fb_store_rows(f16* base, int stride, int row, in
             f16x4 v;
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = (f16)(acc[db][4 * g + e] * s);
-            *reinterpret_cast<f16x4*>(base + (int64_t)row * stride + 32 * db + 8 * g + 4 * h) = v;
+            const int d = 32 * db + 8 * g + 4 * h;
+            if (d < dr) *reinterpret_cast<f16x4*>(base + (int64_t)row * stride + d) = v;
         }
 }
 
@@ -388,13 +400,13 @@ flash_bwd_dq_kernel(BwdArgs p) {
     const int qrow = qw + c32;
 
     f16x8 qf[C::NDS], dof[C::NDS];
-    fb_load_frag<D>(p.Q + G.q_base, G.qs, qrow, Sq, h, qf);
-    fb_load_frag<D>(p.dO + G.q_base, G.qs, qrow, Sq, h, dof);
+    fb_load_frag<D>(p.Q + G.q_base, G.qs, p.dr, qrow, Sq, h, qf);
+    fb_load_frag<D>(p.dO + G.q_base, G.qs, p.dr, qrow, Sq, h, dof);
     // Delta = rowsum(dO o O): this lane's 64 d values, then the other half of the row.
     float delta;
     {
         f16x8 of[C::NDS];
-        fb_load_frag<D>(p.O + G.q_base, G.qs, qrow, Sq, h, of);
+        fb_load_frag<D>(p.O + G.q_base, G.qs, p.dr, qrow, Sq, h, of);
         float acc[2] = {0.0f, 0.0f};
 #pragma unroll
         for (int ds = 0; ds < C::NDS; ++ds)
@@ -417,7 +429,7 @@ flash_bwd_dq_kernel(BwdArgs p) {
     }
 
     FbLane<D, FB_WAVES_Q> L;
-    fb_lane_init<D>(L, wave, lane, G.ks);
+    fb_lane_init<D>(L, wave, lane, G.ks, p.dr);
     const f16* Kb = p.K + G.k_base;
     const f16* Vb = p.V + G.k_base;
     const int kv_end = CAUSAL ? min(Sk, q0 + FB_BLOCK_Q) : Sk;
@@ -449,7 +461,7 @@ flash_bwd_dq_kernel(BwdArgs p) {
         }
         wait_vmcnt<0>();
     }
-    fb_store_rows<D>(p.dQ + G.q_base, G.qs, qrow, Sq, h, dq, p.scale);
+    fb_store_rows<D>(p.dQ + G.q_base, G.qs, p.dr, qrow, Sq, h, dq, p.scale);
 }
 
 // ------------------------------------------------------------------------- dK/dV kernel --
@@ -612,19 +624,19 @@ flash_bwd_dkdv_kernel(BwdArgs p) {
     f16x8 kf[FbKv<D>::KB][C::NDS], vf[FbKv<D>::KB][C::NDS];
 #pragma unroll
     for (int kb = 0; kb < FbKv<D>::KB; ++kb) {
-        fb_load_frag<D>(p.K + G0.k_base, G0.ks, kw + 32 * kb + c32, Sk, h, kf[kb]);
-        fb_load_frag<D>(p.V + G0.k_base, G0.ks, kw + 32 * kb + c32, Sk, h, vf[kb]);
+        fb_load_frag<D>(p.K + G0.k_base, G0.ks, p.dr, kw + 32 * kb + c32, Sk, h, kf[kb]);
+        fb_load_frag<D>(p.V + G0.k_base, G0.ks, p.dr, kw + 32 * kb + c32, Sk, h, vf[kb]);
     }
 
     FbLane<D, FB_WAVES_KV> L;
-    fb_lane_init<D>(L, wave, lane, G0.qs);
+    fb_lane_init<D>(L, wave, lane, G0.qs, p.dr);
     // Query tiles: t0 .. Tq-1 of each of the group's query heads in turn.  Head gi's rows
     // start at q_base0 + gi * qh (Q/dO elements) and r_base0 + gi * rh (statistics).
     const int Tq = (Sq + FB_T - 1) / FB_T;
     const int t0 = CAUSAL ? min(k0 / FB_T, Tq) : 0;
     const int nT = Tq - t0;
     const int U = p.group * nT;
-    const int64_t qh = p.cu_q ? (int64_t)D : (int64_t)Sq * D;
+    const int64_t qh = p.cu_q ? (int64_t)p.dr : (int64_t)Sq * p.dr;
     const int64_t rh = p.cu_q ? (int64_t)p.total_q : (int64_t)Sq;
     const float* ws_lse = p.ws + p.rows;
     const float* ws_delta = p.ws;
@@ -684,8 +696,8 @@ flash_bwd_dkdv_kernel(BwdArgs p) {
     }
 #pragma unroll
     for (int kb = 0; kb < FbKv<D>::KB; ++kb) {
-        fb_store_rows<D>(p.dK + G0.k_base, G0.ks, kw + 32 * kb + c32, Sk, h, dk[kb], p.scale);
-        fb_store_rows<D>(p.dV + G0.k_base, G0.ks, kw + 32 * kb + c32, Sk, h, dv[kb], 1.0f);
+        fb_store_rows<D>(p.dK + G0.k_base, G0.ks, p.dr, kw + 32 * kb + c32, Sk, h, dk[kb], p.scale);
+        fb_store_rows<D>(p.dV + G0.k_base, G0.ks, p.dr, kw + 32 * kb + c32, Sk, h, dv[kb], 1.0f);
     }
 }
 
@@ -736,13 +748,14 @@ hipError_t launch_flash_bwd(const FlashBwdLaunch& f, hipStream_t stream) {
     a.c = f.scale * kLog2e;
     a.scale = f.scale;
     a.group = f.H / f.Hkv;
+    a.dr = f.D;
     a.cu_q = f.cu_q;
     a.cu_k = f.cu_k;
     a.H = f.H;
     a.Hkv = f.Hkv;
     a.total_q = f.total_q;
     a.total_k = f.total_k;
-    if (f.D == 128)
+    if (f.D > 64)
         launch_bwd_d<128>(a, f.B, f.causal, stream);
     else
         launch_bwd_d<64>(a, f.B, f.causal, stream);

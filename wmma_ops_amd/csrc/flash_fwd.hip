@@ -26,6 +26,9 @@
 //    the workgroup's last query are never loaded, tiles past a wave's own last query are
 //    skipped by that wave, masks are applied only on tiles that cross the diagonal or the
 //    end of K, and the heaviest query blocks are dispatched first.
+//  * Head dims: kernels are built for D = 64 and D = 128; any multiple of 8 up to 128 runs
+//    on the smallest that holds it, the d columns past the tensors' head dim arriving as
+//    zeros (no score or output contribution) and never stored.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "plan.hpp"
@@ -43,6 +46,8 @@ struct FlashArgs {
     int nqb;           // query blocks
     float scale_log2;  // scale * log2(e)
     int group;         // query heads per key/value head (1: multi-head attention)
+    int dr;            // head dim of the tensors: a multiple of 8, at most the kernel's D
+                       // (d columns dr .. D-1 load as zeros and are not stored)
     // Variable length (cu_q != nullptr): Q/O packed [total_q][H][D], K/V [total_k][Hkv][D];
     // sequence b spans rows cu_q[b] .. cu_q[b+1] (and cu_k likewise).  Sq/Sk then hold the
     // longest lengths; every row index is clamped into [0, total) so inconsistent offsets
@@ -322,18 +327,18 @@ flash_fwd_kernel(FlashArgs p) {
         const int ke = min(max(p.cu_k[b + 1], ka), p.total_k);
         Sq = min(qe - qa, p.Sq);
         Sk = min(ke - ka, p.Sk);
-        qs = p.H * D;
-        ks = p.Hkv * D;
-        q_base = (int64_t)qa * qs + (int64_t)hq * D;
-        k_base = (int64_t)ka * ks + (int64_t)(hq / p.group) * D;
+        qs = p.H * p.dr;
+        ks = p.Hkv * p.dr;
+        q_base = (int64_t)qa * qs + (int64_t)hq * p.dr;
+        k_base = (int64_t)ka * ks + (int64_t)(hq / p.group) * p.dr;
         lse_base = (int64_t)hq * p.total_q + qa;
     } else {
         Sq = p.Sq;
         Sk = p.Sk;
-        qs = D;
-        ks = D;
-        q_base = (int64_t)bh * Sq * D;
-        k_base = (int64_t)(bh / p.group) * Sk * D;
+        qs = p.dr;
+        ks = p.dr;
+        q_base = (int64_t)bh * Sq * p.dr;
+        k_base = (int64_t)(bh / p.group) * Sk * p.dr;
         lse_base = (int64_t)bh * Sq;
     }
     if (q0 >= Sq) return;  // a query block past this sequence (variable length): no work
@@ -342,7 +347,8 @@ flash_fwd_kernel(FlashArgs p) {
     const f16* Vb = p.V + k_base;
     f16* Ob = p.O + q_base;
 
-    // Q fragments (B operand of S^T): query qw + 32 qb + lane%32, d = 16 ds + 8 h + 0..7.
+    // Q fragments (B operand of S^T): query qw + 32 qb + lane%32, d = 16 ds + 8 h + 0..7
+    // (zeros for d >= dr, so padded d columns add nothing to the scores).
     f16x8 qf[FA_NQB][C::NDS];
     {
         const __amdgpu_buffer_rsrc_t rs = make_rsrc(Qb);
@@ -352,7 +358,9 @@ flash_fwd_kernel(FlashArgs p) {
 #pragma unroll
             for (int ds = 0; ds < C::NDS; ++ds)
                 qf[qb][ds] = as_f16x8(buf_load16(
-                    rs, q < Sq ? (uint32_t)(((int64_t)q * qs + 16 * ds + 8 * h) * 2) : kOobOffset));
+                    rs, q < Sq && 16 * ds + 8 * h < p.dr
+                            ? (uint32_t)(((int64_t)q * qs + 16 * ds + 8 * h) * 2)
+                            : kOobOffset));
         }
     }
 
@@ -360,14 +368,16 @@ flash_fwd_kernel(FlashArgs p) {
     L.h = h;
     L.dma_k = wave * (C::DMA * 1024);
     L.dma_v = wave * (C::DMA * 1024);
+    // LDS chunk pc of a row receives global chunk pc ^ swizzle; chunks at d >= dr load zeros.
 #pragma unroll
     for (int i = 0; i < C::DMA; ++i) {
         const int P = 64 * (wave * C::DMA + i) + lane;
         const int row = P / C::DCH, pc = P % C::DCH;
+        const int gk = pc ^ swz_k<D>(row), gv = pc ^ swz_v<D>(row);
         L.k_row[i] = row;
-        L.k_off[i] = (uint32_t)((row * ks + 8 * (pc ^ swz_k<D>(row))) * 2);
+        L.k_off[i] = 8 * gk < p.dr ? (uint32_t)((row * ks + 8 * gk) * 2) : kOobOffset;
         L.v_row[i] = row;
-        L.v_off[i] = (uint32_t)((row * ks + 8 * (pc ^ swz_v<D>(row))) * 2);
+        L.v_off[i] = 8 * gv < p.dr ? (uint32_t)((row * ks + 8 * gv) * 2) : kOobOffset;
     }
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -449,7 +459,7 @@ flash_fwd_kernel(FlashArgs p) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) v[e] = (f16)(O[db][qb][4 * g + e] * inv);
                     const int d = 32 * db + 8 * g + 4 * h;
-                    *reinterpret_cast<f16x4*>(Ob + (int64_t)q * qs + d) = v;
+                    if (d < p.dr) *reinterpret_cast<f16x4*>(Ob + (int64_t)q * qs + d) = v;
                 }
             }
         }
@@ -477,6 +487,7 @@ hipError_t launch_flash_fwd(const FlashLaunch& f, hipStream_t stream) {
     a.Sk = f.Sk;
     a.nqb = ceil_div(f.Sq, FA_BQ);
     a.group = f.H / f.Hkv;
+    a.dr = f.D;
     a.cu_q = f.cu_q;
     a.cu_k = f.cu_k;
     a.H = f.H;
@@ -486,7 +497,8 @@ hipError_t launch_flash_fwd(const FlashLaunch& f, hipStream_t stream) {
     a.lse = f.lse;
     a.scale_log2 = f.scale * 1.4426950408889634f;
     const int BH = f.B * f.H;
-    if (f.D == 128)
+    // head dims up to 64 run the D = 64 kernel, up to 128 the D = 128 kernel
+    if (f.D > 64)
         launch_d<128>(a, BH, f.causal, stream);
     else
         launch_d<64>(a, BH, f.causal, stream);

@@ -184,7 +184,7 @@ void check_flash_dense(const torch::Tensor& Q, const torch::Tensor& K, const tor
                 "Q and K must agree in batch and head_dim");
     TORCH_CHECK(K.size(1) > 0 && Q.size(1) % K.size(1) == 0,
                 "K/V heads must divide Q heads");
-    TORCH_CHECK(Q.size(3) == 64 || Q.size(3) == 128, "head_dim must be 64 or 128");
+    TORCH_CHECK(Q.size(3) >= 1 && Q.size(3) <= 128, "head_dim must be between 1 and 128");
 }
 
 // Checks of the packed inputs q [total_q,H,D], k/v [total_k,Hkv,D], cu_seqlens int32 [B+1].
@@ -205,7 +205,7 @@ void check_flash_varlen(const torch::Tensor& q, const torch::Tensor& k, const to
     TORCH_CHECK(cu_q.dtype() == torch::kInt32 && cu_k.dtype() == torch::kInt32 && cu_q.dim() == 1 &&
                     cu_q.sizes() == cu_k.sizes() && cu_q.size(0) >= 1,
                 "cu_seqlens must be int32 [B+1], equal for Q and K");
-    TORCH_CHECK(q.size(2) == 64 || q.size(2) == 128, "head_dim must be 64 or 128");
+    TORCH_CHECK(q.size(2) >= 1 && q.size(2) <= 128, "head_dim must be between 1 and 128");
 }
 
 // Gradient-side checks: dO and O have Q's shape (fp16, same device), lse is fp32 of the
@@ -222,6 +222,20 @@ void check_flash_grad_inputs(const torch::Tensor& Q, const torch::Tensor& dO, co
                 "lse must be float32 ", lse_shape);
 }
 
+// The kernels take head dims that are multiples of 8 (16-byte rows).  Other head dims run on
+// contiguous copies zero-padded to the next multiple of 8: the zero columns add nothing to
+// the scores, give zero output and gradient columns, and are dropped from the results.
+int64_t padded_head_dim(int64_t D) { return (D + 7) / 8 * 8; }
+
+torch::Tensor pad_head(const torch::Tensor& t, int64_t Dp) {
+    const int64_t D = t.size(-1);
+    return D == Dp ? t.contiguous() : torch::constant_pad_nd(t, {0, Dp - D}).contiguous();
+}
+
+torch::Tensor unpad_head(const torch::Tensor& t, int64_t D) {
+    return t.size(-1) == D ? t : t.narrow(-1, 0, D).contiguous();
+}
+
 float flash_scale(double scale, int64_t D) {
     return scale > 0.0 ? (float)scale : (float)(1.0 / std::sqrt((double)D));
 }
@@ -230,11 +244,11 @@ float flash_scale(double scale, int64_t D) {
 torch::Tensor flash_dense_fwd(torch::Tensor Q, torch::Tensor K, torch::Tensor V, bool causal,
                               double scale, torch::Tensor* lse_out) {
     check_flash_dense(Q, K, V);
-    const int64_t D = Q.size(3);
+    const int64_t D = Q.size(3), Dp = padded_head_dim(D);
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(Q.device());
-    Q = Q.contiguous();
-    K = K.contiguous();
-    V = V.contiguous();
+    Q = pad_head(Q, Dp);
+    K = pad_head(K, Dp);
+    V = pad_head(V, Dp);
     auto O = torch::empty_like(Q);
     float* lse = nullptr;
     if (lse_out) {
@@ -243,16 +257,16 @@ torch::Tensor flash_dense_fwd(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
     }
     int rc = wmma_flash_attn_fwd_lse(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(), lse,
                                      (int)Q.size(0), (int)Q.size(1), (int)K.size(1),
-                                     (int)Q.size(2), (int)K.size(2), (int)D, flash_scale(scale, D),
+                                     (int)Q.size(2), (int)K.size(2), (int)Dp, flash_scale(scale, D),
                                      causal ? 1 : 0, current_stream(Q));
     check_status(rc, "wmma_flash_attn_fwd_lse");
-    return O;
+    return unpad_head(O, D);
 }
 
 // flash_attention(Q, K, V, causal=False, scale=-1.0) (README.md:221-251): Q [B,H,Sq,D],
 // K/V [B,Hkv,Sk,D] fp16 with Hkv dividing H (Hkv < H: grouped-query attention, query head h
-// reads key/value head h / (H/Hkv)); scale <= 0 selects 1/sqrt(D).  Returns fp16
-// [B,H,Sq,D].
+// reads key/value head h / (H/Hkv)); D from 1 to 128; scale <= 0 selects 1/sqrt(D).
+// Returns fp16 [B,H,Sq,D].
 torch::Tensor flash_attention(torch::Tensor Q, torch::Tensor K, torch::Tensor V, bool causal,
                               double scale) {
     return flash_dense_fwd(Q, K, V, causal, scale, nullptr);
@@ -277,13 +291,14 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> flash_attention_backward
     check_flash_dense(Q, K, V);
     check_flash_grad_inputs(Q, dO, O, lse, {Q.size(0), Q.size(1), Q.size(2)});
     const int64_t B = Q.size(0), H = Q.size(1), Sq = Q.size(2), D = Q.size(3);
+    const int64_t Dp = padded_head_dim(D);
     TORCH_CHECK(Sq == 0 || K.size(2) > 0, "K must have keys when Q has queries");
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(Q.device());
-    Q = Q.contiguous();
-    K = K.contiguous();
-    V = V.contiguous();
-    O = O.contiguous();
-    dO = dO.contiguous();
+    Q = pad_head(Q, Dp);
+    K = pad_head(K, Dp);
+    V = pad_head(V, Dp);
+    O = pad_head(O, Dp);
+    dO = pad_head(dO, Dp);
     lse = lse.contiguous();
     auto dQ = torch::empty_like(Q);
     auto dK = torch::empty_like(K);
@@ -293,21 +308,21 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> flash_attention_backward
     int rc = wmma_flash_attn_bwd(dO.data_ptr(), Q.data_ptr(), K.data_ptr(), V.data_ptr(),
                                  O.data_ptr(), lse.data_ptr<float>(), dQ.data_ptr(), dK.data_ptr(),
                                  dV.data_ptr(), ws.data_ptr(), ws_bytes, (int)B, (int)H,
-                                 (int)K.size(1), (int)Sq, (int)K.size(2), (int)D,
+                                 (int)K.size(1), (int)Sq, (int)K.size(2), (int)Dp,
                                  flash_scale(scale, D), causal ? 1 : 0, current_stream(Q));
     check_status(rc, "wmma_flash_attn_bwd");
-    return {dQ, dK, dV};
+    return {unpad_head(dQ, D), unpad_head(dK, D), unpad_head(dV, D)};
 }
 
 torch::Tensor flash_varlen_fwd(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor cu_q,
                                torch::Tensor cu_k, int64_t max_q, int64_t max_k, bool causal,
                                double scale, torch::Tensor* lse_out) {
     check_flash_varlen(q, k, v, cu_q, cu_k);
-    const int64_t D = q.size(2);
+    const int64_t D = q.size(2), Dp = padded_head_dim(D);
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
-    q = q.contiguous();
-    k = k.contiguous();
-    v = v.contiguous();
+    q = pad_head(q, Dp);
+    k = pad_head(k, Dp);
+    v = pad_head(v, Dp);
     cu_q = cu_q.contiguous();
     cu_k = cu_k.contiguous();
     auto O = torch::empty_like(q);
@@ -319,10 +334,10 @@ torch::Tensor flash_varlen_fwd(torch::Tensor q, torch::Tensor k, torch::Tensor v
     int rc = wmma_flash_attn_varlen_fwd_lse(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(), lse, cu_q.data_ptr<int32_t>(),
         cu_k.data_ptr<int32_t>(), (int)(cu_q.size(0) - 1), (int)q.size(1), (int)k.size(1),
-        (int)q.size(0), (int)k.size(0), (int)max_q, (int)max_k, (int)D, flash_scale(scale, D),
+        (int)q.size(0), (int)k.size(0), (int)max_q, (int)max_k, (int)Dp, flash_scale(scale, D),
         causal ? 1 : 0, current_stream(q));
     check_status(rc, "wmma_flash_attn_varlen_fwd_lse");
-    return O;
+    return unpad_head(O, D);
 }
 
 // flash_attention_varlen(q [total_q, H, D], k/v [total_k, Hkv, D], cu_seqlens_q/k int32
@@ -350,13 +365,13 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> flash_attention_varlen_b
     bool causal, double scale) {
     check_flash_varlen(q, k, v, cu_q, cu_k);
     check_flash_grad_inputs(q, dO, O, lse, {q.size(1), q.size(0)});
-    const int64_t H = q.size(1), D = q.size(2);
+    const int64_t H = q.size(1), D = q.size(2), Dp = padded_head_dim(D);
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
-    q = q.contiguous();
-    k = k.contiguous();
-    v = v.contiguous();
-    O = O.contiguous();
-    dO = dO.contiguous();
+    q = pad_head(q, Dp);
+    k = pad_head(k, Dp);
+    v = pad_head(v, Dp);
+    O = pad_head(O, Dp);
+    dO = pad_head(dO, Dp);
     lse = lse.contiguous();
     cu_q = cu_q.contiguous();
     cu_k = cu_k.contiguous();
@@ -376,9 +391,9 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> flash_attention_varlen_b
         lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
         cu_q.data_ptr<int32_t>(), cu_k.data_ptr<int32_t>(), ws.data_ptr(), ws_bytes,
         (int)(cu_q.size(0) - 1), (int)H, (int)k.size(1), (int)q.size(0), (int)k.size(0),
-        (int)max_q, (int)max_k, (int)D, flash_scale(scale, D), causal ? 1 : 0, current_stream(q));
+        (int)max_q, (int)max_k, (int)Dp, flash_scale(scale, D), causal ? 1 : 0, current_stream(q));
     check_status(rc, "wmma_flash_attn_varlen_bwd");
-    return {dq, dk, dv};
+    return {unpad_head(dq, D), unpad_head(dk, D), unpad_head(dv, D)};
 }
 
 void check_qweight(const torch::Tensor& q) {
