@@ -167,13 +167,14 @@ def test_w4a16_plan_make(lib):
     assert plan(16, 4096, 4096) == (4, 1, 4096, 0)     # skinny, 128 tiles: half the CUs, no split
     k, s, kps, ws = plan(16, 2048, 4096)               # skinny, 64 tiles: K split
     assert (k, s, kps) == (4, 2, 2048) and ws == 2 * 16 * 2048 * 4
-    assert plan(128, 14336, 4096)[:2] == (5, 2)        # 112 tiles of 128x128: split 2
-    assert plan(128, 4096, 4096)[:2] == (5, 4)         # 32 tiles: split capped at 4 ...
-    assert plan(64, 4096, 4096)[:2] == (5, 8)          # ... and at 8 for M <= 64
+    assert plan(128, 14336, 4096)[:2] == (5, 1)        # 224 tiles of 64x128: no split
+    assert plan(128, 4096, 4096)[:2] == (5, 4)         # 64 tiles: 256 / 64 ways
+    assert plan(64, 4096, 4096)[:2] == (5, 8)          # 32 tiles: 8 ways (the cap)
+    assert plan(64, 11008, 4096)[:2] == (5, 2)         # 86 tiles: 2 ways
     # skinny with two 32-column tiles per workgroup (256 pairs) and a 2-way K split
     assert plan(16, 8192, 8192) == (4, 2, 4096, 2 * 16 * 8192 * 4)
     assert plan(2048, 4096, 4096)[:2] == (5, 1)        # 512 tiles of 128x128, no split
-    assert plan(1024, 14336, 4096)[:2] == (5, 1)       # 224 tiles of 256x256
+    assert plan(1024, 14336, 4096)[:2] == (5, 1)       # 448 tiles of 128x256
     assert plan(32, 14336, 4096)[0] == 4
     assert plan(33, 14336, 4096)[0] == 5               # LDS-DMA GEMM beyond 32 rows
     assert plan(2048, 14336, 4096)[:2] == (5, 1)

@@ -100,13 +100,15 @@ def test_w4a16_skinny(wo, M, K, N, G):
     assert torch.equal(Yp, Yu)
 
 
-# The M > 32 LDS-DMA kernel: both tile configurations (128x128 below 512 rows, 256x256
-# from 512), partial M and N tiles, K shorter than the stage ring (K=192), K split
-# (M=64, N=1024: few tiles), G=32 (the two K halves of a chunk in different groups), lda > K,
-# both zero formats.
+# The M > 32 LDS-DMA kernel: the three tile configurations (64x128 up to 128 rows, 128x256
+# for grids of many such tiles -- M=4000, N=4128: 544, partial in M and N -- else 128x128),
+# partial M and N tiles, K shorter than the stage ring (K=192), K split (M=64, N=1024: few
+# tiles), G=32 (the two K halves of a chunk in different groups), lda > K, both zero
+# formats.
 @pytest.mark.parametrize("M,K,N,G", [(33, 1024, 4096, 128), (64, 2048, 1024, 64), (200, 192, 288, 32),
                                      (512, 1024, 2048, 128), (600, 512, 288, 256),
-                                     (1030, 2048, 1056, 128)])
+                                     (1030, 2048, 1056, 128), (100, 768, 4128, 64),
+                                     (4000, 512, 4128, 128)])
 def test_w4a16_gemm_tiles(wo, M, K, N, G):
     plan = wo.w4a16_plan(M, N, K, G)
     report("w4a16_gemm", M=M, K=K, N=N, G=G, plan=plan)

@@ -1218,10 +1218,15 @@ w4a16_gemm_kernel(W4Args p) {
 
     W4GSlot<FN> ring[NS];
     if (nk > 0) {
-        // Prologue: stages 0 .. NS-2 in flight.
+        // Prologue: stages 0 .. NS-2 in flight, in stage order.  The empty asm between the
+        // stages keeps the compiler from regrouping their loads (it would otherwise issue
+        // every scale and zero load last, and the main loop's first stages would then wait
+        // for all but the last few loads -- NS - 2 stages too early).
 #pragma unroll
-        for (int q = 0; q < NS - 1; ++q)
+        for (int q = 0; q < NS - 1; ++q) {
             w4g_issue<C, ZF>(p, L, ra, rw, rs, rz, q < nk ? kc0 + q : -1, lds + q * C::A_BYTES, ring[q]);
+            asm volatile("" ::: "memory");
+        }
         // Main loop, unrolled by NS so every register-ring slot is a static index.  Stage
         // t reads LDS slot t % NS and ring[t % NS]; it issues stage t + NS - 1 into LDS slot
         // (t - 1) % NS and ring[(t - 1) % NS], both free once this stage's barrier passed.
@@ -1301,18 +1306,27 @@ w4a16_gemm_kernel(W4Args p) {
             }
 }
 
-// W4A16 GEMM configurations: BM x BN, WM x WN waves, NS stages.
-//   big  256 x 256, 2 x 4 waves, 4 stages (128 KB LDS): from 512 rows
-//   mid  128 x 128, 1 x 4 waves, 4 stages (64 KB LDS):  otherwise.  One wave row, so each
-//        weight of the tile is dequantised once (a 2 x 2 grid dequantises every weight in
-//        both wave rows; measured 4-11% slower at M = 64..256).  6 or 8 stages measured no
-//        faster.
+// W4A16 GEMM configurations: BM x BN, all with one row of 4 waves (each weight of a tile
+// is dequantised by one wave only; a 2 x 2 grid dequantises every weight in both wave
+// rows and measured 4-11% slower at M = 64..256) and a 4-deep ring (6 or 8 stages
+// measured no faster).
+//   wide   128 x 256, wave tile 128 x 64 (64 KB LDS): grids of at least one tile per CU
+//   mid    128 x 128, wave tile 128 x 32 (64 KB LDS)
+//   short   64 x 128, wave tile  64 x 32 (32 KB LDS): M <= 128
+// (A 256 x 256 tile of 2 x 4 waves spills registers at two waves per SIMD; measured 5-26%
+// slower than 128 x 256 at M = 1024 .. 2048.)
+enum { W4G_TILE_WIDE = 0, W4G_TILE_MID = 1, W4G_TILE_SHORT = 2 };
+constexpr int kW4gTileM[3] = {128, 128, 64};
+constexpr int kW4gTileN[3] = {256, 128, 128};
+
 template <int ZF>
 void launch_w4g(const W4Args& a, int cfg, dim3 grid, hipStream_t stream) {
-    if (cfg == 0)
-        hipLaunchKernelGGL((w4a16_gemm_kernel<256, 256, 2, 4, 4, ZF>), grid, dim3(8 * kWave), 0, stream, a);
-    else
+    if (cfg == W4G_TILE_WIDE)
+        hipLaunchKernelGGL((w4a16_gemm_kernel<128, 256, 1, 4, 4, ZF>), grid, dim3(4 * kWave), 0, stream, a);
+    else if (cfg == W4G_TILE_MID)
         hipLaunchKernelGGL((w4a16_gemm_kernel<128, 128, 1, 4, 4, ZF>), grid, dim3(4 * kWave), 0, stream, a);
+    else
+        hipLaunchKernelGGL((w4a16_gemm_kernel<64, 128, 1, 4, 4, ZF>), grid, dim3(4 * kWave), 0, stream, a);
 }
 
 // ------------------------------------------------------------------ MFMA (M > GV_MAXM) --
@@ -1587,22 +1601,29 @@ W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
     }
     const int KC = K / 64;
     if (M > 32) {
-        // LDS-DMA W4A16 GEMM: 256x256 tiles when they alone occupy at least 3/4 of the
-        // CUs (from 512 rows), else 128x128 tiles; K split only to fill the chip.
-        // (Measured: M = 2048, N = 4096 -- 128 big tiles need a 2-way split whose
-        // partial-sum pass costs 16 us of 90, 512 small tiles none; M = 1024, N = 14336 --
-        // 224 big tiles beat 896 small ones by 20%.)
-        const int64_t big_tiles = (int64_t)ceil_div(M, 256) * ceil_div(N, 256);
-        const bool big = M >= 512 && 4 * big_tiles >= 3 * (int64_t)num_cus;
-        const int bm = big ? 256 : 128, bn = big ? 256 : 128;
-        const int64_t tiles = (int64_t)ceil_div(M, bm) * ceil_div(N, bn);
-        pl.big = big ? 1 : 0;
-        // Split only while every split keeps at least one CU's worth of tiles: the partial
-        // sums cost a second pass over M x N fp32 per split.  At most 4 ways, 8 for M <= 64
-        // (whose partial sums are half as large; measured at N = 4096: M = 48, 64 18.0 / 18.7 us
-        // with 4 ways, 15.6 / 16.9 with 8; M = 128 22.1 with 4 ways, 23.1 with 8).
+        // LDS-DMA W4A16 GEMM.  Tile (measured on MI355X at K = 4096, N in {4096, 11008,
+        // 14336}):
+        //   M <= 128: 64 x 128 -- 2-20% faster than 128 x 128 at M = 48..128;
+        //   128 x 256 when those tiles give at least one per CU, in whole multiples of the
+        //     CU count or 1.7 of them (M = 2048: 5-26% faster than 128 x 128; M = 1024,
+        //     N = 11008, 1.34 tiles per CU: 4% slower);
+        //   else 128 x 128.
+        // K split only to fill the chip.
+        const int64_t wide_tiles = (int64_t)ceil_div(M, 128) * ceil_div(N, 256);
+        int cfg = W4G_TILE_MID;
+        if (M <= 128)
+            cfg = W4G_TILE_SHORT;
+        else if (wide_tiles >= num_cus &&
+                 (wide_tiles % num_cus == 0 || 10 * wide_tiles >= 17 * (int64_t)num_cus))
+            cfg = W4G_TILE_WIDE;
+        const int64_t tiles = (int64_t)ceil_div(M, kW4gTileM[cfg]) * ceil_div(N, kW4gTileN[cfg]);
+        pl.big = cfg;
+        // Split while the tiles do not give one per CU: num_cus / tiles ways (the partial
+        // sums cost a second pass over M x N fp32 per split), at most 8 (measured with
+        // 64 x 128 tiles at N = 4096: M = 48, 64 best with 8 ways; M = 96, 128 with 4; at
+        // N = 11008, 14336: M = 64 with 2, M = 128 unsplit).
         int s = 1;
-        const int max_split = M <= 64 ? 8 : 4;
+        const int max_split = 8;
         if (tiles < num_cus)
             s = (int)std::min<int64_t>(std::max<int64_t>(num_cus / tiles, 1), max_split);
         s = std::max(1, std::min(s, KC / 4));
@@ -1670,10 +1691,9 @@ hipError_t launch_w4a16_zf(const W4Args& a, const W4A16Launch& w, hipStream_t st
         return hipGetLastError();
     }
     if (pl.kind == W4_GEMM) {
-        const bool big = pl.big != 0;
-        const int bm = big ? 256 : 128, bn = big ? 256 : 128;
+        const int bm = kW4gTileM[pl.big], bn = kW4gTileN[pl.big];
         const dim3 grid(ceil_div(w.M, bm) * ceil_div(w.N, bn), pl.split);
-        launch_w4g<ZF>(a, big ? 0 : 1, grid, stream);
+        launch_w4g<ZF>(a, pl.big, grid, stream);
     } else if (pl.kind == W4_SKINNY) {
         const int U = pl.k_per_split / (SK_NW * 128);
         const dim3 grid(pl.big ? ntiles / 2 : ntiles, pl.split);
