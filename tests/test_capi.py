@@ -176,7 +176,8 @@ def test_w4a16_plan_make(lib):
     assert plan(2048, 4096, 4096)[:2] == (5, 1)        # 512 tiles of 128x128, no split
     assert plan(1024, 14336, 4096)[:2] == (5, 1)       # 448 tiles of 128x256
     assert plan(32, 14336, 4096)[0] == 4
-    assert plan(33, 14336, 4096)[0] == 5               # LDS-DMA GEMM beyond 32 rows
+    assert plan(33, 14336, 4096)[0] == 5               # LDS-DMA GEMM beyond 32 rows ...
+    assert plan(64, 4096, 4608, 384)[0] == 3           # ... for group sizes 2^j only
     assert plan(2048, 14336, 4096)[:2] == (5, 1)
     assert plan(16, 14336, 4096, 64)[0] == 3           # G not 128 * 2^j: older tiled kernel
     assert plan(16, 14336, 4608, 384)[0] == 3

@@ -59,7 +59,8 @@ def test_w4a16_baseline(wo, M, N):
 
 
 @pytest.mark.parametrize("M,K,N,G", [(1, 256, 64, 32), (3, 512, 96, 64), (5, 1024, 128, 256),
-                                     (40, 512, 160, 128), (300, 1024, 96, 1024), (2, 64, 32, 64)])
+                                     (40, 512, 160, 128), (300, 1024, 96, 1024), (2, 64, 32, 64),
+                                     (40, 384, 96, 96), (129, 1152, 64, 384)])
 def test_w4a16_group_sizes_and_u8_zeros(wo, M, K, N, G):
     report("w4a16_g", M=M, K=K, N=N, G=G)
     A, q, s, z = oi.make_inputs(M, K, N, G, seed=M + K + N + G)

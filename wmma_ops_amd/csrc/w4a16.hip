@@ -231,6 +231,7 @@ struct W4Args {
     int split;
     int kc_per_split;     // 64-deep chunks per split
     int pp_shift;         // decode-MFMA kernel: log2(G / 128)
+    int g_shift;          // LDS-DMA GEMM: log2(G) (G a power of two there)
     int kg;               // K / G (groups)
     int y_half;           // Y is fp16 (each fp32 result rounded once), else fp32
 };
@@ -1028,8 +1029,10 @@ void launch_skinny_mb(const W4Args& a, int U, dim3 grid, hipStream_t stream) {
 //     one being dequantised.
 // k-step j of a stage (j = 0..3) uses word j of every lane: K offsets 32*(l/32) + 8j .. +7,
 // matched on the A side by chunk 4*(l/32) + j of the lane's row.  Dequantisation per word:
-// pair i = ((w >> 4i) & 0x000F000F) | 0x6400.. (= 1024 + q, exact), minus (1024 + z)
-// (exact), times s (one fp16 rounding) -- W = fp16((q - z) s), the A operand stays raw.
+// pair i, the nibbles at bits 4i and 16 + 4i, as 1024 + q (i even: (w >> 4i) & 0x000F000F
+// | 0x6400..) or 64 + q (i odd: bits 4..7 kept in place, | 0x5400..), exact, minus the
+// same encoding of z (exact), times s (one fp16 rounding) -- W = fp16((q - z) s), the A
+// operand stays raw.  G is a power of two (a shift finds a K offset's group).
 // One barrier per stage, after this wave's share of the stage has landed (vmcnt): from
 // then on every wave's copy is visible and every wave has finished reading the slot the
 // new DMA overwrites.
@@ -1078,7 +1081,7 @@ __device__ __forceinline__ void w4g_issue(const W4Args& p, const W4GLane& L,
 #pragma unroll
     for (int i = 0; i < C::A_DMA; ++i)
         lds_dma16(ra, (L.a_off[i] + k * 128u) | dead, dst + L.a_dst + i * 1024);
-    const uint32_t g = (64u * k + 32u * (uint32_t)L.h) / (uint32_t)p.G;
+    const uint32_t g = (64u * k + 32u * (uint32_t)L.h) >> p.g_shift;  // G = 2^g_shift
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) {
         R.w[j] = buf_load16(rw, (L.w_off[j] + k * 512u) | dead);
@@ -1107,7 +1110,7 @@ __device__ __forceinline__ void w4g_stage(const W4Args& p, const W4GLane& L,
                                           WMMA_LDS unsigned char* __restrict__ dst, int kc_next,
                                           const W4GSlot<C::FN>& R, W4GSlot<C::FN>& Rn,
                                           bool compute, int lane, uint32_t magic,
-                                          f32x16 (&acc)[C::FM][C::FN]) {
+                                          uint32_t magic_hi, f32x16 (&acc)[C::FM][C::FN]) {
     w4g_issue<C, ZF>(p, L, ra, rw, rs, rz, kc_next, dst, Rn);
     if (!compute) return;
     // This stage's register slot passes through an empty asm first: without it the
@@ -1117,7 +1120,11 @@ __device__ __forceinline__ void w4g_stage(const W4Args& p, const W4GLane& L,
     W4GSlot<C::FN> r = R;
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) asm volatile("" : "+v"(r.w[j]), "+v"(r.s[j]), "+v"(r.z[j]));
-    f16x2 zs[C::FN], ss[C::FN];
+    // Nibble pairs q = 0, 2 (bits 4q and 16 + 4q) become 1024 + q through the 0x6400
+    // exponent, pairs 1, 3 -- left in place at bits 4..7 -- become 64 + q through 0x5400;
+    // each is less the same encoding of z (exact), times s (one rounding).  One shift per
+    // word instead of three.
+    f16x2 zs[C::FN], zshi[C::FN], ss[C::FN];
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) {
         uint32_t z;
@@ -1125,8 +1132,9 @@ __device__ __forceinline__ void w4g_stage(const W4Args& p, const W4GLane& L,
             z = (r.z[j] >> (4 * (lane & 7))) & 0xFu;  // column % 8 == lane % 8
         else
             z = r.z[j] & 0xFu;
-        const uint32_t zh = 0x6400u | z, sv = r.s[j] & 0xFFFFu;
+        const uint32_t zh = 0x6400u | z, zhh = 0x5400u | (z << 4), sv = r.s[j] & 0xFFFFu;
         zs[j] = as_h2(zh | (zh << 16));
+        zshi[j] = as_h2(zhh | (zhh << 16));
         ss[j] = as_h2(sv | (sv << 16));
     }
 #pragma unroll
@@ -1134,11 +1142,12 @@ __device__ __forceinline__ void w4g_stage(const W4Args& p, const W4GLane& L,
         f16x8 b[C::FN];
 #pragma unroll
         for (int j = 0; j < C::FN; ++j) {
-            const uint32_t x = r.w[j][ks];
+            const uint32_t x = r.w[j][ks], x8 = x >> 8;
             u32x4 bv;
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                bv[q] = as_u32((as_h2(((x >> (4 * q)) & 0x000F000Fu) | magic) - zs[j]) * ss[j]);
+            bv[0] = as_u32((as_h2((x & 0x000F000Fu) | magic) - zs[j]) * ss[j]);
+            bv[1] = as_u32((as_h2((x & 0x00F000F0u) | magic_hi) - zshi[j]) * ss[j]);
+            bv[2] = as_u32((as_h2((x8 & 0x000F000Fu) | magic) - zs[j]) * ss[j]);
+            bv[3] = as_u32((as_h2((x8 & 0x00F000F0u) | magic_hi) - zshi[j]) * ss[j]);
             b[j] = as_f16x8(bv);
         }
         f16x8 a[C::FM];
@@ -1213,8 +1222,8 @@ w4a16_gemm_kernel(W4Args p) {
     for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
-    uint32_t magic = 0x64006400u;
-    asm volatile("" : "+v"(magic));
+    uint32_t magic = 0x64006400u, magic_hi = 0x54005400u;
+    asm volatile("" : "+v"(magic), "+v"(magic_hi));
 
     W4GSlot<FN> ring[NS];
     if (nk > 0) {
@@ -1244,7 +1253,7 @@ w4a16_gemm_kernel(W4Args p) {
                 w4g_stage<C, ZF>(p, L, ra, rw, rs, rz, lds + q * C::A_BYTES,
                                  lds + ((q + NS - 1) % NS) * C::A_BYTES,
                                  tn_ < nk ? kc0 + tn_ : -1, ring[q], ring[(q + NS - 1) % NS],
-                                 true, lane, magic, acc);
+                                 true, lane, magic, magic_hi, acc);
             }
         }
         const int t1 = full_turns * NS;
@@ -1256,7 +1265,7 @@ w4a16_gemm_kernel(W4Args p) {
                 asm volatile("" ::: "memory");
                 w4g_stage<C, ZF>(p, L, ra, rw, rs, rz, lds + q * C::A_BYTES,
                                  lds + ((q + NS - 1) % NS) * C::A_BYTES, -1, ring[q],
-                                 ring[(q + NS - 1) % NS], true, lane, magic, acc);
+                                 ring[(q + NS - 1) % NS], true, lane, magic, magic_hi, acc);
             }
         }
         wait_vmcnt<0>();
@@ -1566,9 +1575,9 @@ hipError_t launch_int4_params_slice(const void* scales, const void* zeros, int z
 //                pass) only when fewer than 2*CUs workgroups would exist.
 //   skinny       4 < M <= 32 with G = 128 * 2^j: 32 or 64 columns per workgroup, K split (plus
 //                a reduce pass) only when the tiles alone give under half a workgroup per CU.
-//   gemm         M > 32: LDS-DMA MFMA GEMM (256x256 tiles from 512 rows, else 128x128),
-//                K split (plus a reduce pass) only when the tiles cannot fill the chip.
-//   mfma         everything else (M <= 32 shapes the kernels above do not take).
+//   gemm         M > 32 with G a power of two: LDS-DMA MFMA GEMM (tile below), K split
+//                (plus a reduce pass) only when the tiles cannot fill the chip.
+//   mfma         everything else (the shapes the kernels above do not take).
 W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
     if (num_cus <= 0) num_cus = 256;
     W4A16Plan pl{};
@@ -1600,7 +1609,7 @@ W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
         return pl;
     }
     const int KC = K / 64;
-    if (M > 32) {
+    if (M > 32 && (G & (G - 1)) == 0) {
         // LDS-DMA W4A16 GEMM.  Tile (measured on MI355X at K = 4096, N in {4096, 11008,
         // 14336}):
         //   M <= 128: 64 x 128 -- 2-20% faster than 128 x 128 at M = 48..128;
@@ -1760,6 +1769,8 @@ hipError_t launch_w4a16(const W4A16Launch& w, hipStream_t stream) {
     a.y_half = w.y_half ? 1 : 0;
     a.pp_shift = 0;
     while (w.G >= 128 && (128 << (a.pp_shift + 1)) <= w.G) ++a.pp_shift;
+    a.g_shift = 0;
+    while ((2 << a.g_shift) <= w.G) ++a.g_shift;
     if (w.zeros_format == WMMA_ZEROS_PACKED) return launch_w4a16_zf<WMMA_ZEROS_PACKED>(a, w, stream);
     if (w.zeros_format == WMMA_ZEROS_SLICED) return launch_w4a16_zf<WMMA_ZEROS_SLICED>(a, w, stream);
     return launch_w4a16_zf<WMMA_ZEROS_U8>(a, w, stream);
