@@ -72,12 +72,14 @@ struct GemmArgs {
 // ------------------------------------------------------------------------------------
 template <int KCH>
 __device__ __forceinline__ int swz_a(int r) {
-    // Conflict-free for 16-byte reads of 16 consecutive rows (64 banks) and of 8
-    // consecutive rows (32 banks).
+    // Chunk XOR of row r for the fragment reads (ds_read_b128 of 32 consecutive rows at
+    // one logical chunk per half-wave).  Both forms measured conflict-free on gfx950
+    // (SQ_LDS_BANK_CONFLICT = 0 in a probe of this exact access pattern); for 64-byte rows
+    // ((r >> 1) ^ (r >> 3)) & 3 measured 4 conflict cycles per read.
     if constexpr (KCH == 8)
         return (r ^ (r >> 3)) & 7;
     else
-        return ((r >> 1) ^ (r >> 3)) & 3;
+        return (r >> 2) & 3;
 }
 
 template <int BNC>
