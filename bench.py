@@ -15,8 +15,9 @@ timed steps between two synchronisations; `value` = 2*M*N*K / time.
 `roofline.achieved` divides the same FLOPs by the kernel's mean duration measured with
 HIP events on the stream the kernel is launched on (the current stream).  The W4A16 M=1
 decode figures (configs[3], K=4096, N in {4096, 14336}, G=128) ride along in the same
-line; the CPU baseline (N=1 only) is the oracle's fp32 torch.matmul on the host cores
-over a bounded sample of the same 4096^3 workload.
+line; the CPU baseline (N=1 only) is the oracle on the host cores over bounded samples
+of the same workloads: fp32 torch.matmul at 4096^3 (`value`), the W4A16 M=1 dequant +
+matmul at N=14336, and fp32 SDPA on 2 heads of configs[4].
 
 Workload families (--workload):
   gemm       configs[0..1]: M=N=K in {512,1024,2048,4096} and 4096x4096x2048
@@ -30,6 +31,8 @@ Workload families (--workload):
              traffic (libwmma_calib.so): the ceiling the GEMM main loop is held against
   read_floor a plain streaming read of the W4A16 M=1 weight sizes and of 1 GiB, graph
              replayed over rotating buffers: the floor of the HBM-bound kernels
+  vendor     torch.mm (hipBLASLt/rocBLAS, fp32 and fp16 output) and torch's flash SDPA on
+             the same shapes, for comparison
 HBM-bound cases rotate their inputs over more than 512 MB (twice the 256 MB MALL) so the
 bytes really come from HBM; microsecond-scale kernels are replayed from a HIP graph.
 
@@ -156,6 +159,17 @@ def line(**kw):
     print(json.dumps(kw), flush=True)
 
 
+def roofline(nbytes, flops, ms):
+    """The binding roofline of a case: the larger of its HBM time (bytes / 8 TB/s) and its
+    matrix-pipe time (FLOPs / 2.5 PFLOP/s), as a fraction of the measured time, with each
+    fraction beside it."""
+    t = ms * 1e-3
+    f_hbm = nbytes / PEAK_HBM_BPS / t
+    f_mfma = flops / PEAK_FP16_FLOPS / t
+    return {"bound": "hbm" if f_hbm >= f_mfma else "mfma", "roofline_frac": round(max(f_hbm, f_mfma), 4),
+            "frac_hbm": round(f_hbm, 4), "frac_mfma": round(f_mfma, 4)}
+
+
 def copies_for(nbytes):
     return max(2, math.ceil(ROTATE_BYTES / max(nbytes, 1)))
 
@@ -232,8 +246,8 @@ def fam_skinny(wo):
         err = og.max_rel_err(wo.matmul(As[0], Bs[0]), og.gemm_ref(A, B))
         line(family="skinny", M=m, N=n, K=k, plan=wo.gemm_plan(m, n, k), us=round(ms * 1e3, 2),
              bytes=nbytes, GBps=round(nbytes / (ms * 1e-3) / 1e9, 1),
-             frac_hbm=round(nbytes / (ms * 1e-3) / PEAK_HBM_BPS, 4),
-             TFLOPS=round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 2), rotation_copies=cp,
+             TFLOPS=round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 2),
+             **roofline(nbytes, 2.0 * m * n * k, ms), rotation_copies=cp,
              max_rel_err=float(f"{err:.3e}"))
         del As, Bs
 
@@ -268,8 +282,8 @@ def w4a16_case(wo, m, n, use_graph=True):
     fl = 2.0 * m * n * kw
     return {"M": m, "N": n, "K": kw, "G": G, "bytes": nbytes, "us_per_call": round(ms * 1e3, 3),
             "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-            "hbm_frac": round(nbytes / (ms * 1e-3) / PEAK_HBM_BPS, 4),
-            "TFLOPS": round(fl / (ms * 1e-3) / 1e12, 2), "rotation_copies": cp,
+            "TFLOPS": round(fl / (ms * 1e-3) / 1e12, 2), **roofline(nbytes, fl, ms),
+            "rotation_copies": cp,
             "timing": "graph replay" if use_graph else "stream launches",
             "max_rel_err": float(f"{err:.3e}")}
 
@@ -325,17 +339,8 @@ def fam_flash(wo):
     # CPU baseline: fp32 SDPA on the host cores (forward, and forward + autograd backward)
     # over a bounded sample of (batch, head) slices of the same workload
     if not QUICK:
-        threads = cpu_threads()
-        Q, Kt, V = oatt.make_inputs(1, 2, S, D, seed=42 + 4)
-        dO = torch.randn(1, 2, S, D, generator=torch.Generator().manual_seed(77)).half()
         for causal in (False, True):
-            t, n = cpu_time(lambda: oatt.sdpa_ref(Q, Kt, V, causal), 3.0, 10)
-            tb, nb = cpu_time(lambda: oatt.sdpa_bwd_ref(Q, Kt, V, dO, causal), 3.0, 10)
-            fl = 4.0 * 2 * S * S * D if not causal else 4.0 * 2 * D * S * (S + 1) / 2
-            line(family="flash_cpu", S=S, D=D, causal=causal, cores=threads, cpu_model=cpu_model(),
-                 fwd_TFLOPS=round(fl / t / 1e12, 4), bwd_TFLOPS=round(2.5 * fl / tb / 1e12, 4),
-                 sample=f"2 heads of [1,2,{S},{D}]: sdpa_ref {n} calls, median {t * 1e3:.0f} ms; "
-                        f"sdpa_bwd_ref {nb} calls, median {tb * 1e3:.0f} ms")
+            line(family="flash_cpu", causal=causal, **cpu_flash_sample(causal, 3.0, backward=True))
     # packed variable-length batch (flash_attention_varlen): six ragged sequences, 16384
     # tokens, 32 query / 8 key-value heads; FLOPs counted per sequence
     lens = [1024, 3072, 2048, 4096, 512, 5632]
@@ -360,6 +365,52 @@ def fam_flash(wo):
              TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
              frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4),
              max_rel_err=float(f"{err:.3e}"))
+
+
+def fam_vendor(wo):
+    """The vendor libraries torch dispatches to on the same inputs, for comparison (not
+    this library's code): torch.mm fp16 x fp16 with fp32 output (out_dtype) and with fp16
+    output (hipBLASLt / rocBLAS), and torch's flash scaled_dot_product_attention on
+    configs[4] (the FLASH_ATTENTION backend only; reported unavailable otherwise)."""
+    import torch
+
+    for (m, n, k) in [(2048, 2048, 2048), (4096, 4096, 4096), (4096, 4096, 2048)]:
+        g = torch.Generator().manual_seed(42 + 1)
+        Ad = torch.randn(m, k, generator=g).half().cuda()
+        Bd = torch.randn(k, n, generator=g).half().cuda()
+        fl = 2.0 * m * n * k
+        for out in ("f32", "f16"):
+            if out == "f32":
+                fn = lambda i: torch.mm(Ad, Bd, out_dtype=torch.float32)
+            else:
+                fn = lambda i: torch.mm(Ad, Bd)
+            ms = time_batches(fn, 50)
+            line(family="vendor_gemm", M=m, N=n, K=k, out=out, library="torch.mm (hipBLASLt/rocBLAS)",
+                 us=round(ms * 1e3, 2), TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
+                 frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4))
+            # this library on the same inputs, timed the same way
+            if out == "f32":
+                ms2 = time_batches(lambda i: wo.matmul(Ad, Bd), 50)
+                line(family="vendor_gemm", M=m, N=n, K=k, out=out, library="wmma_ops_amd.matmul",
+                     us=round(ms2 * 1e3, 2), TFLOPS=round(fl / (ms2 * 1e-3) / 1e12, 1),
+                     frac_mfma_peak=round(fl / (ms2 * 1e-3) / PEAK_FP16_FLOPS, 4))
+        del Ad, Bd
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    B, H, S, D = 4, 32, 4096, 128
+    g = torch.Generator().manual_seed(42 + 4)
+    Q, Kt, V = (torch.randn(B, H, S, D, generator=g).half().cuda() for _ in range(3))
+    for causal in (False, True):
+        fl = 4.0 * B * H * S * S * D if not causal else 4.0 * B * H * D * S * (S + 1) / 2
+        try:
+            with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+                fn = lambda i: torch.nn.functional.scaled_dot_product_attention(Q, Kt, V, is_causal=causal)
+                ms = time_batches(fn, 5)
+            line(family="vendor_flash", B=B, H=H, S=S, D=D, causal=causal,
+                 library="torch SDPA (FLASH_ATTENTION backend)", us=round(ms * 1e3, 1),
+                 TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1))
+        except RuntimeError as e:
+            line(family="vendor_flash", causal=causal, library="torch SDPA", unavailable=str(e)[:200])
 
 
 def fam_copy(wo):
@@ -449,7 +500,7 @@ def fam_read_floor(wo):
 
 FAMILIES = {"gemm": fam_gemm, "epilogue": fam_epilogue, "skinny": fam_skinny,
             "w4a16": fam_w4a16, "flash": fam_flash, "copy": fam_copy,
-            "mfma_ceiling": fam_mfma_ceiling, "read_floor": fam_read_floor}
+            "mfma_ceiling": fam_mfma_ceiling, "read_floor": fam_read_floor, "vendor": fam_vendor}
 
 
 # ------------------------------------------------------------------------ headline --
@@ -483,15 +534,26 @@ def gemm_bench(wo, steps, warmup):
 
 
 def cpu_model() -> str:
-    """The host CPU's model name (what lscpu prints), read from /proc/cpuinfo."""
+    """The host CPU as /proc/cpuinfo describes it: model name, family / model / stepping
+    (a virtualised host may report only a generic name), clock, and the widest x86 vector
+    extension the matmul kernels can use."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for ln in f:
-                if ln.startswith("model name"):
-                    return ln.split(":", 1)[1].strip()
+                if ":" not in ln:
+                    if info:
+                        break  # first processor only
+                    continue
+                k, v = (x.strip() for x in ln.split(":", 1))
+                info.setdefault(k, v)
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    flags = set(info.get("flags", "").split())
+    simd = "avx512" if "avx512f" in flags else "avx2" if "avx2" in flags else "sse"
+    return (f"{info.get('model name', 'unknown')} (family {info.get('cpu family', '?')}, model "
+            f"{info.get('model', '?')}, stepping {info.get('stepping', '?')}, "
+            f"{info.get('cpu MHz', '?')} MHz, {simd})")
 
 
 def cpu_threads() -> int:
@@ -519,10 +581,35 @@ def cpu_time(fn, seconds, max_calls=50):
     return statistics.median(times), len(times)
 
 
+def cpu_flash_sample(causal, seconds, backward=False):
+    """fp32 SDPA of the oracle (oracle.attention.sdpa_ref; with backward=True also its
+    autograd backward) on the host cores, over 2 (batch, head) slices of configs[4]
+    ([4,32,4096,128]): a bounded sample of the flash workload, FLOPs counted as on the GPU."""
+    import torch
+
+    from oracle import attention as oatt
+
+    threads = cpu_threads()
+    S, D = 4096, 128
+    Q, Kt, V = oatt.make_inputs(1, 2, S, D, seed=42 + 4)
+    fl = 4.0 * 2 * S * S * D if not causal else 4.0 * 2 * D * S * (S + 1) / 2
+    t, n = cpu_time(lambda: oatt.sdpa_ref(Q, Kt, V, causal), seconds, 10)
+    out = {"value": round(fl / t / 1e12, 4), "unit": "TFLOPS", "cores": threads, "kind": "port",
+           "sample": f"2 heads of [4,32,{S},{D}] (causal={causal}): {n} calls of "
+                     f"oracle.attention.sdpa_ref, median {t * 1e3:.0f} ms"}
+    if backward:
+        dO = torch.randn(1, 2, S, D, generator=torch.Generator().manual_seed(77)).half()
+        tb, nb = cpu_time(lambda: oatt.sdpa_bwd_ref(Q, Kt, V, dO, causal), seconds, 10)
+        out["bwd_TFLOPS"] = round(2.5 * fl / tb / 1e12, 4)
+        out["sample"] += f"; {nb} calls of sdpa_bwd_ref, median {tb * 1e3:.0f} ms"
+    out["cpu_model"] = cpu_model()
+    return out
+
+
 def cpu_baseline(seconds):
     """The oracle on host cores, bounded samples of the headline workloads: fp32
-    torch.matmul at 4096^3, and the W4A16 M = 1 decode (GPTQ unpack, fp16((q - z) * s)
-    dequantisation and matmul, N = 14336)."""
+    torch.matmul at 4096^3, the W4A16 M = 1 decode (GPTQ unpack, fp16((q - z) * s)
+    dequantisation and matmul, N = 14336), and fp32 SDPA on 2 heads of configs[4]."""
     import torch
 
     from oracle import gemm as og
@@ -546,6 +633,9 @@ def cpu_baseline(seconds):
     out["w4a16_m1"] = {"value": round(nbytes / tw / 1e9, 3), "unit": "GB/s", "cores": threads,
                        "sample": f"{nw} calls of unpack_gptq + dequant + matmul at M=1, N=14336, "
                                  f"K=4096, G=128 (oracle.int4), median {tw * 1e3:.1f} ms"}
+    fs = cpu_flash_sample(False, seconds / 4)
+    fs.pop("cpu_model")
+    out["flash"] = fs
     return out
 
 
