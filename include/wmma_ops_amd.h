@@ -253,10 +253,11 @@ int wmma_int4_permute_rows(const int32_t* qweight, const int32_t* perm, int K, i
  * Flash-attention forward.  Q [B,H,Sq,D], K and V [B,H,Sk,D], O [B,H,Sq,D]; fp16,
  * contiguous.  O = softmax(scale * Q K^T (+ causal mask: key j <= query i, aligned to
  * the top left for any Sq, Sk, as torch's scaled_dot_product_attention(is_causal=True)))
- * V, FP32 online softmax and accumulation.  D: a multiple of 8 from 8 to 128 (other head
- * dims return WMMA_ERR_UNSUPPORTED; the torch layer zero-pads D to a multiple of 8).  The
- * same holds for every flash entry point below.  A query row whose keys are all masked
- * (i.e. none, since key 0 is always kept) cannot occur.
+ * V, FP32 online softmax and accumulation.  D: a multiple of 8 from 8 to 256 for this and
+ * every forward entry point below, from 8 to 128 for the backward entry points (other
+ * head dims return WMMA_ERR_UNSUPPORTED; the torch layer zero-pads D to a multiple of 8).
+ * A query row whose keys are all masked (i.e. none, since key 0 is always kept) cannot
+ * occur.
  * Replaces the documented (unbound) flash_attention(Q,K,V,causal=False,scale=-1.0)
  * (README.md:221-251).  A caller's scale <= 0 is resolved to 1/sqrt(D) before this call.
  */

@@ -293,10 +293,10 @@ def test_prepack_params_validation_codes(lib):
 def test_flash_validation_codes(lib):
     f = lambda **kw: lib.wmma_flash_attn_fwd(FAKE, FAKE, FAKE, kw.get("O", FAKE), 1, 1, kw.get("S", 128),
                                              kw.get("S", 128), kw.get("D", 128), kw.get("scale", 0.1), 0, None)
-    # head dims: multiples of 8 from 8 to 128 (the torch layer pads other sizes)
-    for D in (0, 4, 100, 136, 256):
+    # head dims: multiples of 8 from 8 to 256 (the torch layer pads other sizes)
+    for D in (0, 4, 100, 264, 512):
         assert f(D=D) == UNSUPPORTED, D
-    assert b"multiples of 8" in lib.wmma_last_error()
+    assert b"multiples of 8 from 8 to 256" in lib.wmma_last_error()
     assert f(scale=0.0) == INVALID
     assert f(scale=float("nan")) == INVALID
     assert f(O=None) == INVALID
@@ -319,7 +319,7 @@ def test_flash_training_validation_codes(lib):
     # forward with log-sum-exp
     f = lambda **kw: lib.wmma_flash_attn_fwd_lse(FAKE, FAKE, FAKE, FAKE, kw.get("lse", FAKE), 1, 4, 2,
                                                  128, 128, kw.get("D", 128), 0.1, 0, None)
-    for D in (4, 100, 136):
+    for D in (4, 100, 264):
         assert f(D=D) == UNSUPPORTED, D
     assert f(lse=FAKE + 2) == MISALIGNED
     # workspace: two fp32 statistics per query row
@@ -334,6 +334,8 @@ def test_flash_training_validation_codes(lib):
                                        kw.get("Sq", 128), kw.get("Sk", 128), kw.get("D", 128),
                                        kw.get("scale", 0.1), 0, None)
     assert bwd(D=36) == UNSUPPORTED
+    assert bwd(D=136) == UNSUPPORTED               # the backward pass: D up to 128
+    assert b"from 8 to 128" in lib.wmma_last_error()
     assert bwd(Hkv=3) == INVALID
     assert bwd(scale=-1.0) == INVALID
     assert bwd(dO=None) == INVALID

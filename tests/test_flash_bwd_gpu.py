@@ -222,6 +222,15 @@ def test_flash_bwd_no_queries(wo):
 
 
 def test_flash_bwd_errors(wo):
+    # the backward pass takes head dims up to 128: larger ones are refused up front
+    Qd = torch.zeros(1, 1, 8, 160, dtype=torch.half, device="cuda", requires_grad=True)
+    with pytest.raises(RuntimeError, match="backward pass supports head_dim up to 128"):
+        wo.flash_attention(Qd, Qd, Qd)
+    with torch.no_grad():
+        assert wo.flash_attention(Qd, Qd, Qd).shape == Qd.shape
+    O, lse = wo.flash_attention_forward(Qd.detach(), Qd.detach(), Qd.detach())
+    with pytest.raises(RuntimeError, match="backward pass supports head_dim up to 128"):
+        wo.flash_attention_backward(O, Qd.detach(), Qd.detach(), Qd.detach(), O, lse)
     Q, K, V = (X.cuda() for X in oatt.make_inputs(1, 2, 16, 64, seed=1))
     O, lse = wo.flash_attention_forward(Q, K, V)
     with pytest.raises(RuntimeError, match="lse must be float32"):

@@ -66,12 +66,13 @@ def test_flash_shapes(wo, causal, B, H, Sq, Sk, D):
     _check(O, oatt.sdpa_ref(Q, K, V, causal))
 
 
-# Head dims other than the kernels' 64 and 128: multiples of 8 run on the D = 64 or D = 128
-# kernel with the missing d columns loaded as zeros and not stored; other sizes are
-# zero-padded to a multiple of 8 by the torch layer.  Default scale 1/sqrt(D) of the
+# Head dims other than the kernels' 64, 128 and 256: multiples of 8 run on the smallest
+# kernel that holds them with the missing d columns loaded as zeros and not stored; other
+# sizes are zero-padded to a multiple of 8 by the torch layer.  Default scale 1/sqrt(D) of the
 # caller's D throughout.  Ragged Sq != Sk, both masks, grouped-query heads.
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("D", [8, 16, 24, 32, 40, 48, 56, 72, 80, 96, 104, 112, 120, 1, 33, 100, 127])
+@pytest.mark.parametrize("D", [8, 16, 24, 32, 40, 48, 56, 72, 80, 96, 104, 112, 120, 1, 33, 100, 127,
+                               136, 160, 192, 200, 248, 256, 129, 250])
 def test_flash_head_dims(wo, causal, D):
     B, H, Hkv, Sq, Sk = 2, 4, 2, 200, 333
     report("flash_head_dim", B=B, H=H, Hkv=Hkv, Sq=Sq, Sk=Sk, D=D, causal=causal)
@@ -94,6 +95,17 @@ def test_flash_head_dim_equals_padded(wo):
         Op = wo.flash_attention(pad(Q), pad(K), pad(V), causal=causal, scale=1.0 / math.sqrt(D))
         assert torch.equal(O, Op[..., :D])
         assert torch.count_nonzero(Op[..., D:]) == 0
+
+
+# D = 256 (4 waves, 2-deep ring) at a longer sequence: many key tiles through the ring,
+# ragged ends, grouped-query heads, both masks.
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_head_dim_256(wo, causal):
+    B, H, Hkv, Sq, Sk, D = 2, 8, 2, 1000, 1300, 256
+    report("flash_d256", B=B, H=H, Hkv=Hkv, Sq=Sq, Sk=Sk, D=D, causal=causal)
+    Q, K, V = oatt.make_inputs(B, H, Sq, D, seed=256, Sk=Sk, Hkv=Hkv)
+    O = wo.flash_attention(Q.cuda(), K.cuda(), V.cuda(), causal=causal)
+    _check(O, oatt.sdpa_ref(Q, K, V, causal))
 
 
 def test_flash_custom_scale(wo):
@@ -198,9 +210,9 @@ def test_flash_varlen_equals_dense(wo):
 
 
 def test_flash_errors(wo):
-    for D in (136, 256):
+    for D in (264, 512):
         x = torch.zeros(1, 1, 8, D, dtype=torch.half, device="cuda")
-        with pytest.raises(RuntimeError, match="head_dim must be between 1 and 128"):
+        with pytest.raises(RuntimeError, match="head_dim must be between 1 and 256"):
             wo.flash_attention(x, x, x)
     y = torch.zeros(1, 1, 8, 64, dtype=torch.float32, device="cuda")
     with pytest.raises(RuntimeError, match="float16"):

@@ -456,17 +456,20 @@ int wmma_int4_permute_rows(const int32_t* qweight, const int32_t* perm, int K, i
 // ----------------------------------------------------------------------------- flash --
 namespace {
 
-// Head dims the kernels take: multiples of 8 (16-byte rows) from 8 to 128.
-int flash_head_dim_check(int D) {
-    if (D < 8 || D > 128 || D % 8 != 0)
-        return fail(WMMA_ERR_UNSUPPORTED, "head_dim %d (supported: multiples of 8 from 8 to 128)", D);
+// Head dims the kernels take: multiples of 8 (16-byte rows) from 8 to 256 for the forward
+// pass, to 128 for the backward pass.
+constexpr int kFlashMaxDFwd = 256, kFlashMaxDBwd = 128;
+int flash_head_dim_check(int D, int max_d) {
+    if (D < 8 || D > max_d || D % 8 != 0)
+        return fail(WMMA_ERR_UNSUPPORTED, "head_dim %d (supported: multiples of 8 from 8 to %d)", D,
+                    max_d);
     return WMMA_OK;
 }
 
 // Shape checks shared by the dense forward and backward entry points.
-int flash_dense_check(int B, int H, int Hkv, int Sq, int Sk, int D, float scale) {
+int flash_dense_check(int B, int H, int Hkv, int Sq, int Sk, int D, float scale, int max_d) {
     if (B < 0 || H < 0 || Sq < 0 || Sk < 0) return fail(WMMA_ERR_INVALID_ARG, "negative dimension");
-    if (int rc = flash_head_dim_check(D)) return rc;
+    if (int rc = flash_head_dim_check(D, max_d)) return rc;
     if (!(scale > 0.0f) || !std::isfinite(scale))
         return fail(WMMA_ERR_INVALID_ARG, "scale must be positive and finite");
     if (H > 0 && (Hkv <= 0 || H % Hkv != 0))
@@ -478,10 +481,10 @@ int flash_dense_check(int B, int H, int Hkv, int Sq, int Sk, int D, float scale)
 }
 
 int flash_varlen_check(int B, int H, int Hkv, int total_q, int total_k, int max_q, int max_k,
-                       int D, float scale) {
+                       int D, float scale, int max_d) {
     if (B < 0 || H < 0 || total_q < 0 || total_k < 0 || max_q < 0 || max_k < 0)
         return fail(WMMA_ERR_INVALID_ARG, "negative dimension");
-    if (int rc = flash_head_dim_check(D)) return rc;
+    if (int rc = flash_head_dim_check(D, max_d)) return rc;
     if (!(scale > 0.0f) || !std::isfinite(scale))
         return fail(WMMA_ERR_INVALID_ARG, "scale must be positive and finite");
     if (H > 0 && (Hkv <= 0 || H % Hkv != 0))
@@ -500,7 +503,7 @@ bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0
 int wmma_flash_attn_fwd_lse(const void* Q, const void* K, const void* V, void* O, float* lse,
                             int B, int H, int Hkv, int Sq, int Sk, int D, float scale, int causal,
                             void* stream) {
-    if (int rc = flash_dense_check(B, H, Hkv, Sq, Sk, D, scale)) return rc;
+    if (int rc = flash_dense_check(B, H, Hkv, Sq, Sk, D, scale, kFlashMaxDFwd)) return rc;
     if (B == 0 || H == 0 || Sq == 0) return ok();
     if (Sk == 0) return fail(WMMA_ERR_INVALID_ARG, "Sk must be positive when Sq > 0");
     if (!Q || !K || !V || !O) return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
@@ -534,7 +537,8 @@ int wmma_flash_attn_varlen_fwd_lse(const void* Q, const void* K, const void* V, 
                                    const int32_t* cu_seqlens_k, int B, int H, int Hkv,
                                    int total_q, int total_k, int max_seqlen_q, int max_seqlen_k,
                                    int D, float scale, int causal, void* stream) {
-    if (int rc = flash_varlen_check(B, H, Hkv, total_q, total_k, max_seqlen_q, max_seqlen_k, D, scale))
+    if (int rc = flash_varlen_check(B, H, Hkv, total_q, total_k, max_seqlen_q, max_seqlen_k, D,
+                                    scale, kFlashMaxDFwd))
         return rc;
     if (B == 0 || H == 0 || total_q == 0 || max_seqlen_q == 0) return ok();
     if (!Q || !K || !V || !O || !cu_seqlens_q || !cu_seqlens_k)
@@ -612,7 +616,7 @@ int wmma_flash_attn_bwd(const void* dO, const void* Q, const void* K, const void
                         const float* lse, void* dQ, void* dK, void* dV, void* workspace,
                         size_t workspace_bytes, int B, int H, int Hkv, int Sq, int Sk, int D,
                         float scale, int causal, void* stream) {
-    if (int rc = flash_dense_check(B, H, Hkv, Sq, Sk, D, scale)) return rc;
+    if (int rc = flash_dense_check(B, H, Hkv, Sq, Sk, D, scale, kFlashMaxDBwd)) return rc;
     if (B == 0 || H == 0 || (Sq == 0 && Sk == 0)) return ok();
     if (Sk == 0) return fail(WMMA_ERR_INVALID_ARG, "Sk must be positive when Sq > 0");
     FlashBwdLaunch f{};
@@ -642,7 +646,8 @@ int wmma_flash_attn_varlen_bwd(const void* dO, const void* Q, const void* K, con
                                void* workspace, size_t workspace_bytes, int B, int H, int Hkv,
                                int total_q, int total_k, int max_seqlen_q, int max_seqlen_k,
                                int D, float scale, int causal, void* stream) {
-    if (int rc = flash_varlen_check(B, H, Hkv, total_q, total_k, max_seqlen_q, max_seqlen_k, D, scale))
+    if (int rc = flash_varlen_check(B, H, Hkv, total_q, total_k, max_seqlen_q, max_seqlen_k, D,
+                                    scale, kFlashMaxDBwd))
         return rc;
     if (B == 0 || H == 0 || (total_q == 0 && total_k == 0)) return ok();
     if (!cu_seqlens_q || !cu_seqlens_k) return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");

@@ -26,9 +26,10 @@
 //    the workgroup's last query are never loaded, tiles past a wave's own last query are
 //    skipped by that wave, masks are applied only on tiles that cross the diagonal or the
 //    end of K, and the heaviest query blocks are dispatched first.
-//  * Head dims: kernels are built for D = 64 and D = 128; any multiple of 8 up to 128 runs
+//  * Head dims: kernels are built for D = 64, 128 and 256; any multiple of 8 up to 256 runs
 //    on the smallest that holds it, the d columns past the tensors' head dim arriving as
-//    zeros (no score or output contribution) and never stored.
+//    zeros (no score or output contribution) and never stored.  D = 256 runs 4 waves of
+//    the whole register file each and a 2-deep ring (see FaCfg).
 #include "common.hpp"
 #include "kernels.hpp"
 #include "plan.hpp"
@@ -61,24 +62,29 @@ struct FlashArgs {
     float* lse;
 };
 
-constexpr int FA_WAVES = 8;                 // waves per workgroup (two per SIMD)
 constexpr int FA_WQ = 32;                   // queries per wave
 constexpr int FA_NQB = FA_WQ / 32;          // 32-query MFMA blocks per wave
-constexpr int FA_BQ = FA_WAVES * FA_WQ;     // queries per workgroup
 constexpr int FA_BKV = 64;                  // keys per tile
-constexpr int FA_NS = 4;                    // LDS ring depth
 constexpr float kNegInf = -__builtin_huge_valf();
 
+// Per head dim: D <= 128 runs 8 waves (two per SIMD, so one wave's softmax overlaps the
+// other's matrix work) and a 4-deep ring; D = 256 -- whose O accumulators and Q fragments
+// alone take 192 registers a lane -- runs 4 waves (one per SIMD, the whole register file)
+// and a 2-deep ring of 64 KB stages (the DMA of tile t + 1 overlaps tile t).
 template <int D>
 struct FaCfg {
+    static constexpr int WAVES = D > 128 ? 4 : 8;      // waves per workgroup
+    static constexpr int NS = D > 128 ? 2 : 4;         // LDS ring depth
+    static constexpr int BQ = WAVES * FA_WQ;           // queries per workgroup
     static constexpr int DCH = D / 8;                  // 16-byte chunks per row
     static constexpr int NDS = D / 16;                 // d-steps of S^T
     static constexpr int NDB = D / 32;                 // 32-wide d blocks of O
     static constexpr int TILE = FA_BKV * D * 2;        // bytes of one K (or V) tile
     static constexpr int STAGE = 2 * TILE;             // K then V
-    static constexpr int DMA = TILE / 1024 / FA_WAVES; // 1 KB DMA instructions per wave per tile
+    static constexpr int DMA = TILE / 1024 / WAVES;    // 1 KB DMA instructions per wave per tile
     static constexpr int PER_STAGE = 2 * DMA;          // vmcnt per stage
-    static_assert(TILE % (1024 * FA_WAVES) == 0, "DMA split");
+    static_assert(TILE % (1024 * WAVES) == 0, "DMA split");
+    static_assert(NS * STAGE <= 160 * 1024, "LDS ring");
 };
 
 // Row swizzles (16-byte chunk index XOR).  K rows are read by ds_read_b128 with 32 lanes
@@ -86,11 +92,11 @@ struct FaCfg {
 // rows at one chunk pair.
 template <int D>
 __device__ __forceinline__ int swz_k(int row) {
-    return D == 128 ? (row & 15) : ((row ^ (row >> 3)) & 7);
+    return D >= 128 ? (row & 15) : ((row ^ (row >> 3)) & 7);
 }
 template <int D>
 __device__ __forceinline__ int swz_v(int row) {
-    return D == 128 ? 4 * (row & 3) : 2 * (row & 3);
+    return D >= 128 ? 4 * (row & 3) : 2 * (row & 3);
 }
 
 template <int D>
@@ -271,7 +277,7 @@ __device__ __forceinline__ void fa_iter(const WMMA_LDS unsigned char* __restrict
                                         float (&l_run)[FA_NQB], float c, int kv0, int qrow0, int Sk,
                                         bool live, bool masked) {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads are done
-    wait_vmcnt<(FA_NS - 2) * FaCfg<D>::PER_STAGE>();
+    wait_vmcnt<(FaCfg<D>::NS - 2) * FaCfg<D>::PER_STAGE>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     fa_dma<D>(dst, L, rk, rv, kleft_dma);
@@ -298,11 +304,11 @@ __device__ __forceinline__ void fa_iter(const WMMA_LDS unsigned char* __restrict
 }
 
 template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(FA_WAVES * kWave)
-__attribute__((amdgpu_waves_per_eu(FA_WAVES / 4, FA_WAVES / 4)))
+__global__ void __launch_bounds__(FaCfg<D>::WAVES * kWave)
+__attribute__((amdgpu_waves_per_eu(FaCfg<D>::WAVES / 4, FaCfg<D>::WAVES / 4)))
 flash_fwd_kernel(FlashArgs p) {
     using C = FaCfg<D>;
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[FA_NS * C::STAGE];
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[C::NS * C::STAGE];
     WMMA_LDS unsigned char* lds = (WMMA_LDS unsigned char*)smem;
 
     const int lane = threadIdx.x & 63;
@@ -310,7 +316,7 @@ flash_fwd_kernel(FlashArgs p) {
     const int h = lane >> 5, c32 = lane & 31;
     const int bh = blockIdx.x;
     const int qb_idx = CAUSAL ? (p.nqb - 1 - (int)blockIdx.y) : (int)blockIdx.y;
-    const int q0 = qb_idx * FA_BQ;
+    const int q0 = qb_idx * C::BQ;
     const int qw = q0 + wave * FA_WQ;
     const float c = p.scale_log2;
 
@@ -398,7 +404,7 @@ flash_fwd_kernel(FlashArgs p) {
         }
     }
 
-    const int kv_end = CAUSAL ? min(Sk, q0 + FA_BQ) : Sk;
+    const int kv_end = CAUSAL ? min(Sk, q0 + C::BQ) : Sk;
     const int T = (kv_end + FA_BKV - 1) / FA_BKV;
     // Tiles this wave needs (causal: keys <= its last query).
     const int Tw = CAUSAL ? min(T, (qw + FA_WQ - 1) / FA_BKV + 1) : T;
@@ -427,10 +433,10 @@ flash_fwd_kernel(FlashArgs p) {
     if (T > 0) {
         // Prologue: tiles 0 .. NS-2 in flight (tiles past the end load zeros).
 #pragma unroll
-        for (int s = 0; s < FA_NS - 1; ++s) fa_dma<D>(lds + s * C::STAGE, L, rk_of(s), rv_of(s), kleft(s));
+        for (int s = 0; s < C::NS - 1; ++s) fa_dma<D>(lds + s * C::STAGE, L, rk_of(s), rv_of(s), kleft(s));
         for (int t = 0; t < T; ++t) {
-            const int tf = t + FA_NS - 1;
-            fa_iter<D, CAUSAL>(lds + (t % FA_NS) * C::STAGE, lds + (tf % FA_NS) * C::STAGE, L,
+            const int tf = t + C::NS - 1;
+            fa_iter<D, CAUSAL>(lds + (t % C::NS) * C::STAGE, lds + (tf % C::NS) * C::STAGE, L,
                                rk_of(tf), rv_of(tf), kleft(tf), qf, O, m_run, l_run, c,
                                t * FA_BKV, qrow0, Sk, t < Tw, masked(t));
         }
@@ -467,12 +473,14 @@ flash_fwd_kernel(FlashArgs p) {
 }
 
 template <int D>
-void launch_d(const FlashArgs& a, int BH, bool causal, hipStream_t stream) {
+void launch_d(FlashArgs a, int BH, bool causal, hipStream_t stream) {
+    a.nqb = ceil_div(a.Sq, FaCfg<D>::BQ);
     dim3 grid(BH, a.nqb);
+    const dim3 block(FaCfg<D>::WAVES * kWave);
     if (causal)
-        hipLaunchKernelGGL((flash_fwd_kernel<D, true>), grid, dim3(FA_WAVES * kWave), 0, stream, a);
+        hipLaunchKernelGGL((flash_fwd_kernel<D, true>), grid, block, 0, stream, a);
     else
-        hipLaunchKernelGGL((flash_fwd_kernel<D, false>), grid, dim3(FA_WAVES * kWave), 0, stream, a);
+        hipLaunchKernelGGL((flash_fwd_kernel<D, false>), grid, block, 0, stream, a);
 }
 
 }  // namespace
@@ -485,7 +493,6 @@ hipError_t launch_flash_fwd(const FlashLaunch& f, hipStream_t stream) {
     a.O = static_cast<f16*>(f.O);
     a.Sq = f.Sq;
     a.Sk = f.Sk;
-    a.nqb = ceil_div(f.Sq, FA_BQ);
     a.group = f.H / f.Hkv;
     a.dr = f.D;
     a.cu_q = f.cu_q;
@@ -497,8 +504,11 @@ hipError_t launch_flash_fwd(const FlashLaunch& f, hipStream_t stream) {
     a.lse = f.lse;
     a.scale_log2 = f.scale * 1.4426950408889634f;
     const int BH = f.B * f.H;
-    // head dims up to 64 run the D = 64 kernel, up to 128 the D = 128 kernel
-    if (f.D > 64)
+    // head dims up to 64 run the D = 64 kernel, up to 128 the D = 128 kernel, up to 256 the
+    // D = 256 kernel
+    if (f.D > 128)
+        launch_d<256>(a, BH, f.causal, stream);
+    else if (f.D > 64)
         launch_d<128>(a, BH, f.causal, stream);
     else
         launch_d<64>(a, BH, f.causal, stream);

@@ -184,7 +184,7 @@ void check_flash_dense(const torch::Tensor& Q, const torch::Tensor& K, const tor
                 "Q and K must agree in batch and head_dim");
     TORCH_CHECK(K.size(1) > 0 && Q.size(1) % K.size(1) == 0,
                 "K/V heads must divide Q heads");
-    TORCH_CHECK(Q.size(3) >= 1 && Q.size(3) <= 128, "head_dim must be between 1 and 128");
+    TORCH_CHECK(Q.size(3) >= 1 && Q.size(3) <= 256, "head_dim must be between 1 and 256");
 }
 
 // Checks of the packed inputs q [total_q,H,D], k/v [total_k,Hkv,D], cu_seqlens int32 [B+1].
@@ -205,7 +205,7 @@ void check_flash_varlen(const torch::Tensor& q, const torch::Tensor& k, const to
     TORCH_CHECK(cu_q.dtype() == torch::kInt32 && cu_k.dtype() == torch::kInt32 && cu_q.dim() == 1 &&
                     cu_q.sizes() == cu_k.sizes() && cu_q.size(0) >= 1,
                 "cu_seqlens must be int32 [B+1], equal for Q and K");
-    TORCH_CHECK(q.size(2) >= 1 && q.size(2) <= 128, "head_dim must be between 1 and 128");
+    TORCH_CHECK(q.size(2) >= 1 && q.size(2) <= 256, "head_dim must be between 1 and 256");
 }
 
 // Gradient-side checks: dO and O have Q's shape (fp16, same device), lse is fp32 of the
@@ -265,7 +265,8 @@ torch::Tensor flash_dense_fwd(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
 
 // flash_attention(Q, K, V, causal=False, scale=-1.0) (README.md:221-251): Q [B,H,Sq,D],
 // K/V [B,Hkv,Sk,D] fp16 with Hkv dividing H (Hkv < H: grouped-query attention, query head h
-// reads key/value head h / (H/Hkv)); D from 1 to 128; scale <= 0 selects 1/sqrt(D).
+// reads key/value head h / (H/Hkv)); D from 1 to 256 (the backward pass: to 128); scale
+// <= 0 selects 1/sqrt(D).
 // Returns fp16 [B,H,Sq,D].
 torch::Tensor flash_attention(torch::Tensor Q, torch::Tensor K, torch::Tensor V, bool causal,
                               double scale) {
@@ -289,6 +290,7 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> flash_attention_backward
     torch::Tensor dO, torch::Tensor Q, torch::Tensor K, torch::Tensor V, torch::Tensor O,
     torch::Tensor lse, bool causal, double scale) {
     check_flash_dense(Q, K, V);
+    TORCH_CHECK(Q.size(3) <= 128, "the flash-attention backward pass supports head_dim up to 128");
     check_flash_grad_inputs(Q, dO, O, lse, {Q.size(0), Q.size(1), Q.size(2)});
     const int64_t B = Q.size(0), H = Q.size(1), Sq = Q.size(2), D = Q.size(3);
     const int64_t Dp = padded_head_dim(D);
@@ -364,6 +366,7 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> flash_attention_varlen_b
     torch::Tensor lse, torch::Tensor cu_q, torch::Tensor cu_k, int64_t max_q, int64_t max_k,
     bool causal, double scale) {
     check_flash_varlen(q, k, v, cu_q, cu_k);
+    TORCH_CHECK(q.size(2) <= 128, "the flash-attention backward pass supports head_dim up to 128");
     check_flash_grad_inputs(q, dO, O, lse, {q.size(1), q.size(0)});
     const int64_t H = q.size(1), D = q.size(2), Dp = padded_head_dim(D);
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
