@@ -45,10 +45,18 @@ namespace wmma_amd {
 
 namespace {
 
-constexpr int FB_WAVES_Q = 8;             // dQ kernel: waves per workgroup (two per SIMD)
 constexpr int FB_WAVES_KV = 4;            // dK/dV kernel: one wave per SIMD (see below)
 constexpr int FB_ROWS = 32;               // queries per dQ wave
-constexpr int FB_BLOCK_Q = FB_WAVES_Q * FB_ROWS;  // queries owned by a dQ workgroup
+// dQ kernel waves per workgroup and LDS ring depth (both kernels) per head dim: D <= 128
+// runs 8 dQ waves (two per SIMD) and a 4-deep ring; a D = 256 configuration would take 4
+// dQ waves (Q, dO fragments and dQ accumulators alone are 256 registers a lane) and a
+// 2-deep ring of 64 KB stages.
+template <int D>
+struct FbGeom {
+    static constexpr int WQ = D > 128 ? 4 : 8;
+    static constexpr int NS = D > 128 ? 2 : 4;
+    static constexpr int BLOCK_Q = WQ * FB_ROWS;  // queries owned by a dQ workgroup
+};
 // dK/dV wave: KB 32-key blocks (each LDS read of Q or dO feeds KB matrix instructions).  Two
 // for D = 64; for D = 128 the resident K, V, dK and dV of two blocks (384 registers) leave
 // too few for the rest and the kernel spills.
@@ -59,7 +67,6 @@ struct FbKv {
     static constexpr int BLOCK = FB_WAVES_KV * ROWS;  // keys per workgroup
 };
 constexpr int FB_T = 64;                  // rows per streamed tile
-constexpr int FB_NS = 4;                  // LDS ring depth
 constexpr float kNegInfB = -__builtin_huge_valf();
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -94,7 +101,7 @@ struct FbCfg : FbDim<D> {
 // only, so offsets of 16 rows are plain additions.
 template <int D>
 __host__ __device__ constexpr int swz2(int row) {
-    return D == 128 ? (((row & 3) << 2) | ((row >> 2) & 3))
+    return D >= 128 ? (((row & 3) << 2) | ((row >> 2) & 3))
                     : ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
 }
 
@@ -125,7 +132,8 @@ constexpr bool swz2_conflict_free() {
         if (swz2<D>(r) != swz2<D>(r & 15)) return false;
     return true;
 }
-static_assert(swz2_conflict_free<128>() && swz2_conflict_free<64>(), "swizzle");
+static_assert(swz2_conflict_free<256>() && swz2_conflict_free<128>() && swz2_conflict_free<64>(),
+              "swizzle");
 
 struct BwdArgs {
     const f16* Q;
@@ -252,7 +260,8 @@ constexpr bool tr_addr_identity() {
     }
     return true;
 }
-static_assert(tr_addr_identity<128>() && tr_addr_identity<64>(), "transposing-read addresses");
+static_assert(tr_addr_identity<256>() && tr_addr_identity<128>() && tr_addr_identity<64>(),
+              "transposing-read addresses");
 
 // DMA of one 64-row tile (rows >= left load zeros).
 template <int D, int W>
@@ -337,16 +346,16 @@ __device__ __forceinline__ void fb_store_rows(f16* base, int stride, int dr, int
 template <int D, bool CAUSAL>
 __device__ __forceinline__ void fb_dq_iter(const WMMA_LDS unsigned char* __restrict__ cur,
                                            WMMA_LDS unsigned char* __restrict__ dst,
-                                           const FbLane<D, FB_WAVES_Q>& L, __amdgpu_buffer_rsrc_t rk,
+                                           const FbLane<D, FbGeom<D>::WQ>& L, __amdgpu_buffer_rsrc_t rk,
                                            __amdgpu_buffer_rsrc_t rv, int kleft_dma,
-                                           const f16x8 (&qf)[FbCfg<D, FB_WAVES_Q>::NDS],
-                                           const f16x8 (&dof)[FbCfg<D, FB_WAVES_Q>::NDS],
-                                           f32x16 (&dq)[FbCfg<D, FB_WAVES_Q>::NDB], float c, float lse2,
+                                           const f16x8 (&qf)[FbCfg<D, FbGeom<D>::WQ>::NDS],
+                                           const f16x8 (&dof)[FbCfg<D, FbGeom<D>::WQ>::NDS],
+                                           f32x16 (&dq)[FbCfg<D, FbGeom<D>::WQ>::NDB], float c, float lse2,
                                            float delta, int kv0, int qrow, int Sk, bool live,
                                            bool masked) {
-    using C = FbCfg<D, FB_WAVES_Q>;
+    using C = FbCfg<D, FbGeom<D>::WQ>;
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads are done
-    wait_vmcnt<(FB_NS - 2) * C::PER_STAGE_Q>();
+    wait_vmcnt<(FbGeom<D>::NS - 2) * C::PER_STAGE_Q>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     fb_dma_tile<D>(dst, L, rk, kleft_dma);
@@ -380,11 +389,12 @@ __device__ __forceinline__ void fb_dq_iter(const WMMA_LDS unsigned char* __restr
 }
 
 template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(FB_WAVES_Q * kWave)
-__attribute__((amdgpu_waves_per_eu(FB_WAVES_Q / 4, FB_WAVES_Q / 4)))
+__global__ void __launch_bounds__(FbGeom<D>::WQ * kWave)
+__attribute__((amdgpu_waves_per_eu(FbGeom<D>::WQ / 4, FbGeom<D>::WQ / 4)))
 flash_bwd_dq_kernel(BwdArgs p) {
-    using C = FbCfg<D, FB_WAVES_Q>;
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[FB_NS * C::STAGE_Q];
+    using C = FbCfg<D, FbGeom<D>::WQ>;
+    constexpr int NS = FbGeom<D>::NS;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * C::STAGE_Q];
     WMMA_LDS unsigned char* lds = (WMMA_LDS unsigned char*)smem;
 
     const int lane = threadIdx.x & 63;
@@ -392,7 +402,7 @@ flash_bwd_dq_kernel(BwdArgs p) {
     const int h = lane >> 5, c32 = lane & 31;
     const int bh = blockIdx.x;
     const int qb_idx = CAUSAL ? (p.nqb - 1 - (int)blockIdx.y) : (int)blockIdx.y;
-    const int q0 = qb_idx * FB_BLOCK_Q;
+    const int q0 = qb_idx * FbGeom<D>::BLOCK_Q;
     const int qw = q0 + wave * FB_ROWS;
     const SeqGeo G = seq_geo<D>(p, bh / p.H, bh % p.H);
     if (q0 >= G.Sq) return;
@@ -428,11 +438,11 @@ flash_bwd_dq_kernel(BwdArgs p) {
         p.ws[p.rows + G.r_base + qrow] = -lse / p.scale;
     }
 
-    FbLane<D, FB_WAVES_Q> L;
+    FbLane<D, FbGeom<D>::WQ> L;
     fb_lane_init<D>(L, wave, lane, G.ks, p.dr);
     const f16* Kb = p.K + G.k_base;
     const f16* Vb = p.V + G.k_base;
-    const int kv_end = CAUSAL ? min(Sk, q0 + FB_BLOCK_Q) : Sk;
+    const int kv_end = CAUSAL ? min(Sk, q0 + FbGeom<D>::BLOCK_Q) : Sk;
     const int T = (kv_end + FB_T - 1) / FB_T;
     const int Tw = CAUSAL ? min(T, (qw + FB_ROWS - 1) / FB_T + 1) : T;
     auto rk_of = [&](int t) { return make_rsrc(Kb + (int64_t)min(t, T - 1) * FB_T * G.ks); };
@@ -449,13 +459,13 @@ flash_bwd_dq_kernel(BwdArgs p) {
 
     if (T > 0) {
 #pragma unroll
-        for (int s = 0; s < FB_NS - 1; ++s) {
+        for (int s = 0; s < NS - 1; ++s) {
             fb_dma_tile<D>(lds + s * C::STAGE_Q, L, rk_of(s), kleft(s));
             fb_dma_tile<D>(lds + s * C::STAGE_Q + C::TILE, L, rv_of(s), kleft(s));
         }
         for (int t = 0; t < T; ++t) {
-            const int tf = t + FB_NS - 1;
-            fb_dq_iter<D, CAUSAL>(lds + (t % FB_NS) * C::STAGE_Q, lds + (tf % FB_NS) * C::STAGE_Q, L,
+            const int tf = t + NS - 1;
+            fb_dq_iter<D, CAUSAL>(lds + (t % NS) * C::STAGE_Q, lds + (tf % NS) * C::STAGE_Q, L,
                                   rk_of(tf), rv_of(tf), kleft(tf), qf, dof, dq, c, lse2, delta,
                                   t * FB_T, qrow, Sk, t < Tw, masked(t));
         }
@@ -517,7 +527,7 @@ __device__ __forceinline__ void fb_kv_iter(const WMMA_LDS unsigned char* __restr
                                            int key0) {
     using C = FbCfg<D, FB_WAVES_KV>;
     __builtin_amdgcn_s_waitcnt(0xC07F);
-    wait_vmcnt<(FB_NS - 2) * C::PER_STAGE_KV>();
+    wait_vmcnt<(FbGeom<D>::NS - 2) * C::PER_STAGE_KV>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     fb_dma_tile<D>(dst, L, rq, qleft_dma);
@@ -607,7 +617,8 @@ __global__ void __launch_bounds__(FB_WAVES_KV * kWave)
 __attribute__((amdgpu_waves_per_eu(FB_WAVES_KV / 4, FB_WAVES_KV / 4)))
 flash_bwd_dkdv_kernel(BwdArgs p) {
     using C = FbCfg<D, FB_WAVES_KV>;
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[FB_NS * C::STAGE_KV];
+    constexpr int NS = FbGeom<D>::NS;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * C::STAGE_KV];
     WMMA_LDS unsigned char* lds = (WMMA_LDS unsigned char*)smem;
 
     const int lane = threadIdx.x & 63;
@@ -672,15 +683,15 @@ flash_bwd_dkdv_kernel(BwdArgs p) {
                      dst + 2 * C::TILE + wave * C::STAT);
         };
 #pragma unroll
-        for (int s = 0; s < FB_NS - 1; ++s) issue(lds + s * C::STAGE_KV, s);
+        for (int s = 0; s < NS - 1; ++s) issue(lds + s * C::STAGE_KV, s);
         auto step = [&](auto mask_tag, int u) {
-            const int uf = u + FB_NS - 1;
+            const int uf = u + NS - 1;
             int gi, t, gf, tf;
             tile_of(u, gi, t);
             tile_of(uf, gf, tf);
             const int64_t qoff = G0.q_base + gf * qh + (int64_t)tf * FB_T * G0.qs;
             fb_kv_iter<D, decltype(mask_tag)::value>(
-                lds + (u % FB_NS) * C::STAGE_KV, lds + (uf % FB_NS) * C::STAGE_KV, L, wave,
+                lds + (u % NS) * C::STAGE_KV, lds + (uf % NS) * C::STAGE_KV, L, wave,
                 make_rsrc(p.Q + qoff), make_rsrc(p.dO + qoff),
                 make_rsrc(st_src + G0.r_base + gf * rh + (int64_t)tf * FB_T), qleft(uf, tf), kf, vf,
                 dk, dv, c, t * FB_T, kw + c32);
@@ -702,8 +713,9 @@ flash_bwd_dkdv_kernel(BwdArgs p) {
 }
 
 template <int D>
-void launch_bwd_d(const BwdArgs& a, int B, bool causal, hipStream_t stream) {
-    const dim3 bq(FB_WAVES_Q * kWave), bk(FB_WAVES_KV * kWave);
+void launch_bwd_d(BwdArgs a, int B, bool causal, hipStream_t stream) {
+    a.nqb = ceil_div(a.Sq, FbGeom<D>::BLOCK_Q);
+    const dim3 bq(FbGeom<D>::WQ * kWave), bk(FB_WAVES_KV * kWave);
     const dim3 gq(B * a.H, a.nqb);
     const dim3 gk(B * a.Hkv, ceil_div(a.Sk, FbKv<D>::BLOCK));
     // The dQ kernel writes the row statistics the dK/dV kernel reads: same stream, in order.
@@ -744,7 +756,6 @@ hipError_t launch_flash_bwd(const FlashBwdLaunch& f, hipStream_t stream) {
     a.rows = flash_bwd_workspace_rows(f);
     a.Sq = f.Sq;
     a.Sk = f.Sk;
-    a.nqb = ceil_div(f.Sq, FB_BLOCK_Q);
     a.c = f.scale * kLog2e;
     a.scale = f.scale;
     a.group = f.H / f.Hkv;
@@ -755,6 +766,9 @@ hipError_t launch_flash_bwd(const FlashBwdLaunch& f, hipStream_t stream) {
     a.Hkv = f.Hkv;
     a.total_q = f.total_q;
     a.total_k = f.total_k;
+    // (the entry points take D <= 128 here: a D = 256 build of these kernels spills -- its
+    // K, V fragments and dK, dV accumulators need 384 registers a lane before any working
+    // set)
     if (f.D > 64)
         launch_bwd_d<128>(a, f.B, f.causal, stream);
     else

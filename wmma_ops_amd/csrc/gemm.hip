@@ -619,7 +619,12 @@ constexpr int SK_WAVES = 4;
 template <bool VEC>
 __global__ void __launch_bounds__(SK_WAVES * kWave)
 gemm_skinny_kernel(GemmArgs p) {
-    __shared__ float red[SK_WAVES][kSkinnyMaxM][SK_COLS];
+    // Partial sums, row m = lane%16 of each wave, column n at n ^ ((n >> 2) & 16) of a row
+    // padded to 129 floats: one store instruction (64 lanes: 16 rows x 4 K quarters) then
+    // hits 64 distinct banks (unpadded rows put all 16 rows of a column on one bank), and a
+    // reader walking consecutive columns still sees distinct banks.
+    __shared__ float red[SK_WAVES][kSkinnyMaxM][SK_COLS + 1];
+    auto red_col = [](int n) { return n ^ ((n >> 2) & 16); };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -726,7 +731,7 @@ gemm_skinny_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < 8; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[wave][c16][8 * (4 * q + r) + j] = acc[j][r];
+        for (int r = 0; r < 4; ++r) red[wave][c16][red_col(8 * (4 * q + r) + j)] = acc[j][r];
     __syncthreads();
 
     const bool use_c = p.beta != 0.0f && p.Cin != nullptr;
@@ -734,9 +739,10 @@ gemm_skinny_kernel(GemmArgs p) {
         for (int idx = tid; idx < kSkinnyMaxM * SK_COLS; idx += SK_WAVES * kWave) {
             const int m = idx / SK_COLS, n = idx % SK_COLS;
             if (m < M && n0 + n < N) {
-                float v = red[0][m][n];
+                const int cn = red_col(n);
+                float v = red[0][m][cn];
 #pragma unroll
-                for (int w = 1; w < SK_WAVES; ++w) v += red[w][m][n];
+                for (int w = 1; w < SK_WAVES; ++w) v += red[w][m][cn];
                 v = p.alpha * v;
                 if (use_c) v += p.beta * p.Cin[(int64_t)m * p.ldcin + n0 + n];
                 p.Cout[(int64_t)m * p.ldc + n0 + n] = v;
@@ -750,9 +756,10 @@ gemm_skinny_kernel(GemmArgs p) {
     for (int idx = tid; idx < kSkinnyMaxM * SK_COLS; idx += SK_WAVES * kWave) {
         const int m = idx / SK_COLS, n = idx % SK_COLS;
         if (m < M && n0 + n < N) {
-            float v = red[0][m][n];
+            const int cn = red_col(n);
+            float v = red[0][m][cn];
 #pragma unroll
-            for (int w = 1; w < SK_WAVES; ++w) v += red[w][m][n];
+            for (int w = 1; w < SK_WAVES; ++w) v += red[w][m][cn];
             part[(int64_t)m * N + n0 + n] = v;
         }
     }
