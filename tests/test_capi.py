@@ -164,9 +164,10 @@ def test_w4a16_plan_make(lib):
     assert plan(1, 14336, 4096)[:2] == (0, 1)          # decode on the matrix pipe
     assert plan(4, 4096, 4096)[:2] == (0, 1)
     assert plan(16, 14336, 4096) == (4, 1, 4096, 0)    # skinny, 448 tiles: no split
-    assert plan(16, 4096, 4096) == (4, 1, 4096, 0)     # skinny, 128 tiles: half the CUs, no split
-    k, s, kps, ws = plan(16, 2048, 4096)               # skinny, 64 tiles: K split
-    assert (k, s, kps) == (4, 2, 2048) and ws == 2 * 16 * 2048 * 4
+    assert plan(16, 4096, 4096) == (4, 1, 4096, 0)     # skinny, 256 16-column workgroups
+    assert plan(16, 2048, 4096) == (4, 1, 4096, 0)     # 128 of them: half the CUs, no split
+    k, s, kps, ws = plan(16, 1024, 4096)               # 64 of them: K split
+    assert (k, s, kps) == (4, 2, 2048) and ws == 2 * 16 * 1024 * 4
     assert plan(128, 14336, 4096)[:2] == (5, 1)        # 224 tiles of 64x128: no split
     assert plan(128, 4096, 4096)[:2] == (5, 4)         # 64 tiles: 256 / 64 ways
     assert plan(64, 4096, 4096)[:2] == (5, 8)          # 32 tiles: 8 ways (the cap)

@@ -62,7 +62,7 @@ struct W4A16Plan {
     int kind;         // W4A16Kind
     int split;        // K partitions (1: no workspace)
     int k_per_split;  // multiple of 64 (and of G when split > 1)
-    int big = 0;      // W4_GEMM: tile (W4G_TILE_*); W4_SKINNY: 1 = two 32-column tiles per workgroup
+    int big = 0;      // W4_GEMM: tile (W4G_TILE_*); W4_SKINNY: 16-column slices per workgroup
 };
 
 struct W4A16Launch {

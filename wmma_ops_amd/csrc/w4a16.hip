@@ -868,22 +868,23 @@ void launch_decode_mfma(const W4Args& a, int M, dim3 grid, dim3 block, size_t ld
 //    go to the workspace for w4a16_reduce_kernel.
 // The B operand is the decode kernel's nibble encoding (1024 + q, and 64 + q at offsets
 // {2,3,6,7}) less the same encoding of z, times s: W = fp16((q - z) s), one rounding.
-//  * NT = 2 puts two adjacent 32-column tiles in one workgroup: every activation fragment
-//    feeds four MFMAs and the activation bytes a CU reads per weight byte halve (at
-//    M = 16 they are twice the weight bytes of a one-tile workgroup).
-// D layout per 16-row block b and 16-column half sc (0 .. 2*NT-1): lane l holds column
-// 32*NT*wg + 16*sc + l%16 and rows 16*b + 4*(l/16) + r.
+//  * NH 16-column slices per workgroup (1, 2 or 4): each activation fragment feeds NH
+//    MFMAs.  NH = 4 halves the activation bytes a CU reads per weight byte against NH = 2
+//    (at M = 16 they are twice the weight bytes of a 32-column workgroup); NH = 1 gives
+//    twice the workgroups of NH = 2 where 32-column tiles would leave CUs idle.
+// D layout per 16-row block b and slice sc (0 .. NH-1): lane l holds column
+// 16*NH*wg + 16*sc + l%16 and rows 16*b + 4*(l/16) + r.
 constexpr int SK_NW = 8;
 
-template <int ZF, int MB, int U, int NT>
+template <int ZF, int MB, int U, int NH>
 __global__ void __launch_bounds__(SK_NW * kWave)
 w4a16_skinny_kernel(W4Args p) {
-    constexpr int NH = 2 * NT;  // 16-column halves per workgroup
-    __shared__ float red[SK_NW][MB * 16][32 * NT + 1];
+    constexpr int NC = 16 * NH;  // columns per workgroup
+    __shared__ float red[SK_NW][MB * 16][NC + 1];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wg = xcd_remap(blockIdx.x, gridDim.x);
-    const int n0 = 32 * NT * wg;  // first column of the workgroup
+    const int n0 = NC * wg;  // first column of the workgroup
     const int col = lane & 15, sub = lane >> 4, dc = sub >> 1, h = sub & 1;
     const int K = p.K, M = p.M, KC = K / 64, KP = KC / 2;
     const int kp0 = blockIdx.y * (SK_NW * U);
@@ -980,8 +981,8 @@ w4a16_skinny_kernel(W4Args p) {
             for (int r = 0; r < 4; ++r) red[wave][16 * b + 4 * sub + r][16 * sc + col] = d[b][sc][r];
     __syncthreads();
     const bool partial = gridDim.y > 1;
-    for (int i = tid; i < M * 32 * NT; i += SK_NW * kWave) {
-        const int m = i / (32 * NT), c = i % (32 * NT);
+    for (int i = tid; i < M * NC; i += SK_NW * kWave) {
+        const int m = i / NC, c = i % NC;
         float acc = red[0][m][c];
 #pragma unroll
         for (int w = 1; w < SK_NW; ++w) acc += red[w][m][c];
@@ -1006,15 +1007,15 @@ int skinny_u(int M, int N, int K, int num_cus) {
     return 1;
 }
 
-template <int ZF, int MB, int NT>
+template <int ZF, int MB, int NH>
 void launch_skinny_mb(const W4Args& a, int U, dim3 grid, hipStream_t stream) {
     const dim3 block(SK_NW * kWave);
     if (U == 4)
-        hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, (MB == 1 ? 4 : 2), NT>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, (MB == 1 ? 4 : 2), NH>), grid, block, 0, stream, a);
     else if (U == 2)
-        hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, 2, NT>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, 2, NH>), grid, block, 0, stream, a);
     else
-        hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, 1, NT>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, 1, NH>), grid, block, 0, stream, a);
 }
 
 // ------------------------------------------------------ W4A16 GEMM (M > 32), LDS-DMA --
@@ -1600,9 +1601,16 @@ W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
         // Measured at K = 4096: M = 16 11.8 -> 10.2-10.7 us at N = 14336 and 11.6 -> 10.0 at
         // N = 11008; M = 24, 32 gain at N = 14336 only; at N = 4096 pairs need a K split
         // and lose (5.9 -> 7.9 us at M = 8).
+        // Fewer 32-column tiles than CUs at M <= 16: one 16-column slice per workgroup
+        // (twice the workgroups; each reads the activations once more).
         const int tiles = N / 32;
-        pl.big = tiles % 2 == 0 && (M <= 16 ? tiles >= num_cus : 2 * tiles >= 3 * num_cus);
-        const int u = skinny_u(M, pl.big ? N / 2 : N, K, num_cus);
+        if (tiles % 2 == 0 && (M <= 16 ? tiles >= num_cus : 2 * tiles >= 3 * num_cus))
+            pl.big = 4;
+        else if (M <= 16 && tiles < num_cus)
+            pl.big = 1;
+        else
+            pl.big = 2;
+        const int u = skinny_u(M, N * 2 / pl.big, K, num_cus);
         pl.kind = W4_SKINNY;
         pl.k_per_split = SK_NW * u * 128;
         pl.split = ceil_div(K, pl.k_per_split);
@@ -1705,17 +1713,19 @@ hipError_t launch_w4a16_zf(const W4Args& a, const W4A16Launch& w, hipStream_t st
         launch_w4g<ZF>(a, pl.big, grid, stream);
     } else if (pl.kind == W4_SKINNY) {
         const int U = pl.k_per_split / (SK_NW * 128);
-        const dim3 grid(pl.big ? ntiles / 2 : ntiles, pl.split);
-        if (pl.big) {
-            if (w.M <= 16)
+        const dim3 grid(w.N / (16 * pl.big), pl.split);
+        if (w.M <= 16) {
+            if (pl.big == 4)
+                launch_skinny_mb<ZF, 1, 4>(a, U, grid, stream);
+            else if (pl.big == 2)
                 launch_skinny_mb<ZF, 1, 2>(a, U, grid, stream);
             else
-                launch_skinny_mb<ZF, 2, 2>(a, U, grid, stream);
-        } else {
-            if (w.M <= 16)
                 launch_skinny_mb<ZF, 1, 1>(a, U, grid, stream);
+        } else {
+            if (pl.big == 4)
+                launch_skinny_mb<ZF, 2, 4>(a, U, grid, stream);
             else
-                launch_skinny_mb<ZF, 2, 1>(a, U, grid, stream);
+                launch_skinny_mb<ZF, 2, 2>(a, U, grid, stream);
         }
     } else if (pl.kind == W4_GEMV_SPLIT) {
         hipLaunchKernelGGL((w4a16_gemv_kernel<ZF>), dim3(ntiles, pl.split), dim3(GV_NW * kWave), 0,
