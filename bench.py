@@ -25,7 +25,7 @@ Workload families (--workload):
   skinny     configs[2]: M in {1,16,64,128} x N in {4096,11008,14336}, K=4096; K=14336,N=4096
   w4a16      configs[3]: M in {1,16,128,2048} x N in {4096,14336}, K=4096, G=128
   flash      configs[4]: [4,32,4096,128], causal and non-causal, forward and backward; with
-             8 K/V heads (GQA); head dims 64 and 256 (forward); a packed variable-length batch
+             8 K/V heads (GQA); head dims 64 and 256; a packed variable-length batch
   copy       a plain 256 MiB device copy (calibrates the rocprofv3 byte counters)
   mfma_ceiling  the matrix pipe's sustained rate with register operands and no memory
              traffic (libwmma_calib.so): the ceiling the GEMM main loop is held against
@@ -336,7 +336,7 @@ def fam_flash(wo):
                  max_rel_err=float(f"{errb:.3e}"))
             del O, lse, dOd, grads
         del Qd, Kd, Vd
-    # other head dims (forward): D = 64 and D = 256 at the same B, H, S
+    # other head dims: D = 64 and D = 256 at the same B, H, S
     for D2 in (64, 256):
         Q, Kt, V = oatt.make_inputs(B, H, S, D2, seed=42 + 4)
         Qd, Kd, Vd = Q.cuda(), Kt.cuda(), V.cuda()
@@ -349,6 +349,17 @@ def fam_flash(wo):
                  TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
                  frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4),
                  max_rel_err=float(f"{err:.3e}"))
+            O, lse = wo.flash_attention_forward(Qd, Kd, Vd, causal)
+            dOd = torch.randn(B, H, S, D2, generator=torch.Generator().manual_seed(77)).half().cuda()
+            msb = time_batches(lambda i: wo.flash_attention_backward(dOd, Qd, Kd, Vd, O, lse, causal), 5)
+            grads = wo.flash_attention_backward(dOd, Qd, Kd, Vd, O, lse, causal)
+            ref = oatt.sdpa_bwd_ref(Q[0:1, 0:1], Kt[0:1, 0:1], V[0:1, 0:1], dOd[0:1, 0:1].cpu(), causal)
+            errb = max(og.max_rel_err(x[0:1, 0:1].float(), y) for x, y in zip(grads, ref))
+            line(family="flash_bwd", B=B, H=H, S=S, D=D2, causal=causal, us=round(msb * 1e3, 1),
+                 TFLOPS=round(2.5 * fl / (msb * 1e-3) / 1e12, 1),
+                 frac_mfma_peak=round(2.5 * fl / (msb * 1e-3) / PEAK_FP16_FLOPS, 4),
+                 max_rel_err=float(f"{errb:.3e}"))
+            del O, lse, dOd, grads
         del Qd, Kd, Vd
     # CPU baseline: fp32 SDPA on the host cores (forward, and forward + autograd backward)
     # over a bounded sample of (batch, head) slices of the same workload

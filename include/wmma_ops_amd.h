@@ -254,8 +254,8 @@ int wmma_int4_permute_rows(const int32_t* qweight, const int32_t* perm, int K, i
  * contiguous.  O = softmax(scale * Q K^T (+ causal mask: key j <= query i, aligned to
  * the top left for any Sq, Sk, as torch's scaled_dot_product_attention(is_causal=True)))
  * V, FP32 online softmax and accumulation.  D: a multiple of 8 from 8 to 256 for this and
- * every forward entry point below, from 8 to 128 for the backward entry points (other
- * head dims return WMMA_ERR_UNSUPPORTED; the torch layer zero-pads D to a multiple of 8).
+ * every flash entry point below (other head dims return WMMA_ERR_UNSUPPORTED; the torch
+ * layer zero-pads D to a multiple of 8).
  * A query row whose keys are all masked (i.e. none, since key 0 is always kept) cannot
  * occur.
  * Replaces the documented (unbound) flash_attention(Q,K,V,causal=False,scale=-1.0)

@@ -335,8 +335,8 @@ def test_flash_training_validation_codes(lib):
                                        kw.get("Sq", 128), kw.get("Sk", 128), kw.get("D", 128),
                                        kw.get("scale", 0.1), 0, None)
     assert bwd(D=36) == UNSUPPORTED
-    assert bwd(D=136) == UNSUPPORTED               # the backward pass: D up to 128
-    assert b"from 8 to 128" in lib.wmma_last_error()
+    assert bwd(D=264) == UNSUPPORTED
+    assert b"from 8 to 256" in lib.wmma_last_error()
     assert bwd(Hkv=3) == INVALID
     assert bwd(scale=-1.0) == INVALID
     assert bwd(dO=None) == INVALID

@@ -66,10 +66,11 @@ def test_flash_bwd_shapes(wo, causal, B, H, Sq, Sk, D):
     print(f"[err] dQ {errs[0]:.2e} dK {errs[1]:.2e} dV {errs[2]:.2e}", flush=True)
 
 
-# Head dims other than 64 and 128 (see the forward's head-dim test): the dQ and dK/dV
-# kernels load the missing d columns as zeros and do not store them; grouped-query heads.
+# Head dims other than 64, 128 and 256 (see the forward's head-dim test): the dQ and dK/dV
+# kernels load the missing d columns as zeros and do not store them; D = 256 splits the
+# dK/dV columns over two workgroups; grouped-query heads.
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("D", [16, 32, 48, 80, 96, 112, 33, 100])
+@pytest.mark.parametrize("D", [16, 32, 48, 80, 96, 112, 33, 100, 136, 160, 200, 256, 250])
 def test_flash_bwd_head_dims(wo, causal, D):
     B, H, Hkv, Sq, Sk = 1, 4, 2, 300, 200
     report("flash_bwd_head_dim", B=B, H=H, Hkv=Hkv, Sq=Sq, Sk=Sk, D=D, causal=causal)
@@ -79,6 +80,20 @@ def test_flash_bwd_head_dims(wo, causal, D):
     got = wo.flash_attention_backward(dO.cuda(), Q.cuda(), K.cuda(), V.cuda(), O, lse, causal)
     errs = _grads_close(got, oatt.sdpa_bwd_ref(Q, K, V, dO, causal))
     print(f"[err] D {D} dQ {errs[0]:.2e} dK {errs[1]:.2e} dV {errs[2]:.2e}", flush=True)
+
+
+# D = 256 over many key and query tiles (the 2-deep rings, the dK/dV column split), ragged
+# lengths, grouped-query heads.
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_bwd_head_dim_256_long(wo, causal):
+    B, H, Hkv, Sq, Sk, D = 1, 4, 2, 1100, 900, 256
+    report("flash_bwd_d256", B=B, H=H, Hkv=Hkv, Sq=Sq, Sk=Sk, D=D, causal=causal)
+    Q, K, V = oatt.make_inputs(B, H, Sq, D, seed=2560, Sk=Sk, Hkv=Hkv)
+    dO = _dout((B, H, Sq, D), 2561)
+    O, lse = wo.flash_attention_forward(Q.cuda(), K.cuda(), V.cuda(), causal)
+    got = wo.flash_attention_backward(dO.cuda(), Q.cuda(), K.cuda(), V.cuda(), O, lse, causal)
+    errs = _grads_close(got, oatt.sdpa_bwd_ref(Q, K, V, dO, causal))
+    print(f"[err] dQ {errs[0]:.2e} dK {errs[1]:.2e} dV {errs[2]:.2e}", flush=True)
 
 
 @pytest.mark.parametrize("causal", [False, True])
@@ -138,7 +153,7 @@ def test_flash_bwd_baseline_config(wo, causal):
 # Ragged packed sequences: lengths 1, 0, not multiples of the tiles, different query and
 # key lengths, a sequence with no keys (dQ = 0) and one with no queries (dK = dV = 0).
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("H,Hkv,D", [(4, 4, 128), (8, 2, 64), (4, 2, 80), (4, 4, 36)])
+@pytest.mark.parametrize("H,Hkv,D", [(4, 4, 128), (8, 2, 64), (4, 2, 80), (4, 4, 36), (4, 2, 256)])
 def test_flash_bwd_varlen(wo, causal, H, Hkv, D):
     lens_q = [300, 1, 0, 700, 64, 5]
     lens_k = [300, 1, 9, 700, 77, 0]
@@ -222,15 +237,9 @@ def test_flash_bwd_no_queries(wo):
 
 
 def test_flash_bwd_errors(wo):
-    # the backward pass takes head dims up to 128: larger ones are refused up front
-    Qd = torch.zeros(1, 1, 8, 160, dtype=torch.half, device="cuda", requires_grad=True)
-    with pytest.raises(RuntimeError, match="backward pass supports head_dim up to 128"):
-        wo.flash_attention(Qd, Qd, Qd)
-    with torch.no_grad():
-        assert wo.flash_attention(Qd, Qd, Qd).shape == Qd.shape
-    O, lse = wo.flash_attention_forward(Qd.detach(), Qd.detach(), Qd.detach())
-    with pytest.raises(RuntimeError, match="backward pass supports head_dim up to 128"):
-        wo.flash_attention_backward(O, Qd.detach(), Qd.detach(), Qd.detach(), O, lse)
+    Qd = torch.zeros(1, 1, 8, 264, dtype=torch.half, device="cuda")
+    with pytest.raises(RuntimeError, match="head_dim must be between 1 and 256"):
+        wo.flash_attention_backward(Qd, Qd, Qd, Qd, Qd, torch.zeros(1, 1, 8, device="cuda"))
     Q, K, V = (X.cuda() for X in oatt.make_inputs(1, 2, 16, 64, seed=1))
     O, lse = wo.flash_attention_forward(Q, K, V)
     with pytest.raises(RuntimeError, match="lse must be float32"):

@@ -84,22 +84,12 @@ def _needs_grad(*ts) -> bool:
     return _torch.is_grad_enabled() and any(t.requires_grad for t in ts)
 
 
-_FLASH_BWD_MAX_D = 128
-
-
-def _check_trainable_head_dim(D: int) -> None:
-    if D > _FLASH_BWD_MAX_D:
-        raise RuntimeError(f"the flash-attention backward pass supports head_dim up to "
-                           f"{_FLASH_BWD_MAX_D} (got {D}); run the forward under torch.no_grad()")
-
-
 def flash_attention(Q, K, V, causal: bool = False, scale: float = -1.0):
     """flash_attention(Q, K, V, causal=False, scale=-1.0) (the reference's README.md:221-251):
-    fp16 [B,H,Sq,D] attention output, D up to 256.  Differentiable (D up to 128) when an
-    input requires grad (the reference's op is forward-only; inference calls take the plain
-    forward kernel)."""
+    fp16 [B,H,Sq,D] attention output, D up to 256.  Differentiable when an input requires
+    grad (the reference's op is forward-only; inference calls take the plain forward
+    kernel)."""
     if _needs_grad(Q, K, V):
-        _check_trainable_head_dim(Q.shape[-1])
         return FlashAttentionFunction.apply(Q, K, V, causal, scale)
     return _C.flash_attention(Q, K, V, causal, scale)
 
@@ -116,7 +106,6 @@ def flash_attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
     packed tensors are clamped, so inconsistent cu_seqlens give wrong rows, never an access
     outside the tensors."""
     if _needs_grad(q, k, v):
-        _check_trainable_head_dim(q.shape[-1])
         return FlashAttentionVarlenFunction.apply(q, k, v, cu_seqlens_q, cu_seqlens_k,
                                                   max_seqlen_q, max_seqlen_k, causal, scale)
     return _C.flash_attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,

@@ -456,9 +456,8 @@ int wmma_int4_permute_rows(const int32_t* qweight, const int32_t* perm, int K, i
 // ----------------------------------------------------------------------------- flash --
 namespace {
 
-// Head dims the kernels take: multiples of 8 (16-byte rows) from 8 to 256 for the forward
-// pass, to 128 for the backward pass.
-constexpr int kFlashMaxDFwd = 256, kFlashMaxDBwd = 128;
+// Head dims the kernels take: multiples of 8 (16-byte rows) from 8 to 256.
+constexpr int kFlashMaxDFwd = 256, kFlashMaxDBwd = 256;
 int flash_head_dim_check(int D, int max_d) {
     if (D < 8 || D > max_d || D % 8 != 0)
         return fail(WMMA_ERR_UNSUPPORTED, "head_dim %d (supported: multiples of 8 from 8 to %d)", D,

@@ -48,9 +48,9 @@ namespace {
 constexpr int FB_WAVES_KV = 4;            // dK/dV kernel: one wave per SIMD (see below)
 constexpr int FB_ROWS = 32;               // queries per dQ wave
 // dQ kernel waves per workgroup and LDS ring depth (both kernels) per head dim: D <= 128
-// runs 8 dQ waves (two per SIMD) and a 4-deep ring; a D = 256 configuration would take 4
-// dQ waves (Q, dO fragments and dQ accumulators alone are 256 registers a lane) and a
-// 2-deep ring of 64 KB stages.
+// runs 8 dQ waves (two per SIMD) and a 4-deep ring; D = 256 -- Q, dO fragments and dQ
+// accumulators alone take 256 registers a lane -- 4 dQ waves (one per SIMD) and a 2-deep
+// ring of 64 KB stages.
 template <int D>
 struct FbGeom {
     static constexpr int WQ = D > 128 ? 4 : 8;
@@ -60,11 +60,17 @@ struct FbGeom {
 // dK/dV wave: KB 32-key blocks (each LDS read of Q or dO feeds KB matrix instructions).  Two
 // for D = 64; for D = 128 the resident K, V, dK and dV of two blocks (384 registers) leave
 // too few for the rest and the kernel spills.
+// D = 256 splits the dK/dV output columns over DSPLIT = 2 workgroups (blockIdx.z): each
+// recomputes S and dP over the whole head dim but accumulates dK, dV for half of it, so
+// the resident K, V fragments (128 registers a lane) and the dK, dV accumulators (128)
+// fit one wave's register file.
 template <int D>
 struct FbKv {
     static constexpr int KB = D == 64 ? 2 : 1;
     static constexpr int ROWS = 32 * KB;              // keys per wave
     static constexpr int BLOCK = FB_WAVES_KV * ROWS;  // keys per workgroup
+    static constexpr int DSPLIT = D > 128 ? 2 : 1;    // workgroups over the dK/dV columns
+    static constexpr int NDB_OUT = D / 32 / DSPLIT;   // 32-wide d blocks of dK, dV per workgroup
 };
 constexpr int FB_T = 64;                  // rows per streamed tile
 constexpr float kNegInfB = -__builtin_huge_valf();
@@ -321,20 +327,20 @@ __device__ __forceinline__ void fb_load_frag(const f16* base, int stride, int dr
                     : kOobOffset));
 }
 
-// Store a transposed accumulator (lane%32 = row, element r = d 32 db + 8 (r/4) + 4 h + r%4)
-// as fp16 rows of the output, scaled by s; columns d >= dr are not stored.
-template <int D>
+// Store a transposed accumulator (lane%32 = row, element r = d d0 + 32 db + 8 (r/4) + 4 h +
+// r%4) as fp16 rows of the output, scaled by s; columns d >= dr are not stored.
+template <int NDB>
 __device__ __forceinline__ void fb_store_rows(f16* base, int stride, int dr, int row, int n, int h,
-                                              const f32x16 (&acc)[FbDim<D>::NDB], float s) {
+                                              const f32x16 (&acc)[NDB], float s, int d0 = 0) {
     if (row >= n) return;
 #pragma unroll
-    for (int db = 0; db < FbDim<D>::NDB; ++db)
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             f16x4 v;
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = (f16)(acc[db][4 * g + e] * s);
-            const int d = 32 * db + 8 * g + 4 * h;
+            const int d = d0 + 32 * db + 8 * g + 4 * h;
             if (d < dr) *reinterpret_cast<f16x4*>(base + (int64_t)row * stride + d) = v;
         }
 }
@@ -471,7 +477,7 @@ flash_bwd_dq_kernel(BwdArgs p) {
         }
         wait_vmcnt<0>();
     }
-    fb_store_rows<D>(p.dQ + G.q_base, G.qs, p.dr, qrow, Sq, h, dq, p.scale);
+    fb_store_rows<C::NDB>(p.dQ + G.q_base, G.qs, p.dr, qrow, Sq, h, dq, p.scale);
 }
 
 // ------------------------------------------------------------------------- dK/dV kernel --
@@ -492,17 +498,17 @@ __device__ __forceinline__ void fb_rows_x_frags(const WMMA_LDS unsigned char* ti
     }
 }
 
-// acc[kb][db] += T^T B_kb over the 16-row step `step` of tile T: each transposing read feeds
-// KB matrix instructions.
-template <int D, int W, int KB>
+// acc[kb][db] += T^T B_kb over the 16-row step `step` of tile T for the NDBO d blocks from
+// db0: each transposing read feeds KB matrix instructions.
+template <int D, int W, int KB, int NDBO>
 __device__ __forceinline__ void fb_tr_x_multi(const WMMA_LDS unsigned char* tile,
                                               const FbLane<D, W>& L, int step, const f16x8 (&b)[KB],
-                                              f32x16 (&acc)[KB][FbDim<D>::NDB]) {
+                                              f32x16 (&acc)[KB][NDBO], int db0) {
     const int off = 16 * step * FbDim<D>::RB;
 #pragma unroll
-    for (int db = 0; db < FbDim<D>::NDB; ++db) {
-        const f16x4 lo = lds_read_tr16(tile + fb_tr_addr<D, W>(L, db, false) + off);
-        const f16x4 hi = lds_read_tr16(tile + fb_tr_addr<D, W>(L, db, true) + off);
+    for (int db = 0; db < NDBO; ++db) {
+        const f16x4 lo = lds_read_tr16(tile + fb_tr_addr<D, W>(L, db0 + db, false) + off);
+        const f16x4 hi = lds_read_tr16(tile + fb_tr_addr<D, W>(L, db0 + db, true) + off);
         const f16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) acc[kb][db] = mfma32(a, b[kb], acc[kb][db]);
@@ -522,9 +528,9 @@ __device__ __forceinline__ void fb_kv_iter(const WMMA_LDS unsigned char* __restr
                                            __amdgpu_buffer_rsrc_t rst, int qleft_dma,
                                            const f16x8 (&kf)[FbKv<D>::KB][FbDim<D>::NDS],
                                            const f16x8 (&vf)[FbKv<D>::KB][FbDim<D>::NDS],
-                                           f32x16 (&dk)[FbKv<D>::KB][FbDim<D>::NDB],
-                                           f32x16 (&dv)[FbKv<D>::KB][FbDim<D>::NDB], float c, int q0,
-                                           int key0) {
+                                           f32x16 (&dk)[FbKv<D>::KB][FbKv<D>::NDB_OUT],
+                                           f32x16 (&dv)[FbKv<D>::KB][FbKv<D>::NDB_OUT], float c, int q0,
+                                           int key0, int db0) {
     using C = FbCfg<D, FB_WAVES_KV>;
     __builtin_amdgcn_s_waitcnt(0xC07F);
     wait_vmcnt<(FbGeom<D>::NS - 2) * C::PER_STAGE_KV>();
@@ -595,8 +601,10 @@ __device__ __forceinline__ void fb_kv_iter(const WMMA_LDS unsigned char* __restr
             for (int r = 0; r < 16; ++r) dS[r >> 3][kb][r & 7] = (f16)(S[kb][r] * dP[kb][r]);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-            fb_tr_x_multi<D, FB_WAVES_KV, FbKv<D>::KB>(cur + C::TILE, L, 2 * qb + hh, P[hh], dv);
-            fb_tr_x_multi<D, FB_WAVES_KV, FbKv<D>::KB>(cur, L, 2 * qb + hh, dS[hh], dk);
+            fb_tr_x_multi<D, FB_WAVES_KV, FbKv<D>::KB, FbKv<D>::NDB_OUT>(cur + C::TILE, L, 2 * qb + hh,
+                                                                         P[hh], dv, db0);
+            fb_tr_x_multi<D, FB_WAVES_KV, FbKv<D>::KB, FbKv<D>::NDB_OUT>(cur, L, 2 * qb + hh, dS[hh],
+                                                                         dk, db0);
         }
     }
     if constexpr (D == 64) {
@@ -660,11 +668,13 @@ flash_bwd_dkdv_kernel(BwdArgs p) {
     };
     auto qleft = [&](int u, int t) { return u < U ? Sq - t * FB_T : 0; };
 
-    f32x16 dk[FbKv<D>::KB][C::NDB], dv[FbKv<D>::KB][C::NDB];
+    constexpr int NDBO = FbKv<D>::NDB_OUT;
+    const int db0 = (int)blockIdx.z * NDBO;  // first d block of this workgroup's dK, dV columns
+    f32x16 dk[FbKv<D>::KB][NDBO], dv[FbKv<D>::KB][NDBO];
 #pragma unroll
     for (int kb = 0; kb < FbKv<D>::KB; ++kb)
 #pragma unroll
-        for (int db = 0; db < C::NDB; ++db) {
+        for (int db = 0; db < NDBO; ++db) {
             dk[kb][db] = f32x16{};
             dv[kb][db] = f32x16{};
         }
@@ -694,7 +704,7 @@ flash_bwd_dkdv_kernel(BwdArgs p) {
                 lds + (u % NS) * C::STAGE_KV, lds + (uf % NS) * C::STAGE_KV, L, wave,
                 make_rsrc(p.Q + qoff), make_rsrc(p.dO + qoff),
                 make_rsrc(st_src + G0.r_base + gf * rh + (int64_t)tf * FB_T), qleft(uf, tf), kf, vf,
-                dk, dv, c, t * FB_T, kw + c32);
+                dk, dv, c, t * FB_T, kw + c32, db0);
         };
         // Causal: the first BLOCK/64 tiles of each query head hold queries below the
         // workgroup's last key (k0 is a multiple of the tile, so exactly these).
@@ -707,8 +717,10 @@ flash_bwd_dkdv_kernel(BwdArgs p) {
     }
 #pragma unroll
     for (int kb = 0; kb < FbKv<D>::KB; ++kb) {
-        fb_store_rows<D>(p.dK + G0.k_base, G0.ks, p.dr, kw + 32 * kb + c32, Sk, h, dk[kb], p.scale);
-        fb_store_rows<D>(p.dV + G0.k_base, G0.ks, p.dr, kw + 32 * kb + c32, Sk, h, dv[kb], 1.0f);
+        fb_store_rows<NDBO>(p.dK + G0.k_base, G0.ks, p.dr, kw + 32 * kb + c32, Sk, h, dk[kb], p.scale,
+                            32 * db0);
+        fb_store_rows<NDBO>(p.dV + G0.k_base, G0.ks, p.dr, kw + 32 * kb + c32, Sk, h, dv[kb], 1.0f,
+                            32 * db0);
     }
 }
 
@@ -717,7 +729,7 @@ void launch_bwd_d(BwdArgs a, int B, bool causal, hipStream_t stream) {
     a.nqb = ceil_div(a.Sq, FbGeom<D>::BLOCK_Q);
     const dim3 bq(FbGeom<D>::WQ * kWave), bk(FB_WAVES_KV * kWave);
     const dim3 gq(B * a.H, a.nqb);
-    const dim3 gk(B * a.Hkv, ceil_div(a.Sk, FbKv<D>::BLOCK));
+    const dim3 gk(B * a.Hkv, ceil_div(a.Sk, FbKv<D>::BLOCK), FbKv<D>::DSPLIT);
     // The dQ kernel writes the row statistics the dK/dV kernel reads: same stream, in order.
     // An empty side (no query or no key rows) launches nothing for it; with no query rows
     // the dK/dV kernel still runs and stores zeros.
@@ -766,10 +778,9 @@ hipError_t launch_flash_bwd(const FlashBwdLaunch& f, hipStream_t stream) {
     a.Hkv = f.Hkv;
     a.total_q = f.total_q;
     a.total_k = f.total_k;
-    // (the entry points take D <= 128 here: a D = 256 build of these kernels spills -- its
-    // K, V fragments and dK, dV accumulators need 384 registers a lane before any working
-    // set)
-    if (f.D > 64)
+    if (f.D > 128)
+        launch_bwd_d<256>(a, f.B, f.causal, stream);
+    else if (f.D > 64)
         launch_bwd_d<128>(a, f.B, f.causal, stream);
     else
         launch_bwd_d<64>(a, f.B, f.causal, stream);

@@ -265,8 +265,7 @@ torch::Tensor flash_dense_fwd(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
 
 // flash_attention(Q, K, V, causal=False, scale=-1.0) (README.md:221-251): Q [B,H,Sq,D],
 // K/V [B,Hkv,Sk,D] fp16 with Hkv dividing H (Hkv < H: grouped-query attention, query head h
-// reads key/value head h / (H/Hkv)); D from 1 to 256 (the backward pass: to 128); scale
-// <= 0 selects 1/sqrt(D).
+// reads key/value head h / (H/Hkv)); D from 1 to 256; scale <= 0 selects 1/sqrt(D).
 // Returns fp16 [B,H,Sq,D].
 torch::Tensor flash_attention(torch::Tensor Q, torch::Tensor K, torch::Tensor V, bool causal,
                               double scale) {
@@ -290,7 +289,6 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> flash_attention_backward
     torch::Tensor dO, torch::Tensor Q, torch::Tensor K, torch::Tensor V, torch::Tensor O,
     torch::Tensor lse, bool causal, double scale) {
     check_flash_dense(Q, K, V);
-    TORCH_CHECK(Q.size(3) <= 128, "the flash-attention backward pass supports head_dim up to 128");
     check_flash_grad_inputs(Q, dO, O, lse, {Q.size(0), Q.size(1), Q.size(2)});
     const int64_t B = Q.size(0), H = Q.size(1), Sq = Q.size(2), D = Q.size(3);
     const int64_t Dp = padded_head_dim(D);
@@ -366,7 +364,6 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> flash_attention_varlen_b
     torch::Tensor lse, torch::Tensor cu_q, torch::Tensor cu_k, int64_t max_q, int64_t max_k,
     bool causal, double scale) {
     check_flash_varlen(q, k, v, cu_q, cu_k);
-    TORCH_CHECK(q.size(2) <= 128, "the flash-attention backward pass supports head_dim up to 128");
     check_flash_grad_inputs(q, dO, O, lse, {q.size(1), q.size(0)});
     const int64_t H = q.size(1), D = q.size(2), Dp = padded_head_dim(D);
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
