@@ -29,8 +29,9 @@ Workload families (--workload):
   copy       a plain 256 MiB device copy (calibrates the rocprofv3 byte counters)
   mfma_ceiling  the matrix pipe's sustained rate with register operands and no memory
              traffic (libwmma_calib.so): the ceiling the GEMM main loop is held against
-  read_floor a plain streaming read of the W4A16 M=1 weight sizes and of 1 GiB, graph
-             replayed over rotating buffers: the floor of the HBM-bound kernels
+  read_floor a plain streaming read of the W4A16 M=1 weight sizes and of 1 GiB in several
+             launch shapes, graph replayed over rotating buffers: the floor of the
+             HBM-bound kernels (the fastest shape)
   vendor     torch.mm (hipBLASLt/rocBLAS, fp32 and fp16 output) and torch's flash SDPA on
              the same shapes, for comparison
 HBM-bound cases rotate their inputs over more than 512 MB (twice the 256 MB MALL) so the
@@ -461,6 +462,7 @@ def calib_lib():
     L.wmma_calib_mfma_ceiling_flops.argtypes = [i32, i32]
     L.wmma_calib_mfma_ceiling_flops.restype = ctypes.c_double
     L.wmma_calib_read_stream.argtypes = [vp, ctypes.c_size_t, i32, vp, vp]
+    L.wmma_calib_read_stream_shape.argtypes = [vp, ctypes.c_size_t, i32, i32, vp, vp]
     return L
 
 
@@ -500,27 +502,36 @@ def fam_mfma_ceiling(wo):
 
 def fam_read_floor(wo):
     """Streaming reads of the W4A16 M=1 weight sizes (K=4096, N=4096 / 14336: 8 MiB, 28 MiB)
-    and of 1 GiB, buffers rotated over > 512 MB and replayed from a HIP graph, like the
-    W4A16 figures: the floor of an HBM-bound kernel reading that many bytes."""
+    and of 1 GiB in several launch shapes (threads per workgroup x 16-byte loads per lane),
+    buffers rotated over > 512 MB and replayed from a HIP graph, like the W4A16 figures: the
+    floor of an HBM-bound kernel reading that many bytes is the fastest shape's time."""
     import torch
 
     L = calib_lib()
+    shapes = [(64, 16), (256, 2), (256, 4), (256, 8), (512, 2), (512, 4), (512, 8), (1024, 2),
+              (1024, 4)]
     for nbytes in (4096 * 4096 // 2, 4096 * 14336 // 2, 1 << 30):
-        for loads in (4, 8):
-            cp = copies_for(nbytes)
-            bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(i & 255) for i in range(cp)]
-            sink = torch.zeros(nbytes // (8192 * loads) + 1, device="cuda")
-
+        cp = copies_for(nbytes)
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(i & 255) for i in range(cp)]
+        sink = torch.zeros(nbytes // 8192 + 1, device="cuda")
+        best = None
+        for threads, loads in shapes:
             def fn(i):
-                rc = L.wmma_calib_read_stream(bufs[i % cp].data_ptr(), nbytes, loads, sink.data_ptr(),
-                                              torch.cuda.current_stream().cuda_stream)
+                rc = L.wmma_calib_read_stream_shape(bufs[i % cp].data_ptr(), nbytes, threads, loads,
+                                                    sink.data_ptr(), torch.cuda.current_stream().cuda_stream)
                 assert rc == 0
 
             ms, _ = time_graph(fn, cp)
-            line(family="read_floor", bytes=nbytes, loads_per_wave=loads, us=round(ms * 1e3, 3),
-                 GBps=round(nbytes / (ms * 1e-3) / 1e9, 1),
+            line(family="read_floor", bytes=nbytes, threads=threads, loads_per_lane=loads,
+                 us=round(ms * 1e3, 3), GBps=round(nbytes / (ms * 1e-3) / 1e9, 1),
                  frac_hbm=round(nbytes / (ms * 1e-3) / PEAK_HBM_BPS, 4), rotation_copies=cp)
-            del bufs
+            if best is None or ms < best[0]:
+                best = (ms, threads, loads)
+        line(family="read_floor_best", bytes=nbytes, us=round(best[0] * 1e3, 3),
+             GBps=round(nbytes / (best[0] * 1e-3) / 1e9, 1),
+             frac_hbm=round(nbytes / (best[0] * 1e-3) / PEAK_HBM_BPS, 4),
+             shape=f"{best[1]} threads x {best[2]} loads per lane")
+        del bufs
 
 
 FAMILIES = {"gemm": fam_gemm, "epilogue": fam_epilogue, "skinny": fam_skinny,

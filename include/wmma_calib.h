@@ -32,6 +32,13 @@ double wmma_calib_mfma_ceiling_flops(int workgroups, int iters);
 int wmma_calib_read_stream(const void* src, size_t bytes, int loads_per_wave, float* sink,
                            void* stream);
 
+/* The same with the launch shape chosen: workgroups of `threads` threads, every lane
+ * `loads_per_lane` 16-byte loads (one contiguous run of threads * loads_per_lane * 16 bytes
+ * per workgroup).  Shapes (threads x loads): 64x16, 256x{2,4,8}, 512x{2,4,8}, 1024x{2,4};
+ * others return 2.  sink: device float[bytes / (16 * threads * loads_per_lane) + 1]. */
+int wmma_calib_read_stream_shape(const void* src, size_t bytes, int threads, int loads_per_lane,
+                                 float* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

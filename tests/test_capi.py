@@ -86,7 +86,7 @@ def test_calibration_library_exports_its_header():
     calib = ctypes.CDLL(os.path.join(ROOT, "wmma_ops_amd", "libwmma_calib.so"))
     names = declared_functions(os.path.join(ROOT, "include", "wmma_calib.h"))
     assert names == ["wmma_calib_mfma_ceiling", "wmma_calib_mfma_ceiling_flops",
-                     "wmma_calib_read_stream"], names
+                     "wmma_calib_read_stream", "wmma_calib_read_stream_shape"], names
     assert not [n for n in names if not hasattr(calib, n)]
     calib.wmma_calib_mfma_ceiling_flops.restype = ctypes.c_double
     assert calib.wmma_calib_mfma_ceiling_flops(512, 1000) == 512 * 4 * 8 * 1000 * 2.0 * 32 * 32 * 16
@@ -95,6 +95,10 @@ def test_calibration_library_exports_its_header():
                                              ctypes.c_void_p, ctypes.c_void_p]
     assert calib.wmma_calib_read_stream(None, 1024, 4, 0x10000, None) == 1
     assert calib.wmma_calib_read_stream(0x10000, 1024, 3, 0x10000, None) == 2
+    calib.wmma_calib_read_stream_shape.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                                   ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    assert calib.wmma_calib_read_stream_shape(0x10000, 1024, 128, 8, 0x10000, None) == 2
+    assert calib.wmma_calib_read_stream_shape(0x10002, 1024, 256, 2, 0x10000, None) == 1
     calib.wmma_calib_mfma_ceiling.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                               ctypes.c_void_p, ctypes.c_void_p]
     assert calib.wmma_calib_mfma_ceiling(512, 3, None, 0x10000, None) == 1    # odd iters

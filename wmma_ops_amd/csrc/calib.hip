@@ -8,9 +8,9 @@
 //    board (clock and power limits included), the ceiling a GEMM main loop can approach;
 //    with random operands the operand bits switch as in a GEMM on random data.
 //  * read_stream_kernel -- streams a buffer once with 16-byte nontemporal loads (each
-//    workgroup a contiguous run, each wave `loads` 1 KB loads in flight) and folds the
-//    words into one value per workgroup, the floor of an HBM-bound kernel that reads the
-//    same bytes with the same launch shape.
+//    workgroup a contiguous run of THREADS x LOADS 16-byte units, every lane LOADS loads in
+//    flight) and folds the words into one value per wave, the floor of an HBM-bound kernel
+//    that reads the same bytes with the same launch shape.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -61,11 +61,11 @@ __global__ void __launch_bounds__(256) mfma_ceiling_kernel(int iters, const u32x
     if (s == 1234.5f) sink[blockIdx.x] = s;  // never true; keeps the work alive
 }
 
-template <int LOADS>
-__global__ void __launch_bounds__(512) read_stream_kernel(const u32x4* src, int64_t units,
-                                                          float* sink) {
+template <int THREADS, int LOADS>
+__global__ void __launch_bounds__(THREADS) read_stream_kernel(const u32x4* src, int64_t units,
+                                                              float* sink) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t per_wg = (int64_t)8 * LOADS * 64;  // 16-byte units per workgroup
+    const int64_t per_wg = (int64_t)THREADS * LOADS;  // 16-byte units per workgroup
     const int64_t base = (int64_t)blockIdx.x * per_wg;
     u32x4 w[LOADS];
 #pragma unroll
@@ -105,19 +105,29 @@ double wmma_calib_mfma_ceiling_flops(int workgroups, int iters) {
     return (double)workgroups * 4 * 8 * iters * (2.0 * 32 * 32 * 16);
 }
 
-int wmma_calib_read_stream(const void* src, size_t bytes, int loads_per_wave, float* sink,
-                           void* stream) {
+int wmma_calib_read_stream_shape(const void* src, size_t bytes, int threads, int loads_per_lane,
+                                 float* sink, void* stream) {
     if (!src || !sink || bytes < 16 || (reinterpret_cast<uintptr_t>(src) & 15u) != 0) return 1;
     const int64_t units = (int64_t)(bytes / 16);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    auto grid = [&](int loads) { return (int)((units + 8 * loads * 64 - 1) / (8 * loads * 64)); };
-    switch (loads_per_wave) {
-        case 2: hipLaunchKernelGGL(read_stream_kernel<2>, dim3(grid(2)), dim3(512), 0, st, (const u32x4*)src, units, sink); break;
-        case 4: hipLaunchKernelGGL(read_stream_kernel<4>, dim3(grid(4)), dim3(512), 0, st, (const u32x4*)src, units, sink); break;
-        case 8: hipLaunchKernelGGL(read_stream_kernel<8>, dim3(grid(8)), dim3(512), 0, st, (const u32x4*)src, units, sink); break;
-        default: return 2;
+    const int64_t per_wg = (int64_t)threads * loads_per_lane;
+    const dim3 grid(per_wg > 0 ? (unsigned)((units + per_wg - 1) / per_wg) : 0u);
+#define WMMA_CALIB_RS(T, L)                                                                      \
+    if (threads == (T) && loads_per_lane == (L)) {                                               \
+        hipLaunchKernelGGL((read_stream_kernel<T, L>), grid, dim3(T), 0, st, (const u32x4*)src,   \
+                           units, sink);                                                          \
+        return hipGetLastError() == hipSuccess ? 0 : 5;                                          \
     }
-    return hipGetLastError() == hipSuccess ? 0 : 5;
+    WMMA_CALIB_RS(64, 16) WMMA_CALIB_RS(256, 2) WMMA_CALIB_RS(256, 4) WMMA_CALIB_RS(256, 8)
+    WMMA_CALIB_RS(512, 2) WMMA_CALIB_RS(512, 4) WMMA_CALIB_RS(512, 8) WMMA_CALIB_RS(1024, 2)
+    WMMA_CALIB_RS(1024, 4)
+#undef WMMA_CALIB_RS
+    return 2;
+}
+
+int wmma_calib_read_stream(const void* src, size_t bytes, int loads_per_wave, float* sink,
+                           void* stream) {
+    return wmma_calib_read_stream_shape(src, bytes, 512, loads_per_wave, sink, stream);
 }
 
 }  // extern "C"
