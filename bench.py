@@ -28,7 +28,8 @@ Workload families (--workload):
              8 K/V heads (GQA); head dims 64 and 256; a packed variable-length batch
   copy       a plain 256 MiB device copy (calibrates the rocprofv3 byte counters)
   mfma_ceiling  the matrix pipe's sustained rate with register operands and no memory
-             traffic (libwmma_calib.so): the ceiling the GEMM main loop is held against
+             traffic (libwmma_calib.so): the ceiling the GEMM main loop is held against;
+             and the 4096^3 GEMM itself on random and on constant operands
   read_floor a plain streaming read of the W4A16 M=1 weight sizes and of 1 GiB in several
              launch shapes, graph replayed over rotating buffers: the floor of the
              HBM-bound kernels (the fastest shape)
@@ -243,14 +244,16 @@ def fam_skinny(wo):
         cp = copies_for(nbytes)
         As = [A.cuda() for _ in range(cp)]
         Bs = [B.cuda() for _ in range(cp)]
-        ms = time_batches(lambda i: wo.matmul(As[i % cp], Bs[i % cp]), 4 * cp)
-        err = og.max_rel_err(wo.matmul(As[0], Bs[0]), og.gemm_ref(A, B))
+        C0 = wo.matmul(As[0], Bs[0])
+        ms, outs = time_graph(lambda i: wo.matmul(As[i % cp], Bs[i % cp]), cp)
+        assert torch.equal(outs[0], C0), "graph replay differs from eager"
+        err = og.max_rel_err(C0, og.gemm_ref(A, B))
         line(family="skinny", M=m, N=n, K=k, plan=wo.gemm_plan(m, n, k), us=round(ms * 1e3, 2),
              bytes=nbytes, GBps=round(nbytes / (ms * 1e-3) / 1e9, 1),
              TFLOPS=round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 2),
-             **roofline(nbytes, 2.0 * m * n * k, ms), rotation_copies=cp,
+             **roofline(nbytes, 2.0 * m * n * k, ms), rotation_copies=cp, timing="graph replay",
              max_rel_err=float(f"{err:.3e}"))
-        del As, Bs
+        del As, Bs, outs
 
 
 def w4a16_case(wo, m, n, use_graph=True):
@@ -292,7 +295,7 @@ def w4a16_case(wo, m, n, use_graph=True):
 def fam_w4a16(wo):
     for m in (1, 16, 128, 2048):
         for n in (4096, 14336):
-            r = w4a16_case(wo, m, n, use_graph=m <= 16)
+            r = w4a16_case(wo, m, n, use_graph=m <= 128)
             r["family"] = "w4a16"
             line(**r)
 
@@ -498,6 +501,26 @@ def fam_mfma_ceiling(wo):
              us_per_launch=round(ms * 1e3, 1),
              config="512 workgroups x 4 waves, each wave 4000 x 8 independent "
                     "v_mfma_f32_32x32x16_f16 on register operands (no memory traffic)")
+    # The same 4096^3 GEMM (same kernel, same memory traffic) on random and on constant
+    # operands: a kernel limited by issue or memory runs both in the same time; a
+    # power-limited one runs faster when the operand bits do not switch.
+    import torch
+
+    g = torch.Generator().manual_seed(42 + 1)
+    for name in ("random N(0,1) fp16", "all ones", "all zeros"):
+        if name.startswith("random"):
+            A = torch.randn(4096, 4096, generator=g).half().cuda()
+            B = torch.randn(4096, 4096, generator=g).half().cuda()
+        else:
+            v = 1.0 if name == "all ones" else 0.0
+            A = torch.full((4096, 4096), v, dtype=torch.float16, device="cuda")
+            B = torch.full((4096, 4096), v, dtype=torch.float16, device="cuda")
+        ms = time_batches(lambda i: wo.matmul(A, B), 100 if not QUICK else 2)
+        fl = 2.0 * 4096 ** 3
+        line(family="gemm_operands", M=4096, N=4096, K=4096, operands=name, us=round(ms * 1e3, 2),
+             TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
+             frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4))
+        del A, B
 
 
 def fam_read_floor(wo):
