@@ -30,6 +30,8 @@ Workload families (--workload):
   mfma_ceiling  the matrix pipe's sustained rate with register operands and no memory
              traffic (libwmma_calib.so): the ceiling the GEMM main loop is held against;
              and the 4096^3 GEMM itself on random and on constant operands
+  lds_read   the LDS read rate of ds_read_b128 and ds_read_b64_tr_b16 (contiguous and in the
+             flash forward's V-fragment pattern), the LDS side of the MFMA kernels
   read_floor a plain streaming read of the W4A16 M=1 weight sizes and of 1 GiB in several
              launch shapes, graph replayed over rotating buffers: the floor of the
              HBM-bound kernels (the fastest shape)
@@ -466,6 +468,9 @@ def calib_lib():
     L.wmma_calib_mfma_ceiling_flops.restype = ctypes.c_double
     L.wmma_calib_read_stream.argtypes = [vp, ctypes.c_size_t, i32, vp, vp]
     L.wmma_calib_read_stream_shape.argtypes = [vp, ctypes.c_size_t, i32, i32, vp, vp]
+    L.wmma_calib_lds_read.argtypes = [i32, i32, i32, vp, vp]
+    L.wmma_calib_lds_read_bytes.argtypes = [i32, i32]
+    L.wmma_calib_lds_read_bytes.restype = ctypes.c_double
     return L
 
 
@@ -523,6 +528,30 @@ def fam_mfma_ceiling(wo):
         del A, B
 
 
+def fam_lds_read(wo):
+    """LDS read rate of the fragment-read patterns of the MFMA kernels (libwmma_calib.so):
+    one workgroup of 8 waves per CU, each wave reading 8 KB per iteration of a 64 KB LDS
+    buffer, ~0.3 ms launches back to back after the clock settles."""
+    import torch
+
+    L = calib_lib()
+    wgs, iters = 256, 2000
+    sink = torch.zeros(wgs, device="cuda")
+    names = {0: "ds_read_b128, 1 KB contiguous per instruction",
+             1: "ds_read_b64_tr_b16, 512 contiguous bytes per instruction",
+             2: "ds_read_b64_tr_b16, flash forward V-fragment pattern (D = 128)"}
+    nbytes = L.wmma_calib_lds_read_bytes(wgs, iters)
+    for mode in (0, 1, 2):
+        st = torch.cuda.current_stream().cuda_stream
+        fn = lambda i: L.wmma_calib_lds_read(mode, wgs, iters, sink.data_ptr(), st)
+        assert fn(0) == 0
+        ms = time_batches(fn, 50 if not QUICK else 2, batches=3)
+        line(family="lds_read", pattern=names[mode], us_per_launch=round(ms * 1e3, 1),
+             TBps_chip=round(nbytes / (ms * 1e-3) / 1e12, 1),
+             GBps_per_cu=round(nbytes / (ms * 1e-3) / 1e9 / wgs, 1),
+             config=f"{wgs} workgroups x 8 waves x {iters} iterations x 8 KB")
+
+
 def fam_read_floor(wo):
     """Streaming reads of the W4A16 M=1 weight sizes (K=4096, N=4096 / 14336: 8 MiB, 28 MiB)
     and of 1 GiB in several launch shapes (threads per workgroup x 16-byte loads per lane),
@@ -559,7 +588,7 @@ def fam_read_floor(wo):
 
 FAMILIES = {"gemm": fam_gemm, "epilogue": fam_epilogue, "skinny": fam_skinny,
             "w4a16": fam_w4a16, "flash": fam_flash, "copy": fam_copy,
-            "mfma_ceiling": fam_mfma_ceiling, "read_floor": fam_read_floor, "vendor": fam_vendor}
+            "mfma_ceiling": fam_mfma_ceiling, "read_floor": fam_read_floor, "lds_read": fam_lds_read, "vendor": fam_vendor}
 
 
 # ------------------------------------------------------------------------ headline --

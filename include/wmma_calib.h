@@ -26,6 +26,15 @@ int wmma_calib_mfma_ceiling(int workgroups, int iters, const void* operands, flo
 /* FLOPs one wmma_calib_mfma_ceiling launch performs (2 per multiply-add). */
 double wmma_calib_mfma_ceiling_flops(int workgroups, int iters);
 
+/* LDS read rate: `workgroups` workgroups of 8 waves, each wave reading 8 KB of a 64 KB LDS
+ * buffer per iteration, `iters` iterations.  mode 0: ds_read_b128, 1 KB contiguous per
+ * instruction; 1: ds_read_b64_tr_b16, 512 contiguous bytes per instruction; 2:
+ * ds_read_b64_tr_b16 in the flash forward's V-fragment pattern (D = 128).  Other modes
+ * return 2.  sink: device float[workgroups]. */
+int wmma_calib_lds_read(int mode, int workgroups, int iters, float* sink, void* stream);
+/* Bytes one wmma_calib_lds_read launch reads from LDS. */
+double wmma_calib_lds_read_bytes(int workgroups, int iters);
+
 /* Reads `bytes` (a multiple of 16; src 16-byte aligned) once: workgroups of 8 waves, each
  * wave `loads_per_wave` (2, 4 or 8) 1 KB nontemporal loads of one contiguous run.
  * sink: device float[bytes / (8 KB * loads_per_wave) + 1]. */

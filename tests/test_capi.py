@@ -85,7 +85,8 @@ def test_calibration_library_exports_its_header():
     # bench.py's measuring instruments (include/wmma_calib.h, libwmma_calib.so)
     calib = ctypes.CDLL(os.path.join(ROOT, "wmma_ops_amd", "libwmma_calib.so"))
     names = declared_functions(os.path.join(ROOT, "include", "wmma_calib.h"))
-    assert names == ["wmma_calib_mfma_ceiling", "wmma_calib_mfma_ceiling_flops",
+    assert names == ["wmma_calib_lds_read", "wmma_calib_lds_read_bytes",
+                     "wmma_calib_mfma_ceiling", "wmma_calib_mfma_ceiling_flops",
                      "wmma_calib_read_stream", "wmma_calib_read_stream_shape"], names
     assert not [n for n in names if not hasattr(calib, n)]
     calib.wmma_calib_mfma_ceiling_flops.restype = ctypes.c_double
@@ -99,6 +100,12 @@ def test_calibration_library_exports_its_header():
                                                    ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     assert calib.wmma_calib_read_stream_shape(0x10000, 1024, 128, 8, 0x10000, None) == 2
     assert calib.wmma_calib_read_stream_shape(0x10002, 1024, 256, 2, 0x10000, None) == 1
+    calib.wmma_calib_lds_read.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                          ctypes.c_void_p]
+    assert calib.wmma_calib_lds_read(3, 256, 10, 0x10000, None) == 2
+    assert calib.wmma_calib_lds_read(0, 0, 10, 0x10000, None) == 1
+    calib.wmma_calib_lds_read_bytes.restype = ctypes.c_double
+    assert calib.wmma_calib_lds_read_bytes(2, 3) == 2 * 8 * 3 * 8192
     calib.wmma_calib_mfma_ceiling.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                               ctypes.c_void_p, ctypes.c_void_p]
     assert calib.wmma_calib_mfma_ceiling(512, 3, None, 0x10000, None) == 1    # odd iters

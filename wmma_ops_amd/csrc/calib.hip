@@ -11,6 +11,12 @@
 //    workgroup a contiguous run of THREADS x LOADS 16-byte units, every lane LOADS loads in
 //    flight) and folds the words into one value per wave, the floor of an HBM-bound kernel
 //    that reads the same bytes with the same launch shape.
+//  * lds_read_kernel -- eight waves per workgroup read a 64 KB LDS buffer over and over, in
+//    one of three patterns: ds_read_b128 (1 KB contiguous per instruction, the K rows of
+//    the flash kernels and the A rows of the GEMM), ds_read_b64_tr_b16 on 512 contiguous
+//    bytes, and ds_read_b64_tr_b16 in the flash forward's V-fragment pattern at D = 128
+//    (eight 256-byte rows, 64 bytes each, chunk swizzle 4 * (row % 4)).  The LDS read rate
+//    the MFMA kernels' fragment reads share with their matrix instructions.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -86,6 +92,49 @@ __global__ void __launch_bounds__(THREADS) read_stream_kernel(const u32x4* src, 
     if (x == 0x9E3779B9u && lane == 0) sink[blockIdx.x] = (float)wave;
 }
 
+// Every wave reads 8 KB per iteration (eight ds_read_b128, or eight pairs of
+// ds_read_b64_tr_b16); addresses are fixed per lane, offsets per iteration wave-uniform.
+template <int MODE>
+__global__ void __launch_bounds__(512) lds_read_kernel(int iters, float* sink) {
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[65536];
+    for (int i = threadIdx.x; i < 65536 / 4; i += 512)
+        reinterpret_cast<uint32_t*>(smem)[i] = (uint32_t)i * 2654435761u;
+    __syncthreads();
+    const WMMA_LDS unsigned char* lds = (const WMMA_LDS unsigned char*)smem;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int vbase[4];
+    {
+        // flash forward V fragments (D = 128): lane 4j + a of 16-lane group g reads row
+        // 4 (g / 2) + j, columns 32 db + 16 (g % 2) + 4 a .. +3 of a 256-byte-row tile
+        const int g = lane >> 4, jj = (lane & 15) >> 2, aa = lane & 3;
+        const int row = 4 * (g >> 1) + jj, sw = 4 * (row & 3);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const int col = 32 * db + 16 * (g & 1) + 4 * aa;
+            vbase[db] = row * 256 + (((col >> 3) ^ sw) << 4) + ((col & 7) << 1);
+        }
+    }
+    uint32_t x = 0;
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int blk = (it * 64 + u * 8 + wave) & 63;  // wave-uniform 1 KB block
+            if constexpr (MODE == 0) {
+                const u32x4 v = *(const volatile WMMA_LDS u32x4*)(lds + blk * 1024 + lane * 16);
+                x ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+            } else {
+                const int a0 = MODE == 1 ? blk * 1024 + lane * 8
+                                         : vbase[u & 3] + 16 * ((it + (u >> 2) + wave) & 3) * 256;
+                const u32x2 lo = __builtin_bit_cast(u32x2, lds_read_tr16(lds + a0));
+                const u32x2 hi = __builtin_bit_cast(u32x2, lds_read_tr16(lds + a0 + (MODE == 1 ? 512 : 2048)));
+                x ^= lo[0] ^ lo[1] ^ hi[0] ^ hi[1];
+            }
+        }
+    }
+    if (x == 0x9E3779B9u) sink[blockIdx.x] = 1.0f;  // keeps the reads observable
+}
+
 }  // namespace
 
 extern "C" {
@@ -123,6 +172,22 @@ int wmma_calib_read_stream_shape(const void* src, size_t bytes, int threads, int
     WMMA_CALIB_RS(1024, 4)
 #undef WMMA_CALIB_RS
     return 2;
+}
+
+int wmma_calib_lds_read(int mode, int workgroups, int iters, float* sink, void* stream) {
+    if (workgroups <= 0 || iters <= 0 || !sink) return 1;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    switch (mode) {
+        case 0: hipLaunchKernelGGL(lds_read_kernel<0>, dim3(workgroups), dim3(512), 0, st, iters, sink); break;
+        case 1: hipLaunchKernelGGL(lds_read_kernel<1>, dim3(workgroups), dim3(512), 0, st, iters, sink); break;
+        case 2: hipLaunchKernelGGL(lds_read_kernel<2>, dim3(workgroups), dim3(512), 0, st, iters, sink); break;
+        default: return 2;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+double wmma_calib_lds_read_bytes(int workgroups, int iters) {
+    return (double)workgroups * 8.0 * (double)iters * 8192.0;
 }
 
 int wmma_calib_read_stream(const void* src, size_t bytes, int loads_per_wave, float* sink,
