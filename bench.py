@@ -426,6 +426,18 @@ def fam_vendor(wo):
                      us=round(ms2 * 1e3, 2), TFLOPS=round(fl / (ms2 * 1e-3) / 1e12, 1),
                      frac_mfma_peak=round(fl / (ms2 * 1e-3) / PEAK_FP16_FLOPS, 4))
         del Ad, Bd
+    # 4096^3 fp32-output on all-ones operands (the operand bits never switch, so the board's
+    # power limit holds the clock less): both kernels' pipelines without the data's energy.
+    Ad = torch.ones(4096, 4096, dtype=torch.float16, device="cuda")
+    Bd = torch.ones(4096, 4096, dtype=torch.float16, device="cuda")
+    fl = 2.0 * 4096 ** 3
+    for lib, fn in (("torch.mm (hipBLASLt/rocBLAS)", lambda i: torch.mm(Ad, Bd, out_dtype=torch.float32)),
+                    ("wmma_ops_amd.matmul", lambda i: wo.matmul(Ad, Bd))):
+        ms = time_batches(fn, 50)
+        line(family="vendor_gemm", M=4096, N=4096, K=4096, out="f32", operands="all ones", library=lib,
+             us=round(ms * 1e3, 2), TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
+             frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4))
+    del Ad, Bd
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
     B, H, S, D = 4, 32, 4096, 128
