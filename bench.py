@@ -26,6 +26,8 @@ Workload families (--workload):
   w4a16      configs[3]: M in {1,16,128,2048} x N in {4096,14336}, K=4096, G=128
   flash      configs[4]: [4,32,4096,128], causal and non-causal, forward and backward; with
              8 K/V heads (GQA); head dims 64 and 256; a packed variable-length batch
+  flash_operands  configs[4] non-causal forward and backward on all-ones inputs (the power
+             limit's share of the random-input figures)
   copy       a plain 256 MiB device copy (calibrates the rocprofv3 byte counters)
   mfma_ceiling  the matrix pipe's sustained rate with register operands and no memory
              traffic (libwmma_calib.so): the ceiling the GEMM main loop is held against;
@@ -398,6 +400,27 @@ def fam_flash(wo):
              max_rel_err=float(f"{err:.3e}"))
 
 
+def fam_flash_operands(wo):
+    """configs[4] non-causal, forward and backward, on all-ones Q, K, V (and dO): the same
+    kernels and traffic with operand bits that never switch -- against the random-input
+    lines of the flash family, how far the board's power limit holds these kernels on
+    random data.  A family of its own so that the flash family's kernel trace holds only
+    random-input launches."""
+    import torch
+
+    B, H, S, D = 4, 32, 4096, 128
+    ones = torch.ones(B, H, S, D, dtype=torch.float16, device="cuda")
+    fl = 4.0 * B * H * S * S * D
+    ms = time_batches(lambda i: wo.flash_attention(ones, ones, ones, False), 10)
+    line(family="flash", B=B, H=H, S=S, D=D, causal=False, operands="all ones", us=round(ms * 1e3, 1),
+         TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1), frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4))
+    O, lse = wo.flash_attention_forward(ones, ones, ones, False)
+    msb = time_batches(lambda i: wo.flash_attention_backward(ones, ones, ones, ones, O, lse, False), 5)
+    line(family="flash_bwd", B=B, H=H, S=S, D=D, causal=False, operands="all ones", us=round(msb * 1e3, 1),
+         TFLOPS=round(2.5 * fl / (msb * 1e-3) / 1e12, 1),
+         frac_mfma_peak=round(2.5 * fl / (msb * 1e-3) / PEAK_FP16_FLOPS, 4))
+
+
 def fam_vendor(wo):
     """The vendor libraries torch dispatches to on the same inputs, for comparison (not
     this library's code): torch.mm fp16 x fp16 with fp32 output (out_dtype) and with fp16
@@ -600,7 +623,8 @@ def fam_read_floor(wo):
 
 FAMILIES = {"gemm": fam_gemm, "epilogue": fam_epilogue, "skinny": fam_skinny,
             "w4a16": fam_w4a16, "flash": fam_flash, "copy": fam_copy,
-            "mfma_ceiling": fam_mfma_ceiling, "read_floor": fam_read_floor, "lds_read": fam_lds_read, "vendor": fam_vendor}
+            "mfma_ceiling": fam_mfma_ceiling, "read_floor": fam_read_floor, "lds_read": fam_lds_read,
+            "flash_operands": fam_flash_operands, "vendor": fam_vendor}
 
 
 # ------------------------------------------------------------------------ headline --
@@ -802,7 +826,7 @@ def main():
     global QUICK
     QUICK = args.quick and bool(args.suite or args.workload)
     if args.suite:
-        for name in ("gemm", "epilogue", "skinny", "w4a16", "flash"):
+        for name in ("gemm", "epilogue", "skinny", "w4a16", "flash", "flash_operands"):
             FAMILIES[name](wo)
     elif args.workload:
         FAMILIES[args.workload](wo)
