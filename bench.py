@@ -15,7 +15,8 @@ timed steps between two synchronisations; `value` = 2*M*N*K / time.
 `roofline.achieved` divides the same FLOPs by the kernel's mean duration measured with
 HIP events on the stream the kernel is launched on (the current stream).  The W4A16 M=1
 decode figures (configs[3], K=4096, N in {4096, 14336}, G=128) ride along in the same
-line; the CPU baseline (N=1 only) is the oracle on the host cores over bounded samples
+line, each with the time a plain streaming read of the same byte count takes in its
+fastest launch shape in the same run (`read_floor`); the CPU baseline (N=1 only) is the oracle on the host cores over bounded samples
 of the same workloads: fp32 torch.matmul at 4096^3 (`value`), the W4A16 M=1 dequant +
 matmul at N=14336, and fp32 SDPA on 2 heads of configs[4].
 
@@ -587,6 +588,30 @@ def fam_lds_read(wo):
              config=f"{wgs} workgroups x 8 waves x {iters} iterations x 8 KB")
 
 
+def read_floor_best(nbytes, shapes=((64, 16), (256, 2), (512, 2))):
+    """(us, shape) of the fastest plain streaming read of nbytes (rounded down to 16) over
+    the given launch shapes, graph-replayed over rotating buffers like the W4A16 figures."""
+    import torch
+
+    L = calib_lib()
+    nb = nbytes // 16 * 16
+    cp = copies_for(nb)
+    bufs = [torch.empty(nb, dtype=torch.uint8, device="cuda").fill_(i & 255) for i in range(cp)]
+    sink = torch.zeros(nb // 8192 + 1, device="cuda")
+    best = None
+    for threads, loads in shapes:
+        def fn(i):
+            rc = L.wmma_calib_read_stream_shape(bufs[i % cp].data_ptr(), nb, threads, loads,
+                                                sink.data_ptr(), torch.cuda.current_stream().cuda_stream)
+            assert rc == 0
+
+        ms, _ = time_graph(fn, cp)
+        if best is None or ms < best[0]:
+            best = (ms, f"{threads} threads x {loads} loads per lane")
+    del bufs
+    return best[0] * 1e3, best[1]
+
+
 def fam_read_floor(wo):
     """Streaming reads of the W4A16 M=1 weight sizes (K=4096, N=4096 / 14336: 8 MiB, 28 MiB)
     and of 1 GiB in several launch shapes (threads per workgroup x 16-byte loads per lane),
@@ -807,6 +832,16 @@ def headline(wo, args):
     }
     if not args.no_w4a16:
         out["w4a16_m1"] = [w4a16_case(wo, 1, n) for n in (4096, 14336)]
+        for r in out["w4a16_m1"]:
+            # the same bytes read by a plain streaming kernel in its fastest launch shape, in
+            # the same run (libwmma_calib.so): the floor of one launch reading that much
+            fl_us, shape = read_floor_best(r["bytes"])
+            r["read_floor"] = {"us": round(fl_us, 3), "shape": shape,
+                               "frac": round(fl_us / r["us_per_call"], 4),
+                               "what": "streaming read of the same byte count, fastest of "
+                                       "64x16, 256x2, 512x2 threads x 16-byte loads per lane, "
+                                       "graph-replayed over rotating buffers "
+                                       "(bench.py --workload read_floor)"}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)
