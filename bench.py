@@ -24,6 +24,9 @@ Workload families (--workload):
   gemm       configs[0..1]: M=N=K in {512,1024,2048,4096} and 4096x4096x2048
   epilogue   configs[1]: C = 2.0*A@B + 0.5*C, out-of-place and in-place, 1024^3/4096^3
   skinny     configs[2]: M in {1,16,64,128} x N in {4096,11008,14336}, K=4096; K=14336,N=4096
+  ragged     N or K off a multiple of 8 (4096x4100x4096, 2048x32001x4096, M = 1..4096): the
+             repacked product path, the element-wise in-place path and the aligned neighbour
+             shape, in one process (inputs not rotated)
   w4a16      configs[3]: M in {1,16,128,2048} x N in {4096,14336}, K=4096, G=128
   flash      configs[4]: [4,32,4096,128], causal and non-causal, forward and backward; with
              8 K/V heads (GQA); head dims 64 and 256; a packed variable-length batch
@@ -259,6 +262,68 @@ def fam_skinny(wo):
              **roofline(nbytes, 2.0 * m * n * k, ms), rotation_copies=cp, timing="graph replay",
              max_rel_err=float(f"{err:.3e}"))
         del As, Bs, outs
+
+
+def fam_ragged(wo):
+    """GEMMs whose B rows (N not a multiple of 8) or A rows (K not) break 16-byte vectors,
+    three ways in one process: the product path (wo.matmul: the operand is repacked into a
+    zero-padded copy in the workspace, then the vector kernels run), the same call through
+    the C-ABI with only the split-K workspace (the element-wise kernels read the operand in
+    place), and the aligned neighbour shape (N or K rounded up to 8) for the repack's cost."""
+    import ctypes
+
+    import torch
+
+    from oracle import gemm as og
+
+    L = ctypes.CDLL(wo.LIBRARY_PATH)
+    vp, i64, i32, f32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    L.wmma_gemm_f16f32.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32,
+                                   f32, f32, i32, vp, sz, vp]
+    stream = torch.cuda.current_stream().cuda_stream
+    for (m, n, k) in [(4096, 4100, 4096), (4096, 4096, 4100), (2048, 32001, 4096),
+                      (1024, 4100, 4096), (128, 4100, 4096), (16, 4100, 4096), (1, 4100, 4096),
+                      (1, 4096, 4100)]:
+        g = torch.Generator().manual_seed(42 + 5)
+        A = torch.randn(m, k, generator=g).half()
+        B = (torch.randn(k, n, generator=g) * 0.02).half()
+        Ad, Bd = A.cuda(), B.cuda()
+        fl = 2.0 * m * n * k
+        calls = 20 if fl > 1e11 else 100
+        plan = wo.gemm_plan(m, n, k)
+        ws = torch.empty(max(plan[7], 1), dtype=torch.uint8, device="cuda")
+        C = torch.empty(m, n, device="cuda")
+
+        def inplace(i):
+            rc = L.wmma_gemm_f16f32(Ad.data_ptr(), k, Bd.data_ptr(), n, None, n, C.data_ptr(), n,
+                                    m, n, k, 1.0, 0.0, -1, ws.data_ptr(), plan[7], stream)
+            assert rc == 0
+
+        n8, k8 = (n + 7) // 8 * 8, (k + 7) // 8 * 8
+        # same random values, zero padded (all-zero operands would run faster than random
+        # ones: the board's power limit holds the clock less)
+        A8 = torch.zeros(m, k8, dtype=torch.half, device="cuda")
+        B8 = torch.zeros(k8, n8, dtype=torch.half, device="cuda")
+        A8[:, :k] = Ad
+        B8[:k, :n] = Bd
+        rows = min(m, 64)
+        ref = og.gemm_ref(A[:rows], B)
+        for path, fn in (("repack", lambda i: wo.matmul(Ad, Bd)), ("in place", inplace),
+                         ("aligned neighbour", lambda i: wo.matmul(A8, B8))):
+            ms = time_batches(fn, calls)
+            if path == "repack":
+                err = og.max_rel_err(wo.matmul(Ad, Bd)[:rows], ref)
+            elif path == "in place":
+                inplace(0)
+                err = og.max_rel_err(C[:rows], ref)
+            else:
+                err = None
+            shape = (m, n8, k8) if path == "aligned neighbour" else (m, n, k)
+            line(family="ragged", path=path, M=shape[0], N=shape[1], K=shape[2],
+                 plan=wo.gemm_plan(*shape), us=round(ms * 1e3, 2),
+                 TFLOPS=round(2.0 * shape[0] * shape[1] * shape[2] / (ms * 1e-3) / 1e12, 1),
+                 max_rel_err=None if err is None else float(f"{err:.3e}"))
+        del Ad, Bd, A8, B8, C, ws
 
 
 def w4a16_case(wo, m, n, use_graph=True):
@@ -646,7 +711,7 @@ def fam_read_floor(wo):
         del bufs
 
 
-FAMILIES = {"gemm": fam_gemm, "epilogue": fam_epilogue, "skinny": fam_skinny,
+FAMILIES = {"gemm": fam_gemm, "epilogue": fam_epilogue, "skinny": fam_skinny, "ragged": fam_ragged,
             "w4a16": fam_w4a16, "flash": fam_flash, "copy": fam_copy,
             "mfma_ceiling": fam_mfma_ceiling, "read_floor": fam_read_floor, "lds_read": fam_lds_read,
             "flash_operands": fam_flash_operands, "vendor": fam_vendor}
@@ -861,7 +926,7 @@ def main():
     global QUICK
     QUICK = args.quick and bool(args.suite or args.workload)
     if args.suite:
-        for name in ("gemm", "epilogue", "skinny", "w4a16", "flash", "flash_operands"):
+        for name in ("gemm", "epilogue", "skinny", "ragged", "w4a16", "flash", "flash_operands"):
             FAMILIES[name](wo)
     elif args.workload:
         FAMILIES[args.workload](wo)

@@ -75,15 +75,25 @@ int wmma_device_cu_count(int device);
  * split_k::compute_config (wmma_xor_swizzle.hpp:293-332). */
 int wmma_gemm_plan_make(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* out);
 
-/* Workspace bytes wmma_gemm_f16f32 needs for this shape on the current device. */
+/* Workspace bytes wmma_gemm_f16f32 uses for this shape on the current device, for
+ * contiguous 16-byte-aligned operands (lda = K, ldb = N): the split-K partial sums
+ * (plan.workspace_bytes) plus, when K or N is not a multiple of 8, room for zero-padded
+ * copies of the operands whose rows then break 16-byte vectors (A [M][K rounded up to 8],
+ * B [K][N rounded up to 8], 256-byte aligned, 256 bytes of slack). */
 size_t wmma_gemm_workspace_size(int M, int N, int K, int tile_cfg);
 
 /*
  * C_out[M,N] = alpha * (A[M,K] @ B[K,N]) + beta * C_in[M,N]      (fp16 in, fp32 accumulate
  * and out).  C_in is read only when beta != 0 and C_in != NULL; C_in may equal C_out
  * (in-place).  tile_cfg: WMMA_TILE_AUTO or 0..WMMA_TILE_COUNT-1.  workspace: device
- * memory of at least wmma_gemm_workspace_size(M,N,K,tile_cfg) bytes (may be NULL when
- * that is 0).
+ * memory of at least plan.workspace_bytes (the split-K partial sums; may be NULL when that
+ * is 0), 4-byte aligned.  An operand whose rows break 16-byte vectors (K or N not a
+ * multiple of 8, lda or ldb not a multiple of 8, A or B not 16-byte aligned) is copied into
+ * a zero-padded dense buffer taken from the workspace behind the partial sums when the
+ * workspace holds it (wmma_gemm_workspace_size(M,N,K,tile_cfg) bytes always do for
+ * contiguous operands), and the 16-byte vector kernels run on the copy; with less
+ * workspace the element-wise kernels read it in place (same result, several times
+ * slower).
  * Replaces wmma_matmul (wmma_gemm.hip:1432-1470), wmma_matmul_tiled (:1473-1528),
  * wmma_matmul_adaptive (:1197-1263), wmma_gemm (:1891-1945), wmma_gemm_inplace
  * (:1949-1994) and wmma_gemm_adaptive (:1997-2078), and the unreachable split-K wrapper
@@ -103,8 +113,10 @@ int wmma_gemm_f16f32(const void* A, int64_t lda, const void* B, int64_t ldb,
  * gives the need).  Every call on one GPU shares that GPU's array and nothing in it has to
  * start at zero (each split writes its whole partial tile before the reduction reads it);
  * calls that overlap on one GPU (other streams, other threads) race on it and must be
- * serialised by the caller.  No counterpart in the reference: for callers that cannot
- * allocate (code under stream capture, tight serving loops, harnesses that forbid it).
+ * serialised by the caller.  Operands whose rows break 16-byte vectors are read in place
+ * by the element-wise kernels (no repacked copy).  No counterpart in the reference: for
+ * callers that cannot allocate (code under stream capture, tight serving loops, harnesses
+ * that forbid it).
  */
 int wmma_gemm_f16f32_noalloc(const void* A, int64_t lda, const void* B, int64_t ldb,
                              const float* C_in, int64_t ldc_in, float* C_out, int64_t ldc, int M,

@@ -164,6 +164,24 @@ class W4Plan(ctypes.Structure):
                 ("workspace_bytes", ctypes.c_size_t)]
 
 
+def test_gemm_workspace_size_covers_repacked_operands(lib):
+    # Contiguous operands: K or N off a multiple of 8 adds a zero-padded copy of A [M][K8]
+    # and/or B [K][N8] (256-byte rounded, plus 256 bytes of alignment slack) to the split-K
+    # partial sums; aligned shapes need only the partial sums.
+    r256 = lambda x: (x + 255) // 256 * 256
+    p = Plan()
+    for M, N, K in [(4096, 4100, 4096), (4096, 4096, 4100), (4095, 4101, 4099), (1, 4100, 4096),
+                    (13, 1027, 300), (1, 1, 1), (4096, 4096, 4096), (1, 4096, 4096)]:
+        assert lib.wmma_gemm_plan_make(M, N, K, -1, 256, ctypes.byref(p)) == OK
+        K8, N8 = (K + 7) // 8 * 8, (N + 7) // 8 * 8
+        extra = 0
+        if K % 8 or N % 8:
+            extra = 256 + (r256(M * K8 * 2) if K % 8 else 0) + (r256(K * N8 * 2) if N % 8 else 0)
+        assert lib.wmma_gemm_workspace_size(M, N, K, -1) == p.workspace_bytes + extra, (M, N, K)
+    assert lib.wmma_gemm_workspace_size(0, 4100, 4096, -1) == 0
+    assert lib.wmma_gemm_workspace_size(16, 4100, 0, -1) == 0
+
+
 def test_w4a16_plan_make(lib):
     lib.wmma_w4a16_plan_make.argtypes = [ctypes.c_int] * 5 + [ctypes.POINTER(W4Plan)]
     p = W4Plan()

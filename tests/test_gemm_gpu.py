@@ -249,13 +249,82 @@ def test_matmul_tiled_invalid_config(wo):
 @pytest.mark.parametrize("M,N,K", [(33, 40, 24), (130, 72, 200), (17, 19, 23), (5, 3, 7),
                                    (1, 1, 1), (70, 129, 513), (3, 4096, 520), (640, 8, 8)])
 def test_ragged_shapes(wo, M, N, K):
-    # N or K not multiples of 8 take the element-wise load path.
+    # N or K not multiples of 8: the operand is repacked into a zero-padded copy.
     report("ragged", M=M, N=N, K=K)
     A, B = _inputs(M, N, K, M * 1000 + N + K)
     ref = og.gemm_ref(A, B)
     _check(wo.matmul(A.cuda(), B.cuda()), ref)
     C = torch.randn(M, N)
     _check(wo.gemm(A.cuda(), B.cuda(), 0.5, -2.0, C.cuda()), og.gemm_ref(A, B, 0.5, -2.0, C))
+
+
+def _repack_bytes(M, N, K, a, b):
+    r256 = lambda x: (x + 255) // 256 * 256
+    if not (a or b):
+        return 0
+    return 256 + (r256(M * ((K + 7) // 8 * 8) * 2) if a else 0) + (r256(K * ((N + 7) // 8 * 8) * 2) if b else 0)
+
+
+# Operands whose rows break 16-byte vectors, through the C-ABI two ways: with the workspace
+# wmma_gemm_workspace_size reports (or, for strided / misaligned operands, the partial sums
+# plus room for the padded copies) the operand is repacked and the vector kernels run; with
+# only the partial-sum workspace the element-wise kernels read it in place.  Both match the
+# oracle; the products (alpha = 1, beta = 0) match each other bit for bit (same MFMA inputs
+# in the same K order), the alpha/beta epilogue to rounding (the two kernels' epilogues
+# contract alpha*acc + beta*c into different fused multiply-adds); no byte of the workspace
+# past the reported size is written.
+@pytest.mark.parametrize("M,N,K,case", [
+    (300, 4100, 520, "contig"), (640, 1000, 1004, "contig"), (70, 129, 513, "contig"),
+    (1, 4100, 4096, "contig"), (13, 1027, 300, "contig"), (257, 3001, 64, "contig"),
+    (96, 256, 320, "a_off"), (200, 136, 256, "b_ld"), (5, 640, 1024, "both")])
+def test_ragged_repack_matches_inplace(wo, M, N, K, case):
+    report("ragged_repack", M=M, N=N, K=K, case=case, plan=wo.gemm_plan(M, N, K))
+    lib = _capi()
+    A, B = _inputs(M, N, K, 5 * M + N + K, bstd=0.05)
+    Cin = torch.randn(M, N, generator=torch.Generator().manual_seed(M + K))
+    ref = og.gemm_ref(A, B, 1.5, -0.5, Cin)
+    plan_ws = wo.gemm_plan(M, N, K)[7]
+    if case in ("a_off", "both"):   # A one element off 16-byte alignment, lda = K + 3
+        Abuf = torch.zeros(M * (K + 3) + 1, dtype=torch.half)
+        Abuf[1:].view(M, K + 3)[:, :K] = A
+        Ad, a_ptr, lda = Abuf.cuda(), None, K + 3
+        a_ptr = Ad.data_ptr() + 2
+    else:
+        Ad = A.cuda()
+        a_ptr, lda = Ad.data_ptr(), K
+    if case in ("b_ld", "both"):    # B rows at an odd stride
+        Bbuf = torch.zeros(K, N + 5, dtype=torch.half)
+        Bbuf[:, :N] = B
+        Bd, ldb = Bbuf.cuda(), N + 5
+    else:
+        Bd, ldb = B.cuda(), N
+    a_bad = K % 8 != 0 or lda % 8 != 0 or case in ("a_off", "both")
+    b_bad = N % 8 != 0 or ldb % 8 != 0
+    need = plan_ws + _repack_bytes(M, N, K, a_bad, b_bad)
+    assert need > plan_ws
+    if case == "contig":
+        assert lib.wmma_gemm_workspace_size(M, N, K, -1) == need
+    stream = torch.cuda.current_stream().cuda_stream
+    prods, outs = [], []
+    for wsb in (need, plan_ws):
+        ws = torch.full((need + 4096,), 0xA5, dtype=torch.uint8, device="cuda")
+        wsp = ws.data_ptr() if wsb else None
+        P = torch.full((M, N), float("nan"), device="cuda")
+        rc = lib.wmma_gemm_f16f32(a_ptr, lda, Bd.data_ptr(), ldb, None, N, P.data_ptr(), N,
+                                  M, N, K, 1.0, 0.0, -1, wsp, wsb, stream)
+        assert rc == 0
+        Ci = Cin.cuda()
+        rc = lib.wmma_gemm_f16f32(a_ptr, lda, Bd.data_ptr(), ldb, Ci.data_ptr(), N, Ci.data_ptr(), N,
+                                  M, N, K, 1.5, -0.5, -1, wsp, wsb, stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert torch.all(ws[need:] == 0xA5), "workspace written past the reported size"
+        _check(P.cpu(), og.gemm_ref(A, B))
+        _check(Ci.cpu(), ref)
+        prods.append(P.cpu())
+        outs.append(Ci.cpu())
+    assert torch.equal(prods[0], prods[1])
+    assert og.max_rel_err(outs[0], outs[1]) <= 1e-6
 
 
 def test_empty_and_zero_k(wo):

@@ -58,6 +58,17 @@ int current_cus() {
 // 0x80000000 and above mark masked lanes).
 constexpr int64_t kMaxOffset = 0x7fffffffLL;
 
+size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Workspace bytes, behind the split-K partial sums, for zero-padded dense copies of the
+// operands whose rows break 16-byte vectors: A [M][K8] when `a`, B [K][N8] when `b` (K8, N8
+// rounded up to 8), each copy 256-byte aligned (256 bytes of slack align the first).
+size_t repack_bytes(int M, int N, int K, bool a, bool b) {
+    if ((!a && !b) || M <= 0 || N <= 0 || K <= 0) return 0;
+    const size_t K8 = ((size_t)K + 7) & ~(size_t)7, N8 = ((size_t)N + 7) & ~(size_t)7;
+    return 256 + (a ? round256((size_t)M * K8 * 2) : 0) + (b ? round256((size_t)K * N8 * 2) : 0);
+}
+
 }  // namespace
 
 // Scratch of the allocation-free GEMM entry point (wmma_gemm_f16f32_noalloc): the split-K
@@ -122,7 +133,9 @@ int wmma_gemm_plan_make(int M, int N, int K, int tile_cfg, int num_cus, wmma_gem
 size_t wmma_gemm_workspace_size(int M, int N, int K, int tile_cfg) {
     wmma_gemm_plan p{};
     if (make_plan(M, N, K, tile_cfg, current_cus(), &p) != WMMA_OK) return 0;
-    return p.workspace_bytes;
+    // Contiguous operands (lda = K, ldb = N, 16-byte aligned) break 16-byte rows exactly
+    // when K or N is not a multiple of 8.
+    return p.workspace_bytes + repack_bytes(M, N, K, K % 8 != 0, N % 8 != 0);
 }
 
 // Shared checks and launch of wmma_gemm_f16f32 / wmma_gemm_f16f32_plan /
@@ -149,9 +162,10 @@ static int gemm_run(const void* A, int64_t lda, const void* B, int64_t ldb, cons
         if (!A || !B) return fail(WMMA_ERR_INVALID_ARG, "A or B is NULL");
         if (lda < K) return fail(WMMA_ERR_INVALID_ARG, "lda (%lld) < K (%d)", (long long)lda, K);
         if (ldb < N) return fail(WMMA_ERR_INVALID_ARG, "ldb (%lld) < N (%d)", (long long)ldb, N);
-        // 32-bit buffer offsets: one 256-row A tile and one 64-row B stage must fit.
-        if ((256 + 1) * lda * 2 > kMaxOffset || (64 + 1) * ldb * 2 > kMaxOffset ||
-            (int64_t)kSkinnyMaxM * lda * 2 > kMaxOffset)
+        // 32-bit buffer offsets: one 256-row A tile and one 64-row B stage must fit (also
+        // with the leading dimensions of repacked copies, at most 7 elements longer).
+        if ((256 + 1) * (lda + 7) * 2 > kMaxOffset || (64 + 1) * (ldb + 7) * 2 > kMaxOffset ||
+            (int64_t)kSkinnyMaxM * (lda + 7) * 2 > kMaxOffset)
             return fail(WMMA_ERR_UNSUPPORTED, "leading dimension too large for 32-bit offsets");
     }
     wmma_gemm_plan plan{};
@@ -187,6 +201,37 @@ static int gemm_run(const void* A, int64_t lda, const void* B, int64_t ldb, cons
         if ((reinterpret_cast<uintptr_t>(workspace) & 3u) != 0)
             return fail(WMMA_ERR_MISALIGNED, "workspace must be 4-byte aligned");
     }
+    // An operand whose rows break 16-byte vectors (K or N not a multiple of 8, a leading
+    // dimension that is not, or an address off 16 bytes) is copied into a zero-padded dense
+    // buffer behind the partial sums when the workspace holds it, and the vector kernels
+    // run on the copy; without that room (or from the allocation-free entry point) the
+    // element-wise kernels read it in place.  The padding is zero and every kernel masks
+    // rows and columns at M, N and K, so the result is the same either way.
+    const bool a_vec = K % 8 == 0 && lda % 8 == 0 && aligned16(A);
+    const bool b_vec = N % 8 == 0 && ldb % 8 == 0 && aligned16(B);
+    bool vec = K > 0 && a_vec && b_vec;
+    if (K > 0 && !vec && !use_scratch && workspace &&
+        workspace_bytes >= plan.workspace_bytes + repack_bytes(M, N, K, !a_vec, !b_vec)) {
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        unsigned char* dst = reinterpret_cast<unsigned char*>(
+            round256(reinterpret_cast<uintptr_t>(workspace) + plan.workspace_bytes));
+        if (!a_vec) {
+            const int64_t K8 = ((int64_t)K + 7) & ~(int64_t)7;
+            if (int rc = hip_status(launch_gemm_repack(A, lda, M, K, dst, st), "gemm repack A"))
+                return rc;
+            A = dst;
+            lda = K8;
+            dst += round256((size_t)M * (size_t)K8 * 2);
+        }
+        if (!b_vec) {
+            const int64_t N8 = ((int64_t)N + 7) & ~(int64_t)7;
+            if (int rc = hip_status(launch_gemm_repack(B, ldb, K, N, dst, st), "gemm repack B"))
+                return rc;
+            B = dst;
+            ldb = N8;
+        }
+        vec = true;
+    }
     GemmLaunch g{};
     g.A = A;
     g.B = B;
@@ -202,8 +247,7 @@ static int gemm_run(const void* A, int64_t lda, const void* B, int64_t ldb, cons
     g.K = K;
     g.alpha = alpha;
     g.beta = beta;
-    g.vec = K > 0 && (K % 8 == 0) && (N % 8 == 0) && (lda % 8 == 0) && (ldb % 8 == 0) &&
-            aligned16(A) && aligned16(B);
+    g.vec = vec;
     g.plan = plan;
     return hip_status(launch_gemm(g, static_cast<hipStream_t>(stream)), "gemm launch");
 }

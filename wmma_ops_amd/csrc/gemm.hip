@@ -791,6 +791,49 @@ splitk_reduce_kernel(const float* ws, int split, const float* Cin, int64_t ldcin
     }
 }
 
+// ------------------------------------------------------------------------------------
+// Operand repack for rows that break 16-byte vectors: a [rows][cols] fp16 matrix with
+// leading dimension ld (any alignment) becomes a dense [rows][cols_p] copy, cols_p = cols
+// rounded up to 8, whose columns cols..cols_p-1 are zero.  One wave per row, one output
+// dword (two fp16) per lane and step; a row whose start is 4-byte aligned is read a dword
+// at a time, any other row in 16-bit halves.  Both sides are contiguous across the lanes
+// of a wave.
+// ------------------------------------------------------------------------------------
+constexpr int RP_WAVES = 4;  // rows per workgroup
+constexpr int RP_STEPS = 4;  // dwords per lane and row (a workgroup covers 256 of a row)
+
+__global__ void __launch_bounds__(RP_WAVES * kWave)
+gemm_repack_kernel(const f16* src, int64_t ld, int rows, int cols, uint32_t* dst) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int dw_row = ((cols + 7) & ~7) >> 1;
+    const int w0 = blockIdx.x * (kWave * RP_STEPS) + lane;
+    for (int r = blockIdx.y * RP_WAVES + wave; r < rows; r += gridDim.y * RP_WAVES) {
+        const f16* s = src + (int64_t)r * ld;
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(s);
+        const bool al4 = (reinterpret_cast<uintptr_t>(s) & 3u) == 0;
+        uint32_t v[RP_STEPS];
+#pragma unroll
+        for (int u = 0; u < RP_STEPS; ++u) {
+            const int c = 2 * (w0 + u * kWave);  // first column of this dword
+            if (al4) {
+                v[u] = buf_load4(rs, c + 1 < cols ? (uint32_t)c * 2 : kOobOffset);
+                if (c + 1 == cols) v[u] = buf_load2(rs, (uint32_t)c * 2);  // odd cols: last one
+            } else {
+                const uint32_t lo = buf_load2(rs, c < cols ? (uint32_t)c * 2 : kOobOffset);
+                const uint32_t hi = buf_load2(rs, c + 1 < cols ? (uint32_t)(c + 1) * 2 : kOobOffset);
+                v[u] = lo | (hi << 16);
+            }
+        }
+        uint32_t* d = dst + (int64_t)r * dw_row;
+#pragma unroll
+        for (int u = 0; u < RP_STEPS; ++u) {
+            const int w = w0 + u * kWave;
+            if (w < dw_row) d[w] = v[u];
+        }
+    }
+}
+
 template <int CFG, bool VEC>
 void launch_tiled(const GemmArgs& a, hipStream_t stream) {
     constexpr TileShape t = kTiles[CFG];
@@ -840,6 +883,16 @@ void launch_mfma_cfg(int cfg, const GemmArgs& a, hipStream_t stream) {
 }
 
 }  // namespace
+
+hipError_t launch_gemm_repack(const void* src, int64_t ld, int rows, int cols, void* dst,
+                              hipStream_t stream) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    const int dw_row = ((cols + 7) & ~7) >> 1;
+    const dim3 grid(ceil_div(dw_row, kWave * RP_STEPS), std::min(ceil_div(rows, RP_WAVES), 65535));
+    hipLaunchKernelGGL(gemm_repack_kernel, grid, dim3(RP_WAVES * kWave), 0, stream,
+                       static_cast<const f16*>(src), ld, rows, cols, static_cast<uint32_t*>(dst));
+    return hipGetLastError();
+}
 
 hipError_t launch_gemm(const GemmLaunch& g, hipStream_t stream) {
     const wmma_gemm_plan& pl = g.plan;

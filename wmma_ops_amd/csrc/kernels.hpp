@@ -23,6 +23,10 @@ struct GemmLaunch {
     wmma_gemm_plan plan;
 };
 hipError_t launch_gemm(const GemmLaunch& g, hipStream_t stream);
+// Dense zero-padded copy of a [rows][cols] fp16 matrix (leading dimension ld, any
+// alignment) into dst [rows][cols rounded up to 8]; dst 4-byte aligned.
+hipError_t launch_gemm_repack(const void* src, int64_t ld, int rows, int cols, void* dst,
+                              hipStream_t stream);
 
 // INT4 weight layout conversions (w4a16.hip).
 hipError_t launch_int4_prepack(const int32_t* qweight, int K, int N, int32_t* packed,
