@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define WMMA_OPS_AMD_ABI_VERSION 1
+#define WMMA_OPS_AMD_ABI_VERSION 2
 
 /* Status codes. */
 #define WMMA_OK 0
@@ -49,6 +49,15 @@ extern "C" {
 #define WMMA_KERNEL_TILED 0   /* MFMA tiled kernel (optionally split-K + reduce)        */
 #define WMMA_KERNEL_SKINNY 1  /* M <= 16 streaming kernel, split-K + reduce             */
 
+/* Two-part GEMMs (wmma_gemm_plan.edge_dim).  A shape whose 256x256 tiles fill some whole
+ * waves of the chip plus a small partial one can run as two launches: the bulk (rows or
+ * columns [0, edge_at)) on whole waves of 256x256 tiles, then the edge (the rest) as a
+ * GEMM of its own, with the plan wmma_gemm_plan_make gives for that shape (always a
+ * one-launch plan). */
+#define WMMA_EDGE_NONE 0  /* one launch                                                  */
+#define WMMA_EDGE_ROWS 1  /* rows [edge_at, M) run as the second GEMM                    */
+#define WMMA_EDGE_COLS 2  /* columns [edge_at, N) run as the second GEMM                 */
+
 typedef struct wmma_gemm_plan {
     int kernel;            /* WMMA_KERNEL_*                                              */
     int tile_cfg;          /* WMMA_TILE_* actually used (-1 for the skinny kernel)       */
@@ -56,7 +65,10 @@ typedef struct wmma_gemm_plan {
     int split_k;           /* number of K partitions (1 = no split, no workspace)        */
     int k_per_split;       /* K elements per partition (multiple of 64)                  */
     int grid;              /* workgroups of the main kernel                              */
-    size_t workspace_bytes;/* fp32 partial sums: split_k * M * N * 4, 0 when split_k==1  */
+    size_t workspace_bytes;/* fp32 partial sums: split_k * M * N * 4, 0 when split_k==1;
+                              for a two-part plan the larger of the two parts' needs      */
+    int edge_dim;          /* WMMA_EDGE_*; the fields above then describe the bulk launch */
+    int edge_at;           /* first row / column of the edge GEMM (0 without one)        */
 } wmma_gemm_plan;
 
 /* Text of the last error reported on this thread ("" if none). */
@@ -70,7 +82,8 @@ int wmma_abi_version(void);
 int wmma_device_cu_count(int device);
 
 /* Host-only planner: the kernel, tile, split-K and workspace a GEMM of this shape uses
- * on a device with `num_cus` compute units.  tile_cfg as for wmma_gemm_f16f32.
+ * on a device with `num_cus` compute units, and whether it runs as two parts (edge_dim;
+ * only with tile_cfg WMMA_TILE_AUTO).  tile_cfg as for wmma_gemm_f16f32.
  * Replaces the reference's select_optimal_tile (wmma_tile_selection.hpp:30-66) and
  * split_k::compute_config (wmma_xor_swizzle.hpp:293-332). */
 int wmma_gemm_plan_make(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* out);

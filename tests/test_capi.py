@@ -24,7 +24,8 @@ OK, INVALID, UNSUPPORTED, MISALIGNED, WORKSPACE = 0, 1, 2, 3, 4
 class Plan(ctypes.Structure):
     _fields_ = [("kernel", ctypes.c_int), ("tile_cfg", ctypes.c_int), ("tile_m", ctypes.c_int),
                 ("tile_n", ctypes.c_int), ("split_k", ctypes.c_int), ("k_per_split", ctypes.c_int),
-                ("grid", ctypes.c_int), ("workspace_bytes", ctypes.c_size_t)]
+                ("grid", ctypes.c_int), ("workspace_bytes", ctypes.c_size_t),
+                ("edge_dim", ctypes.c_int), ("edge_at", ctypes.c_int)]
 
 
 @pytest.fixture(scope="module")
@@ -78,7 +79,8 @@ def test_header_declares_expected_entry_points():
 def test_library_exports_every_declared_symbol(lib):
     missing = [n for n in declared_functions() if not hasattr(lib, n)]
     assert not missing, missing
-    assert lib.wmma_abi_version() == 1
+    assert lib.wmma_abi_version() == 2
+    assert ctypes.sizeof(Plan) == 48   # the C struct: 7 ints, size_t, 2 ints
 
 
 def test_calibration_library_exports_its_header():
@@ -167,19 +169,59 @@ class W4Plan(ctypes.Structure):
 def test_gemm_workspace_size_covers_repacked_operands(lib):
     # Contiguous operands: K or N off a multiple of 8 adds a zero-padded copy of A [M][K8]
     # and/or B [K][N8] (256-byte rounded, plus 256 bytes of alignment slack) to the split-K
-    # partial sums; aligned shapes need only the partial sums.
+    # partial sums -- except B under the skinny kernel (M <= 16), which reads it in place;
+    # aligned shapes need only the partial sums.
     r256 = lambda x: (x + 255) // 256 * 256
     p = Plan()
     for M, N, K in [(4096, 4100, 4096), (4096, 4096, 4100), (4095, 4101, 4099), (1, 4100, 4096),
-                    (13, 1027, 300), (1, 1, 1), (4096, 4096, 4096), (1, 4096, 4096)]:
+                    (13, 1027, 300), (1, 1, 1), (4096, 4096, 4096), (1, 4096, 4096),
+                    (17, 4100, 4096)]:
         assert lib.wmma_gemm_plan_make(M, N, K, -1, 256, ctypes.byref(p)) == OK
         K8, N8 = (K + 7) // 8 * 8, (N + 7) // 8 * 8
         extra = 0
-        if K % 8 or N % 8:
-            extra = 256 + (r256(M * K8 * 2) if K % 8 else 0) + (r256(K * N8 * 2) if N % 8 else 0)
+        b_copy = N % 8 != 0 and p.kernel != 1
+        if K % 8 or b_copy:
+            extra = 256 + (r256(M * K8 * 2) if K % 8 else 0) + (r256(K * N8 * 2) if b_copy else 0)
         assert lib.wmma_gemm_workspace_size(M, N, K, -1) == p.workspace_bytes + extra, (M, N, K)
     assert lib.wmma_gemm_workspace_size(0, 4100, 4096, -1) == 0
     assert lib.wmma_gemm_workspace_size(16, 4100, 0, -1) == 0
+
+
+# Bulk + edge plans, pinned to decisions measured on MI355X (each two-part plan below ran
+# 7-31% faster than the planner's previous one-launch plan; the one-launch shapes either
+# fill whole waves or gained nothing from a split).
+TWO_PART = {(4100, 4096, 4096): (1, 4096), (4352, 4096, 4096): (1, 4096),
+            (5000, 4096, 4096): (1, 4096), (6000, 4096, 4096): (1, 4096),
+            (4096, 4104, 4096): (2, 4096), (4096, 5000, 4096): (2, 4096),
+            (9192, 4096, 4096): (1, 8192), (2560, 14336, 4096): (1, 2304),
+            (4096, 14336, 4096): (2, 12288), (4100, 4096, 1024): (1, 4096)}
+ONE_LAUNCH = [(7000, 4096, 4096), (3000, 4096, 4096), (2100, 4096, 4096), (4100, 14336, 4096),
+              (512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096),
+              (4096, 4096, 2048), (8192, 8192, 4096), (1, 4100, 4096), (128, 4100, 4096)]
+
+
+def test_plan_two_part_decisions(lib):
+    p, e = Plan(), Plan()
+    for (M, N, K), (dim, at) in TWO_PART.items():
+        assert lib.wmma_gemm_plan_make(M, N, K, -1, 256, ctypes.byref(p)) == OK
+        assert (p.edge_dim, p.edge_at) == (dim, at), (M, N, K)
+        # the bulk: 256x256 tiles, no split, the whole tile rows (columns) that fit in the
+        # whole waves of the 256 CUs
+        assert (p.kernel, p.tile_cfg, p.split_k) == (0, 5, 1)
+        tm, tn = -(-M // 256), -(-N // 256)
+        whole = tm * tn // 256 * 256
+        across = tn if dim == 1 else tm
+        assert at % 256 == 0 and p.grid == (at // 256) * across
+        assert whole - across < p.grid <= whole
+        # the edge: the planner's own one-launch plan for the rest
+        em, en = (M - at, N) if dim == 1 else (M, N - at)
+        assert lib.wmma_gemm_plan_make(em, en, K, -1, 256, ctypes.byref(e)) == OK
+        assert e.edge_dim == 0 and p.workspace_bytes == e.workspace_bytes
+        # an explicit tile never splits in two
+        assert lib.wmma_gemm_plan_make(M, N, K, 3, 256, ctypes.byref(p)) == OK and p.edge_dim == 0
+    for (M, N, K) in ONE_LAUNCH:
+        assert lib.wmma_gemm_plan_make(M, N, K, -1, 256, ctypes.byref(p)) == OK
+        assert (p.edge_dim, p.edge_at) == (0, 0), (M, N, K)
 
 
 def test_w4a16_plan_make(lib):
@@ -410,7 +452,7 @@ def test_torch_extension_reference_errors(wo):
 
 
 def test_torch_plan_binding(wo):
-    assert wo.gemm_plan(4096, 4096, 4096) == [0, 5, 256, 256, 1, 4096, 256, 0]
+    assert wo.gemm_plan(4096, 4096, 4096) == [0, 5, 256, 256, 1, 4096, 256, 0, 0, 0]
 
 
 def test_import_name_of_the_reference():

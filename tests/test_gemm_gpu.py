@@ -275,8 +275,8 @@ def _repack_bytes(M, N, K, a, b):
 # past the reported size is written.
 @pytest.mark.parametrize("M,N,K,case", [
     (300, 4100, 520, "contig"), (640, 1000, 1004, "contig"), (70, 129, 513, "contig"),
-    (1, 4100, 4096, "contig"), (13, 1027, 300, "contig"), (257, 3001, 64, "contig"),
-    (96, 256, 320, "a_off"), (200, 136, 256, "b_ld"), (5, 640, 1024, "both")])
+    (17, 4100, 4096, "contig"), (257, 3001, 64, "contig"),
+    (96, 256, 320, "a_off"), (200, 136, 256, "b_ld"), (40, 640, 1024, "both")])
 def test_ragged_repack_matches_inplace(wo, M, N, K, case):
     report("ragged_repack", M=M, N=N, K=K, case=case, plan=wo.gemm_plan(M, N, K))
     lib = _capi()
@@ -325,6 +325,108 @@ def test_ragged_repack_matches_inplace(wo, M, N, K, case):
         outs.append(Ci.cpu())
     assert torch.equal(prods[0], prods[1])
     assert og.max_rel_err(outs[0], outs[1]) <= 1e-6
+
+
+# The skinny kernel (M <= 16) reads a B whose rows break 16-byte vectors in place: with B
+# 4-byte aligned, rows are fetched by dword-aligned 16-byte loads (ldb even), or every other
+# row by a load from 2 bytes earlier plus one dword, realigned (ldb odd); the chunk that
+# straddles column N element-wise.  A with K off a multiple of 8 is repacked.  The same
+# operands with B moved 2 bytes off a dword and only the split-K workspace take the
+# element-wise kernel: the products match it bit for bit and the oracle to the 1e-3 bar.
+@pytest.mark.parametrize("M,N,K,ldb_pad", [
+    (1, 4100, 4096, 0), (16, 4100, 4096, 0), (1, 4101, 4096, 0), (7, 1027, 300, 0),
+    (3, 4096, 520, 3), (16, 32001, 256, 0), (1, 9, 64, 0), (2, 5, 16, 0), (9, 130, 1000, 1)])
+def test_skinny_unaligned_b_in_place(wo, M, N, K, ldb_pad):
+    plan = wo.gemm_plan(M, N, K)
+    report("skinny_unaligned_b", M=M, N=N, K=K, ldb=N + ldb_pad, plan=plan)
+    assert plan[0] == 1
+    lib = _capi()
+    A, B = _inputs(M, N, K, 3 * M + N + K, bstd=0.05)
+    Cin = torch.randn(M, N, generator=torch.Generator().manual_seed(N))
+    ldb = N + ldb_pad
+    Bbuf = torch.zeros(K * ldb + 8, dtype=torch.half)
+    Bbuf[:K * ldb].view(K, ldb)[:, :N] = B
+    Bbuf1 = torch.zeros(K * ldb + 8, dtype=torch.half)   # the same rows, 2 bytes later
+    Bbuf1[1:1 + K * ldb].view(K, ldb)[:, :N] = B
+    Ad, Bd, Bd1 = A.cuda(), Bbuf.cuda(), Bbuf1.cuda()
+    plan_ws = plan[7]
+    need = plan_ws + _repack_bytes(M, N, K, K % 8 != 0, False)
+    if ldb_pad == 0:
+        assert lib.wmma_gemm_workspace_size(M, N, K, -1) == need
+    stream = torch.cuda.current_stream().cuda_stream
+    prods = []
+    for b_ptr, wsb in ((Bd.data_ptr(), need), (Bd1.data_ptr() + 2, plan_ws)):
+        ws = torch.full((need + 4096,), 0xA5, dtype=torch.uint8, device="cuda")
+        wsp = ws.data_ptr() if wsb else None
+        P = torch.full((M, N), float("nan"), device="cuda")
+        rc = lib.wmma_gemm_f16f32(Ad.data_ptr(), K, b_ptr, ldb, None, N, P.data_ptr(), N,
+                                  M, N, K, 1.0, 0.0, -1, wsp, wsb, stream)
+        assert rc == 0
+        Ci = Cin.cuda()
+        rc = lib.wmma_gemm_f16f32(Ad.data_ptr(), K, b_ptr, ldb, Ci.data_ptr(), N, Ci.data_ptr(), N,
+                                  M, N, K, 1.5, -0.5, -1, wsp, wsb, stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert torch.all(ws[need:] == 0xA5), "workspace written past the reported size"
+        _check(P.cpu(), og.gemm_ref(A, B))
+        _check(Ci.cpu(), og.gemm_ref(A, B, 1.5, -0.5, Cin))
+        prods.append(P.cpu())
+    assert torch.equal(prods[0], prods[1])
+
+
+# Two-part plans (a bulk on whole waves of 256x256 tiles, then the edge rows or columns as
+# a GEMM of their own): the edge as a split-K skinny GEMM, a one-launch tile and a column
+# strip; with B repacked (N off a multiple of 8); through matmul, gemm out of place and in
+# place (bitwise equal), the C-ABI with row strides of C_in / C_out above N (padding left
+# alone) and wmma_gemm_f16f32_plan with the planner's own two-part plan (bitwise equal).
+@pytest.mark.parametrize("M,N,K,dim", [(4100, 4096, 512, 1), (4103, 4096, 520, 1),
+                                       (4352, 4096, 256, 1), (8200, 2048, 512, 1),
+                                       (4100, 4100, 1000, 1), (4096, 4101, 1024, 2),
+                                       (4096, 4200, 1024, 2)])
+def test_two_part_plans(wo, M, N, K, dim):
+    import ctypes
+    from wmma_ops_amd.autotune import Plan
+    plan = wo.gemm_plan(M, N, K)
+    report("two_part", M=M, N=N, K=K, plan=plan)
+    assert plan[8] == dim
+    A, B = _inputs(M, N, K, M + N + K, bstd=0.05)
+    Cin = torch.randn(M, N, generator=torch.Generator().manual_seed(11))
+    Ad, Bd, Cd = A.cuda(), B.cuda(), Cin.cuda()
+    Y = wo.matmul(Ad, Bd)
+    _check(Y.cpu(), og.gemm_ref(A, B))
+    ref = og.gemm_ref(A, B, 1.5, -0.5, Cin)
+    out = wo.gemm(Ad, Bd, 1.5, -0.5, Cd)
+    _check(out.cpu(), ref)
+    Ci = Cd.clone()
+    wo.gemm_inplace(Ad, Bd, Ci, 1.5, -0.5)
+    assert torch.equal(Ci, out)
+    lib = _capi()
+    stream = torch.cuda.current_stream().cuda_stream
+    need = lib.wmma_gemm_workspace_size(M, N, K, -1)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+    ldcin, ldc = N + 40, N + 72
+    Cs = torch.full((M, ldcin), 3.0, device="cuda")
+    Cs[:, :N] = Cd
+    Co = torch.full((M, ldc), 7.0, device="cuda")
+    rc = lib.wmma_gemm_f16f32(Ad.data_ptr(), K, Bd.data_ptr(), N, Cs.data_ptr(), ldcin, Co.data_ptr(), ldc,
+                              M, N, K, 1.5, -0.5, -1, ws.data_ptr(), need, stream)
+    assert rc == 0
+    assert torch.equal(Co[:, :N], out)
+    assert torch.all(Co[:, N:] == 7.0) and torch.all(Cs[:, N:] == 3.0)
+    p = Plan()
+    lib.wmma_gemm_plan_make.argtypes = [ctypes.c_int] * 5 + [ctypes.POINTER(Plan)]
+    assert lib.wmma_gemm_plan_make(M, N, K, -1, 256, ctypes.byref(p)) == 0 and p.edge_dim == dim
+    vp, i64, i32, f32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    lib.wmma_gemm_f16f32_plan.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, f32, f32,
+                                          ctypes.POINTER(Plan), vp, sz, vp]
+    Yp = torch.empty(M, N, device="cuda")
+    rc = lib.wmma_gemm_f16f32_plan(Ad.data_ptr(), K, Bd.data_ptr(), N, None, N, Yp.data_ptr(), N, M, N, K,
+                                   1.0, 0.0, ctypes.byref(p), ws.data_ptr(), need, stream)
+    assert rc == 0
+    assert torch.equal(Yp, Y)
+    p.edge_at += 256   # an edited two-part plan is rejected, not launched
+    assert lib.wmma_gemm_f16f32_plan(Ad.data_ptr(), K, Bd.data_ptr(), N, None, N, Yp.data_ptr(), N, M, N, K,
+                                     1.0, 0.0, ctypes.byref(p), ws.data_ptr(), need, stream) == 1
 
 
 def test_empty_and_zero_k(wo):

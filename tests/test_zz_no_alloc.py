@@ -35,11 +35,13 @@ def _lib():
 
 # (first, second): the second call is smaller.  Plans: tiled 128x128 split 2 (14 MiB of
 # partial sums) then skinny split 8; the tuned tiled split 8 (16 MiB) then skinny split 8;
-# tiled 64x64 split 4 then a ragged skinny split; a shape without a split (no scratch).
+# tiled 64x64 split 4 then a ragged skinny split; a shape without a split (no scratch); a
+# two-part plan whose edge is a skinny split 4 then a tiled split 4.
 PAIRS = [((128, 14336, 4096), (16, 4096, 4096)),
          ((128, 4096, 14336), (1, 4096, 4096)),
          ((64, 4096, 4096), (3, 1024, 520)),
-         ((1024, 1024, 1024), (300, 264, 640))]
+         ((1024, 1024, 1024), (300, 264, 640)),
+         ((4100, 4096, 1024), (64, 4096, 4096))]
 
 
 @pytest.mark.parametrize("first,second", PAIRS)

@@ -39,7 +39,8 @@ ROTATE_BYTES = 600e6
 class Plan(ctypes.Structure):
     _fields_ = [("kernel", ctypes.c_int), ("tile_cfg", ctypes.c_int), ("tile_m", ctypes.c_int),
                 ("tile_n", ctypes.c_int), ("split_k", ctypes.c_int), ("k_per_split", ctypes.c_int),
-                ("grid", ctypes.c_int), ("workspace_bytes", ctypes.c_size_t)]
+                ("grid", ctypes.c_int), ("workspace_bytes", ctypes.c_size_t),
+                ("edge_dim", ctypes.c_int), ("edge_at", ctypes.c_int)]
 
 
 def load_lib(path: str = LIB_PATH):

@@ -134,8 +134,9 @@ size_t wmma_gemm_workspace_size(int M, int N, int K, int tile_cfg) {
     wmma_gemm_plan p{};
     if (make_plan(M, N, K, tile_cfg, current_cus(), &p) != WMMA_OK) return 0;
     // Contiguous operands (lda = K, ldb = N, 16-byte aligned) break 16-byte rows exactly
-    // when K or N is not a multiple of 8.
-    return p.workspace_bytes + repack_bytes(M, N, K, K % 8 != 0, N % 8 != 0);
+    // when K or N is not a multiple of 8; the skinny kernel reads such a B in place.
+    return p.workspace_bytes +
+           repack_bytes(M, N, K, K % 8 != 0, N % 8 != 0 && p.kernel != WMMA_KERNEL_SKINNY);
 }
 
 // Shared checks and launch of wmma_gemm_f16f32 / wmma_gemm_f16f32_plan /
@@ -171,11 +172,18 @@ static int gemm_run(const void* A, int64_t lda, const void* B, int64_t ldb, cons
     wmma_gemm_plan plan{};
     if (explicit_plan) {
         // Rebuild the plan from its choices for this shape: a plan made for another shape,
-        // or edited by hand, is rejected rather than launched.
-        int rc = make_custom_plan(M, N, K, explicit_plan->kernel, explicit_plan->tile_cfg,
-                                  explicit_plan->split_k, &plan);
-        if (rc != WMMA_OK || plan.k_per_split != explicit_plan->k_per_split ||
-            plan.split_k != explicit_plan->split_k || plan.workspace_bytes != explicit_plan->workspace_bytes)
+        // or edited by hand, is rejected rather than launched.  A two-part plan is the
+        // planner's own for this shape or nothing.
+        int rc = explicit_plan->edge_dim != WMMA_EDGE_NONE
+                     ? make_plan(M, N, K, WMMA_TILE_AUTO, current_cus(), &plan)
+                     : make_custom_plan(M, N, K, explicit_plan->kernel, explicit_plan->tile_cfg,
+                                        explicit_plan->split_k, &plan);
+        if (rc != WMMA_OK || plan.kernel != explicit_plan->kernel ||
+            plan.k_per_split != explicit_plan->k_per_split ||
+            plan.split_k != explicit_plan->split_k ||
+            plan.workspace_bytes != explicit_plan->workspace_bytes ||
+            plan.edge_dim != explicit_plan->edge_dim || plan.edge_at != explicit_plan->edge_at ||
+            (plan.kernel == WMMA_KERNEL_TILED && plan.tile_cfg != explicit_plan->tile_cfg))
             return fail(WMMA_ERR_INVALID_ARG, "plan does not describe this shape (make it with "
                                               "wmma_gemm_plan_custom or wmma_gemm_plan_make)");
     } else {
@@ -205,13 +213,17 @@ static int gemm_run(const void* A, int64_t lda, const void* B, int64_t ldb, cons
     // dimension that is not, or an address off 16 bytes) is copied into a zero-padded dense
     // buffer behind the partial sums when the workspace holds it, and the vector kernels
     // run on the copy; without that room (or from the allocation-free entry point) the
-    // element-wise kernels read it in place.  The padding is zero and every kernel masks
-    // rows and columns at M, N and K, so the result is the same either way.
-    const bool a_vec = K % 8 == 0 && lda % 8 == 0 && aligned16(A);
-    const bool b_vec = N % 8 == 0 && ldb % 8 == 0 && aligned16(B);
-    bool vec = K > 0 && a_vec && b_vec;
-    if (K > 0 && !vec && !use_scratch && workspace &&
-        workspace_bytes >= plan.workspace_bytes + repack_bytes(M, N, K, !a_vec, !b_vec)) {
+    // element-wise kernels read it in place.  The skinny kernel streams B once, so there a
+    // 4-byte-aligned B is read in place by dword-aligned 16-byte loads instead (a copy
+    // would triple its traffic).  The padding is zero and every kernel masks rows and
+    // columns at M, N and K, so the result is the same either way.
+    bool a_vec = K % 8 == 0 && lda % 8 == 0 && aligned16(A);
+    bool b_vec = N % 8 == 0 && ldb % 8 == 0 && aligned16(B);
+    const bool skinny = plan.kernel == WMMA_KERNEL_SKINNY;
+    const bool b_al4 = (reinterpret_cast<uintptr_t>(B) & 3u) == 0;
+    const bool b_copy = !b_vec && !(skinny && b_al4);
+    if (K > 0 && (!a_vec || b_copy) && !use_scratch && workspace &&
+        workspace_bytes >= plan.workspace_bytes + repack_bytes(M, N, K, !a_vec, b_copy)) {
         const hipStream_t st = static_cast<hipStream_t>(stream);
         unsigned char* dst = reinterpret_cast<unsigned char*>(
             round256(reinterpret_cast<uintptr_t>(workspace) + plan.workspace_bytes));
@@ -221,35 +233,57 @@ static int gemm_run(const void* A, int64_t lda, const void* B, int64_t ldb, cons
                 return rc;
             A = dst;
             lda = K8;
+            a_vec = true;
             dst += round256((size_t)M * (size_t)K8 * 2);
         }
-        if (!b_vec) {
+        if (b_copy) {
             const int64_t N8 = ((int64_t)N + 7) & ~(int64_t)7;
             if (int rc = hip_status(launch_gemm_repack(B, ldb, K, N, dst, st), "gemm repack B"))
                 return rc;
             B = dst;
             ldb = N8;
+            b_vec = true;
         }
-        vec = true;
     }
-    GemmLaunch g{};
-    g.A = A;
-    g.B = B;
-    g.C_in = use_c ? C_in : nullptr;
-    g.C_out = C_out;
-    g.workspace = workspace;
-    g.lda = lda;
-    g.ldb = ldb;
-    g.ldc_in = ldc_in;
-    g.ldc = ldc;
-    g.M = M;
-    g.N = N;
-    g.K = K;
-    g.alpha = alpha;
-    g.beta = beta;
-    g.vec = vec;
-    g.plan = plan;
-    return hip_status(launch_gemm(g, static_cast<hipStream_t>(stream)), "gemm launch");
+    const bool vec = K > 0 && a_vec && b_vec;
+    // One launch of plan `pl` on the sub-GEMM whose output starts at row r0, column c0.
+    auto launch_part = [&](const wmma_gemm_plan& pl, int r0, int c0, int Mp, int Np) {
+        GemmLaunch g{};
+        g.A = static_cast<const uint16_t*>(A) + (int64_t)r0 * lda;
+        g.B = static_cast<const uint16_t*>(B) + c0;
+        g.C_in = use_c ? C_in + (int64_t)r0 * ldc_in + c0 : nullptr;
+        g.C_out = C_out + (int64_t)r0 * ldc + c0;
+        g.workspace = workspace;
+        g.lda = lda;
+        g.ldb = ldb;
+        g.ldc_in = ldc_in;
+        g.ldc = ldc;
+        g.M = Mp;
+        g.N = Np;
+        g.K = K;
+        g.alpha = alpha;
+        g.beta = beta;
+        g.vec = vec;
+        g.skinny_b = pl.kernel == WMMA_KERNEL_SKINNY && !vec && K > 0 && a_vec && b_al4
+                         ? (ldb % 2 == 0 ? 2 : 3)
+                         : 0;
+        g.plan = pl;
+        return hip_status(launch_gemm(g, static_cast<hipStream_t>(stream)), "gemm launch");
+    };
+    if (plan.edge_dim == WMMA_EDGE_NONE) return launch_part(plan, 0, 0, M, N);
+    // Two parts, one after the other on the stream (the edge's split-K partial sums reuse
+    // the workspace): the bulk on whole waves of 256x256 tiles, then the edge with the plan
+    // the planner gives its own shape.  Column offsets keep 16-byte alignment (edge_at is a
+    // multiple of 256) and 4-byte alignment of B for the skinny kernel.
+    const bool rows = plan.edge_dim == WMMA_EDGE_ROWS;
+    const int at = plan.edge_at;
+    wmma_gemm_plan edge{};
+    if (make_plan(rows ? M - at : M, rows ? N : N - at, K, WMMA_TILE_AUTO, current_cus(), &edge) !=
+            WMMA_OK ||
+        edge.edge_dim != WMMA_EDGE_NONE || edge.workspace_bytes > plan.workspace_bytes)
+        return fail(WMMA_ERR_INVALID_ARG, "inconsistent two-part plan");
+    if (int rc = launch_part(plan, 0, 0, rows ? at : M, rows ? N : at)) return rc;
+    return rows ? launch_part(edge, at, 0, M - at, N) : launch_part(edge, 0, at, M, N - at);
 }
 
 int wmma_gemm_f16f32(const void* A, int64_t lda, const void* B, int64_t ldb, const float* C_in,

@@ -616,7 +616,19 @@ gemm_tiled_kernel(GemmArgs p) {
 constexpr int SK_COLS = kSkinnyBlockN;
 constexpr int SK_WAVES = 4;
 
-template <bool VEC>
+// B row modes of the skinny kernel.  In every mode but SKB_ELEM, A is read in 16-byte
+// vectors (K, lda multiples of 8, A 16-byte aligned).
+enum SkinnyB {
+    SKB_ELEM = 0,   // A and B element-wise (any alignment)
+    SKB_VEC = 1,    // B rows 16-byte aligned: one 16-byte load per row chunk
+    SKB_AL4 = 2,    // B 4-byte aligned, ldb even: every row 4-byte aligned.  A 16-byte load
+                    // at a 4-byte-aligned address is a legal dword-aligned access.
+    SKB_AL4_ODD = 3 // B 4-byte aligned, ldb odd: rows k0+r with r even are 4-byte aligned
+                    // (k0 is even), odd ones start 2 bytes past a dword: a 16-byte load from
+                    // 2 bytes earlier plus the next dword, shifted together by v_alignbyte.
+};
+
+template <int BMODE>
 __global__ void __launch_bounds__(SK_WAVES * kWave)
 gemm_skinny_kernel(GemmArgs p) {
     // Partial sums, row m = lane%16 of each wave, column n at n ^ ((n >> 2) & 16) of a row
@@ -644,11 +656,13 @@ gemm_skinny_kernel(GemmArgs p) {
     const bool m_ok = c16 < M;
     const int ncol = n0 + 8 * c16;
 
-    if constexpr (VEC) {
+    if constexpr (BMODE != SKB_ELEM) {
         // Straight-line double buffering: slab i+1's loads are in flight while slab i is
         // transposed and multiplied.  Every load is unconditional -- rows past kend and
         // columns past N come back as zeros through the buffer range check -- so each
-        // wait covers exactly the slab it needs; slabs past the end are all zeros.
+        // wait covers exactly the slab it needs; slabs past the end are all zeros.  In the
+        // 4-byte modes the chunk that straddles column N (N not a multiple of 8) is read
+        // element-wise by the lanes that own it.
         struct Slab {
             u32x4 b[8];
             u32x4 a;
@@ -661,9 +675,36 @@ gemm_skinny_kernel(GemmArgs p) {
             const __amdgpu_buffer_rsrc_t b_rs = make_rsrc(p.B + (int64_t)k0 * p.ldb + n0);
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
-                const bool ok = (ka + r < kend) && (ncol < N);
-                S.b[r] = buf_load16_nt(b_rs, ok ? (uint32_t)(((8 * q + r) * p.ldb + 8 * c16) * 2)
-                                                : kOobOffset);
+                const uint32_t off = (uint32_t)(((8 * q + r) * p.ldb + 8 * c16) * 2);
+                if constexpr (BMODE == SKB_VEC) {
+                    const bool ok = (ka + r < kend) && (ncol < N);
+                    S.b[r] = buf_load16_nt(b_rs, ok ? off : kOobOffset);
+                } else {
+                    const bool k_ok = ka + r < kend;
+                    const bool whole = k_ok && ncol + 8 <= N;
+                    if (BMODE == SKB_AL4 || (r & 1) == 0) {
+                        S.b[r] = buf_load16_nt(b_rs, whole ? off : kOobOffset);
+                    } else {
+                        // bytes [off-2, off+14) and [off+14, off+18): the dword at off+14
+                        // holds the chunk's last element, so it lies inside B
+                        const u32x4 x = buf_load16_nt(b_rs, whole ? off - 2 : kOobOffset);
+                        const uint32_t y = buf_load4(b_rs, whole ? off + 14 : kOobOffset);
+                        S.b[r] = u32x4{__builtin_amdgcn_alignbyte(x[1], x[0], 2),
+                                       __builtin_amdgcn_alignbyte(x[2], x[1], 2),
+                                       __builtin_amdgcn_alignbyte(x[3], x[2], 2),
+                                       __builtin_amdgcn_alignbyte(y, x[3], 2)};
+                    }
+                    if (k_ok && ncol < N && ncol + 8 > N) {
+                        u32x4 v4;
+#pragma unroll
+                        for (int e = 0; e < 8; e += 2) {
+                            const uint32_t lo = buf_load2(b_rs, ncol + e < N ? off + 2 * e : kOobOffset);
+                            const uint32_t hi = buf_load2(b_rs, ncol + e + 1 < N ? off + 2 * e + 2 : kOobOffset);
+                            v4[e >> 1] = lo | (hi << 16);
+                        }
+                        S.b[r] = v4;
+                    }
+                }
             }
             S.a = buf_load16(a_rs, (m_ok && ka < kend) ? (uint32_t)((c16 * p.lda + ka) * 2)
                                                        : kOobOffset);
@@ -918,10 +959,15 @@ hipError_t launch_gemm(const GemmLaunch& g, hipStream_t stream) {
 
     if (pl.kernel == WMMA_KERNEL_SKINNY) {
         dim3 grid(ceil_div(g.N, SK_COLS), pl.split_k);
-        if (g.vec)
-            hipLaunchKernelGGL(gemm_skinny_kernel<true>, grid, dim3(SK_WAVES * kWave), 0, stream, a);
-        else
-            hipLaunchKernelGGL(gemm_skinny_kernel<false>, grid, dim3(SK_WAVES * kWave), 0, stream, a);
+        const dim3 block(SK_WAVES * kWave);
+        switch (g.vec ? (int)SKB_VEC : g.skinny_b) {
+            case SKB_VEC: hipLaunchKernelGGL(gemm_skinny_kernel<SKB_VEC>, grid, block, 0, stream, a); break;
+            case SKB_AL4: hipLaunchKernelGGL(gemm_skinny_kernel<SKB_AL4>, grid, block, 0, stream, a); break;
+            case SKB_AL4_ODD:
+                hipLaunchKernelGGL(gemm_skinny_kernel<SKB_AL4_ODD>, grid, block, 0, stream, a);
+                break;
+            default: hipLaunchKernelGGL(gemm_skinny_kernel<SKB_ELEM>, grid, block, 0, stream, a); break;
+        }
     } else {
         if (g.vec)
             launch_mfma_cfg(pl.tile_cfg, a, stream);

@@ -20,6 +20,9 @@ struct GemmLaunch {
     int M, N, K;
     float alpha, beta;
     bool vec;  // 16-byte vector path: K, N, lda, ldb multiples of 8, A and B 16-byte aligned
+    // Skinny kernel when !vec: 0 = element-wise; 2 / 3 = A in 16-byte vectors, B 4-byte
+    // aligned with ldb even / odd (rows read in place by dword-aligned 16-byte loads)
+    int skinny_b;
     wmma_gemm_plan plan;
 };
 hipError_t launch_gemm(const GemmLaunch& g, hipStream_t stream);

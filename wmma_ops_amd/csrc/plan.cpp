@@ -25,6 +25,24 @@ static void finish_split(int M, int N, int K, int tiles, int split, wmma_gemm_pl
     p->workspace_bytes = split > 1 ? (size_t)split * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
+double plan_time_us(const wmma_gemm_plan& p, int M, int N, int K, int num_cus) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0.0;
+    if (num_cus <= 0) num_cus = 256;
+    const double hbm = (2.0 * M * K + 2.0 * K * N + 4.0 * M * N) / kHbmBytesPerUs;
+    const int split = std::max(p.split_k, 1);
+    double t = hbm;
+    if (p.kernel == WMMA_KERNEL_TILED) {
+        const TileShape& ts = kTiles[p.tile_cfg];
+        const double area = (double)ts.bm * ts.bn / 65536.0;
+        const int64_t wgs = (int64_t)ceil_div(M, ts.bm) * ceil_div(N, ts.bn) * split;
+        const int kps = split > 1 ? p.k_per_split : K;
+        const double wave = area * (kEpiUs256 + kWaveUsPerK256 * kps / kWaveEff[p.tile_cfg]);
+        t = std::max((double)ceil_div64(wgs, num_cus) * wave, hbm);
+    }
+    if (split > 1) t += (split + 1) * 4.0 * M * N / kHbmBytesPerUs + kReduceUs;
+    return t + kLaunchUs;
+}
+
 // The autotuned table: exact shapes measured on a 256-CU MI355X.
 #include "tuned_table.inc"
 
@@ -61,6 +79,40 @@ int make_custom_plan(int M, int N, int K, int kernel, int tile_cfg, int split,
     finish_split(M, N, K, tiles, split, &p);
     *out = p;
     return WMMA_OK;
+}
+
+// Bulk + edge: when the 256x256 tiles of the shape fill W >= 1 whole waves plus part of
+// another, the whole tile rows (or columns) that fit in W waves run as one launch and the
+// rest as a GEMM of its own, planned on its own (it is small, so it may take a smaller
+// tile or a K split and spread over the chip).  Measured on MI355X (N = K = 4096): M = 4352
+// one launch of 128x128 tiles 193 us, 4096 + 256 rows 148 us; M = 5000: 209 vs 171 us;
+// M = 9192: 347 vs 295 us.  Taken when plan_time_us says it gains more than 7%.
+static void two_part(int M, int N, int K, int num_cus, wmma_gemm_plan* p) {
+    const int64_t tm = ceil_div(M, 256), tn = ceil_div(N, 256);
+    const int64_t whole = tm * tn / num_cus * num_cus;  // 256x256 tiles in whole waves
+    if (whole == 0) return;
+    double best_t = kEdgeGain * plan_time_us(*p, M, N, K, num_cus);
+    for (int dim : {WMMA_EDGE_ROWS, WMMA_EDGE_COLS}) {
+        const int64_t lines = whole / (dim == WMMA_EDGE_ROWS ? tn : tm);
+        const int extent = dim == WMMA_EDGE_ROWS ? M : N;
+        if (lines < 1 || lines * 256 >= extent) continue;
+        const int at = (int)(lines * 256);
+        const int bm = dim == WMMA_EDGE_ROWS ? at : M, bn = dim == WMMA_EDGE_ROWS ? N : at;
+        const int em = dim == WMMA_EDGE_ROWS ? M - at : M, en = dim == WMMA_EDGE_ROWS ? N : N - at;
+        wmma_gemm_plan bulk{}, edge{};
+        if (make_custom_plan(bm, bn, K, WMMA_KERNEL_TILED, WMMA_TILE_256x256, 1, &bulk) != WMMA_OK ||
+            make_plan(em, en, K, WMMA_TILE_AUTO, num_cus, &edge) != WMMA_OK ||
+            edge.edge_dim != WMMA_EDGE_NONE)
+            continue;
+        const double t = plan_time_us(bulk, bm, bn, K, num_cus) + plan_time_us(edge, em, en, K, num_cus);
+        if (t < best_t) {
+            best_t = t;
+            bulk.workspace_bytes = edge.workspace_bytes;
+            bulk.edge_dim = dim;
+            bulk.edge_at = at;
+            *p = bulk;
+        }
+    }
 }
 
 int make_plan(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* out) {
@@ -158,17 +210,18 @@ int make_plan(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* ou
         return WMMA_OK;
     }
 
-    // Tiled MFMA kernel: rank tiles by estimated time = waves of workgroups x tile area
-    // / tile efficiency.  A wave of workgroups is num_cus of them (one per CU).
+    // Tiled MFMA kernel: the tile with the shortest estimated time (plan_time_us: waves of
+    // workgroups, one per CU, times the tile's wave time), the larger tile on a tie.
     const int order[] = {WMMA_TILE_256x256, WMMA_TILE_256x128, WMMA_TILE_128x128,
-                         WMMA_TILE_128x64, WMMA_TILE_64x64};
+                         WMMA_TILE_256x64, WMMA_TILE_128x64, WMMA_TILE_64x64};
     int best = WMMA_TILE_64x64;
     double best_cost = 1e300;
     for (int cfg : order) {
-        const TileShape& t = kTiles[cfg];
-        int64_t tiles = (int64_t)ceil_div(std::max(M, 1), t.bm) * ceil_div(std::max(N, 1), t.bn);
-        int64_t waves = ceil_div64(tiles, num_cus);
-        double cost = (double)waves * t.bm * t.bn / kTileEff[cfg];
+        wmma_gemm_plan c{};
+        if (make_custom_plan(std::max(M, 1), std::max(N, 1), std::max(K, 1), WMMA_KERNEL_TILED, cfg,
+                             1, &c) != WMMA_OK)
+            continue;
+        const double cost = plan_time_us(c, std::max(M, 1), std::max(N, 1), std::max(K, 1), num_cus);
         if (cost < best_cost * 0.999) {
             best_cost = cost;
             best = cfg;
@@ -189,6 +242,7 @@ int make_plan(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* ou
         split = std::max(split, 1);
     }
     finish_split(M, N, K, tiles, split, &p);
+    if (tile_cfg == WMMA_TILE_AUTO && split == 1) two_part(M, N, K, num_cus, &p);
     *out = p;
     return WMMA_OK;
 }

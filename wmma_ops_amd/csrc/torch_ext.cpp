@@ -654,13 +654,13 @@ torch::Tensor matmul_int4(torch::Tensor A, torch::Tensor packed, torch::Tensor s
 }
 
 // Planner introspection: (kernel, tile_cfg, tile_m, tile_n, split_k, k_per_split, grid,
-// workspace_bytes) for a shape on the current device.
+// workspace_bytes, edge_dim, edge_at) for a shape on the current device.
 std::vector<int64_t> gemm_plan(int64_t M, int64_t N, int64_t K, int64_t tile_cfg, int64_t num_cus) {
     wmma_gemm_plan p{};
     check_status(wmma_gemm_plan_make((int)M, (int)N, (int)K, (int)tile_cfg, (int)num_cus, &p),
                  "wmma_gemm_plan_make");
     return {p.kernel, p.tile_cfg, p.tile_m, p.tile_n, p.split_k, p.k_per_split, p.grid,
-            (int64_t)p.workspace_bytes};
+            (int64_t)p.workspace_bytes, p.edge_dim, p.edge_at};
 }
 
 // W4A16 planner introspection: (kernel, split_k, k_per_split, workspace_bytes).
