@@ -26,7 +26,8 @@ Workload families (--workload):
   skinny     configs[2]: M in {1,16,64,128} x N in {4096,11008,14336}, K=4096; K=14336,N=4096
   ragged     N or K off a multiple of 8 (4096x4100x4096, 2048x32001x4096, M = 1..4096): the
              repacked product path, the element-wise in-place path and the aligned neighbour
-             shape, in one process (inputs not rotated)
+             shape; shapes off the 256 grid (M = 4100..8200, N = 4352..14336): the planner's
+             two-part plans against one launch -- in one process (inputs not rotated)
   w4a16      configs[3]: M in {1,16,128,2048} x N in {4096,14336}, K=4096, G=128
   flash      configs[4]: [4,32,4096,128], causal and non-causal, forward and backward; with
              8 K/V heads (GQA); head dims 64 and 256; a packed variable-length batch
@@ -68,6 +69,7 @@ ROTATE_BYTES = 600e6       # > 2 x 256 MB MALL
 M = N = K = 4096
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_f16f32_4096_traffic.json")
 METRIC = "FP16 GEMM TFLOPS (% MFMA peak) @4096^3; W4A16 M=1 HBM GB/s"
+TILE_NAMES = ["64x64", "128x64", "256x64", "128x128", "256x128", "256x256"]
 
 
 def parse():
@@ -269,7 +271,8 @@ def fam_ragged(wo):
     three ways in one process: the product path (wo.matmul: the operand is repacked into a
     zero-padded copy in the workspace, then the vector kernels run), the same call through
     the C-ABI with only the split-K workspace (the element-wise kernels read the operand in
-    place), and the aligned neighbour shape (N or K rounded up to 8) for the repack's cost."""
+    place), and the aligned neighbour shape (N or K rounded up to 8) for the repack's cost.
+    Then shapes off the 256 grid: the planner's two-part plans against one launch."""
     import ctypes
 
     import torch
@@ -324,6 +327,26 @@ def fam_ragged(wo):
                  TFLOPS=round(2.0 * shape[0] * shape[1] * shape[2] / (ms * 1e-3) / 1e12, 1),
                  max_rel_err=None if err is None else float(f"{err:.3e}"))
         del Ad, Bd, A8, B8, C, ws
+    # Off the 256 grid: the planner's plan (two launches where it splits off an edge)
+    # against the faster one-launch plan of the 256x256 and 128x128 tiles (matmul_tiled:
+    # one launch, no split), timed in one process.
+    for (m, n, k) in [(4100, 4096, 4096), (5000, 4096, 4096), (8200, 4096, 4096),
+                      (4096, 4352, 4096), (2560, 14336, 4096), (4096, 14336, 4096),
+                      (7000, 4096, 4096)]:
+        g = torch.Generator().manual_seed(42 + 6)
+        A = torch.randn(m, k, generator=g).half()
+        B = torch.randn(k, n, generator=g).half()
+        Ad, Bd = A.cuda(), B.cuda()
+        fl = 2.0 * m * n * k
+        ms = time_batches(lambda i: wo.matmul(Ad, Bd), 10)
+        err = og.max_rel_err(wo.matmul(Ad, Bd)[-64:], og.gemm_ref(A[-64:], B))
+        one = min((time_batches(lambda i: wo.matmul_tiled(Ad, Bd, cfg), 10), cfg) for cfg in (5, 3))
+        line(family="ragged", path="planner", M=m, N=n, K=k, plan=wo.gemm_plan(m, n, k),
+             us=round(ms * 1e3, 2), TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
+             max_rel_err=float(f"{err:.3e}"))
+        line(family="ragged", path="one launch", M=m, N=n, K=k, tile=TILE_NAMES[one[1]],
+             us=round(one[0] * 1e3, 2), TFLOPS=round(fl / (one[0] * 1e-3) / 1e12, 1))
+        del Ad, Bd
 
 
 def w4a16_case(wo, m, n, use_graph=True):
