@@ -1322,7 +1322,7 @@ w4a16_gemm_kernel(W4Args p) {
 // measured no faster).
 //   wide   128 x 256, wave tile 128 x 64 (64 KB LDS): grids of at least one tile per CU
 //   mid    128 x 128, wave tile 128 x 32 (64 KB LDS)
-//   short   64 x 128, wave tile  64 x 32 (32 KB LDS): M <= 128
+//   short   64 x 128, wave tile  64 x 32 (32 KB LDS): M <= 128, or tiles within one wave
 // (A 256 x 256 tile of 2 x 4 waves spills registers at two waves per SIMD; measured 5-26%
 // slower than 128 x 256 at M = 1024 .. 2048.)
 enum { W4G_TILE_WIDE = 0, W4G_TILE_MID = 1, W4G_TILE_SHORT = 2 };
@@ -1620,15 +1620,20 @@ W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
     if (M > 32 && (G & (G - 1)) == 0) {
         // LDS-DMA W4A16 GEMM.  Tile (measured on MI355X at K = 4096, N in {4096, 11008,
         // 14336}):
-        //   M <= 128: 64 x 128 -- 2-20% faster than 128 x 128 at M = 48..128;
+        //   64 x 128 for M <= 128 (2-20% faster than 128 x 128 at M = 48..128), and above
+        //     while its tiles fit one wave of the CUs (N = 4096: M = 160 / 192 / 256 / 384 /
+        //     512 19.0 / 19.2 / 21.2 / 22.8 / 25.1 us against 20.4 / 22.3 / 22.4 / 25.9 /
+        //     30.1 for 128 x 128 with its best split; where they take more than a wave,
+        //     M = 768 or N = 14336, 128 x 128 is the faster);
         //   128 x 256 when those tiles give at least one per CU, in whole multiples of the
         //     CU count or 1.7 of them (M = 2048: 5-26% faster than 128 x 128; M = 1024,
         //     N = 11008, 1.34 tiles per CU: 4% slower);
         //   else 128 x 128.
         // K split only to fill the chip.
         const int64_t wide_tiles = (int64_t)ceil_div(M, 128) * ceil_div(N, 256);
+        const int64_t short_tiles = (int64_t)ceil_div(M, 64) * ceil_div(N, 128);
         int cfg = W4G_TILE_MID;
-        if (M <= 128)
+        if (M <= 128 || short_tiles <= num_cus)
             cfg = W4G_TILE_SHORT;
         else if (wide_tiles >= num_cus &&
                  (wide_tiles % num_cus == 0 || 10 * wide_tiles >= 17 * (int64_t)num_cus))
