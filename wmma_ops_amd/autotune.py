@@ -88,7 +88,8 @@ def candidate_plans(lib, M, N, K):
 
 def describe(p: Plan) -> str:
     name = "skinny" if p.kernel == KERNEL_SKINNY else TILE_NAMES[p.tile_cfg]
-    return f"{name} split {p.split_k}"
+    edge = f" + edge {'rows' if p.edge_dim == 1 else 'cols'} from {p.edge_at}" if p.edge_dim else ""
+    return f"{name} split {p.split_k}{edge}"
 
 
 class Shape:
@@ -151,8 +152,9 @@ def settle(lib, torch, s: Shape, plan: Plan, ws, ms=100.0):
 
 
 def same_plan(a: Plan, b: Plan) -> bool:
-    return (a.kernel, a.tile_cfg if a.kernel == KERNEL_TILED else -1, a.split_k) == \
-           (b.kernel, b.tile_cfg if b.kernel == KERNEL_TILED else -1, b.split_k)
+    # a two-part plan (the planner's bulk + edge) is never the same as a one-launch candidate
+    return (a.kernel, a.tile_cfg if a.kernel == KERNEL_TILED else -1, a.split_k, a.edge_dim, a.edge_at) == \
+           (b.kernel, b.tile_cfg if b.kernel == KERNEL_TILED else -1, b.split_k, b.edge_dim, b.edge_at)
 
 
 def tune_shape(lib, torch, M, N, K, first: bool):
