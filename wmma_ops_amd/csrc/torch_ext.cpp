@@ -731,6 +731,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("qweight"), py::arg("qzeros"));
     m.def("w4a16_plan", &w4a16_plan, "Planner decision for a W4A16 shape", py::arg("M"),
           py::arg("N"), py::arg("K"), py::arg("group_size") = 128, py::arg("num_cus") = 256);
-    m.def("gemm_plan", &gemm_plan, "Planner decision for a GEMM shape", py::arg("M"), py::arg("N"),
+    m.def("gemm_plan", &gemm_plan,
+          "Planner decision for a GEMM shape: [kernel, tile_cfg, tile_m, tile_n, split_k, "
+          "k_per_split, grid, workspace_bytes, edge_dim, edge_at] (edge_dim 1 / 2: rows / "
+          "columns from edge_at run as a second GEMM)",
+          py::arg("M"), py::arg("N"),
           py::arg("K"), py::arg("tile_cfg") = -1, py::arg("num_cus") = 256);
 }
