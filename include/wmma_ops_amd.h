@@ -327,6 +327,25 @@ int wmma_flash_attn_fwd_lse(const void* Q, const void* K, const void* V, void* O
                             int B, int H, int Hkv, int Sq, int Sk, int D, float scale, int causal,
                             void* stream);
 
+/*
+ * wmma_flash_attn_fwd_lse with a workspace.  When the (batch, head, 256-query block)
+ * workgroups would leave more than half the GPU's CUs idle -- decoding: few queries against
+ * many keys -- the key range is split over more workgroups, each writing its chunk's
+ * unnormalised output, running max and row sum to the workspace, and a second kernel
+ * merges them (results within fp32 rounding of the one-pass forward, not bit-identical).
+ * workspace: at least wmma_flash_attn_fwd_workspace_size(...) bytes (same shape and causal
+ * flag), 16-byte aligned, or NULL / smaller: the one-pass forward.  Every dense forward
+ * (this one, wmma_flash_attn_fwd_lse / _gqa / wmma_flash_attn_fwd) runs the query heads
+ * of a grouped-query group as one sequence when there is no causal mask, so each K/V tile
+ * is read once per group (bit-identical results).  No counterpart in the reference (its
+ * flash_attention, README.md:221-251, has no decoding path).
+ */
+size_t wmma_flash_attn_fwd_workspace_size(int B, int H, int Hkv, int Sq, int Sk, int D,
+                                          int causal);
+int wmma_flash_attn_fwd_ws(const void* Q, const void* K, const void* V, void* O, float* lse,
+                           int B, int H, int Hkv, int Sq, int Sk, int D, float scale, int causal,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
 /* The variable-length forward with lse [H, total_q] (row r of head h at h * total_q + r). */
 int wmma_flash_attn_varlen_fwd_lse(const void* Q, const void* K, const void* V, void* O,
                                    float* lse, const int32_t* cu_seqlens_q,

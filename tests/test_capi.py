@@ -387,6 +387,30 @@ def test_flash_validation_codes(lib):
     assert v(cu=FAKE + 2) == MISALIGNED
 
 
+def test_flash_split_workspace(lib):
+    # the decoding split: 0 bytes for the BASELINE prefill shape (its query blocks fill the
+    # CUs); for one query against 4096 keys on 32 heads, 8 chunks of 512 keys, each holding
+    # fp32 O (D values) plus the running max and row sum per query row
+    ws = lib.wmma_flash_attn_fwd_workspace_size
+    ws.restype = ctypes.c_size_t
+    ws.argtypes = [ctypes.c_int] * 7
+    assert ws(4, 32, 32, 4096, 4096, 128, 0) == 0
+    assert ws(1, 32, 32, 1, 4096, 128, 0) == 8 * 32 * 1 * (128 + 2) * 4
+    assert ws(1, 32, 32, 1, 600, 128, 0) == 2 * 32 * (128 + 2) * 4    # chunks of >= 4 tiles
+    assert ws(1, 32, 32, 1024, 1024, 128, 0) == 0                    # partial sums too large
+    assert ws(1, 32, 32, 1, 4096, 100, 0) == 0 and ws(0, 32, 32, 1, 4096, 128, 0) == 0
+    # grouped-query heads without a causal mask run as one sequence per K/V head: 8 rows of
+    # 4 queries, 32 chunks of 256 keys; with the mask, 32 heads of one query, 8 chunks
+    assert ws(1, 32, 8, 1, 8192, 128, 0) == 32 * (8 * 4) * (128 + 2) * 4
+    assert ws(1, 32, 8, 1, 8192, 128, 1) == 8 * 32 * (128 + 2) * 4
+    f = lib.wmma_flash_attn_fwd_ws
+    f.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 6 + [ctypes.c_float, ctypes.c_int,
+                                                                ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    # a misaligned workspace large enough to be used is rejected before any launch
+    assert f(FAKE, FAKE, FAKE, FAKE, None, 1, 32, 32, 1, 4096, 128, 0.1, 0, FAKE + 4, 1 << 20, None) == MISALIGNED
+    assert f(None, FAKE, FAKE, FAKE, None, 1, 32, 32, 1, 4096, 128, 0.1, 0, FAKE, 1 << 20, None) == INVALID
+
+
 def test_flash_training_validation_codes(lib):
     # forward with log-sum-exp
     f = lambda **kw: lib.wmma_flash_attn_fwd_lse(FAKE, FAKE, FAKE, FAKE, kw.get("lse", FAKE), 1, 4, 2,

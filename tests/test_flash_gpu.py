@@ -247,3 +247,70 @@ def test_flash_many_items(wo, causal, B, H, Hkv, Sq, Sk, D):
         assert torch.allclose(lse[b:b + 1, h:h + 1].cpu(), lref, atol=1e-4, rtol=1e-5)
     # the inference entry point computes the same bits
     assert torch.equal(O, wo.flash_attention(Q.cuda(), K.cuda(), V.cuda(), causal))
+
+
+# Decoding shapes (few queries, many keys): the forward splits the key range over more
+# workgroups and merges the chunks (wmma_flash_attn_fwd_ws; the torch layer always passes
+# the workspace).  Checked against the CPU oracle (O and lse) and against the one-pass
+# forward of the same inputs through the C-ABI (no workspace); causal shapes whose later
+# chunks hold no live key (top-left alignment), GQA, ragged Sk, head dims 64-256.
+@pytest.mark.parametrize("B,H,Hkv,Sq,Sk,D,causal", [
+    (1, 32, 32, 1, 4096, 128, False), (1, 32, 8, 1, 8192, 128, False), (2, 8, 2, 4, 3000, 64, False),
+    (1, 16, 16, 16, 4096, 256, False), (1, 8, 8, 3, 5003, 72, True), (1, 4, 4, 200, 4096, 128, True),
+    (1, 32, 32, 1, 600, 128, False), (3, 4, 4, 2, 2048, 128, True)])
+def test_flash_decode_split(wo, B, H, Hkv, Sq, Sk, D, causal):
+    import ctypes
+    lib = ctypes.CDLL(wo.LIBRARY_PATH)
+    vp, i32, f32, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    lib.wmma_flash_attn_fwd_workspace_size.restype = sz
+    lib.wmma_flash_attn_fwd_workspace_size.argtypes = [i32] * 7
+    lib.wmma_flash_attn_fwd_lse.argtypes = [vp] * 5 + [i32] * 6 + [f32, i32, vp]
+    need = lib.wmma_flash_attn_fwd_workspace_size(B, H, Hkv, Sq, Sk, D, 1 if causal else 0)
+    report("flash_decode_split", B=B, H=H, Hkv=Hkv, Sq=Sq, Sk=Sk, D=D, causal=causal, ws=need)
+    assert need > 0, "the shape should take the split path"
+    Q, K, V = oatt.make_inputs(B, H, Sq, D, seed=Sq * 7 + Sk, Sk=Sk, Hkv=Hkv)
+    Qd, Kd, Vd = Q.cuda(), K.cuda(), V.cuda()
+    O, lse = wo.flash_attention_forward(Qd, Kd, Vd, causal=causal)
+    ref = oatt.sdpa_ref(Q, K, V, causal)
+    _check(O.cpu(), ref)
+    lref = oatt.lse_ref(Q, K, causal)
+    fin = torch.isfinite(lref)
+    assert torch.equal(torch.isfinite(lse.cpu()), fin)
+    assert (lse.cpu()[fin] - lref[fin]).abs().max().item() <= 1e-3
+    assert torch.equal(wo.flash_attention(Qd, Kd, Vd, causal=causal), O)
+    # the one-pass forward of the same inputs (C-ABI without a workspace)
+    O1 = torch.empty_like(Qd)
+    lse1 = torch.empty(B, H, Sq, device="cuda")
+    rc = lib.wmma_flash_attn_fwd_lse(Qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), O1.data_ptr(),
+                                     lse1.data_ptr(), B, H, Hkv, Sq, Sk, D, 1.0 / math.sqrt(D),
+                                     1 if causal else 0, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    _check(O1.cpu(), ref)
+    assert og.max_rel_err(O.float(), O1.float()) <= 1e-3
+
+
+# Grouped-query heads without a causal mask run as one sequence per K/V head (each K/V tile
+# read once per group): the same query rows compute the same arithmetic, so the result is
+# bit-identical to multi-head attention on K/V expanded to every query head (both through
+# the one-pass C-ABI forward, no workspace), lse included.
+@pytest.mark.parametrize("B,H,Hkv,Sq,Sk,D", [(2, 8, 2, 300, 300, 128), (1, 32, 8, 1, 4096, 128),
+                                             (2, 6, 3, 77, 100, 64), (1, 4, 1, 513, 640, 256)])
+def test_flash_gqa_packed_equals_expanded(wo, B, H, Hkv, Sq, Sk, D):
+    import ctypes
+    report("flash_gqa_packed", B=B, H=H, Hkv=Hkv, Sq=Sq, Sk=Sk, D=D)
+    lib = ctypes.CDLL(wo.LIBRARY_PATH)
+    vp, i32, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+    lib.wmma_flash_attn_fwd_lse.argtypes = [vp] * 5 + [i32] * 6 + [f32, i32, vp]
+    Q, K, V = oatt.make_inputs(B, H, Sq, D, seed=B + H + Sq, Sk=Sk, Hkv=Hkv)
+    Qd, Kd, Vd = Q.cuda(), K.cuda(), V.cuda()
+    Kx, Vx = oatt.expand_kv(K, H).contiguous().cuda(), oatt.expand_kv(V, H).contiguous().cuda()
+    st = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for kk, vv, hkv in ((Kd, Vd, Hkv), (Kx, Vx, H)):
+        O = torch.empty_like(Qd)
+        lse = torch.empty(B, H, Sq, device="cuda")
+        assert lib.wmma_flash_attn_fwd_lse(Qd.data_ptr(), kk.data_ptr(), vv.data_ptr(), O.data_ptr(),
+                                           lse.data_ptr(), B, H, hkv, Sq, Sk, D, 1.0 / math.sqrt(D), 0, st) == 0
+        outs.append((O, lse))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    _check(outs[0][0].cpu(), oatt.sdpa_ref(Q, K, V, False))

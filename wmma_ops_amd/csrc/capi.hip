@@ -577,9 +577,23 @@ bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0
 
 }  // namespace
 
-int wmma_flash_attn_fwd_lse(const void* Q, const void* K, const void* V, void* O, float* lse,
-                            int B, int H, int Hkv, int Sq, int Sk, int D, float scale, int causal,
-                            void* stream) {
+// Grouped-query attention without a causal mask, dense layout: the H/Hkv query heads of a
+// group are consecutive rows of Q, O and lse and attend to the same keys, so they run as one
+// sequence of (H/Hkv) Sq rows against their key/value head -- every query row computes
+// exactly as before, and each K/V tile is read once per group instead of once per query
+// head (for decoding, H/Hkv times fewer bytes).  A causal mask depends on the row's position
+// in its own head's sequence, so causal shapes keep one sequence per query head.
+static void flash_pack_groups(int causal, int* H, int Hkv, int* Sq) {
+    if (causal || Hkv <= 0 || *H <= Hkv || (int64_t)*Sq * (*H / Hkv) > INT32_MAX) return;
+    *Sq *= *H / Hkv;
+    *H = Hkv;
+}
+
+// Dense forward; `workspace` (may be NULL) enables the key-range split when it holds the
+// split's partial sums.
+static int flash_fwd_run(const void* Q, const void* K, const void* V, void* O, float* lse, int B,
+                         int H, int Hkv, int Sq, int Sk, int D, float scale, int causal,
+                         void* workspace, size_t workspace_bytes, void* stream) {
     if (int rc = flash_dense_check(B, H, Hkv, Sq, Sk, D, scale, kFlashMaxDFwd)) return rc;
     if (B == 0 || H == 0 || Sq == 0) return ok();
     if (Sk == 0) return fail(WMMA_ERR_INVALID_ARG, "Sk must be positive when Sq > 0");
@@ -601,7 +615,41 @@ int wmma_flash_attn_fwd_lse(const void* Q, const void* K, const void* V, void* O
     f.scale = scale;
     f.causal = causal != 0;
     f.lse = lse;
+    flash_pack_groups(causal, &f.H, f.Hkv, &f.Sq);
+    if (workspace) {
+        const int split = flash_kv_split(B, f.H, Hkv, f.Sq, Sk, D, current_cus());
+        const size_t need = flash_fwd_workspace_bytes(B, f.H, f.Sq, Sk, D, split);
+        if (split > 1 && workspace_bytes >= need) {
+            if (!aligned16(workspace))
+                return fail(WMMA_ERR_MISALIGNED, "workspace must be 16-byte aligned");
+            f.kv_split = split;
+            f.workspace = workspace;
+        }
+    }
     return hip_status(launch_flash_fwd(f, static_cast<hipStream_t>(stream)), "flash launch");
+}
+
+int wmma_flash_attn_fwd_lse(const void* Q, const void* K, const void* V, void* O, float* lse,
+                            int B, int H, int Hkv, int Sq, int Sk, int D, float scale, int causal,
+                            void* stream) {
+    return flash_fwd_run(Q, K, V, O, lse, B, H, Hkv, Sq, Sk, D, scale, causal, nullptr, 0, stream);
+}
+
+size_t wmma_flash_attn_fwd_workspace_size(int B, int H, int Hkv, int Sq, int Sk, int D,
+                                          int causal) {
+    if (B <= 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0 || Sq <= 0 || Sk <= 0 || D <= 0 ||
+        D % 8 != 0 || D > kFlashMaxDFwd)
+        return 0;
+    flash_pack_groups(causal, &H, Hkv, &Sq);
+    return flash_fwd_workspace_bytes(B, H, Sq, Sk, D,
+                                     flash_kv_split(B, H, Hkv, Sq, Sk, D, current_cus()));
+}
+
+int wmma_flash_attn_fwd_ws(const void* Q, const void* K, const void* V, void* O, float* lse,
+                           int B, int H, int Hkv, int Sq, int Sk, int D, float scale, int causal,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+    return flash_fwd_run(Q, K, V, O, lse, B, H, Hkv, Sq, Sk, D, scale, causal, workspace,
+                         workspace_bytes, stream);
 }
 
 int wmma_flash_attn_fwd_gqa(const void* Q, const void* K, const void* V, void* O, int B, int H,

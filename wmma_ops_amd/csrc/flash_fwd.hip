@@ -60,6 +60,13 @@ struct FlashArgs {
     // Optional per-row log-sum-exp of the scaled scores (natural log; +inf for a row with
     // no key): [B*H][Sq] dense, [H][total_q] variable length.
     float* lse;
+    // Split key range (dense layout only; kv_chunk = 0: one pass).  Workgroup z of the grid
+    // takes keys [z kv_chunk, (z + 1) kv_chunk) and writes, for each of its query rows r =
+    // bh Sq + q, the unnormalised O (o_part[z][r][dr]) and its running max (base-2 scaled
+    // scores) and row sum (ml_part[z][r][2]); flash_combine_kernel merges the chunks.
+    int kv_chunk;
+    float* o_part;
+    float* ml_part;
 };
 
 constexpr int FA_WQ = 32;                   // queries per wave
@@ -406,11 +413,19 @@ flash_fwd_kernel(FlashArgs p) {
 
     const int kv_end = CAUSAL ? min(Sk, q0 + C::BQ) : Sk;
     const int T = (kv_end + FA_BKV - 1) / FA_BKV;
-    // Tiles this wave needs (causal: keys <= its last query).
-    const int Tw = CAUSAL ? min(T, (qw + FA_WQ - 1) / FA_BKV + 1) : T;
-    auto rk_of = [&](int t) { return make_rsrc(Kb + (int64_t)min(t, T - 1) * FA_BKV * ks); };
-    auto rv_of = [&](int t) { return make_rsrc(Vb + (int64_t)min(t, T - 1) * FA_BKV * ks); };
-    auto kleft = [&](int t) { return t < T ? Sk - t * FA_BKV : 0; };
+    // Key tiles [tb, te) of this workgroup: all of them, or one chunk of a split key range.
+    int tb = 0, te = T;
+    if (p.kv_chunk) {
+        const int per = p.kv_chunk / FA_BKV;
+        tb = min(T, (int)blockIdx.z * per);
+        te = min(T, tb + per);
+    }
+    // Tiles this wave needs (causal: keys <= its last query); none for a wave whose queries
+    // all lie past Sq (it still loads its share of every tile).
+    const int Tw = qw >= Sq ? 0 : CAUSAL ? min(T, (qw + FA_WQ - 1) / FA_BKV + 1) : T;
+    auto rk_of = [&](int t) { return make_rsrc(Kb + (int64_t)min(t, te - 1) * FA_BKV * ks); };
+    auto rv_of = [&](int t) { return make_rsrc(Vb + (int64_t)min(t, te - 1) * FA_BKV * ks); };
+    auto kleft = [&](int t) { return t < te ? Sk - t * FA_BKV : 0; };
     // A tile needs masking if it reaches past Sk or (causal) past this wave's first query.
     auto masked = [&](int t) {
         const int kv0 = t * FA_BKV;
@@ -430,17 +445,48 @@ flash_fwd_kernel(FlashArgs p) {
     }
     const int qrow0 = qw + c32;
 
-    if (T > 0) {
-        // Prologue: tiles 0 .. NS-2 in flight (tiles past the end load zeros).
+    if (te > tb) {
+        // Prologue: tiles tb .. tb+NS-2 in flight (tiles past te load zeros).
 #pragma unroll
-        for (int s = 0; s < C::NS - 1; ++s) fa_dma<D>(lds + s * C::STAGE, L, rk_of(s), rv_of(s), kleft(s));
-        for (int t = 0; t < T; ++t) {
+        for (int s = 0; s < C::NS - 1; ++s)
+            fa_dma<D>(lds + s * C::STAGE, L, rk_of(tb + s), rv_of(tb + s), kleft(tb + s));
+        for (int t = tb; t < te; ++t) {
             const int tf = t + C::NS - 1;
-            fa_iter<D, CAUSAL>(lds + (t % C::NS) * C::STAGE, lds + (tf % C::NS) * C::STAGE, L,
-                               rk_of(tf), rv_of(tf), kleft(tf), qf, O, m_run, l_run, c,
-                               t * FA_BKV, qrow0, Sk, t < Tw, masked(t));
+            fa_iter<D, CAUSAL>(lds + ((t - tb) % C::NS) * C::STAGE,
+                               lds + ((tf - tb) % C::NS) * C::STAGE, L, rk_of(tf), rv_of(tf),
+                               kleft(tf), qf, O, m_run, l_run, c, t * FA_BKV, qrow0, Sk, t < Tw,
+                               masked(t));
         }
         wait_vmcnt<0>();
+    }
+
+    if (p.kv_chunk) {
+        // One chunk of a split key range: unnormalised O, running max and row sum of each
+        // query row (a chunk with no live key leaves O = 0, max = -inf, sum = 0).
+        const int64_t rows = (int64_t)gridDim.x * Sq;
+#pragma unroll
+        for (int qb = 0; qb < FA_NQB; ++qb) {
+            const int q = qrow0 + 32 * qb;
+            const float l_tot = l_run[qb] + __shfl_xor(l_run[qb], 32);
+            if (q >= Sq) continue;
+            const int64_t r = (int64_t)blockIdx.z * rows + (int64_t)bh * Sq + q;
+            if (h == 0) {
+                p.ml_part[2 * r] = m_run[qb];
+                p.ml_part[2 * r + 1] = l_tot;
+            }
+            float* op = p.o_part + r * p.dr;
+#pragma unroll
+            for (int db = 0; db < C::NDB; ++db)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int d = 32 * db + 8 * g + 4 * h;
+                    if (d < p.dr)
+                        *reinterpret_cast<float4*>(op + d) =
+                            make_float4(O[db][qb][4 * g], O[db][qb][4 * g + 1],
+                                        O[db][qb][4 * g + 2], O[db][qb][4 * g + 3]);
+                }
+        }
+        return;
     }
 
     // Normalise and store: lane owns query qw + 32 qb + lane%32, d = 32 db + 8 (r/4) +
@@ -472,10 +518,67 @@ flash_fwd_kernel(FlashArgs p) {
     }
 }
 
+// Merges the chunks of a split key range: O = sum_z w_z O_z / sum_z w_z l_z with chunk
+// weights w_z = exp2(m_z - m), m the largest running max (0 for a row with no key), and
+// lse = (m + log2 l) ln 2 (+inf for a row with no key).  One thread per 4 d columns of a
+// query row.  The chunks are read 8 at a time -- all 8 loads issued before any is used, so
+// a batch costs one memory round trip -- and folded in order with an online rescale.
+constexpr int FA_ZB = 8;
+
+__global__ void __launch_bounds__(256)
+flash_combine_kernel(const float* o_part, const float* ml_part, int split, int64_t rows, int dr,
+                     f16* O, float* lse) {
+    const int dq = dr / 4;
+    const int64_t n = rows * dq;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / dq;
+        const int d = (int)(i - r * dq) * 4;
+        float m = kNegInf, l = 0.0f;
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int z0 = 0; z0 < split; z0 += FA_ZB) {
+            float mz[FA_ZB], lz[FA_ZB];
+            float4 oz[FA_ZB];
+#pragma unroll
+            for (int j = 0; j < FA_ZB; ++j) {
+                const int64_t zr = (int64_t)(z0 + j) * rows + r;
+                const bool in = z0 + j < split;
+                mz[j] = in ? ml_part[2 * zr] : kNegInf;
+                lz[j] = in ? ml_part[2 * zr + 1] : 0.0f;
+                oz[j] = in ? *reinterpret_cast<const float4*>(o_part + zr * dr + d)
+                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+#pragma unroll
+            for (int j = 0; j < FA_ZB; ++j) {
+                if (mz[j] == kNegInf) continue;  // a chunk with no live key
+                const float mn = fmaxf(m, mz[j]);
+                const float a = __builtin_amdgcn_exp2f(m - mn);  // 0 while m is -inf
+                const float w = __builtin_amdgcn_exp2f(mz[j] - mn);
+                l = l * a + w * lz[j];
+                acc.x = acc.x * a + w * oz[j].x;
+                acc.y = acc.y * a + w * oz[j].y;
+                acc.z = acc.z * a + w * oz[j].z;
+                acc.w = acc.w * a + w * oz[j].w;
+                m = mn;
+            }
+        }
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        f16x4 v;
+        v[0] = (f16)(acc.x * inv);
+        v[1] = (f16)(acc.y * inv);
+        v[2] = (f16)(acc.z * inv);
+        v[3] = (f16)(acc.w * inv);
+        *reinterpret_cast<f16x4*>(O + r * dr + d) = v;
+        if (lse && d == 0)
+            lse[r] = l > 0.0f ? (m + __builtin_amdgcn_logf(l)) * 0.6931471805599453f
+                              : __builtin_huge_valf();
+    }
+}
+
 template <int D>
 void launch_d(FlashArgs a, int BH, bool causal, hipStream_t stream) {
     a.nqb = ceil_div(a.Sq, FaCfg<D>::BQ);
-    dim3 grid(BH, a.nqb);
+    dim3 grid(BH, a.nqb, a.kv_chunk ? ceil_div(a.Sk, a.kv_chunk) : 1);
     const dim3 block(FaCfg<D>::WAVES * kWave);
     if (causal)
         hipLaunchKernelGGL((flash_fwd_kernel<D, true>), grid, block, 0, stream, a);
@@ -504,6 +607,15 @@ hipError_t launch_flash_fwd(const FlashLaunch& f, hipStream_t stream) {
     a.lse = f.lse;
     a.scale_log2 = f.scale * 1.4426950408889634f;
     const int BH = f.B * f.H;
+    const int split = f.cu_q ? 1 : f.kv_split;
+    if (split > 1) {
+        // chunks of whole 64-key tiles; the partial sums sit at the start of the workspace
+        a.kv_chunk = ceil_div(ceil_div(f.Sk, split), FA_BKV) * FA_BKV;
+        const int64_t rows = (int64_t)BH * f.Sq;
+        const int nz = ceil_div(f.Sk, a.kv_chunk);
+        a.o_part = static_cast<float*>(f.workspace);
+        a.ml_part = a.o_part + (int64_t)nz * rows * f.D;
+    }
     // head dims up to 64 run the D = 64 kernel, up to 128 the D = 128 kernel, up to 256 the
     // D = 256 kernel
     if (f.D > 128)
@@ -512,7 +624,35 @@ hipError_t launch_flash_fwd(const FlashLaunch& f, hipStream_t stream) {
         launch_d<128>(a, BH, f.causal, stream);
     else
         launch_d<64>(a, BH, f.causal, stream);
+    if (a.kv_chunk == 0) return hipGetLastError();
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    const int64_t rows = (int64_t)BH * f.Sq;
+    const int64_t threads = rows * (f.D / 4);
+    const int grid = (int)std::min<int64_t>(ceil_div64(threads, 256), 8192);
+    hipLaunchKernelGGL(flash_combine_kernel, dim3(grid), dim3(256), 0, stream, a.o_part, a.ml_part,
+                       ceil_div(f.Sk, a.kv_chunk), rows, f.D, a.O, f.lse);
     return hipGetLastError();
+}
+
+int flash_kv_split(int B, int H, int Hkv, int Sq, int Sk, int D, int num_cus) {
+    if (B <= 0 || H <= 0 || Hkv <= 0 || Sq <= 0 || Sk <= 0 || num_cus <= 0) return 1;
+    const int bq = D > 128 ? FaCfg<256>::BQ : FaCfg<128>::BQ;
+    const int64_t wgs = (int64_t)B * H * ceil_div(Sq, bq);
+    if (wgs * 2 > num_cus) return 1;  // at least half the CUs busy without a split
+    // chunks of at least 4 tiles, enough of them to fill the CUs, while the partial sums
+    // (written and read back: 8 bytes per query row and d column per chunk) stay within a
+    // quarter of the K/V bytes read (4 per key and d column of each K/V head)
+    int s = (int)std::min<int64_t>(ceil_div64(num_cus, wgs), ceil_div(Sk, FA_BKV) / 4);
+    const int64_t group = H / Hkv;
+    while (s > 1 && (int64_t)s * Sq * group * 8 > Sk) --s;
+    return std::max(s, 1);
+}
+
+size_t flash_fwd_workspace_bytes(int B, int H, int Sq, int Sk, int D, int split) {
+    if (split <= 1) return 0;
+    const int64_t kv_chunk = ceil_div(ceil_div(Sk, split), FA_BKV) * FA_BKV;
+    const int64_t nz = ceil_div64(Sk, kv_chunk);
+    return (size_t)(nz * B * H * Sq) * (size_t)(D + 2) * sizeof(float);
 }
 
 }  // namespace wmma_amd

@@ -108,8 +108,18 @@ struct FlashLaunch {
     // Optional log-sum-exp output (fp32, natural log): [B*H][Sq], or [H][total_q] for
     // variable length.
     float* lse = nullptr;
+    // Dense layout only: split the key range into kv_split chunks (> 1) whose partial
+    // sums go to workspace (flash_fwd_workspace_bytes, 16-byte aligned), merged by a
+    // second kernel.
+    int kv_split = 1;
+    void* workspace = nullptr;
 };
 hipError_t launch_flash_fwd(const FlashLaunch& f, hipStream_t stream);
+// Key-range split the forward uses for a dense shape on num_cus CUs (1: none): only when
+// the query blocks leave more than half the CUs idle and the partial sums stay small.
+int flash_kv_split(int B, int H, int Hkv, int Sq, int Sk, int D, int num_cus);
+// Workspace bytes of a split (0 for split <= 1); D is the head dim passed to the kernels.
+size_t flash_fwd_workspace_bytes(int B, int H, int Sq, int Sk, int D, int split);
 
 // Flash-attention backward: dQ, dK, dV (fp16, the layouts of Q, K, V) from dO, Q, K, V, O
 // and the forward's log-sum-exp.  ws: fp32 workspace of 2 * flash_bwd_workspace_rows().

@@ -255,11 +255,17 @@ torch::Tensor flash_dense_fwd(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
         *lse_out = torch::empty({Q.size(0), Q.size(1), Q.size(2)}, Q.options().dtype(torch::kFloat32));
         lse = lse_out->data_ptr<float>();
     }
-    int rc = wmma_flash_attn_fwd_lse(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(), lse,
-                                     (int)Q.size(0), (int)Q.size(1), (int)K.size(1),
-                                     (int)Q.size(2), (int)K.size(2), (int)Dp, flash_scale(scale, D),
-                                     causal ? 1 : 0, current_stream(Q));
-    check_status(rc, "wmma_flash_attn_fwd_lse");
+    // decoding shapes split the key range; the partial sums come from the caching allocator
+    const size_t ws_bytes = wmma_flash_attn_fwd_workspace_size(
+        (int)Q.size(0), (int)Q.size(1), (int)K.size(1), (int)Q.size(2), (int)K.size(2), (int)Dp,
+        causal ? 1 : 0);
+    torch::Tensor ws = workspace_for(ws_bytes, Q);
+    int rc = wmma_flash_attn_fwd_ws(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(), lse,
+                                    (int)Q.size(0), (int)Q.size(1), (int)K.size(1),
+                                    (int)Q.size(2), (int)K.size(2), (int)Dp, flash_scale(scale, D),
+                                    causal ? 1 : 0, ws.defined() ? ws.data_ptr() : nullptr,
+                                    ws_bytes, current_stream(Q));
+    check_status(rc, "wmma_flash_attn_fwd_ws");
     return unpad_head(O, D);
 }
 
