@@ -33,6 +33,8 @@ Workload families (--workload):
              8 K/V heads (GQA); head dims 64 and 256; a packed variable-length batch
   flash_operands  configs[4] non-causal forward and backward on all-ones inputs (the power
              limit's share of the random-input figures)
+  decode     flash attention with 1-16 queries against 4096-32768 keys (MHA and 8 K/V heads,
+             D 128 / 256): the split-key-range forward against the one-pass forward
   copy       a plain 256 MiB device copy (calibrates the rocprofv3 byte counters)
   mfma_ceiling  the matrix pipe's sustained rate with register operands and no memory
              traffic (libwmma_calib.so): the ceiling the GEMM main loop is held against;
@@ -489,6 +491,52 @@ def fam_flash(wo):
              max_rel_err=float(f"{err:.3e}"))
 
 
+def fam_decode(wo):
+    """Flash attention on decoding shapes (few queries against many keys): the product path
+    (wo.flash_attention: key range split over more workgroups, grouped-query heads packed
+    into one sequence per K/V head) against the one-pass forward through the C-ABI without a
+    workspace.  Both replayed from a HIP graph over K/V rotated past the MALL; bytes = the
+    K and V read once (+ Q and O), HBM roofline."""
+    import ctypes
+
+    import torch
+
+    from oracle import attention as oatt
+    from oracle import gemm as og
+
+    L = ctypes.CDLL(wo.LIBRARY_PATH)
+    vp, i32, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+    L.wmma_flash_attn_fwd_lse.argtypes = [vp] * 5 + [i32] * 6 + [f32, i32, vp]
+    for (B, H, Hkv, Sq, Sk, D) in [(1, 32, 32, 1, 4096, 128), (1, 32, 8, 1, 8192, 128),
+                                   (1, 32, 8, 1, 32768, 128), (8, 32, 8, 1, 4096, 128),
+                                   (1, 32, 32, 16, 4096, 128), (1, 16, 16, 1, 4096, 256)]:
+        Q, K, V = oatt.make_inputs(B, H, Sq, D, seed=42 + 7, Sk=Sk, Hkv=Hkv)
+        nbytes = 2 * 2 * B * Hkv * Sk * D + 2 * 2 * B * H * Sq * D
+        cp = copies_for(nbytes)
+        Qd = Q.cuda()
+        Ks = [K.cuda() for _ in range(cp)]
+        Vs = [V.cuda() for _ in range(cp)]
+        ref = oatt.sdpa_ref(Q[:1, :4], oatt.expand_kv(K, H)[:1, :4], oatt.expand_kv(V, H)[:1, :4])
+
+        def one(i):
+            O = torch.empty_like(Qd)
+            rc = L.wmma_flash_attn_fwd_lse(Qd.data_ptr(), Ks[i % cp].data_ptr(), Vs[i % cp].data_ptr(),
+                                           O.data_ptr(), None, B, H, Hkv, Sq, Sk, D, 1.0 / math.sqrt(D), 0,
+                                           torch.cuda.current_stream().cuda_stream)
+            assert rc == 0
+            return O
+
+        for path, fn in (("split", lambda i: wo.flash_attention(Qd, Ks[i % cp], Vs[i % cp])),
+                         ("one pass", one)):
+            ms, outs = time_graph(fn, cp)
+            err = og.max_rel_err(outs[0][:1, :4].float().cpu(), ref)
+            line(family="decode", path=path, B=B, H=H, Hkv=Hkv, Sq=Sq, Sk=Sk, D=D,
+                 us=round(ms * 1e3, 2), bytes=nbytes, GBps=round(nbytes / (ms * 1e-3) / 1e9, 1),
+                 frac_hbm=round(nbytes / PEAK_HBM_BPS / (ms * 1e-3), 4), rotation_copies=cp,
+                 timing="graph replay", max_rel_err=float(f"{err:.3e}"))
+        del Ks, Vs
+
+
 def fam_flash_operands(wo):
     """configs[4] non-causal, forward and backward, on all-ones Q, K, V (and dO): the same
     kernels and traffic with operand bits that never switch -- against the random-input
@@ -737,7 +785,7 @@ def fam_read_floor(wo):
 FAMILIES = {"gemm": fam_gemm, "epilogue": fam_epilogue, "skinny": fam_skinny, "ragged": fam_ragged,
             "w4a16": fam_w4a16, "flash": fam_flash, "copy": fam_copy,
             "mfma_ceiling": fam_mfma_ceiling, "read_floor": fam_read_floor, "lds_read": fam_lds_read,
-            "flash_operands": fam_flash_operands, "vendor": fam_vendor}
+            "flash_operands": fam_flash_operands, "decode": fam_decode, "vendor": fam_vendor}
 
 
 # ------------------------------------------------------------------------ headline --
@@ -949,7 +997,8 @@ def main():
     global QUICK
     QUICK = args.quick and bool(args.suite or args.workload)
     if args.suite:
-        for name in ("gemm", "epilogue", "skinny", "ragged", "w4a16", "flash", "flash_operands"):
+        for name in ("gemm", "epilogue", "skinny", "ragged", "w4a16", "flash", "flash_operands",
+                     "decode"):
             FAMILIES[name](wo)
     elif args.workload:
         FAMILIES[args.workload](wo)
