@@ -1,6 +1,7 @@
 """The allocation-free GEMM entry point, wmma_gemm_f16f32_noalloc, against wmma_gemm_f16f32.
 
-Both run the same plan and kernels; the only difference is where the split-K partial sums
+On aligned shapes both run the same plan and kernels (on ragged ones see
+test_noalloc_ragged_shapes); the only difference is where the split-K partial sums
 live (the library's own device array instead of a caller workspace), so every output must
 be bit-identical, and within the oracle's 1e-3 max-relative bound.  Each case makes two
 calls in a row, the second on a smaller shape, so the second call runs on a scratch array
@@ -86,3 +87,48 @@ def test_noalloc_scratch_covers_baseline_shapes():
              [(s, s, s) for s in (512, 1024, 2048, 4096)] + [(4096, 4096, 2048)]
     for (M, N, K) in shapes:
         assert lib.wmma_gemm_workspace_size(M, N, K, -1) <= cap, (M, N, K)
+
+
+# Ragged shapes (N or K off a multiple of 8): the allocation-free entry point makes no
+# padded copies, so its operands go to the element-wise kernels (split-K partials in the
+# scratch array) or, at M <= 16, the skinny kernel's in-place B modes, while
+# wmma_gemm_f16f32 with its full workspace repacks them for the vector kernels.  Both are
+# held to the oracle's 1e-3 bar and to each other (products bit-equal: the same MFMA
+# inputs in the same order; the alpha/beta epilogue to rounding).  Two calls in a row, the
+# second smaller.
+RAGGED_PAIRS = [((128, 4100, 4096), (7, 1027, 300)),
+                ((300, 1000, 1004), (1, 4101, 4096))]
+
+
+@pytest.mark.parametrize("first,second", RAGGED_PAIRS)
+def test_noalloc_ragged_shapes(first, second):
+    lib = _lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    for (M, N, K) in (first, second):
+        report("noalloc_ragged", M=M, N=N, K=K)
+        need = lib.wmma_gemm_workspace_size(M, N, K, -1)
+        g = torch.Generator().manual_seed(M * 3 + N + K)
+        A = torch.randn(M, K, generator=g).half()
+        B = (torch.randn(K, N, generator=g) * 0.05).half()
+        C0 = torch.randn(M, N, generator=g)
+        Ad, Bd = A.cuda(), B.cuda()
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+        prods = []
+        for alpha, beta in [(1.0, 0.0), (2.0, 0.5)]:
+            Cref, Cna = C0.cuda(), C0.cuda()
+            out_ref, out_na = torch.empty(M, N, device="cuda"), torch.empty(M, N, device="cuda")
+            rc = lib.wmma_gemm_f16f32(Ad.data_ptr(), K, Bd.data_ptr(), N, Cref.data_ptr(), N,
+                                      out_ref.data_ptr(), N, M, N, K, alpha, beta, -1,
+                                      ws.data_ptr(), need, stream)
+            assert rc == 0, lib.wmma_last_error()
+            rc = lib.wmma_gemm_f16f32_noalloc(Ad.data_ptr(), K, Bd.data_ptr(), N, Cna.data_ptr(), N,
+                                              out_na.data_ptr(), N, M, N, K, alpha, beta, -1, stream)
+            assert rc == 0, lib.wmma_last_error()
+            torch.cuda.synchronize()
+            ref = og.gemm_ref(A, B, alpha, beta, C0 if beta != 0.0 else None)
+            assert og.max_rel_err(out_ref, ref) <= 1e-3
+            assert og.max_rel_err(out_na, ref) <= 1e-3
+            if beta == 0.0:
+                assert torch.equal(out_na, out_ref), (M, N, K)
+            else:
+                assert og.max_rel_err(out_na, out_ref) <= 1e-6
