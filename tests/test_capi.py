@@ -411,6 +411,23 @@ def test_flash_split_workspace(lib):
     assert f(None, FAKE, FAKE, FAKE, None, 1, 32, 32, 1, 4096, 128, 0.1, 0, FAKE, 1 << 20, None) == INVALID
 
 
+def test_flash_bwd_split_workspace(lib):
+    # grouped-query backward with few K/V heads: the row statistics (256-byte rounded) plus
+    # fp32 partial dK and dV per part; unchanged where the dK/dV workgroups fill the CUs
+    lib.wmma_flash_attn_bwd_workspace_size.restype = ctypes.c_size_t
+    f = lib.wmma_flash_attn_bwd_split_workspace_size
+    f.restype = ctypes.c_size_t
+    f.argtypes = [ctypes.c_int] * 6
+    stats = lambda B, H, S: 2 * 4 * B * H * S
+    # 8 K/V heads x 16 key blocks = 128 workgroups: 2 parts of 2 query heads each
+    assert f(1, 32, 8, 2048, 2048, 128) == stats(1, 32, 2048) + 2 * 2 * 8 * 2048 * 128 * 4
+    assert f(4, 32, 32, 4096, 4096, 128) == stats(4, 32, 4096)     # no group
+    assert f(1, 32, 8, 4096, 4096, 128) == stats(1, 32, 4096)      # 256 workgroups: full
+    # D = 64 (256 keys per workgroup): 4 workgroups, one part per query head
+    assert f(1, 32, 1, 1024, 1024, 64) == stats(1, 32, 1024) + 2 * 32 * 1024 * 64 * 4
+    assert f(1, 8, 2, 0, 100, 64) == 0
+
+
 def test_flash_training_validation_codes(lib):
     # forward with log-sum-exp
     f = lambda **kw: lib.wmma_flash_attn_fwd_lse(FAKE, FAKE, FAKE, FAKE, kw.get("lse", FAKE), 1, 4, 2,

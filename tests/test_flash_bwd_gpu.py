@@ -248,3 +248,50 @@ def test_flash_bwd_errors(wo):
         wo.flash_attention_backward(Q[:, :, :8], Q, K, V, O, lse)
     with pytest.raises(RuntimeError, match="dO and O must be float16"):
         wo.flash_attention_backward(Q.float(), Q, K, V, O, lse)
+
+
+# Grouped-query split of the dK/dV kernel (few K/V heads, short sequences): with the
+# workspace wmma_flash_attn_bwd_split_workspace_size reports, the group's query heads run
+# on separate workgroups whose fp32 partial dK, dV are added in part order; with only the
+# row statistics, one workgroup sums the group in registers.  Both match the oracle; dQ is
+# the same computation either way (bit-equal), dK and dV agree to fp32 summation order.
+@pytest.mark.parametrize("B,H,Hkv,Sq,Sk,D,causal", [
+    (1, 16, 4, 1024, 1024, 128, False), (1, 16, 4, 1024, 1024, 128, True),
+    (2, 8, 1, 300, 500, 64, True), (1, 8, 2, 257, 257, 256, False), (1, 6, 3, 130, 130, 72, True)])
+def test_flash_bwd_group_split(wo, B, H, Hkv, Sq, Sk, D, causal):
+    import ctypes
+    lib = ctypes.CDLL(wo.LIBRARY_PATH)
+    vp, i32, f32, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    lib.wmma_flash_attn_bwd_workspace_size.restype = sz
+    lib.wmma_flash_attn_bwd_workspace_size.argtypes = [i32] * 3
+    lib.wmma_flash_attn_bwd_split_workspace_size.restype = sz
+    lib.wmma_flash_attn_bwd_split_workspace_size.argtypes = [i32] * 6
+    lib.wmma_flash_attn_bwd.argtypes = [vp] * 10 + [sz] + [i32] * 6 + [f32, i32, vp]
+    base = lib.wmma_flash_attn_bwd_workspace_size(B, H, Sq)
+    full = lib.wmma_flash_attn_bwd_split_workspace_size(B, H, Hkv, Sq, Sk, D)
+    report("flash_bwd_group_split", B=B, H=H, Hkv=Hkv, Sq=Sq, Sk=Sk, D=D, causal=causal, ws=full)
+    assert full > base, "the shape should take the split"
+    Q, K, V = oatt.make_inputs(B, H, Sq, D, seed=B + H + Sq + D, Sk=Sk, Hkv=Hkv)
+    dO = _dout((B, H, Sq, D), H * 3 + Sq)
+    Qd, Kd, Vd, dOd = Q.cuda(), K.cuda(), V.cuda(), dO.cuda()
+    O, lse = wo.flash_attention_forward(Qd, Kd, Vd, causal)
+    res = []
+    for wsb in (full, base):
+        ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+        dQ, dK, dV = torch.empty_like(Qd), torch.empty_like(Kd), torch.empty_like(Vd)
+        rc = lib.wmma_flash_attn_bwd(dOd.data_ptr(), Qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), O.data_ptr(),
+                                     lse.data_ptr(), dQ.data_ptr(), dK.data_ptr(), dV.data_ptr(), ws.data_ptr(),
+                                     wsb, B, H, Hkv, Sq, Sk, D, 1.0 / math.sqrt(D), 1 if causal else 0,
+                                     torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        res.append((dQ, dK, dV))
+    want = oatt.sdpa_bwd_ref(Q, K, V, dO, causal)
+    _grads_close(res[0], want)
+    _grads_close(res[1], want)
+    assert torch.equal(res[0][0], res[1][0])
+    for a, b in zip(res[0][1:], res[1][1:]):
+        assert og.max_rel_err(a.float(), b.float()) <= 1e-3
+    # the torch layer passes the split workspace: its gradients are the split ones
+    got = wo.flash_attention_backward(dOd, Qd, Kd, Vd, O, lse, causal)
+    for a, b in zip(got, res[0]):
+        assert torch.equal(a, b)

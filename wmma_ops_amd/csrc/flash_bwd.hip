@@ -164,6 +164,13 @@ struct BwdArgs {
     const int* cu_k;
     int H, Hkv;
     int total_q, total_k;
+    // Grouped-query split of the dK/dV kernel (dense layout; gsplit = 1: none): part gp of
+    // blockIdx.z / DSPLIT takes query heads [gp gper, (gp + 1) gper) of the group and
+    // writes fp32 partial dK, dV (scaled as the final ones) to kv_part[gp] and
+    // kv_part[gsplit + gp], each laid out like K; flash_bwd_kv_sum_kernel adds the parts.
+    int gsplit, gper;
+    float* kv_part;
+    int64_t kv_elems;  // elements of K (B * Hkv * Sk * dr)
 };
 
 // Geometry of one (batch entry, query head): lengths, row strides (elements) and bases.
@@ -342,6 +349,24 @@ __device__ __forceinline__ void fb_store_rows(f16* base, int stride, int dr, int
             for (int e = 0; e < 4; ++e) v[e] = (f16)(acc[db][4 * g + e] * s);
             const int d = d0 + 32 * db + 8 * g + 4 * h;
             if (d < dr) *reinterpret_cast<f16x4*>(base + (int64_t)row * stride + d) = v;
+        }
+}
+
+// The same rows as fp32 partial sums (the grouped-query split of the dK/dV kernel).
+template <int NDB>
+__device__ __forceinline__ void fb_store_rows_f32(float* base, int stride, int dr, int row, int n,
+                                                  int h, const f32x16 (&acc)[NDB], float s,
+                                                  int d0) {
+    if (row >= n) return;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = d0 + 32 * db + 8 * g + 4 * h;
+            if (d < dr)
+                *reinterpret_cast<float4*>(base + (int64_t)row * stride + d) =
+                    make_float4(acc[db][4 * g] * s, acc[db][4 * g + 1] * s, acc[db][4 * g + 2] * s,
+                                acc[db][4 * g + 3] * s);
         }
 }
 
@@ -649,12 +674,17 @@ flash_bwd_dkdv_kernel(BwdArgs p) {
 
     FbLane<D, FB_WAVES_KV> L;
     fb_lane_init<D>(L, wave, lane, G0.qs, p.dr);
-    // Query tiles: t0 .. Tq-1 of each of the group's query heads in turn.  Head gi's rows
-    // start at q_base0 + gi * qh (Q/dO elements) and r_base0 + gi * rh (statistics).
+    // Query tiles: t0 .. Tq-1 of each of this workgroup's query heads of the group in turn
+    // (heads g_lo .. g_lo + ng - 1: the whole group, or one part of a grouped-query split).
+    // Head gi's rows start at q_base0 + gi * qh (Q/dO elements) and r_base0 + gi * rh
+    // (statistics).
+    const int gp = (int)blockIdx.z / FbKv<D>::DSPLIT;
+    const int g_lo = gp * p.gper;
+    const int ng = max(0, min(p.group, g_lo + p.gper) - g_lo);
     const int Tq = (Sq + FB_T - 1) / FB_T;
     const int t0 = CAUSAL ? min(k0 / FB_T, Tq) : 0;
     const int nT = Tq - t0;
-    const int U = p.group * nT;
+    const int U = ng * nT;
     const int64_t qh = p.cu_q ? (int64_t)p.dr : (int64_t)Sq * p.dr;
     const int64_t rh = p.cu_q ? (int64_t)p.total_q : (int64_t)Sq;
     const float* ws_lse = p.ws + p.rows;
@@ -663,13 +693,15 @@ flash_bwd_dkdv_kernel(BwdArgs p) {
     const float* st_src = wave == 0 ? ws_lse : ws_delta;
     auto tile_of = [&](int u, int& gi, int& t) {
         const int uu = min(u, U - 1);
-        gi = uu / nT;
-        t = t0 + (uu - gi * nT);
+        const int gr = uu / nT;
+        gi = g_lo + gr;
+        t = t0 + (uu - gr * nT);
     };
     auto qleft = [&](int u, int t) { return u < U ? Sq - t * FB_T : 0; };
 
     constexpr int NDBO = FbKv<D>::NDB_OUT;
-    const int db0 = (int)blockIdx.z * NDBO;  // first d block of this workgroup's dK, dV columns
+    // first d block of this workgroup's dK, dV columns
+    const int db0 = ((int)blockIdx.z % FbKv<D>::DSPLIT) * NDBO;
     f32x16 dk[FbKv<D>::KB][NDBO], dv[FbKv<D>::KB][NDBO];
 #pragma unroll
     for (int kb = 0; kb < FbKv<D>::KB; ++kb)
@@ -709,11 +741,23 @@ flash_bwd_dkdv_kernel(BwdArgs p) {
         // Causal: the first BLOCK/64 tiles of each query head hold queries below the
         // workgroup's last key (k0 is a multiple of the tile, so exactly these).
         const int nmask = CAUSAL ? min(nT, FbKv<D>::BLOCK / FB_T) : 0;
-        for (int gi = 0, u = 0; gi < p.group; ++gi) {
+        for (int gr = 0, u = 0; gr < ng; ++gr) {
             for (const int e = u + nmask; u < e; ++u) step(std::true_type{}, u);
-            for (const int e = (gi + 1) * nT; u < e; ++u) step(std::false_type{}, u);
+            for (const int e = (gr + 1) * nT; u < e; ++u) step(std::false_type{}, u);
         }
         wait_vmcnt<0>();
+    }
+    if (p.gsplit > 1) {
+        float* pk = p.kv_part + (int64_t)gp * p.kv_elems + G0.k_base;
+        float* pv = p.kv_part + (int64_t)(p.gsplit + gp) * p.kv_elems + G0.k_base;
+#pragma unroll
+        for (int kb = 0; kb < FbKv<D>::KB; ++kb) {
+            fb_store_rows_f32<NDBO>(pk, G0.ks, p.dr, kw + 32 * kb + c32, Sk, h, dk[kb], p.scale,
+                                    32 * db0);
+            fb_store_rows_f32<NDBO>(pv, G0.ks, p.dr, kw + 32 * kb + c32, Sk, h, dv[kb], 1.0f,
+                                    32 * db0);
+        }
+        return;
     }
 #pragma unroll
     for (int kb = 0; kb < FbKv<D>::KB; ++kb) {
@@ -724,12 +768,39 @@ flash_bwd_dkdv_kernel(BwdArgs p) {
     }
 }
 
+// dK, dV of a grouped-query split: the gsplit fp32 parts of each element added in part
+// order (deterministic) and rounded once to fp16.  Four elements per thread.
+__global__ void __launch_bounds__(256)
+flash_bwd_kv_sum_kernel(const float* kv_part, int gsplit, int64_t n, f16* dK, f16* dV) {
+    const int64_t n4 = n / 4;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < 2 * n4;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const bool v = i >= n4;
+        const int64_t e = 4 * (v ? i - n4 : i);
+        const float* src = kv_part + (v ? (int64_t)gsplit * n : 0) + e;
+        float4 a = *reinterpret_cast<const float4*>(src);
+        for (int g = 1; g < gsplit; ++g) {
+            const float4 b = *reinterpret_cast<const float4*>(src + (int64_t)g * n);
+            a.x += b.x;
+            a.y += b.y;
+            a.z += b.z;
+            a.w += b.w;
+        }
+        f16x4 o;
+        o[0] = (f16)a.x;
+        o[1] = (f16)a.y;
+        o[2] = (f16)a.z;
+        o[3] = (f16)a.w;
+        *reinterpret_cast<f16x4*>((v ? dV : dK) + e) = o;
+    }
+}
+
 template <int D>
 void launch_bwd_d(BwdArgs a, int B, bool causal, hipStream_t stream) {
     a.nqb = ceil_div(a.Sq, FbGeom<D>::BLOCK_Q);
     const dim3 bq(FbGeom<D>::WQ * kWave), bk(FB_WAVES_KV * kWave);
     const dim3 gq(B * a.H, a.nqb);
-    const dim3 gk(B * a.Hkv, ceil_div(a.Sk, FbKv<D>::BLOCK), FbKv<D>::DSPLIT);
+    const dim3 gk(B * a.Hkv, ceil_div(a.Sk, FbKv<D>::BLOCK), FbKv<D>::DSPLIT * a.gsplit);
     // The dQ kernel writes the row statistics the dK/dV kernel reads: same stream, in order.
     // An empty side (no query or no key rows) launches nothing for it; with no query rows
     // the dK/dV kernel still runs and stores zeros.
@@ -744,13 +815,44 @@ void launch_bwd_d(BwdArgs a, int B, bool causal, hipStream_t stream) {
             hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, true>), gk, bk, 0, stream, a);
         else
             hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, false>), gk, bk, 0, stream, a);
+        if (a.gsplit > 1 && a.kv_elems > 0) {
+            const int grid = (int)std::min<int64_t>(ceil_div64(2 * (a.kv_elems / 4), 256), 8192);
+            hipLaunchKernelGGL(flash_bwd_kv_sum_kernel, dim3(grid), dim3(256), 0, stream,
+                               a.kv_part, a.gsplit, a.kv_elems, a.dK, a.dV);
+        }
     }
+}
+
+// dK/dV workgroups of a dense shape without a grouped-query split.
+template <int D>
+int64_t dkdv_workgroups(int B, int Hkv, int Sk) {
+    return (int64_t)B * Hkv * ceil_div(Sk, FbKv<D>::BLOCK) * FbKv<D>::DSPLIT;
 }
 
 }  // namespace
 
 int64_t flash_bwd_workspace_rows(const FlashBwdLaunch& f) {
     return f.cu_q ? (int64_t)f.H * f.total_q : (int64_t)f.B * f.H * f.Sq;
+}
+
+int flash_bwd_group_split(int B, int H, int Hkv, int Sq, int Sk, int D, int num_cus) {
+    if (B <= 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0 || Sq <= 0 || Sk <= 0 || num_cus <= 0)
+        return 1;
+    const int group = H / Hkv;
+    if (group == 1) return 1;
+    const int64_t wgs = D > 128 ? dkdv_workgroups<256>(B, Hkv, Sk)
+                                : D > 64 ? dkdv_workgroups<128>(B, Hkv, Sk)
+                                         : dkdv_workgroups<64>(B, Hkv, Sk);
+    if (2 * wgs > num_cus) return 1;  // at least half the CUs busy without a split
+    const int s = (int)std::min<int64_t>(group, ceil_div64(num_cus, wgs));
+    // whole heads per part, no empty part
+    const int gper = ceil_div(group, s);
+    return ceil_div(group, gper);
+}
+
+size_t flash_bwd_split_bytes(int B, int Hkv, int Sk, int D, int gsplit) {
+    if (gsplit <= 1) return 0;
+    return (size_t)2 * gsplit * (size_t)B * Hkv * Sk * D * sizeof(float);
 }
 
 hipError_t launch_flash_bwd(const FlashBwdLaunch& f, hipStream_t stream) {
@@ -778,6 +880,14 @@ hipError_t launch_flash_bwd(const FlashBwdLaunch& f, hipStream_t stream) {
     a.Hkv = f.Hkv;
     a.total_q = f.total_q;
     a.total_k = f.total_k;
+    a.gsplit = 1;
+    a.gper = a.group;
+    if (!f.cu_q && f.gsplit > 1 && f.kv_part) {
+        a.gsplit = f.gsplit;
+        a.gper = ceil_div(a.group, f.gsplit);
+        a.kv_part = f.kv_part;
+        a.kv_elems = (int64_t)f.B * f.Hkv * f.Sk * f.D;
+    }
     if (f.D > 128)
         launch_bwd_d<256>(a, f.B, f.causal, stream);
     else if (f.D > 64)

@@ -140,8 +140,17 @@ struct FlashBwdLaunch {
     const int* cu_q = nullptr;
     const int* cu_k = nullptr;
     int total_q = 0, total_k = 0;
+    // Dense grouped-query attention: split the dK/dV kernel's query heads of a group over
+    // gsplit workgroups (> 1) whose fp32 partial dK, dV go to kv_part
+    // (flash_bwd_split_bytes, 16-byte aligned), added by a second kernel.
+    int gsplit = 1;
+    float* kv_part = nullptr;
 };
 int64_t flash_bwd_workspace_rows(const FlashBwdLaunch& f);
+// Grouped-query split of the dK/dV kernel for a dense shape on num_cus CUs (1: none): only
+// when its workgroups would leave more than half the CUs idle.
+int flash_bwd_group_split(int B, int H, int Hkv, int Sq, int Sk, int D, int num_cus);
+size_t flash_bwd_split_bytes(int B, int Hkv, int Sk, int D, int gsplit);
 hipError_t launch_flash_bwd(const FlashBwdLaunch& f, hipStream_t stream);
 
 }  // namespace wmma_amd
