@@ -35,6 +35,8 @@ Workload families (--workload):
              limit's share of the random-input figures)
   decode     flash attention with 1-16 queries against 4096-32768 keys (MHA and 8 K/V heads,
              D 128 / 256): the split-key-range forward against the one-pass forward
+  bwd_gqa    flash-attention backward with 4-8 K/V heads at 1024-4096 tokens: the
+             grouped-query split of the dK/dV kernel against the unsplit backward
   copy       a plain 256 MiB device copy (calibrates the rocprofv3 byte counters)
   mfma_ceiling  the matrix pipe's sustained rate with register operands and no memory
              traffic (libwmma_calib.so): the ceiling the GEMM main loop is held against;
@@ -537,6 +539,52 @@ def fam_decode(wo):
         del Ks, Vs
 
 
+def fam_bwd_gqa(wo):
+    """Flash-attention backward with few key/value heads (grouped-query attention, short
+    sequences): the product path (wo.flash_attention_backward: the group's query heads split
+    over more dK/dV workgroups, partial sums added by a second kernel) against the unsplit
+    backward through the C-ABI with only the row-statistics workspace, in one process."""
+    import ctypes
+
+    import torch
+
+    from oracle import attention as oatt
+
+    L = ctypes.CDLL(wo.LIBRARY_PATH)
+    vp, i32, f32, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    L.wmma_flash_attn_bwd_workspace_size.restype = sz
+    L.wmma_flash_attn_bwd_workspace_size.argtypes = [i32] * 3
+    L.wmma_flash_attn_bwd.argtypes = [vp] * 10 + [sz] + [i32] * 6 + [f32, i32, vp]
+    for (B, H, Hkv, S, D, causal) in [(1, 32, 8, 2048, 128, True), (1, 32, 8, 2048, 128, False),
+                                      (1, 16, 4, 1024, 128, True), (2, 32, 4, 1024, 128, True),
+                                      (1, 32, 8, 4096, 128, True)]:
+        Q, K, V = oatt.make_inputs(B, H, S, D, seed=42 + 8, Hkv=Hkv)
+        g = torch.Generator().manual_seed(43)
+        dO = torch.randn(B, H, S, D, generator=g).half().cuda()
+        Qd, Kd, Vd = Q.cuda(), K.cuda(), V.cuda()
+        O, lse = wo.flash_attention_forward(Qd, Kd, Vd, causal)
+        fl = 2.5 * 4.0 * B * H * D * (S * (S + 1) / 2 if causal else S * S)
+        base = L.wmma_flash_attn_bwd_workspace_size(B, H, S)
+        ws = torch.empty(base, dtype=torch.uint8, device="cuda")
+        dQ, dK, dV = torch.empty_like(Qd), torch.empty_like(Kd), torch.empty_like(Vd)
+
+        def unsplit(i):
+            rc = L.wmma_flash_attn_bwd(dO.data_ptr(), Qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(),
+                                       O.data_ptr(), lse.data_ptr(), dQ.data_ptr(), dK.data_ptr(),
+                                       dV.data_ptr(), ws.data_ptr(), base, B, H, Hkv, S, S, D,
+                                       1.0 / math.sqrt(D), 1 if causal else 0,
+                                       torch.cuda.current_stream().cuda_stream)
+            assert rc == 0
+
+        for path, fn in (("split", lambda i: wo.flash_attention_backward(dO, Qd, Kd, Vd, O, lse, causal)),
+                         ("unsplit", unsplit)):
+            ms = time_batches(fn, 5)
+            line(family="bwd_gqa", path=path, B=B, H=H, Hkv=Hkv, S=S, D=D, causal=causal,
+                 us=round(ms * 1e3, 1), TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
+                 frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4))
+        del ws, dQ, dK, dV
+
+
 def fam_flash_operands(wo):
     """configs[4] non-causal, forward and backward, on all-ones Q, K, V (and dO): the same
     kernels and traffic with operand bits that never switch -- against the random-input
@@ -785,7 +833,8 @@ def fam_read_floor(wo):
 FAMILIES = {"gemm": fam_gemm, "epilogue": fam_epilogue, "skinny": fam_skinny, "ragged": fam_ragged,
             "w4a16": fam_w4a16, "flash": fam_flash, "copy": fam_copy,
             "mfma_ceiling": fam_mfma_ceiling, "read_floor": fam_read_floor, "lds_read": fam_lds_read,
-            "flash_operands": fam_flash_operands, "decode": fam_decode, "vendor": fam_vendor}
+            "flash_operands": fam_flash_operands, "decode": fam_decode, "bwd_gqa": fam_bwd_gqa,
+            "vendor": fam_vendor}
 
 
 # ------------------------------------------------------------------------ headline --
@@ -998,7 +1047,7 @@ def main():
     QUICK = args.quick and bool(args.suite or args.workload)
     if args.suite:
         for name in ("gemm", "epilogue", "skinny", "ragged", "w4a16", "flash", "flash_operands",
-                     "decode"):
+                     "decode", "bwd_gqa"):
             FAMILIES[name](wo)
     elif args.workload:
         FAMILIES[args.workload](wo)

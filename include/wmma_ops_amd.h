@@ -360,16 +360,18 @@ int wmma_flash_attn_varlen_fwd_lse(const void* Q, const void* K, const void* V, 
 size_t wmma_flash_attn_bwd_workspace_size(int B, int H, int Sq);
 
 /*
- * Workspace bytes with which wmma_flash_attn_bwd (dense layout) also splits a grouped-query
- * group's query heads over more dK/dV workgroups, for shapes whose dK/dV workgroups would
- * leave more than half the CUs idle (few key/value heads, short sequences): the row
+ * Workspace bytes with which wmma_flash_attn_bwd (dense layout, same shape and causal flag)
+ * also splits a grouped-query group's query heads over more dK/dV workgroups, for shapes
+ * whose dK/dV workgroups would fill less than half of one wave of the CUs, or with a causal
+ * mask at most one wave (its first key blocks carry twice the average work): the row
  * statistics rounded up to 256 bytes, then fp32 partial dK and dV per part, added by a
  * second kernel in part order (deterministic; within fp32 rounding of the unsplit pass).
  * Equals wmma_flash_attn_bwd_workspace_size(B, H, Sq) when no split applies; any workspace
  * of at least that size (16-byte aligned for the split) works, a smaller one than this
  * runs unsplit.  No counterpart in the reference.
  */
-size_t wmma_flash_attn_bwd_split_workspace_size(int B, int H, int Hkv, int Sq, int Sk, int D);
+size_t wmma_flash_attn_bwd_split_workspace_size(int B, int H, int Hkv, int Sq, int Sk, int D,
+                                                int causal);
 
 /*
  * Flash-attention backward.  Given dO [B,H,Sq,D] and the forward's Q, K, V, O and lse

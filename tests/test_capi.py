@@ -417,15 +417,22 @@ def test_flash_bwd_split_workspace(lib):
     lib.wmma_flash_attn_bwd_workspace_size.restype = ctypes.c_size_t
     f = lib.wmma_flash_attn_bwd_split_workspace_size
     f.restype = ctypes.c_size_t
-    f.argtypes = [ctypes.c_int] * 6
+    f.argtypes = [ctypes.c_int] * 7
     stats = lambda B, H, S: 2 * 4 * B * H * S
+    part = lambda gs, B, Hkv, S, D: 2 * gs * B * Hkv * S * D * 4
     # 8 K/V heads x 16 key blocks = 128 workgroups: 2 parts of 2 query heads each
-    assert f(1, 32, 8, 2048, 2048, 128) == stats(1, 32, 2048) + 2 * 2 * 8 * 2048 * 128 * 4
-    assert f(4, 32, 32, 4096, 4096, 128) == stats(4, 32, 4096)     # no group
-    assert f(1, 32, 8, 4096, 4096, 128) == stats(1, 32, 4096)      # 256 workgroups: full
+    assert f(1, 32, 8, 2048, 2048, 128, 0) == stats(1, 32, 2048) + part(2, 1, 8, 2048, 128)
+    assert f(1, 32, 8, 2048, 2048, 128, 1) == stats(1, 32, 2048) + part(2, 1, 8, 2048, 128)
+    # 2 x 4 K/V heads x 8 key blocks = 64 workgroups: 4 parts
+    assert f(2, 32, 4, 1024, 1024, 128, 1) == stats(2, 32, 1024) + part(4, 2, 4, 1024, 128)
+    assert f(4, 32, 32, 4096, 4096, 128, 1) == stats(4, 32, 4096)     # no group
+    # 256 workgroups fill one wave: unsplit without a mask, 2 parts with one
+    assert f(1, 32, 8, 4096, 4096, 128, 0) == stats(1, 32, 4096)
+    assert f(1, 32, 8, 4096, 4096, 128, 1) == stats(1, 32, 4096) + part(2, 1, 8, 4096, 128)
+    assert f(1, 32, 8, 8192, 8192, 128, 1) == stats(1, 32, 8192)      # two waves already
     # D = 64 (256 keys per workgroup): 4 workgroups, one part per query head
-    assert f(1, 32, 1, 1024, 1024, 64) == stats(1, 32, 1024) + 2 * 32 * 1024 * 64 * 4
-    assert f(1, 8, 2, 0, 100, 64) == 0
+    assert f(1, 32, 1, 1024, 1024, 64, 0) == stats(1, 32, 1024) + part(32, 1, 1, 1024, 64)
+    assert f(1, 8, 2, 0, 100, 64, 0) == 0
 
 
 def test_flash_training_validation_codes(lib):

@@ -265,10 +265,10 @@ def test_flash_bwd_group_split(wo, B, H, Hkv, Sq, Sk, D, causal):
     lib.wmma_flash_attn_bwd_workspace_size.restype = sz
     lib.wmma_flash_attn_bwd_workspace_size.argtypes = [i32] * 3
     lib.wmma_flash_attn_bwd_split_workspace_size.restype = sz
-    lib.wmma_flash_attn_bwd_split_workspace_size.argtypes = [i32] * 6
+    lib.wmma_flash_attn_bwd_split_workspace_size.argtypes = [i32] * 7
     lib.wmma_flash_attn_bwd.argtypes = [vp] * 10 + [sz] + [i32] * 6 + [f32, i32, vp]
     base = lib.wmma_flash_attn_bwd_workspace_size(B, H, Sq)
-    full = lib.wmma_flash_attn_bwd_split_workspace_size(B, H, Hkv, Sq, Sk, D)
+    full = lib.wmma_flash_attn_bwd_split_workspace_size(B, H, Hkv, Sq, Sk, D, 1 if causal else 0)
     report("flash_bwd_group_split", B=B, H=H, Hkv=Hkv, Sq=Sq, Sk=Sk, D=D, causal=causal, ws=full)
     assert full > base, "the shape should take the split"
     Q, K, V = oatt.make_inputs(B, H, Sq, D, seed=B + H + Sq + D, Sk=Sk, Hkv=Hkv)

@@ -737,7 +737,8 @@ int flash_bwd_run(FlashBwdLaunch& f, void* workspace, size_t workspace_bytes, vo
     // group's query heads are split over more workgroups when the workspace also holds their
     // fp32 partial dK, dV (behind the row statistics, 256-byte aligned).
     if (!f.cu_q && has_q && has_k) {
-        const int gs = flash_bwd_group_split(f.B, f.H, f.Hkv, f.Sq, f.Sk, f.D, current_cus());
+        const int gs =
+            flash_bwd_group_split(f.B, f.H, f.Hkv, f.Sq, f.Sk, f.D, f.causal, current_cus());
         const size_t part = flash_bwd_split_bytes(f.B, f.Hkv, f.Sk, f.D, gs);
         if (gs > 1 && workspace_bytes >= round256(need) + part && aligned16(workspace)) {
             f.gsplit = gs;
@@ -748,12 +749,13 @@ int flash_bwd_run(FlashBwdLaunch& f, void* workspace, size_t workspace_bytes, vo
 }
 }  // namespace
 
-size_t wmma_flash_attn_bwd_split_workspace_size(int B, int H, int Hkv, int Sq, int Sk, int D) {
+size_t wmma_flash_attn_bwd_split_workspace_size(int B, int H, int Hkv, int Sq, int Sk, int D,
+                                                int causal) {
     if (B <= 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0 || Sq <= 0 || Sk <= 0 || D <= 0 ||
         D % 8 != 0 || D > kFlashMaxDBwd)
         return wmma_flash_attn_bwd_workspace_size(B, H, Sq);
     const size_t need = wmma_flash_attn_bwd_workspace_size(B, H, Sq);
-    const int gs = flash_bwd_group_split(B, H, Hkv, Sq, Sk, D, current_cus());
+    const int gs = flash_bwd_group_split(B, H, Hkv, Sq, Sk, D, causal != 0, current_cus());
     return gs > 1 ? round256(need) + flash_bwd_split_bytes(B, Hkv, Sk, D, gs) : need;
 }
 

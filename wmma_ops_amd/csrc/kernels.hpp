@@ -147,9 +147,10 @@ struct FlashBwdLaunch {
     float* kv_part = nullptr;
 };
 int64_t flash_bwd_workspace_rows(const FlashBwdLaunch& f);
-// Grouped-query split of the dK/dV kernel for a dense shape on num_cus CUs (1: none): only
-// when its workgroups would leave more than half the CUs idle.
-int flash_bwd_group_split(int B, int H, int Hkv, int Sq, int Sk, int D, int num_cus);
+// Grouped-query split of the dK/dV kernel for a dense shape on num_cus CUs (1: none): when
+// its workgroups would fill less than half of one wave, or (causal) at most one wave.
+int flash_bwd_group_split(int B, int H, int Hkv, int Sq, int Sk, int D, bool causal,
+                          int num_cus);
 size_t flash_bwd_split_bytes(int B, int Hkv, int Sk, int D, int gsplit);
 hipError_t launch_flash_bwd(const FlashBwdLaunch& f, hipStream_t stream);
 

@@ -311,7 +311,7 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> flash_attention_backward
     auto dV = torch::empty_like(V);
     // row statistics, plus the grouped-query split's partial dK/dV where it applies
     const size_t ws_bytes = wmma_flash_attn_bwd_split_workspace_size(
-        (int)B, (int)H, (int)K.size(1), (int)Sq, (int)K.size(2), (int)Dp);
+        (int)B, (int)H, (int)K.size(1), (int)Sq, (int)K.size(2), (int)Dp, causal ? 1 : 0);
     auto ws = torch::empty({(int64_t)((ws_bytes + 3) / 4)}, Q.options().dtype(torch::kFloat32));
     int rc = wmma_flash_attn_bwd(dO.data_ptr(), Q.data_ptr(), K.data_ptr(), V.data_ptr(),
                                  O.data_ptr(), lse.data_ptr<float>(), dQ.data_ptr(), dK.data_ptr(),
