@@ -43,6 +43,8 @@ Workload families (--workload):
              and the 4096^3 GEMM itself on random and on constant operands
   lds_read   the LDS read rate of ds_read_b128 and ds_read_b64_tr_b16 (contiguous and in the
              flash forward's V-fragment pattern), the LDS side of the MFMA kernels
+  l2_read    the activation stage of the small-M LDS-DMA GEMMs alone: 64-row x 128-byte
+             blocks from L2 into LDS, 4 or 8 waves, 7, 3 or no blocks in flight
   read_floor a plain streaming read of the W4A16 M=1 weight sizes and of 1 GiB in several
              launch shapes, graph replayed over rotating buffers: the floor of the
              HBM-bound kernels (the fastest shape)
@@ -691,6 +693,10 @@ def calib_lib():
     L.wmma_calib_lds_read.argtypes = [i32, i32, i32, vp, vp]
     L.wmma_calib_lds_read_bytes.argtypes = [i32, i32]
     L.wmma_calib_lds_read_bytes.restype = ctypes.c_double
+    sz = ctypes.c_size_t
+    L.wmma_calib_l2_stage.argtypes = [i32, i32, i32, vp, sz, sz, i32, i32, vp, vp]
+    L.wmma_calib_l2_stage_bytes.argtypes = [i32, i32]
+    L.wmma_calib_l2_stage_bytes.restype = ctypes.c_double
     return L
 
 
@@ -772,6 +778,34 @@ def fam_lds_read(wo):
              config=f"{wgs} workgroups x 8 waves x {iters} iterations x 8 KB")
 
 
+def fam_l2_read(wo):
+    """The activation stage of the small-M LDS-DMA GEMMs alone (libwmma_calib.so): 224
+    workgroups (the W4A16 GEMM grid at M = 128, N = 14336) copy 64-row x 128-byte blocks of
+    a 1 MB L2-resident buffer (rows 8 KB apart, as A at K = 4096) into LDS, 4 or 8 waves per
+    workgroup, 7, 3 or no blocks in flight; and the same bytes as contiguous 8 KB blocks."""
+    import torch
+
+    L = calib_lib()
+    wgs, iters, row_bytes = 224, 64, 8192
+    nb = 128 * row_bytes
+    src = torch.ones(nb // 2, dtype=torch.float16, device="cuda")
+    sink = torch.zeros(wgs, device="cuda")
+    nbytes = L.wmma_calib_l2_stage_bytes(wgs, iters)
+    for strided, waves, depth in ((1, 4, 4), (1, 4, 8), (1, 4, 1), (1, 8, 4), (1, 8, 8), (1, 8, 1),
+                                  (0, 4, 4), (0, 8, 4)):
+        st = torch.cuda.current_stream().cuda_stream
+        fn = lambda i: L.wmma_calib_l2_stage(waves, depth, strided, src.data_ptr(), nb, row_bytes,
+                                             wgs, iters, sink.data_ptr(), st)
+        assert fn(0) == 0
+        ms = time_batches(fn, 400 if not QUICK else 2, batches=3)
+        line(family="l2_read", pattern="64 rows x 128 B, rows 8 KB apart" if strided else
+             "contiguous 8 KB blocks", waves=waves, blocks_in_flight=depth - 1,
+             us_per_launch=round(ms * 1e3, 2), ns_per_block=round(ms * 1e6 / iters, 1),
+             GBps_per_cu=round(nbytes / (ms * 1e-3) / 1e9 / wgs, 1),
+             TBps_chip=round(nbytes / (ms * 1e-3) / 1e12, 2),
+             config=f"{wgs} workgroups x {iters} blocks of 8 KB")
+
+
 def read_floor_best(nbytes, shapes=((64, 16), (256, 2), (512, 2))):
     """(us, shape) of the fastest plain streaming read of nbytes (rounded down to 16) over
     the given launch shapes, graph-replayed over rotating buffers like the W4A16 figures."""
@@ -833,6 +867,7 @@ def fam_read_floor(wo):
 FAMILIES = {"gemm": fam_gemm, "epilogue": fam_epilogue, "skinny": fam_skinny, "ragged": fam_ragged,
             "w4a16": fam_w4a16, "flash": fam_flash, "copy": fam_copy,
             "mfma_ceiling": fam_mfma_ceiling, "read_floor": fam_read_floor, "lds_read": fam_lds_read,
+            "l2_read": fam_l2_read,
             "flash_operands": fam_flash_operands, "decode": fam_decode, "bwd_gqa": fam_bwd_gqa,
             "vendor": fam_vendor}
 

@@ -48,6 +48,15 @@ int wmma_calib_read_stream(const void* src, size_t bytes, int loads_per_wave, fl
 int wmma_calib_read_stream_shape(const void* src, size_t bytes, int threads, int loads_per_lane,
                                  float* sink, void* stream);
 
+/* The activation stage of the small-M LDS-DMA GEMMs, alone: `workgroups` workgroups of
+ * `waves` (4 or 8) waves each copy `iters` 64-row x 128-byte blocks (rows `row_bytes`
+ * apart; `strided` = 0: contiguous 8 KB blocks of the same buffer) from an L2-resident
+ * buffer of `bytes` (>= 128 rows) into LDS by buffer_load ... lds, `depth` (1, 4 or 8) - 1
+ * blocks in flight.  Bytes moved: wmma_calib_l2_stage_bytes. */
+int wmma_calib_l2_stage(int waves, int depth, int strided, const void* src, size_t bytes,
+                        size_t row_bytes, int workgroups, int iters, float* sink, void* stream);
+double wmma_calib_l2_stage_bytes(int workgroups, int iters);
+
 #ifdef __cplusplus
 }
 #endif

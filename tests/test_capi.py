@@ -87,10 +87,13 @@ def test_calibration_library_exports_its_header():
     # bench.py's measuring instruments (include/wmma_calib.h, libwmma_calib.so)
     calib = ctypes.CDLL(os.path.join(ROOT, "wmma_ops_amd", "libwmma_calib.so"))
     names = declared_functions(os.path.join(ROOT, "include", "wmma_calib.h"))
-    assert names == ["wmma_calib_lds_read", "wmma_calib_lds_read_bytes",
+    assert names == ["wmma_calib_l2_stage", "wmma_calib_l2_stage_bytes",
+                     "wmma_calib_lds_read", "wmma_calib_lds_read_bytes",
                      "wmma_calib_mfma_ceiling", "wmma_calib_mfma_ceiling_flops",
                      "wmma_calib_read_stream", "wmma_calib_read_stream_shape"], names
     assert not [n for n in names if not hasattr(calib, n)]
+    calib.wmma_calib_l2_stage_bytes.restype = ctypes.c_double
+    assert calib.wmma_calib_l2_stage_bytes(224, 64) == 224 * 64 * 8192.0
     calib.wmma_calib_mfma_ceiling_flops.restype = ctypes.c_double
     assert calib.wmma_calib_mfma_ceiling_flops(512, 1000) == 512 * 4 * 8 * 1000 * 2.0 * 32 * 32 * 16
     # argument checks return before any launch
@@ -105,6 +108,12 @@ def test_calibration_library_exports_its_header():
     calib.wmma_calib_lds_read.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                           ctypes.c_void_p]
     assert calib.wmma_calib_lds_read(3, 256, 10, 0x10000, None) == 2
+    sz = ctypes.c_size_t
+    calib.wmma_calib_l2_stage.argtypes = [ctypes.c_int] * 3 + [ctypes.c_void_p, sz, sz] + \
+        [ctypes.c_int] * 2 + [ctypes.c_void_p] * 2
+    assert calib.wmma_calib_l2_stage(4, 4, 1, 0x10000, 1 << 20, 100, 224, 64, 0x10000, None) == 1
+    assert calib.wmma_calib_l2_stage(4, 4, 1, 0x10000, 1 << 19, 8192, 224, 64, 0x10000, None) == 1
+    assert calib.wmma_calib_l2_stage(2, 4, 1, 0x10000, 1 << 20, 8192, 224, 64, 0x10000, None) == 2
     assert calib.wmma_calib_lds_read(0, 0, 10, 0x10000, None) == 1
     calib.wmma_calib_lds_read_bytes.restype = ctypes.c_double
     assert calib.wmma_calib_lds_read_bytes(2, 3) == 2 * 8 * 3 * 8192

@@ -135,9 +135,68 @@ __global__ void __launch_bounds__(512) lds_read_kernel(int iters, float* sink) {
     if (x == 0x9E3779B9u) sink[blockIdx.x] = 1.0f;  // keeps the reads observable
 }
 
+// The activation stage of the small-M LDS-DMA GEMMs: every iteration a workgroup copies a
+// 64-row x 128-byte block (rows `row_bytes` apart, block column it % (row_bytes / 128);
+// workgroups alternate between two 64-row blocks like two M tiles) from an L2-resident
+// buffer into LDS by buffer_load ... lds, NW waves of 8 / NW 1 KB loads each, with
+// DEPTH - 1 stages in flight (DEPTH = 1: each stage waited for before the next is
+// issued).  strided = 0 reads the same bytes as contiguous 8 KB blocks instead.
+template <int NW, int DEPTH>
+__global__ void __launch_bounds__(NW * 64) l2_stage_kernel(const u32x4* src, uint32_t bytes,
+                                                           uint32_t row_bytes, int iters,
+                                                           int strided, float* sink) {
+    constexpr int U = 8 / NW;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[DEPTH * 8192];
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(src);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t cols = row_bytes / 128u;
+    const uint32_t base = (blockIdx.x & 1u) * 64u * row_bytes;
+    for (int it = 0; it < iters; ++it) {
+        const uint32_t kc = (uint32_t)it % cols;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t row = (uint32_t)((wave * U + u) * 8 + (lane >> 3));
+            const uint32_t off = strided ? base + row * row_bytes + kc * 128u + (uint32_t)(lane & 7) * 16u
+                                         : base + (kc * 64u + row) * 128u + (uint32_t)(lane & 7) * 16u;
+            lds_dma16(r, off % bytes,
+                      (WMMA_LDS unsigned char*)smem + (it % DEPTH) * 8192 + (wave * U + u) * 1024);
+        }
+        wait_vmcnt<(DEPTH - 1) * U>();
+        __builtin_amdgcn_s_barrier();
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (smem[threadIdx.x] == 0xAB && smem[threadIdx.x + 1] == 0xCD) sink[blockIdx.x] = 1.0f;
+}
+
 }  // namespace
 
 extern "C" {
+
+int wmma_calib_l2_stage(int waves, int depth, int strided, const void* src, size_t bytes,
+                        size_t row_bytes, int workgroups, int iters, float* sink, void* stream) {
+    if (!src || !sink || workgroups <= 0 || iters <= 0 || row_bytes < 128 || row_bytes % 128 != 0 ||
+        bytes < 128 * row_bytes || bytes > 0x7FFFFFFFu || (reinterpret_cast<uintptr_t>(src) & 15u) != 0)
+        return 1;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const auto s = static_cast<const u32x4*>(src);
+    const uint32_t b = (uint32_t)bytes, rb = (uint32_t)row_bytes;
+#define WMMA_CALIB_L2(W, D)                                                                     \
+    if (waves == (W) && depth == (D)) {                                                         \
+        hipLaunchKernelGGL((l2_stage_kernel<W, D>), dim3(workgroups), dim3((W) * 64), 0, st, s,   \
+                           b, rb, iters, strided, sink);                                         \
+        return hipGetLastError() == hipSuccess ? 0 : 5;                                         \
+    }
+    WMMA_CALIB_L2(4, 1) WMMA_CALIB_L2(4, 4) WMMA_CALIB_L2(4, 8) WMMA_CALIB_L2(8, 1) WMMA_CALIB_L2(8, 4)
+    WMMA_CALIB_L2(8, 8)
+#undef WMMA_CALIB_L2
+    return 2;
+}
+
+double wmma_calib_l2_stage_bytes(int workgroups, int iters) {
+    return (double)workgroups * (double)iters * 8192.0;
+}
 
 int wmma_calib_mfma_ceiling(int workgroups, int iters, const void* operands, float* sink,
                             void* stream) {
