@@ -23,7 +23,8 @@ matmul at N=14336, and fp32 SDPA on 2 heads of configs[4].
 Workload families (--workload):
   gemm       configs[0..1]: M=N=K in {512,1024,2048,4096} and 4096x4096x2048
   epilogue   configs[1]: C = 2.0*A@B + 0.5*C, out-of-place and in-place, 1024^3/4096^3
-  skinny     configs[2]: M in {1,16,64,128} x N in {4096,11008,14336}, K=4096; K=14336,N=4096
+  skinny     configs[2]: M in {1,16,64,128} x N in {4096,11008,14336}, K=4096; K=14336,N=4096;
+             and M=32 on the same shapes
   ragged     N or K off a multiple of 8 (4096x4100x4096, 2048x32001x4096, M = 1..4096): the
              repacked product path, the element-wise in-place path and the aligned neighbour
              shape; shapes off the 256 grid (M = 4100..8200, N = 4352..14336): the planner's
@@ -250,8 +251,10 @@ def fam_skinny(wo):
 
     from oracle import gemm as og
 
+    # configs[2], plus M = 32 (between its rows: the skinny kernel's two-block form)
     shapes = [(m, n, 4096) for m in (1, 16, 64, 128) for n in (4096, 11008, 14336)] + \
-             [(m, 4096, 14336) for m in (1, 16, 64, 128)]
+             [(m, 4096, 14336) for m in (1, 16, 64, 128)] + \
+             [(32, n, 4096) for n in (4096, 11008, 14336)] + [(32, 4096, 14336)]
     for (m, n, k) in shapes:
         g = torch.Generator().manual_seed(42 + 2)
         A = torch.randn(m, k, generator=g).half()

@@ -47,7 +47,7 @@ extern "C" {
 
 /* Kernel families a GEMM plan can select. */
 #define WMMA_KERNEL_TILED 0   /* MFMA tiled kernel (optionally split-K + reduce)        */
-#define WMMA_KERNEL_SKINNY 1  /* M <= 16 streaming kernel, split-K + reduce             */
+#define WMMA_KERNEL_SKINNY 1  /* M <= 64 streaming kernel (planner: M <= 32), split-K   */
 
 /* Two-part GEMMs (wmma_gemm_plan.edge_dim).  A shape whose 256x256 tiles fill some whole
  * waves of the chip plus a small partial one can run as two launches: the bulk (rows or

@@ -168,6 +168,15 @@ def test_plan_make(lib):
         assert (p.tile_m, p.tile_n, p.split_k) == (bm, bn, 1)
     assert lib.wmma_gemm_plan_make(10, 10, 10, 9, 256, ctypes.byref(p)) == INVALID
     assert lib.wmma_gemm_plan_make(10, 10, 10, -1, 256, None) == INVALID
+    # 16 < M <= 32: the skinny kernel with two 16-row blocks, the largest K split whose
+    # workgroups fit one wave of the CUs (measured fastest of splits 1-8)
+    for (M, N, K), split in {(32, 4096, 4096): 8, (17, 11008, 4096): 2, (32, 14336, 4096): 2,
+                             (32, 4096, 14336): 8, (24, 32768, 4096): 1}.items():
+        assert lib.wmma_gemm_plan_make(M, N, K, -1, 256, ctypes.byref(p)) == OK
+        assert (p.kernel, p.tile_m, p.tile_n, p.split_k) == (1, 32, 128, split), (M, N, K)
+    # M = 33..64 keeps the tiled kernel; 48 x 4096 x 4096 (1.5 x 2^29 multiply-adds) splits
+    assert lib.wmma_gemm_plan_make(48, 4096, 4096, -1, 256, ctypes.byref(p)) == OK
+    assert p.kernel == 0 and p.split_k > 1
 
 
 class W4Plan(ctypes.Structure):
@@ -178,7 +187,7 @@ class W4Plan(ctypes.Structure):
 def test_gemm_workspace_size_covers_repacked_operands(lib):
     # Contiguous operands: K or N off a multiple of 8 adds a zero-padded copy of A [M][K8]
     # and/or B [K][N8] (256-byte rounded, plus 256 bytes of alignment slack) to the split-K
-    # partial sums -- except B under the skinny kernel (M <= 16), which reads it in place;
+    # partial sums -- except B under the skinny kernel (M <= 32), which reads it in place;
     # aligned shapes need only the partial sums.
     r256 = lambda x: (x + 255) // 256 * 256
     p = Plan()
@@ -337,7 +346,7 @@ def test_plan_custom_validation(lib):
     assert (p.kernel, p.tile_cfg, p.split_k, p.k_per_split) == (0, 3, 4, 1024)
     assert p.workspace_bytes == 4 * 64 * 64 * 4
     assert lib.wmma_gemm_plan_custom(64, 64, 4096, 0, 6, 1, ctypes.byref(p)) == INVALID   # no such tile
-    assert lib.wmma_gemm_plan_custom(17, 64, 4096, 1, -1, 2, ctypes.byref(p)) == INVALID  # skinny: M <= 16
+    assert lib.wmma_gemm_plan_custom(65, 64, 4096, 1, -1, 2, ctypes.byref(p)) == INVALID  # skinny: M <= 64
     assert lib.wmma_gemm_plan_custom(16, 64, 128, 1, -1, 4, ctypes.byref(p)) == INVALID   # K < 64 per split
     assert lib.wmma_gemm_plan_custom(16, 64, 4096, 2, 0, 1, ctypes.byref(p)) == INVALID   # no such kernel
     assert lib.wmma_gemm_plan_custom(16, 64, 4096, 0, 0, 33, ctypes.byref(p)) == INVALID  # split > 32

@@ -108,7 +108,8 @@ def test_gemm_beta_rules(wo):
 
 # skinny shapes that take the split-K / streaming paths
 SKINNY = [(m, n, 4096) for m in (1, 16, 64, 128) for n in (4096, 11008, 14336)] + \
-         [(m, 4096, 14336) for m in (1, 16, 64, 128)]
+         [(m, 4096, 14336) for m in (1, 16, 64, 128)] + \
+         [(m, n, 4096) for m in (17, 32, 48) for n in (4096, 11008)] + [(32, 4096, 14336)]
 
 
 @pytest.mark.parametrize("M,N,K", SKINNY)
@@ -197,7 +198,8 @@ def test_skinny_split_k_any_workspace(wo, M, N, K):
 # Explicit plans (the autotuner's entry point): every kernel, tile and split gives the
 # oracle's result within tolerance, including the epilogue.
 @pytest.mark.parametrize("kernel,tile,split", [(0, t, s) for t in range(6) for s in (1, 3, 8)] +
-                         [(1, -1, s) for s in (1, 5, 32)])
+                         [(1, -1, s) for s in (1, 5, 32)] + [(1, -2, s) for s in (1, 3)] +
+                         [(1, -4, s) for s in (1, 6)])
 def test_gemm_explicit_plans(wo, kernel, tile, split):
     import ctypes
     from tests.test_capi import Plan
@@ -207,11 +209,15 @@ def test_gemm_explicit_plans(wo, kernel, tile, split):
     vp, i64, i32, f32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
     lib.wmma_gemm_f16f32_plan.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, f32, f32,
                                           ctypes.POINTER(Plan), vp, sz, vp]
-    M, N, K = (13, 200, 4096) if kernel == 1 else (300, 264, 2560)
+    # skinny plans: tile -1 / -2 / -4 picks one, two or four 16-row blocks of A (M = 13,
+    # 29, 61: the last block partly past M)
+    M, N, K = ({-1: 13, -2: 29, -4: 61}[tile], 200, 4096) if kernel == 1 else (300, 264, 2560)
     A, B = _inputs(M, N, K, 5 + tile + split)
     Cin = torch.randn(M, N, generator=torch.Generator().manual_seed(6))
     p = Plan()
-    assert lib.wmma_gemm_plan_custom(M, N, K, kernel, tile, split, ctypes.byref(p)) == 0
+    assert lib.wmma_gemm_plan_custom(M, N, K, kernel, -1 if kernel == 1 else tile, split,
+                                     ctypes.byref(p)) == 0
+    assert p.tile_m == (16 * -tile if kernel == 1 else p.tile_m)
     ws = torch.empty(max(p.workspace_bytes, 1), dtype=torch.uint8, device="cuda")
     Ad, Bd, C = A.cuda(), B.cuda(), Cin.cuda()
     rc = lib.wmma_gemm_f16f32_plan(Ad.data_ptr(), K, Bd.data_ptr(), N, C.data_ptr(), N, C.data_ptr(), N,
@@ -221,9 +227,10 @@ def test_gemm_explicit_plans(wo, kernel, tile, split):
     _check(C, og.gemm_ref(A, B, 2.0, 0.5, Cin))
 
 
-def test_skinny_epilogue_in_place(wo):
-    A, B = _inputs(16, 4096, 4096, 11, bstd=0.02)
-    C = torch.randn(16, 4096, generator=torch.Generator().manual_seed(12))
+@pytest.mark.parametrize("M", [16, 32])
+def test_skinny_epilogue_in_place(wo, M):
+    A, B = _inputs(M, 4096, 4096, 11, bstd=0.02)
+    C = torch.randn(M, 4096, generator=torch.Generator().manual_seed(12))
     ref = og.gemm_ref(A, B, 2.0, 0.5, C)
     Ci = C.cuda()
     wo.gemm_inplace(A.cuda(), B.cuda(), Ci, 2.0, 0.5)
@@ -275,7 +282,7 @@ def _repack_bytes(M, N, K, a, b):
 # past the reported size is written.
 @pytest.mark.parametrize("M,N,K,case", [
     (300, 4100, 520, "contig"), (640, 1000, 1004, "contig"), (70, 129, 513, "contig"),
-    (17, 4100, 4096, "contig"), (257, 3001, 64, "contig"),
+    (33, 4100, 4096, "contig"), (257, 3001, 64, "contig"),
     (96, 256, 320, "a_off"), (200, 136, 256, "b_ld"), (40, 640, 1024, "both")])
 def test_ragged_repack_matches_inplace(wo, M, N, K, case):
     report("ragged_repack", M=M, N=N, K=K, case=case, plan=wo.gemm_plan(M, N, K))
@@ -327,7 +334,7 @@ def test_ragged_repack_matches_inplace(wo, M, N, K, case):
     assert og.max_rel_err(outs[0], outs[1]) <= 1e-6
 
 
-# The skinny kernel (M <= 16) reads a B whose rows break 16-byte vectors in place: with B
+# The skinny kernel (M <= 32) reads a B whose rows break 16-byte vectors in place: with B
 # 4-byte aligned, rows are fetched by dword-aligned 16-byte loads (ldb even), or every other
 # row by a load from 2 bytes earlier plus one dword, realigned (ldb odd); the chunk that
 # straddles column N element-wise.  A with K off a multiple of 8 is repacked.  The same
@@ -335,7 +342,8 @@ def test_ragged_repack_matches_inplace(wo, M, N, K, case):
 # element-wise kernel: the products match it bit for bit and the oracle to the 1e-3 bar.
 @pytest.mark.parametrize("M,N,K,ldb_pad", [
     (1, 4100, 4096, 0), (16, 4100, 4096, 0), (1, 4101, 4096, 0), (7, 1027, 300, 0),
-    (3, 4096, 520, 3), (16, 32001, 256, 0), (1, 9, 64, 0), (2, 5, 16, 0), (9, 130, 1000, 1)])
+    (3, 4096, 520, 3), (16, 32001, 256, 0), (1, 9, 64, 0), (2, 5, 16, 0), (9, 130, 1000, 1),
+    (17, 4100, 4096, 0), (32, 1027, 300, 1), (25, 4101, 520, 3)])
 def test_skinny_unaligned_b_in_place(wo, M, N, K, ldb_pad):
     plan = wo.gemm_plan(M, N, K)
     report("skinny_unaligned_b", M=M, N=N, K=K, ldb=N + ldb_pad, plan=plan)

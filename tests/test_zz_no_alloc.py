@@ -91,7 +91,7 @@ def test_noalloc_scratch_covers_baseline_shapes():
 
 # Ragged shapes (N or K off a multiple of 8): the allocation-free entry point makes no
 # padded copies, so its operands go to the element-wise kernels (split-K partials in the
-# scratch array) or, at M <= 16, the skinny kernel's in-place B modes, while
+# scratch array) or, at M <= 32, the skinny kernel's in-place B modes, while
 # wmma_gemm_f16f32 with its full workspace repacks them for the vector kernels.  Both are
 # held to the oracle's 1e-3 bar and to each other (products bit-equal: the same MFMA
 # inputs in the same order; the alpha/beta epilogue to rounding).  Two calls in a row, the

@@ -6,7 +6,7 @@ select_tuned_tile.
                                     [--report PATH] [--min-gain 0.03]
 
 For every shape it times each plan the kernels can run -- the tiled LDS-DMA kernel with
-every tile (WMMA_TILE_*) and K split 1, 2, 4, 8, 16, and for M <= 16 the streaming skinny
+every tile (WMMA_TILE_*) and K split 1, 2, 4, 8, 16, and for M <= 64 the streaming skinny
 kernel with K splits 1..32 -- through the C-ABI (wmma_gemm_plan_custom,
 wmma_gemm_f16f32_plan), next to the planner's own choice.  Every plan's output is checked
 against the planner's (max relative error <= 1e-3) before it is timed.  Inputs are rotated
@@ -32,7 +32,7 @@ TABLE_PATH = os.path.join(ROOT, "csrc", "tuned_table.inc")
 
 KERNEL_TILED, KERNEL_SKINNY = 0, 1
 TILE_NAMES = ["64x64", "128x64", "256x64", "128x128", "256x128", "256x256"]
-SKINNY_MAX_M = 16
+SKINNY_MAX_M = 64
 ROTATE_BYTES = 600e6
 
 

@@ -166,7 +166,7 @@ static int gemm_run(const void* A, int64_t lda, const void* B, int64_t ldb, cons
         // 32-bit buffer offsets: one 256-row A tile and one 64-row B stage must fit (also
         // with the leading dimensions of repacked copies, at most 7 elements longer).
         if ((256 + 1) * (lda + 7) * 2 > kMaxOffset || (64 + 1) * (ldb + 7) * 2 > kMaxOffset ||
-            (int64_t)kSkinnyMaxM * (lda + 7) * 2 > kMaxOffset)
+            (int64_t)kSkinnyMaxMWide * (lda + 7) * 2 > kMaxOffset)
             return fail(WMMA_ERR_UNSUPPORTED, "leading dimension too large for 32-bit offsets");
     }
     wmma_gemm_plan plan{};

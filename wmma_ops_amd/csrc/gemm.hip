@@ -607,11 +607,13 @@ gemm_tiled_kernel(GemmArgs p) {
 }
 
 // ------------------------------------------------------------------------------------
-// Skinny kernel (M <= 16): C^T[N,M] = B^T[N,K] A^T[K,M] on MFMA 16x16x32.
-// Workgroup: 4 waves, 128 output columns, K range [kbeg,kend) split round-robin over the
-// waves in 32-deep steps.  Lane l loads B rows k0+8*(l/16)+0..7 at columns
+// Skinny kernel (M <= 16 * MB, MB = 1, 2, 4): C^T[N,M] = B^T[N,K] A^T[K,M] on MFMA
+// 16x16x32.  Workgroup: 4 waves, 128 output columns, K range [kbeg,kend) split round-robin
+// over the waves in 32-deep steps.  Lane l loads B rows k0+8*(l/16)+0..7 at columns
 // 8*(l%16)+0..7 (16 lanes read 256 contiguous bytes per row), transposes the 8x8 block
-// in registers, and issues 8 MFMAs: MFMA j covers columns 8*i+j (i = matrix row l%16).
+// in registers, and issues 8 MFMAs per 16 activation rows: MFMA j covers columns 8*i+j
+// (i = matrix row l%16) against rows 16*mb .. +15 of A, so each streamed B byte feeds MB
+// times the multiply-adds.
 // ------------------------------------------------------------------------------------
 constexpr int SK_COLS = kSkinnyBlockN;
 constexpr int SK_WAVES = 4;
@@ -628,14 +630,16 @@ enum SkinnyB {
                     // 2 bytes earlier plus the next dword, shifted together by v_alignbyte.
 };
 
-template <int BMODE>
+template <int BMODE, int MB>
 __global__ void __launch_bounds__(SK_WAVES * kWave)
 gemm_skinny_kernel(GemmArgs p) {
-    // Partial sums, row m = lane%16 of each wave, column n at n ^ ((n >> 2) & 16) of a row
-    // padded to 129 floats: one store instruction (64 lanes: 16 rows x 4 K quarters) then
-    // hits 64 distinct banks (unpadded rows put all 16 rows of a column on one bank), and a
-    // reader walking consecutive columns still sees distinct banks.
-    __shared__ float red[SK_WAVES][kSkinnyMaxM][SK_COLS + 1];
+    // Partial sums of one 16-row block, row m = lane%16 of each wave, column n at
+    // n ^ ((n >> 2) & 16) of a row padded to 129 floats: one store instruction (64 lanes:
+    // 16 rows x 4 K quarters) then hits 64 distinct banks (unpadded rows put all 16 rows of
+    // a column on one bank), and a reader walking consecutive columns still sees distinct
+    // banks.  The MB row blocks take turns in it (the LDS stays small enough for several
+    // workgroups per CU).
+    __shared__ float red[SK_WAVES][16][SK_COLS + 1];
     auto red_col = [](int n) { return n ^ ((n >> 2) & 16); };
 
     const int tid = threadIdx.x;
@@ -648,12 +652,13 @@ gemm_skinny_kernel(GemmArgs p) {
     const int kend = min(p.K, kbeg + p.k_per_split);
     const int M = p.M, N = p.N;
 
-    f32x4 acc[8];
+    f32x4 acc[MB][8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = f32x4{};
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[mb][j] = f32x4{};
 
     const __amdgpu_buffer_rsrc_t a_rs = make_rsrc(p.A);
-    const bool m_ok = c16 < M;
     const int ncol = n0 + 8 * c16;
 
     if constexpr (BMODE != SKB_ELEM) {
@@ -665,7 +670,7 @@ gemm_skinny_kernel(GemmArgs p) {
         // element-wise by the lanes that own it.
         struct Slab {
             u32x4 b[8];
-            u32x4 a;
+            u32x4 a[MB];
         };
         constexpr int STEP = SK_WAVES * 32;
         const int nsl = (kend - kbeg + STEP - 1) / STEP;  // slabs per wave (uniform)
@@ -706,15 +711,22 @@ gemm_skinny_kernel(GemmArgs p) {
                     }
                 }
             }
-            S.a = buf_load16(a_rs, (m_ok && ka < kend) ? (uint32_t)((c16 * p.lda + ka) * 2)
-                                                       : kOobOffset);
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                const int m = 16 * mb + c16;
+                S.a[mb] = buf_load16(a_rs, (m < M && ka < kend) ? (uint32_t)((m * p.lda + ka) * 2)
+                                                               : kOobOffset);
+            }
         };
         auto compute = [&](const Slab& S) {
             u32x4 bt[8];
             transpose8x8(S.b, bt);
-            const f16x8 a8 = as_f16x8(S.a);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[j] = mfma16(as_f16x8(bt[j]), a8, acc[j]);
+            for (int mb = 0; mb < MB; ++mb) {
+                const f16x8 a8 = as_f16x8(S.a[mb]);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[mb][j] = mfma16(as_f16x8(bt[j]), a8, acc[mb][j]);
+            }
         };
         Slab S0, S1;
         load(0, S0);
@@ -728,7 +740,7 @@ gemm_skinny_kernel(GemmArgs p) {
     for (int k0 = kbeg + wave * 32; k0 < kend; k0 += SK_WAVES * 32) {
         const __amdgpu_buffer_rsrc_t b_rs = make_rsrc(p.B + (int64_t)k0 * p.ldb + n0);
         u32x4 rb[8];
-        u32x4 av;
+        u32x4 av[MB];
         const int ka = k0 + 8 * q;
         {
 #pragma unroll
@@ -747,61 +759,63 @@ gemm_skinny_kernel(GemmArgs p) {
                 }
                 rb[r] = v4;
             }
-            u32x4 v4;
 #pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                uint32_t lo = buf_load2(a_rs, (m_ok && ka + e < kend)
-                                                  ? (uint32_t)((c16 * p.lda + ka + e) * 2)
-                                                  : kOobOffset);
-                uint32_t hi = buf_load2(a_rs, (m_ok && ka + e + 1 < kend)
-                                                  ? (uint32_t)((c16 * p.lda + ka + e + 1) * 2)
-                                                  : kOobOffset);
-                v4[e >> 1] = lo | (hi << 16);
+            for (int mb = 0; mb < MB; ++mb) {
+                const int m = 16 * mb + c16;
+                u32x4 v4;
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    uint32_t lo = buf_load2(a_rs, (m < M && ka + e < kend)
+                                                      ? (uint32_t)((m * p.lda + ka + e) * 2)
+                                                      : kOobOffset);
+                    uint32_t hi = buf_load2(a_rs, (m < M && ka + e + 1 < kend)
+                                                      ? (uint32_t)((m * p.lda + ka + e + 1) * 2)
+                                                      : kOobOffset);
+                    v4[e >> 1] = lo | (hi << 16);
+                }
+                av[mb] = v4;
             }
-            av = v4;
         }
         u32x4 bt[8];
         transpose8x8(rb, bt);
-        const f16x8 a8 = as_f16x8(av);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = mfma16(as_f16x8(bt[j]), a8, acc[j]);
+        for (int mb = 0; mb < MB; ++mb) {
+            const f16x8 a8 = as_f16x8(av[mb]);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[mb][j] = mfma16(as_f16x8(bt[j]), a8, acc[mb][j]);
+        }
     }
     }
 
     // D of MFMA j: lane holds m = lane%16, rows 4*(lane/16)+r -> column 8*(4q+r)+j.
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) red[wave][c16][red_col(8 * (4 * q + r) + j)] = acc[j][r];
-    __syncthreads();
-
+    // Without a K split the epilogue is applied here; with one, this workgroup's partial
+    // goes to the workspace and splitk_reduce_kernel sums the partials in split order and
+    // applies the epilogue.
     const bool use_c = p.beta != 0.0f && p.Cin != nullptr;
-    if (p.split == 1) {
-        for (int idx = tid; idx < kSkinnyMaxM * SK_COLS; idx += SK_WAVES * kWave) {
-            const int m = idx / SK_COLS, n = idx % SK_COLS;
+    float* part = p.split > 1 ? p.ws + (size_t)blockIdx.y * (size_t)M * (size_t)N : nullptr;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+        if (mb > 0) __syncthreads();  // the previous block's readers are done with red
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[wave][c16][red_col(8 * (4 * q + r) + j)] = acc[mb][j][r];
+        __syncthreads();
+        for (int idx = tid; idx < 16 * SK_COLS; idx += SK_WAVES * kWave) {
+            const int ml = idx / SK_COLS, n = idx % SK_COLS, m = 16 * mb + ml;
             if (m < M && n0 + n < N) {
                 const int cn = red_col(n);
-                float v = red[0][m][cn];
+                float v = red[0][ml][cn];
 #pragma unroll
-                for (int w = 1; w < SK_WAVES; ++w) v += red[w][m][cn];
-                v = p.alpha * v;
-                if (use_c) v += p.beta * p.Cin[(int64_t)m * p.ldcin + n0 + n];
-                p.Cout[(int64_t)m * p.ldc + n0 + n] = v;
+                for (int w = 1; w < SK_WAVES; ++w) v += red[w][ml][cn];
+                if (p.split == 1) {
+                    v = p.alpha * v;
+                    if (use_c) v += p.beta * p.Cin[(int64_t)m * p.ldcin + n0 + n];
+                    p.Cout[(int64_t)m * p.ldc + n0 + n] = v;
+                } else {
+                    part[(int64_t)m * N + n0 + n] = v;
+                }
             }
-        }
-        return;
-    }
-    // Split K: this workgroup's partial goes to the workspace; splitk_reduce_kernel sums
-    // the partials in split order and applies the epilogue.
-    float* part = p.ws + (size_t)blockIdx.y * (size_t)M * (size_t)N;
-    for (int idx = tid; idx < kSkinnyMaxM * SK_COLS; idx += SK_WAVES * kWave) {
-        const int m = idx / SK_COLS, n = idx % SK_COLS;
-        if (m < M && n0 + n < N) {
-            const int cn = red_col(n);
-            float v = red[0][m][cn];
-#pragma unroll
-            for (int w = 1; w < SK_WAVES; ++w) v += red[w][m][cn];
-            part[(int64_t)m * N + n0 + n] = v;
         }
     }
 }
@@ -912,6 +926,20 @@ void launch_mfma(const GemmArgs& a, hipStream_t stream) {
                        dim3(t.wm * t.wn * kWave), 0, stream, a);
 }
 
+// Skinny kernel with MB 16-row blocks of activations (M <= 16 * MB).
+template <int MB>
+void launch_skinny(int bmode, const GemmArgs& a, hipStream_t stream) {
+    const dim3 grid(ceil_div(a.N, SK_COLS), a.split), block(SK_WAVES * kWave);
+    switch (bmode) {
+        case SKB_VEC: hipLaunchKernelGGL((gemm_skinny_kernel<SKB_VEC, MB>), grid, block, 0, stream, a); break;
+        case SKB_AL4: hipLaunchKernelGGL((gemm_skinny_kernel<SKB_AL4, MB>), grid, block, 0, stream, a); break;
+        case SKB_AL4_ODD:
+            hipLaunchKernelGGL((gemm_skinny_kernel<SKB_AL4_ODD, MB>), grid, block, 0, stream, a);
+            break;
+        default: hipLaunchKernelGGL((gemm_skinny_kernel<SKB_ELEM, MB>), grid, block, 0, stream, a); break;
+    }
+}
+
 void launch_mfma_cfg(int cfg, const GemmArgs& a, hipStream_t stream) {
     switch (cfg) {
         case 0: launch_mfma<0>(a, stream); break;
@@ -958,16 +986,13 @@ hipError_t launch_gemm(const GemmLaunch& g, hipStream_t stream) {
     a.tiles_n = ceil_div(g.N, pl.tile_n);
 
     if (pl.kernel == WMMA_KERNEL_SKINNY) {
-        dim3 grid(ceil_div(g.N, SK_COLS), pl.split_k);
-        const dim3 block(SK_WAVES * kWave);
-        switch (g.vec ? (int)SKB_VEC : g.skinny_b) {
-            case SKB_VEC: hipLaunchKernelGGL(gemm_skinny_kernel<SKB_VEC>, grid, block, 0, stream, a); break;
-            case SKB_AL4: hipLaunchKernelGGL(gemm_skinny_kernel<SKB_AL4>, grid, block, 0, stream, a); break;
-            case SKB_AL4_ODD:
-                hipLaunchKernelGGL(gemm_skinny_kernel<SKB_AL4_ODD>, grid, block, 0, stream, a);
-                break;
-            default: hipLaunchKernelGGL(gemm_skinny_kernel<SKB_ELEM>, grid, block, 0, stream, a); break;
-        }
+        const int bmode = g.vec ? (int)SKB_VEC : g.skinny_b;
+        if (g.M <= 16)
+            launch_skinny<1>(bmode, a, stream);
+        else if (g.M <= 32)
+            launch_skinny<2>(bmode, a, stream);
+        else
+            launch_skinny<4>(bmode, a, stream);
     } else {
         if (g.vec)
             launch_mfma_cfg(pl.tile_cfg, a, stream);

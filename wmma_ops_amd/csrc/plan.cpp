@@ -58,10 +58,10 @@ int make_custom_plan(int M, int N, int K, int kernel, int tile_cfg, int split,
     wmma_gemm_plan p{};
     int tiles;
     if (kernel == WMMA_KERNEL_SKINNY) {
-        if (M > kSkinnyMaxM) return WMMA_ERR_INVALID_ARG;
+        if (M > kSkinnyMaxMWide) return WMMA_ERR_INVALID_ARG;
         p.kernel = WMMA_KERNEL_SKINNY;
         p.tile_cfg = -1;
-        p.tile_m = kSkinnyMaxM;
+        p.tile_m = M <= 16 ? 16 : (M <= 32 ? 32 : 64);
         p.tile_n = kSkinnyBlockN;
         tiles = ceil_div(std::max(N, 1), kSkinnyBlockN);
     } else if (kernel == WMMA_KERNEL_TILED) {
@@ -140,29 +140,37 @@ int make_plan(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* ou
         return WMMA_OK;
     }
 
-    if (M <= kSkinnyMaxM && M > 0 && N > 0 && K > 0) {
+    if (M <= kSkinnyAutoMaxM && M > 0 && N > 0 && K > 0) {
         // Streaming kernel: each workgroup owns kSkinnyBlockN columns and one K range.
         // The launch lasts as long as the busiest CU, which streams ceil(W / CUs) of the
-        // W = tiles x split workgroups, each 1/W of the bytes: pick the split that
-        // minimises ceil(W / CUs) / W over W <= 3 x CUs (measured on MI355X: a split that
-        // leaves some CUs one workgroup more than the rest costs 10-25%, and beyond three
-        // workgroups per CU the extra partial sums cost more than the balance gains), the
-        // smaller split on a tie (fewer partial sums to write and reduce).
+        // W = tiles x split workgroups, each 1/W of the bytes.  M <= 16: pick the split
+        // that minimises ceil(W / CUs) / W over W <= 3 x CUs (measured on MI355X: a split
+        // that leaves some CUs one workgroup more than the rest costs 10-25%, and beyond
+        // three workgroups per CU the extra partial sums cost more than the balance gains),
+        // the smaller split on a tie (fewer partial sums to write and reduce).  16 < M <= 32
+        // (two 16-row blocks, twice the partial sums): the largest split that keeps W
+        // within one wave of the CUs -- the fastest of splits 1-8 in every case measured
+        // (M = 17, 32; N = 4096, 11008, 14336; K = 4096, 14336), e.g. M = 32, N = 11008:
+        // split 2 25.9 us against 27.2-31.6 for 3-8, 27.1 for the tiled kernel.
         p.kernel = WMMA_KERNEL_SKINNY;
         p.tile_cfg = -1;
-        p.tile_m = kSkinnyMaxM;
+        p.tile_m = M <= 16 ? 16 : 32;
         p.tile_n = kSkinnyBlockN;
         const int tiles = ceil_div(N, kSkinnyBlockN);
         const int smax = std::min(std::max(1, K / 256), kMaxSplitK);
         int split = 1;
-        double best = 1e300;
-        for (int sp = 1; sp <= smax; ++sp) {
-            const int64_t w = (int64_t)tiles * sp;
-            if (sp > 1 && w > 3 * (int64_t)num_cus) break;
-            const double cost = (double)ceil_div64(w, num_cus) / (double)w;
-            if (cost < best * 0.99) {
-                best = cost;
-                split = sp;
+        if (M > 16) {
+            split = (int)std::max<int64_t>(1, std::min<int64_t>(smax, num_cus / tiles));
+        } else {
+            double best = 1e300;
+            for (int sp = 1; sp <= smax; ++sp) {
+                const int64_t w = (int64_t)tiles * sp;
+                if (sp > 1 && w > 3 * (int64_t)num_cus) break;
+                const double cost = (double)ceil_div64(w, num_cus) / (double)w;
+                if (cost < best * 0.99) {
+                    best = cost;
+                    split = sp;
+                }
             }
         }
         finish_split(M, N, K, tiles, split, &p);
@@ -187,9 +195,10 @@ int make_plan(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* ou
             const int64_t tiles = (int64_t)ceil_div(M, t.bm) * ceil_div(N, t.bn);
             const double eff = kTileEff[cfg] * std::min(1.0, (double)M / t.bm);
             for (int sp : {1, 2, 4}) {
-                // a split needs K >= 256 per part and a GEMM big enough (>= 2^30
-                // multiply-adds) for the partial-sum pass to pay for itself
-                if (sp > 1 && (K / sp < 256 || (int64_t)M * N * K < (int64_t(1) << 30))) break;
+                // a split needs K >= 256 per part and a GEMM big enough (>= 2^29
+                // multiply-adds) for the partial-sum pass to pay for itself (M = 48,
+                // N = K = 4096: 64x64 split 4 against 26.8 us unsplit)
+                if (sp > 1 && (K / sp < 256 || (int64_t)M * N * K < (int64_t(1) << 29))) break;
                 const int64_t w = tiles * sp;
                 const double cost = (double)ceil_div64(w, num_cus) * t.bm * t.bn / (sp * eff) *
                                     (1.0 + 0.15 * (sp - 1));
