@@ -174,9 +174,11 @@ def test_plan_make(lib):
                              (32, 4096, 14336): 8, (24, 32768, 4096): 1}.items():
         assert lib.wmma_gemm_plan_make(M, N, K, -1, 256, ctypes.byref(p)) == OK
         assert (p.kernel, p.tile_m, p.tile_n, p.split_k) == (1, 32, 128, split), (M, N, K)
-    # M = 33..64 keeps the tiled kernel; 48 x 4096 x 4096 (1.5 x 2^29 multiply-adds) splits
-    assert lib.wmma_gemm_plan_make(48, 4096, 4096, -1, 256, ctypes.byref(p)) == OK
-    assert p.kernel == 0 and p.split_k > 1
+    # M = 33..128 keeps the tiled kernel; few tiles split K from K = 2048 on, never below
+    for (M, N, K), split in {(48, 4096, 4096): 4, (64, 1024, 4096): 4, (48, 1024, 2048): 4,
+                             (64, 1024, 1024): 1, (128, 4096, 512): 1}.items():
+        assert lib.wmma_gemm_plan_make(M, N, K, -1, 256, ctypes.byref(p)) == OK
+        assert (p.kernel, p.split_k) == (0, split), (M, N, K, p.split_k)
 
 
 class W4Plan(ctypes.Structure):

@@ -195,10 +195,12 @@ int make_plan(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* ou
             const int64_t tiles = (int64_t)ceil_div(M, t.bm) * ceil_div(N, t.bn);
             const double eff = kTileEff[cfg] * std::min(1.0, (double)M / t.bm);
             for (int sp : {1, 2, 4}) {
-                // a split needs K >= 256 per part and a GEMM big enough (>= 2^29
-                // multiply-adds) for the partial-sum pass to pay for itself (M = 48,
-                // N = K = 4096: 64x64 split 4 against 26.8 us unsplit)
-                if (sp > 1 && (K / sp < 256 || (int64_t)M * N * K < (int64_t(1) << 29))) break;
+                // a split needs K >= 256 per part and K >= 2048 for the partial-sum pass
+                // to pay for itself: measured on MI355X, every shape with K >= 2048 split
+                // faster (48 x 1024 x 2048: 15.2 -> 11.2 us; 64 x 1024 x 4096: 25.5 ->
+                // 12.7; 48 x 4096 x 4096: 26.8 -> 15.0), every one with K <= 1024 slower
+                // (64 x 1024 x 1024: 9.4 -> 11.7; 128 x 4096 x 512: 7.9 -> 11.0)
+                if (sp > 1 && (K / sp < 256 || K < 2048)) break;
                 const int64_t w = tiles * sp;
                 const double cost = (double)ceil_div64(w, num_cus) * t.bm * t.bn / (sp * eff) *
                                     (1.0 + 0.15 * (sp - 1));
