@@ -358,28 +358,38 @@ def fam_ragged(wo):
         del Ad, Bd
 
 
-def w4a16_case(wo, m, n, use_graph=True):
+def w4a16_case(wo, m, n, use_graph=True, layout=None):
+    """configs[3] W4A16 case: M = m, K = 4096, N = n, G = 128.  layout: "fused" (weights,
+    scales and zeros in one run per 16 columns, prepack_int4_fused: the decode layout, the
+    default for m <= 4) or "sliced" (prepack_int4 + slice-major parameters, the default for
+    larger m).  Same bytes either way."""
     import torch
 
     from oracle import gemm as og
     from oracle import int4 as oi
 
     kw, G = 4096, 128
+    layout = layout or ("fused" if m <= 4 else "sliced")
     A, q, s, z = oi.make_inputs(m, kw, n, G, seed=42 + 3)
-    # one-time layout conversions (outside the timed region): weights to the MFMA layout,
-    # scales/zeros to the slice-major layout (same bytes, contiguous per 16 columns)
-    pk0 = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
-    sd, zd = wo.prepack_int4_params(torch.from_numpy(s).cuda(),
-                                    torch.from_numpy(oi.pack_zeros(z)).cuda())
+    # one-time layout conversions (outside the timed region)
+    qd, s0, z0 = (torch.from_numpy(x).cuda() for x in (oi.pack_gptq(q), s, oi.pack_zeros(z)))
     Ad = A.cuda()
     nbytes = kw * n // 2 + (kw // G) * n * 2 + (kw // G) * n // 2 + 2 * m * kw + 4 * m * n
     cp = copies_for(nbytes)
-    pks = [pk0.clone() for _ in range(cp)]
-    sds = [sd.clone() for _ in range(cp)]
-    zds = [zd.clone() for _ in range(cp)]
-    Y0 = wo.matmul_int4(Ad, pk0, sd, zd, G)
+    if layout == "fused":
+        f0 = wo.prepack_int4_fused(qd, s0, z0, G)
+        fs = [f0.clone() for _ in range(cp)]
+        Y0 = wo.matmul_int4_fused(Ad, f0, G)
+        fn = lambda i: wo.matmul_int4_fused(Ad, fs[i % cp], G)
+    else:
+        pk0 = wo.prepack_int4(qd)
+        sd, zd = wo.prepack_int4_params(s0, z0)
+        pks = [pk0.clone() for _ in range(cp)]
+        sds = [sd.clone() for _ in range(cp)]
+        zds = [zd.clone() for _ in range(cp)]
+        Y0 = wo.matmul_int4(Ad, pk0, sd, zd, G)
+        fn = lambda i: wo.matmul_int4(Ad, pks[i % cp], sds[i % cp], zds[i % cp], G)
     err = og.max_rel_err(Y0, oi.w4a16_ref(A, q, s, z, G))
-    fn = lambda i: wo.matmul_int4(Ad, pks[i % cp], sds[i % cp], zds[i % cp], G)
     if use_graph:
         ms, outs = time_graph(fn, cp)
         assert torch.equal(outs[0], Y0), "graph replay differs from eager"
@@ -389,7 +399,7 @@ def w4a16_case(wo, m, n, use_graph=True):
     return {"M": m, "N": n, "K": kw, "G": G, "bytes": nbytes, "us_per_call": round(ms * 1e3, 3),
             "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "TFLOPS": round(fl / (ms * 1e-3) / 1e12, 2), **roofline(nbytes, fl, ms),
-            "rotation_copies": cp,
+            "rotation_copies": cp, "layout": layout,
             "timing": "graph replay" if use_graph else "stream launches",
             "max_rel_err": float(f"{err:.3e}")}
 

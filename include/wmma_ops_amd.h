@@ -185,6 +185,36 @@ int wmma_int4_prepack_params(const void* scales, const void* zeros, int zeros_fo
                              int N, int group_size, void* scales_out, int32_t* zeros_out,
                              void* stream);
 
+/*
+ * Fused decode layout (zeros_format WMMA_W4_FUSED of wmma_w4a16_gemm): the prepacked
+ * weights, scales and zero points of each 16-column slice in one contiguous run, so that
+ * a decode workgroup streams a single region of memory.  Per slice (wmma_int4_fused_bytes(K,
+ * N) / (N/16) bytes each):
+ *   header   one 160-byte block per four 128-deep K steps 4r .. 4r+3 (the last block covers
+ *            the steps left), zero-padded to a multiple of 128 bytes:
+ *              bytes [0, 128)   scales fp16 [4][16]: entry (u, c) = s[g][16*slice + c] of K
+ *                               step 4r+u, g = 128 (4r+u) / G
+ *              bytes [128, 160) zero points [4][16] as nibbles: byte 128 + 8u + c/2, nibble
+ *                               c % 2 (even columns in the low nibble)
+ *   weights  the slice's run of the prepacked layout above (1 KB per K step).
+ * With G = 128 and K % 4096 == 0 these are exactly the bytes of the prepacked weights plus
+ * the scales and packed zeros; a larger G repeats a group's parameters in each of its K
+ * steps.  Requirements: K % 128 == 0, N % 32 == 0, G % 128 == 0 with G / 128 a power of two.
+ * wmma_w4a16_gemm reads this layout for M <= 4 (decode shapes: the kernel this layout is
+ * for); other M return WMMA_ERR_UNSUPPORTED.  No reference counterpart.
+ */
+#define WMMA_W4_FUSED 3
+size_t wmma_int4_fused_bytes(int K, int N);
+/* GPTQ qweight [K/8, N] + scales fp16 [K/G, N] + zeros (WMMA_ZEROS_PACKED or WMMA_ZEROS_U8)
+ * -> fused buffer (16-byte aligned, wmma_int4_fused_bytes bytes), bit-exact. */
+int wmma_int4_prepack_fused(const int32_t* qweight, const void* scales, const void* zeros,
+                            int zeros_format, int K, int N, int group_size, int32_t* fused,
+                            void* stream);
+/* Inverse: fused buffer -> qweight [K/8, N], scales fp16 [K/G, N], packed zeros int32
+ * [K/G, N/8] (each group's parameters read from its first K step). */
+int wmma_int4_unprepack_fused(const int32_t* fused, int K, int N, int group_size,
+                              int32_t* qweight, void* scales, int32_t* zeros, void* stream);
+
 /* Workspace bytes wmma_w4a16_gemm needs (fp32 split-K partials). */
 size_t wmma_w4a16_workspace_size(int M, int N, int K, int group_size);
 
@@ -211,7 +241,8 @@ int wmma_w4a16_plan_make(int M, int N, int K, int group_size, int num_cus, wmma_
  * Y[M,N] (fp32) = A[M,K] (fp16) @ W[K,N], W[k][n] = fp16((q[k][n] - z[k/G][n]) * s[k/G][n])
  * (dequantised value rounded once to fp16).  packed: output of wmma_int4_prepack.
  * scales: fp16 [K/G, N] (or [N/16][K/G][16] with WMMA_ZEROS_SLICED).  zeros: per
- * zeros_format.  G = group_size, G % 32 == 0, K % G == 0.
+ * zeros_format.  G = group_size, G % 32 == 0, K % G == 0.  With WMMA_W4_FUSED, packed is
+ * the output of wmma_int4_prepack_fused and scales / zeros are not read (may be NULL).
  * Arithmetic by path (wmma_w4a16_plan_make reports the path of a shape).  The tiled
  * kernels (WMMA_W4_KERNEL_SKINNY, _GEMM, _MFMA, _GEMV_SPLIT) and the decode kernel at
  * M = 3, 4 form each weight exactly as written above before its fp32-accumulated product.

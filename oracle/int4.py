@@ -190,6 +190,64 @@ def unprepack(packed: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(t).reshape(kg, N).view(np.int32)
 
 
+# Fused decode layout (this library's WMMA_W4_FUSED, include/wmma_ops_amd.h): per 16-column
+# slice, a header of one 160-byte parameter block per four 128-deep K steps (128 bytes of
+# scales [4][16] fp16, 32 bytes of zero nibbles [4][16], even column low), zero-padded to a
+# multiple of 128 bytes, then the slice's prepacked weights (1 KB per K step).
+FUSED_BLOCK = 160
+
+
+def fused_hdr_bytes(K: int) -> int:
+    return (FUSED_BLOCK * ((K // 128 + 3) // 4) + 127) // 128 * 128
+
+
+def fused_slice_bytes(K: int) -> int:
+    return fused_hdr_bytes(K) + (K // 128) * 1024
+
+
+def prepack_fused(qweight: np.ndarray, scales: np.ndarray, zeros_u8: np.ndarray, G: int) -> np.ndarray:
+    """GPTQ qweight [K/8, N] + scales fp16 [K/G, N] + uint8 zeros [K/G, N] -> int32
+    [N/16, fused_slice_bytes(K)/4].  K step pp (128 values of K) carries the parameters of
+    group pp*128 // G; the weights are the slice's standard prepacked run."""
+    pk = prepack(qweight)
+    NS, KC = pk.shape[:2]
+    K = KC * 64
+    assert K % 128 == 0 and G % 128 == 0 and K % G == 0
+    KP, H = K // 128, fused_hdr_bytes(K)
+    out = np.zeros((NS, fused_slice_bytes(K)), dtype=np.uint8)
+    out[:, H:] = pk.view(np.uint8).reshape(NS, KP * 1024)
+    s16 = np.ascontiguousarray(np.asarray(scales, dtype=np.float16)).view(np.uint16)
+    z = np.asarray(zeros_u8, dtype=np.uint8)
+    for pp in range(KP):
+        r, u = divmod(pp, 4)
+        base, g = r * FUSED_BLOCK, pp * 128 // G
+        out[:, base + 32 * u: base + 32 * (u + 1)] = (
+            np.ascontiguousarray(s16[g].reshape(NS, 16)).view(np.uint8).reshape(NS, 32))
+        zz = z[g].reshape(NS, 8, 2)
+        out[:, base + 128 + 8 * u: base + 128 + 8 * (u + 1)] = (zz[:, :, 0] & 0xF) | ((zz[:, :, 1] & 0xF) << 4)
+    return out.view(np.int32)
+
+
+def unprepack_fused(fused: np.ndarray, K: int, G: int):
+    """Inverse of prepack_fused -> (qweight [K/8, N] int32, scales fp16 [K/G, N], uint8
+    zeros [K/G, N]); each group's parameters are read from its first K step."""
+    b = np.ascontiguousarray(fused).view(np.uint8)
+    NS = b.shape[0]
+    KC, H = K // 64, fused_hdr_bytes(K)
+    assert b.shape[1] == fused_slice_bytes(K)
+    qweight = unprepack(np.ascontiguousarray(b[:, H:]).view(np.int32).reshape(NS, KC, 32, 4))
+    KG = K // G
+    s = np.empty((KG, NS * 16), dtype=np.uint16)
+    z = np.empty((KG, NS * 16), dtype=np.uint8)
+    for g in range(KG):
+        r, u = divmod(g * G // 128, 4)
+        base = r * FUSED_BLOCK
+        s[g] = np.ascontiguousarray(b[:, base + 32 * u: base + 32 * (u + 1)]).view(np.uint16).reshape(-1)
+        zb = b[:, base + 128 + 8 * u: base + 128 + 8 * (u + 1)]
+        z[g] = np.stack([zb & 0xF, zb >> 4], axis=-1).reshape(-1)
+    return qweight, s.view(np.float16), z
+
+
 def dequant(q: np.ndarray, scales: np.ndarray, zeros_u8: np.ndarray, G: int) -> np.ndarray:
     """fp16((q - z) * s): the difference is exact in fp16 and numpy's float16 multiply
     rounds the exact product once."""

@@ -275,6 +275,47 @@ def test_slice_params_layout():
     assert np.array_equal(z_sl.reshape(N // 16, ng, 2).transpose(1, 0, 2).reshape(ng, N // 8), zp)
 
 
+@pytest.mark.parametrize("K,N,G", [(512, 64, 128), (640, 32, 128), (4096, 32, 256), (1152, 96, 128),
+                                   (2048, 64, 512)])
+def test_fused_layout_closed_form(K, N, G):
+    # Every weight nibble, scale and zero point lands at the byte the written layout gives
+    # (an index formula independent of the oracle's construction), the buffer has exactly the
+    # bytes of the separate tensors at G = 128, and unprepack_fused inverts it.
+    rng = np.random.default_rng(K + N + G)
+    q = rng.integers(0, 16, (K, N), dtype=np.uint8)
+    sc = (rng.random((K // G, N)) * 0.02 + 0.001).astype(np.float16)
+    z = rng.integers(0, 16, (K // G, N), dtype=np.uint8)
+    qw = oi.pack_gptq(q)
+    f = oi.prepack_fused(qw, sc, z, G)
+    b = f.view(np.uint8).reshape(N // 16, -1)
+    KP = K // 128
+    hdr = -(-160 * (-(-KP // 4)) // 128) * 128  # 160 B per four K steps, up to 128 B lines
+    assert b.shape[1] == hdr + 1024 * KP and hdr % 128 == 0
+    if G == 128 and K % 4096 == 0:
+        assert f.nbytes == K * N // 2 + (K // G) * N * 2 + (K // G) * N // 2
+    for _ in range(300):
+        k, n = int(rng.integers(K)), int(rng.integers(N))
+        pp, sl, c = k // 128, n // 16, n % 16
+        rec = (pp // 4) * 160
+        # weight nibble: K step pp, block kc % 2, entry 16*h + c (h = (k % 64) // 32),
+        # word (k % 32) // 8, nibble p with PERM[p] = k % 8
+        kc = k // 64
+        p_nib = oi.PERM.index(k % 8)
+        off = hdr + pp * 1024 + (kc % 2) * 512 + (16 * ((k % 64) // 32) + c) * 16 + 4 * ((k % 32) // 8) + p_nib // 2
+        assert (b[sl, off] >> (4 * (p_nib % 2))) & 0xF == q[k, n]
+        g = k // G
+        so = rec + 2 * (16 * (pp % 4) + c)
+        assert int(b[sl, so]) | (int(b[sl, so + 1]) << 8) == int(sc[g, n].view(np.uint16))
+        zo = rec + 128 + 8 * (pp % 4) + c // 2
+        assert (b[sl, zo] >> (4 * (c % 2))) & 0xF == z[g, n]
+    q2, s2, z2 = oi.unprepack_fused(f, K, G)
+    assert np.array_equal(q2, qw) and np.array_equal(z2, z)
+    assert np.array_equal(s2.view(np.uint16), sc.view(np.uint16))
+    # the weights are the standard prepacked run of each slice, and the header padding is zero
+    assert np.array_equal(b[:, hdr:], oi.prepack(qw).view(np.uint8).reshape(N // 16, KP * 1024))
+    assert not b[:, 160 * (-(-KP // 4)):hdr].any()
+
+
 def test_awq_pack_round_trip_and_order():
     rng = np.random.default_rng(11)
     q = rng.integers(0, 16, (32, 64), dtype=np.uint8)

@@ -193,6 +193,65 @@ def test_w4a16_sliced_params_same_bits(wo, M, K, N, G):
     assert og.max_rel_err(Ys, oi.w4a16_ref(A, q, s, z, G)) <= 1e-3
 
 
+# Fused decode layout (prepack_int4_fused): bit-exact against the oracle and round-tripped,
+# including a partial last record (K = 640, 4224) and G > 128 (parameters repeated per step).
+@pytest.mark.parametrize("K,N,G", [(4096, 4096, 128), (4096, 14336, 128), (640, 64, 128),
+                                   (4224, 96, 128), (2048, 160, 256), (8192, 64, 1024)])
+def test_prepack_fused_bit_exact(wo, K, N, G):
+    report("prepack_fused", K=K, N=N, G=G)
+    A, q, s, z = oi.make_inputs(1, K, N, G, seed=K + N + G)
+    qw = oi.pack_gptq(q)
+    ref = oi.prepack_fused(qw, s, z, G)
+    qd, sd = torch.from_numpy(qw).cuda(), torch.from_numpy(s).cuda()
+    for zeros in (oi.pack_zeros(z), z):
+        f = wo.prepack_int4_fused(qd, sd, torch.from_numpy(zeros).cuda(), G)
+        assert np.array_equal(f.cpu().numpy(), ref)
+    q2, s2, z2 = wo.unprepack_int4_fused(f, G)
+    assert torch.equal(q2, qd)
+    assert np.array_equal(s2.cpu().numpy().view(np.uint16), s.view(np.uint16))
+    assert np.array_equal(z2.cpu().numpy(), oi.pack_zeros(z))
+
+
+# configs[3] decode rows (M = 1, K = 4096, N in {4096, 14336}, G = 128, seed 42 + 3) in the
+# fused layout the headline times, plus M = 2..4, K past one round (8192, ragged 4224) and
+# G > 128: within the oracle's bar, and bit-equal to the standard layout wherever the planner
+# gives that layout the same decode kernel (the same arithmetic on values read from other
+# addresses; narrow N, where the standard layout takes a split kernel, only the bar).
+@pytest.mark.parametrize("M,K,N,G", [(1, 4096, 4096, 128), (1, 4096, 14336, 128),
+                                     (2, 4096, 4096, 128), (3, 4096, 1024, 128),
+                                     (4, 4096, 14336, 128), (1, 8192, 1024, 128),
+                                     (2, 4224, 2048, 128), (1, 2048, 4096, 256), (4, 640, 4096, 128)])
+def test_w4a16_fused_decode(wo, M, K, N, G):
+    report("w4a16_fused", M=M, K=K, N=N, G=G)
+    A, q, s, z = oi.make_inputs(M, K, N, G, seed=42 + 3 if K == 4096 and G == 128 else M + K + N)
+    qd, sd = torch.from_numpy(oi.pack_gptq(q)).cuda(), torch.from_numpy(s).cuda()
+    zd = torch.from_numpy(oi.pack_zeros(z)).cuda()
+    f = wo.prepack_int4_fused(qd, sd, zd, G)
+    Ad = A.cuda()
+    Y = wo.matmul_int4_fused(Ad, f, G)
+    assert og.max_rel_err(Y, oi.w4a16_ref(A, q, s, z, G)) <= 1e-3
+    if wo.w4a16_plan(M, N, K, G)[0] == 0:  # the standard layout also takes the decode kernel
+        Ys = wo.matmul_int4(Ad, wo.prepack_int4(qd), sd, zd, G)
+        assert torch.equal(Y, Ys)
+    Yh = wo.matmul_int4_fused(Ad, f, G, out_dtype=torch.float16)
+    assert torch.equal(Yh, Y.half())
+
+
+def test_w4a16_fused_errors(wo):
+    A, q, s, z = oi.make_inputs(5, 512, 64, 128, seed=3)
+    qd, sd = torch.from_numpy(oi.pack_gptq(q)).cuda(), torch.from_numpy(s).cuda()
+    f = wo.prepack_int4_fused(qd, sd, torch.from_numpy(z).cuda(), 128)
+    with pytest.raises(RuntimeError, match="decode kernel only"):
+        wo.matmul_int4_fused(A.cuda(), f, 128)  # M = 5
+    with pytest.raises(RuntimeError, match="Inner dimensions"):
+        wo.matmul_int4_fused(A[:1, :384].contiguous().cuda(), f, 128)
+    with pytest.raises(RuntimeError, match="fused must be"):
+        wo.matmul_int4_fused(A[:1].cuda(), wo.prepack_int4(qd), 128)
+    with pytest.raises(RuntimeError, match="128"):
+        wo.prepack_int4_fused(qd, torch.from_numpy(oi.make_inputs(1, 512, 64, 64, seed=1)[2]).cuda(),
+                              torch.from_numpy(oi.make_inputs(1, 512, 64, 64, seed=1)[3]).cuda(), 64)
+
+
 # AutoAWQ import: bit-exact conversion to the GPTQ layout and packed zeros, and the same
 # product as the GPTQ-layout path.
 @pytest.mark.parametrize("K,N,G", [(256, 64, 64), (4096, 1024, 128)])

@@ -118,6 +118,9 @@ int4_from_gptq = _C.int4_from_gptq
 unprepack_int4 = _C.unprepack_int4
 unpack_int4 = _C.unpack_int4
 matmul_int4 = _C.matmul_int4
+prepack_int4_fused = _C.prepack_int4_fused
+unprepack_int4_fused = _C.unprepack_int4_fused
+matmul_int4_fused = _C.matmul_int4_fused
 gemm_plan = _C.gemm_plan
 w4a16_plan = _C.w4a16_plan
 
@@ -138,6 +141,6 @@ __all__ = [
     "matmul", "matmul_adaptive", "matmul_tiled", "gemm", "gemm_inplace", "gemm_adaptive",
     "flash_attention", "flash_attention_varlen", "flash_attention_forward",
     "flash_attention_backward", "flash_attention_varlen_forward", "flash_attention_varlen_backward",
-    "FlashAttentionFunction", "FlashAttentionVarlenFunction", "prepack_int4", "prepack_int4_params", "int4_from_awq", "int4_from_gptq", "unprepack_int4", "unpack_int4", "matmul_int4",
+    "FlashAttentionFunction", "FlashAttentionVarlenFunction", "prepack_int4", "prepack_int4_params", "int4_from_awq", "int4_from_gptq", "unprepack_int4", "unpack_int4", "matmul_int4", "prepack_int4_fused", "unprepack_int4_fused", "matmul_int4_fused",
     "gemm_plan", "w4a16_plan", "TILE_CONFIGS", "LIBRARY_PATH", "HEADER_PATH", *_REFERENCE_VARIANTS,
 ]

@@ -382,6 +382,61 @@ int wmma_int4_prepack_params(const void* scales, const void* zeros, int zeros_fo
                       "int4 params launch");
 }
 
+// Fused decode layout: G % 128 == 0 with G / 128 a power of two (a 128-deep K step never
+// straddles two groups), K % 128 == 0.
+static bool fused_group_ok(int K, int G) {
+    return G > 0 && G % 128 == 0 && ((G / 128) & (G / 128 - 1)) == 0 && K % G == 0;
+}
+
+size_t wmma_int4_fused_bytes(int K, int N) {
+    if (K <= 0 || N <= 0 || K % 128 != 0 || N % 32 != 0) return 0;
+    return (size_t)(N / 16) * (size_t)fused_slice_bytes(K);
+}
+
+int wmma_int4_prepack_fused(const int32_t* qweight, const void* scales, const void* zeros,
+                            int zeros_format, int K, int N, int group_size, int32_t* fused,
+                            void* stream) {
+    if (int rc = check_int4_shape(K, N)) return rc;
+    if (K % 128 != 0) return fail(WMMA_ERR_UNSUPPORTED, "K (%d) must be a multiple of 128", K);
+    if (!fused_group_ok(K, group_size))
+        return fail(WMMA_ERR_UNSUPPORTED,
+                    "group_size (%d) must be 128 * 2^j and divide K (%d) for the fused layout",
+                    group_size, K);
+    if (zeros_format != WMMA_ZEROS_PACKED && zeros_format != WMMA_ZEROS_U8)
+        return fail(WMMA_ERR_INVALID_ARG, "zeros format %d cannot be fused", zeros_format);
+    if (!qweight || !scales || !zeros || !fused) return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
+    if (!aligned16(fused)) return fail(WMMA_ERR_MISALIGNED, "fused output must be 16-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(qweight) & 3u) != 0)
+        return fail(WMMA_ERR_MISALIGNED, "qweight must be 4-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(scales) & 1u) != 0)
+        return fail(WMMA_ERR_MISALIGNED, "scales must be 2-byte aligned");
+    if (zeros_format == WMMA_ZEROS_PACKED && (reinterpret_cast<uintptr_t>(zeros) & 3u) != 0)
+        return fail(WMMA_ERR_MISALIGNED, "packed zeros must be 4-byte aligned");
+    return hip_status(launch_int4_prepack_fused(qweight, scales, zeros, zeros_format, K, N,
+                                                group_size, fused, static_cast<hipStream_t>(stream)),
+                      "int4 fused prepack launch");
+}
+
+int wmma_int4_unprepack_fused(const int32_t* fused, int K, int N, int group_size,
+                              int32_t* qweight, void* scales, int32_t* zeros, void* stream) {
+    if (int rc = check_int4_shape(K, N)) return rc;
+    if (K % 128 != 0) return fail(WMMA_ERR_UNSUPPORTED, "K (%d) must be a multiple of 128", K);
+    if (!fused_group_ok(K, group_size))
+        return fail(WMMA_ERR_UNSUPPORTED,
+                    "group_size (%d) must be 128 * 2^j and divide K (%d) for the fused layout",
+                    group_size, K);
+    if (!qweight || !scales || !zeros || !fused) return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
+    if (!aligned16(fused)) return fail(WMMA_ERR_MISALIGNED, "fused input must be 16-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(qweight) & 3u) != 0 ||
+        (reinterpret_cast<uintptr_t>(zeros) & 3u) != 0)
+        return fail(WMMA_ERR_MISALIGNED, "qweight and zeros must be 4-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(scales) & 1u) != 0)
+        return fail(WMMA_ERR_MISALIGNED, "scales must be 2-byte aligned");
+    return hip_status(launch_int4_unprepack_fused(fused, K, N, group_size, qweight, scales, zeros,
+                                                  static_cast<hipStream_t>(stream)),
+                      "int4 fused unprepack launch");
+}
+
 size_t wmma_w4a16_workspace_size(int M, int N, int K, int group_size) {
     if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0 || group_size <= 0) return 0;
     // The plan depends on operand alignment only through the choice of the matrix-pipe
@@ -419,17 +474,29 @@ static int w4a16_run(const void* A, int64_t lda, const int32_t* packed, const vo
                     "group_size (%d) must be a positive multiple of 32 dividing K (%d)", group_size,
                     K);
     if (zeros_format != WMMA_ZEROS_PACKED && zeros_format != WMMA_ZEROS_U8 &&
-        zeros_format != WMMA_ZEROS_SLICED)
+        zeros_format != WMMA_ZEROS_SLICED && zeros_format != WMMA_W4_FUSED)
         return fail(WMMA_ERR_INVALID_ARG, "unknown zeros format %d", zeros_format);
+    const bool fused = zeros_format == WMMA_W4_FUSED;
+    if (fused) {
+        if (K % 128 != 0 || !fused_group_ok(K, group_size))
+            return fail(WMMA_ERR_UNSUPPORTED,
+                        "the fused layout needs K %% 128 == 0 and group_size = 128 * 2^j "
+                        "(K=%d, group_size=%d)", K, group_size);
+        if (!w4a16_fused_decode_ok(M, K))
+            return fail(WMMA_ERR_UNSUPPORTED,
+                        "the fused layout is read by the decode kernel only (M <= 4; M=%d, K=%d)",
+                        M, K);
+    }
     if (M == 0) return ok();
-    if (!A || !packed || !scales || !zeros || !Y) return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
+    if (!A || !packed || !Y || (!fused && (!scales || !zeros)))
+        return fail(WMMA_ERR_INVALID_ARG, "NULL pointer");
     if (lda < K || ldy < N) return fail(WMMA_ERR_INVALID_ARG, "leading dimension too small");
     if (!aligned16(A) || lda % 8 != 0)
         return fail(WMMA_ERR_MISALIGNED, "A must be 16-byte aligned with lda a multiple of 8");
     if (!aligned16(packed)) return fail(WMMA_ERR_MISALIGNED, "packed weights must be 16-byte aligned");
-    if ((reinterpret_cast<uintptr_t>(scales) & 1u) != 0)
+    if (!fused && (reinterpret_cast<uintptr_t>(scales) & 1u) != 0)
         return fail(WMMA_ERR_MISALIGNED, "scales must be 2-byte aligned");
-    if (zeros_format != WMMA_ZEROS_U8 && (reinterpret_cast<uintptr_t>(zeros) & 3u) != 0)
+    if (!fused && zeros_format != WMMA_ZEROS_U8 && (reinterpret_cast<uintptr_t>(zeros) & 3u) != 0)
         return fail(WMMA_ERR_MISALIGNED, "packed zeros must be 4-byte aligned");
     // 32-bit buffer offsets: the tiled kernels address A from their first row (at most 256
     // rows), the LDS-DMA GEMM its weights from its first 32-column tile (at most 8 tiles of
@@ -444,7 +511,13 @@ static int w4a16_run(const void* A, int64_t lda, const int32_t* packed, const vo
     const bool aligned = (reinterpret_cast<uintptr_t>(scales) & 7u) == 0 &&
                          (zeros_format != WMMA_ZEROS_U8 ||
                           (reinterpret_cast<uintptr_t>(zeros) & 3u) == 0);
-    w.plan = w4a16_plan(M, N, K, group_size, current_cus(), aligned);
+    if (fused) {
+        w.plan.kind = W4_DECODE_MFMA;
+        w.plan.split = 1;
+        w.plan.k_per_split = K;
+    } else {
+        w.plan = w4a16_plan(M, N, K, group_size, current_cus(), aligned);
+    }
     const size_t need = w.plan.split > 1 ? (size_t)w.plan.split * M * N * sizeof(float) : 0;
     if (need > 0 && (!workspace || workspace_bytes < need))
         return fail(WMMA_ERR_WORKSPACE, "W4A16 split-K needs a workspace of %zu bytes", need);

@@ -54,6 +54,23 @@ hipError_t launch_int4_gptq_zeros(const int32_t* qzeros, int KG, int N, int add,
 // GPTQ-layout weights with rows permuted: output row k = input row perm[k].
 hipError_t launch_int4_permute_rows(const int32_t* qweight, const int32_t* perm, int K, int N,
                                     int32_t* out, hipStream_t stream);
+// Fused decode layout (WMMA_W4_FUSED, w4a16.hip), per 16-column slice: a header of one
+// 160-byte parameter block per four 128-deep K steps, zero-padded to a multiple of 128
+// bytes, then the slice's prepacked weights (1 KB per K step).  K % 128 == 0.
+__host__ __device__ inline int64_t fused_hdr_bytes(int K) {
+    const int blocks = (K / 128 + 3) / 4;
+    return ((int64_t)160 * blocks + 127) / 128 * 128;
+}
+__host__ __device__ inline int64_t fused_slice_bytes(int K) {
+    return fused_hdr_bytes(K) + (int64_t)(K / 128) * 1024;
+}
+// GPTQ qweight + scales [KG][N] + zeros (packed or uint8) -> fused buffer, and back
+// (scales [KG][N], packed zeros [KG][N/8]); G % 128 == 0.
+hipError_t launch_int4_prepack_fused(const int32_t* qweight, const void* scales, const void* zeros,
+                                     int zeros_format, int K, int N, int G, int32_t* fused,
+                                     hipStream_t stream);
+hipError_t launch_int4_unprepack_fused(const int32_t* fused, int K, int N, int G, int32_t* qweight,
+                                       void* scales, int32_t* zeros, hipStream_t stream);
 
 // W4A16 kernel families.
 enum W4A16Kind {
@@ -90,6 +107,9 @@ hipError_t launch_w4a16(const W4A16Launch& w, hipStream_t stream);
 // Planner for the W4A16 kernels (host-only).  `aligned`: scales 8-byte aligned and, for
 // uint8 zeros, zeros 4-byte aligned (the vector loads of the matrix-pipe decode kernel).
 W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned);
+// Whether the matrix-pipe decode kernel (the one reader of the fused layout) takes M rows
+// at this K: M <= 4 and its staged activations within its LDS budget.
+bool w4a16_fused_decode_ok(int M, int K);
 
 struct FlashLaunch {
     const void* Q;

@@ -583,6 +583,126 @@ std::vector<torch::Tensor> prepack_int4_params(torch::Tensor scales, torch::Tens
     return {so, zo};
 }
 
+// prepack_int4_fused(qweight [K/8, N] int32, scales [K/G, N] fp16, zeros [K/G, N/8] int32
+//   or [K/G, N] uint8, group_size=128) -> fused decode layout int32 [N/16, S/4] (S: bytes
+//   per 16-column slice; include/wmma_ops_amd.h, WMMA_W4_FUSED), read by matmul_int4_fused.
+torch::Tensor prepack_int4_fused(torch::Tensor qweight, torch::Tensor scales, torch::Tensor zeros,
+                                 int64_t group_size) {
+    check_qweight(qweight);
+    TORCH_CHECK(scales.is_cuda() && zeros.is_cuda(), "Inputs must be CUDA tensors");
+    TORCH_CHECK(qweight.device() == scales.device() && qweight.device() == zeros.device(),
+                "Inputs must be on same device");
+    const int64_t K = qweight.size(0) * 8, N = qweight.size(1);
+    TORCH_CHECK(K > 0 && N > 0 && K % 128 == 0 && N % 32 == 0,
+                "the fused layout needs K % 128 == 0 and N % 32 == 0");
+    TORCH_CHECK(group_size > 0 && K % group_size == 0, "group_size must divide K");
+    const int64_t ng = K / group_size;
+    TORCH_CHECK(scales.dtype() == torch::kFloat16 && scales.dim() == 2 && scales.size(0) == ng &&
+                    scales.size(1) == N,
+                "scales must be float16 [K/group_size, N]");
+    int zfmt;
+    if (zeros.dtype() == torch::kInt32) {
+        TORCH_CHECK(zeros.dim() == 2 && zeros.size(0) == ng && zeros.size(1) * 8 == N,
+                    "packed zeros must be int32 [K/group_size, N/8]");
+        zfmt = WMMA_ZEROS_PACKED;
+    } else {
+        TORCH_CHECK(zeros.dtype() == torch::kUInt8 && zeros.dim() == 2 && zeros.size(0) == ng &&
+                        zeros.size(1) == N,
+                    "zeros must be int32 [K/group_size, N/8] or uint8 [K/group_size, N]");
+        zfmt = WMMA_ZEROS_U8;
+    }
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(qweight.device());
+    qweight = qweight.contiguous();
+    scales = scales.contiguous();
+    zeros = zeros.contiguous();
+    const int64_t bytes = (int64_t)wmma_int4_fused_bytes((int)K, (int)N);
+    auto out = torch::empty({N / 16, bytes / (N / 16) / 4}, qweight.options());
+    check_status(wmma_int4_prepack_fused(qweight.data_ptr<int32_t>(), scales.data_ptr(),
+                                         zeros.data_ptr(), zfmt, (int)K, (int)N, (int)group_size,
+                                         out.data_ptr<int32_t>(), current_stream(qweight)),
+                 "wmma_int4_prepack_fused");
+    return out;
+}
+
+// K of a fused buffer from its words per slice (a header of 40 words per four 128-deep K
+// steps, padded to 32-word lines, then 256 words per K step), or -1 when no K gives that size.
+int64_t fused_k(int64_t words) {
+    const int64_t bytes = words * 4;
+    for (int64_t kp = bytes / 1024; kp >= 1 && kp * 1024 * 5 >= bytes * 4; --kp) {
+        const int64_t hdr = (160 * ((kp + 3) / 4) + 127) / 128 * 128;
+        if (hdr + kp * 1024 == bytes) return kp * 128;
+    }
+    return -1;
+}
+
+void check_fused(const torch::Tensor& f) {
+    TORCH_CHECK(f.is_cuda(), "fused must be a CUDA tensor");
+    TORCH_CHECK(f.dtype() == torch::kInt32 && f.dim() == 2 && fused_k(f.size(1)) > 0,
+                "fused must be the int32 [N/16, words per slice] output of prepack_int4_fused");
+}
+
+// unprepack_int4_fused(fused [N/16, S/4], group_size=128) -> (qweight [K/8, N] int32,
+//   scales [K/G, N] fp16, zeros [K/G, N/8] int32 packed).
+std::vector<torch::Tensor> unprepack_int4_fused(torch::Tensor fused, int64_t group_size) {
+    check_fused(fused);
+    const int64_t K = fused_k(fused.size(1)), N = fused.size(0) * 16;
+    TORCH_CHECK(group_size > 0 && K % group_size == 0, "group_size must divide K");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(fused.device());
+    fused = fused.contiguous();
+    auto qw = torch::empty({K / 8, N}, fused.options());
+    auto sc = torch::empty({K / group_size, N}, torch::dtype(torch::kFloat16).device(fused.device()));
+    auto zo = torch::empty({K / group_size, N / 8}, fused.options());
+    check_status(wmma_int4_unprepack_fused(fused.data_ptr<int32_t>(), (int)K, (int)N,
+                                           (int)group_size, qw.data_ptr<int32_t>(), sc.data_ptr(),
+                                           zo.data_ptr<int32_t>(), current_stream(fused)),
+                 "wmma_int4_unprepack_fused");
+    return {qw, sc, zo};
+}
+
+// matmul_int4_fused(A [M,K] fp16, fused (from prepack_int4_fused), group_size=128,
+//   out_dtype=None, perm=None) -> [M, N]: the W4A16 product for decode shapes (M <= 4)
+//   with the weights and group parameters read from the fused layout.
+torch::Tensor matmul_int4_fused(torch::Tensor A, torch::Tensor fused, int64_t group_size,
+                                c10::optional<at::ScalarType> out_dtype,
+                                c10::optional<torch::Tensor> perm) {
+    const bool half_out = out_dtype.has_value() && *out_dtype == torch::kFloat16;
+    TORCH_CHECK(!out_dtype.has_value() || *out_dtype == torch::kFloat16 ||
+                    *out_dtype == torch::kFloat32,
+                "out_dtype must be float32 or float16");
+    TORCH_CHECK(A.is_cuda() && fused.is_cuda(), "Inputs must be CUDA tensors");
+    TORCH_CHECK(A.device() == fused.device(), "Inputs must be on same device");
+    TORCH_CHECK(A.dtype() == torch::kFloat16, "A must be float16");
+    TORCH_CHECK(A.dim() == 2, "A must be 2D");
+    check_fused(fused);
+    const int64_t K = fused_k(fused.size(1)), N = fused.size(0) * 16;
+    TORCH_CHECK(A.size(1) == K, "Inner dimensions must match");
+    TORCH_CHECK(group_size > 0 && K % group_size == 0, "group_size must divide K");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(A.device());
+    if (perm.has_value() && perm->defined()) {
+        TORCH_CHECK(perm->device() == A.device() && perm->dim() == 1 && perm->size(0) == K &&
+                        perm->dtype() == torch::kInt64,
+                    "perm must be the int64 [K] permutation returned by int4_from_gptq");
+        A = A.index_select(1, *perm);
+    }
+    A = A.contiguous();
+    fused = fused.contiguous();
+    check_aligned(A, "A must be 16-byte aligned");
+    const int M = (int)A.size(0);
+    auto Y = torch::empty({A.size(0), N},
+                          torch::dtype(half_out ? torch::kFloat16 : torch::kFloat32).device(A.device()));
+    int rc;
+    if (half_out)
+        rc = wmma_w4a16_gemm_f16out(A.data_ptr(), A.stride(0), fused.data_ptr<int32_t>(), nullptr,
+                                    nullptr, WMMA_W4_FUSED, M, (int)N, (int)K, (int)group_size,
+                                    Y.data_ptr(), Y.stride(0), nullptr, 0, current_stream(A));
+    else
+        rc = wmma_w4a16_gemm(A.data_ptr(), A.stride(0), fused.data_ptr<int32_t>(), nullptr, nullptr,
+                             WMMA_W4_FUSED, M, (int)N, (int)K, (int)group_size, Y.data_ptr<float>(),
+                             Y.stride(0), nullptr, 0, current_stream(A));
+    check_status(rc, "wmma_w4a16_gemm");
+    return Y;
+}
+
 // matmul_int4(A[M,K] fp16, packed (from prepack_int4), scales[K/G, N] fp16,
 //             zeros[K/G, N/8] int32 packed or [K/G, N] uint8, group_size=128) -> fp32 [M, N];
 // or scales and zeros as returned by prepack_int4_params.
@@ -725,6 +845,16 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("prepack_int4_params", &prepack_int4_params,
           "scales/zeros -> slice-major layout accepted by matmul_int4", py::arg("scales"),
           py::arg("zeros"));
+    m.def("prepack_int4_fused", &prepack_int4_fused,
+          "GPTQ qweight + scales + zeros -> fused decode layout (one run per 16 columns)",
+          py::arg("qweight"), py::arg("scales"), py::arg("zeros"), py::arg("group_size") = 128);
+    m.def("unprepack_int4_fused", &unprepack_int4_fused,
+          "Inverse of prepack_int4_fused: (qweight, scales, packed zeros)", py::arg("fused"),
+          py::arg("group_size") = 128);
+    m.def("matmul_int4_fused", &matmul_int4_fused,
+          "W4A16 for decode shapes (M <= 4) from the fused layout", py::arg("A"), py::arg("fused"),
+          py::arg("group_size") = 128, py::arg("out_dtype") = py::none(),
+          py::arg("perm") = py::none());
     m.def("matmul_int4", &matmul_int4,
           "W4A16 dequant GEMM: fp16 A @ int4 W -> fp32 (or fp16 with out_dtype=torch.float16)",
           py::arg("A"), py::arg("packed"), py::arg("scales"), py::arg("zeros"),

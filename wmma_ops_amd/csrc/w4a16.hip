@@ -216,6 +216,137 @@ int4_params_slice_kernel(const uint16_t* __restrict__ s, const void* __restrict_
     }
 }
 
+// Fused decode layout (WMMA_W4_FUSED): weights, scales and zero points of a 16-column slice
+// in one contiguous run, so that a decode workgroup streams a single region.  Per slice:
+//   header   one 160-byte parameter block per four 128-deep K steps 4r .. 4r+3 (KP = K/128
+//            steps; the last block covers the steps left), zero-padded to a multiple of 128
+//            bytes so that the weight runs below stay on 128-byte lines:
+//              bytes [0, 128)   scales fp16 [4][16]: entry (u, c) = s[g][16*slice + c],
+//                               g = 128 (4r+u) / G
+//              bytes [128, 160) zero points [4][16] as nibbles: byte 128 + 8u + c/2, nibble
+//                               c % 2 (even columns in the low nibble)
+//   weights  1 KB per K step pp = the prepacked blocks kc = 2pp, 2pp+1 of the slice (its
+//            standard prepacked run, unchanged).
+// With G = 128 and K % 4096 == 0 the buffer holds exactly the bytes of the prepacked weights
+// plus the scales and packed zeros; a larger G repeats each group's parameters in every
+// K step of the group.  Parameter entries of steps past K are zero.
+constexpr int kFusedBlock = 160;
+
+template <int ZF>
+__global__ void __launch_bounds__(256)
+int4_prepack_fused_kernel(const int32_t* __restrict__ qw, const uint16_t* __restrict__ s,
+                          const void* __restrict__ z, int K, int N, int G,
+                          int32_t* __restrict__ out) {
+    const int64_t su = fused_slice_bytes(K) / 16;  // units per slice
+    const int64_t total = (int64_t)(N / 16) * su;
+    const int KP = K / 128;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const int sl = (int)(t / su);
+        const int64_t o = t - (int64_t)sl * su;
+        const int hu = (int)(fused_hdr_bytes(K) / 16);  // header units
+        // header unit o: parameter block r = o / 10, unit ou = o % 10 of it (units past the
+        // last block are padding); weight unit o - hu: K step (o - hu) / 64, lane % 64
+        const int r = o < hu ? (int)(o / 10) : 0;
+        const int ou = o < hu ? (o < 10 * ((KP + 3) / 4) ? (int)(o % 10) : -1) : 10 + (int)(o - hu);
+        u32x4 v = {0, 0, 0, 0};
+        if (ou < 0) {  // header padding
+        } else if (ou < 8) {  // scales: entries 8 ou .. 8 ou + 7 = K step ou/2, columns 8 (ou%2) ..
+            const int u = ou >> 1, pp = 4 * r + u;
+            if (pp < KP) {
+                const int64_t row = (int64_t)(pp * 128 / G) * N + 16 * sl + 8 * (ou & 1);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    v[e] = (uint32_t)s[row + 2 * e] | ((uint32_t)s[row + 2 * e + 1] << 16);
+            }
+        } else if (ou < 10) {  // zero nibbles: pair-steps 2 (ou-8), 2 (ou-8) + 1, 8 bytes each
+#pragma unroll
+            for (int hlf = 0; hlf < 2; ++hlf) {
+                const int pp = 4 * r + 2 * (ou - 8) + hlf;
+                if (pp >= KP) continue;
+                const int g = pp * 128 / G;
+                uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+                for (int c = 0; c < 16; ++c) {
+                    const int n = 16 * sl + c;
+                    uint32_t zz;
+                    if constexpr (ZF == WMMA_ZEROS_PACKED)
+                        zz = ((uint32_t)static_cast<const int32_t*>(z)[(int64_t)g * (N / 8) + n / 8] >>
+                              (4 * (n & 7))) & 0xFu;
+                    else
+                        zz = (uint32_t)static_cast<const uint8_t*>(z)[(int64_t)g * N + n] & 0xFu;
+                    if (c < 8)
+                        w0 |= zz << (4 * c);
+                    else
+                        w1 |= zz << (4 * (c - 8));
+                }
+                v[2 * hlf] = w0;
+                v[2 * hlf + 1] = w1;
+            }
+        } else {  // weights: K step (ou-10)/64, lane (ou-10)%64 of its 1 KB
+            const int wu = ou - 10, pp = wu >> 6, l = wu & 63;
+            const int kc = 2 * pp + (l >> 5), e = l & 31;
+            const int n = 16 * sl + (e & 15);
+            const int kg0 = 8 * kc + 4 * (e >> 4);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const uint32_t src = (uint32_t)qw[(int64_t)(kg0 + w) * N + n];
+                uint32_t dst = 0;
+#pragma unroll
+                for (int pnib = 0; pnib < 8; ++pnib)
+                    dst |= ((src >> (4 * kPermDev[pnib])) & 0xFu) << (4 * pnib);
+                v[w] = dst;
+            }
+        }
+        reinterpret_cast<u32x4*>(out)[t] = v;
+    }
+}
+
+// Inverse: the weight units back to GPTQ words (one thread per 16-byte weight unit), then
+// one thread per (group, slice) reads the parameters of the group's first pair-step.
+__global__ void __launch_bounds__(256)
+int4_unprepack_fused_kernel(const int32_t* __restrict__ in, int K, int N, int G,
+                            int32_t* __restrict__ qw, uint16_t* __restrict__ s,
+                            int32_t* __restrict__ z) {
+    const int KP = K / 128, KG = K / G, NS = N / 16;
+    const int64_t sb = fused_slice_bytes(K);
+    const int64_t nwu = (int64_t)NS * KP * 64;  // weight units
+    const int64_t total = nwu + (int64_t)KG * NS;
+    const unsigned char* base = reinterpret_cast<const unsigned char*>(in);
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        if (t < nwu) {
+            const int sl = (int)(t / ((int64_t)KP * 64));
+            const int rem = (int)(t - (int64_t)sl * KP * 64);
+            const int pp = rem >> 6, l = rem & 63;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(
+                base + sl * sb + fused_hdr_bytes(K) + (int64_t)pp * 1024 + 16 * l);
+            const int kc = 2 * pp + (l >> 5), e = l & 31;
+            const int n = 16 * sl + (e & 15);
+            const int kg0 = 8 * kc + 4 * (e >> 4);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                uint32_t dst = 0;
+#pragma unroll
+                for (int pnib = 0; pnib < 8; ++pnib)
+                    dst |= ((v[w] >> (4 * pnib)) & 0xFu) << (4 * kPermDev[pnib]);
+                qw[(int64_t)(kg0 + w) * N + n] = (int32_t)dst;
+            }
+        } else {
+            const int64_t u = t - nwu;
+            const int g = (int)(u / NS), sl = (int)(u % NS);
+            const int pp = g * G / 128;
+            const unsigned char* rec = base + sl * sb + (int64_t)(pp >> 2) * kFusedBlock;
+            const uint16_t* sp = reinterpret_cast<const uint16_t*>(rec) + 16 * (pp & 3);
+#pragma unroll
+            for (int c = 0; c < 16; ++c) s[(int64_t)g * N + 16 * sl + c] = sp[c];
+            const uint32_t* zp = reinterpret_cast<const uint32_t*>(rec + 128 + 8 * (pp & 3));
+            z[(int64_t)g * (N / 8) + 2 * sl] = (int32_t)zp[0];
+            z[(int64_t)g * (N / 8) + 2 * sl + 1] = (int32_t)zp[1];
+        }
+    }
+}
+
 // --------------------------------------------------------------------- dequantisation --
 struct W4Args {
     const f16* A;
@@ -696,6 +827,12 @@ w4a16_decode_mfma_kernel(W4Args p) {
     // Pair-step u of round r for this wave: each wave streams DM_U consecutive pair-steps
     // (4 KB of its slice's contiguous weights) per round.
     auto pstep = [&](int r, int u) { return DM_NW * DM_U * r + DM_U * wave + u; };
+    // Fused layout: this slice's run -- the parameter block of pair-step pp (block pp / 4,
+    // wave-uniform) in its header, then the weights.
+    const unsigned char* fslice =
+        reinterpret_cast<const unsigned char*>(p.W) + (int64_t)slice * fused_slice_bytes(K);
+    const unsigned char* fw = fslice + fused_hdr_bytes(K);
+    auto frec = [&](int pp) { return fslice + (int64_t)(pp >> 2) * kFusedBlock; };
     auto load_round = [&](int r, DecodeMRound<MM>& R) {
         // this lane's activation chunk / group parameters: pair-step `sub` of the round
         const int ppl = min(pstep(r, sub), KP - 1);
@@ -703,16 +840,26 @@ w4a16_decode_mfma_kernel(W4Args p) {
 #pragma unroll
         for (int m = 0; m < MM; ++m)
             R.a[m] = *reinterpret_cast<const u32x4*>(p.A + (int64_t)m * p.lda + ka);
-        const int g = ppl >> p.pp_shift;  // G = 128 << pp_shift
-        R.s = __builtin_bit_cast(uint16_t, p.S[s_index<ZF>(p, g, n)]);
-        if constexpr (ZF != WMMA_ZEROS_U8)
-            R.z = (uint32_t)static_cast<const int32_t*>(p.Z)[z_index<ZF>(p, g, n)];
-        else
-            R.z = static_cast<const uint8_t*>(p.Z)[z_index<ZF>(p, g, n)];
+        if constexpr (ZF == WMMA_W4_FUSED) {
+            const unsigned char* rec = frec(ppl);
+            R.s = *reinterpret_cast<const uint16_t*>(rec + 2 * (16 * (ppl & 3) + col));
+            R.z = rec[128 + 8 * (ppl & 3) + (col >> 1)];
+        } else {
+            const int g = ppl >> p.pp_shift;  // G = 128 << pp_shift
+            R.s = __builtin_bit_cast(uint16_t, p.S[s_index<ZF>(p, g, n)]);
+            if constexpr (ZF != WMMA_ZEROS_U8)
+                R.z = (uint32_t)static_cast<const int32_t*>(p.Z)[z_index<ZF>(p, g, n)];
+            else
+                R.z = static_cast<const uint8_t*>(p.Z)[z_index<ZF>(p, g, n)];
+        }
 #pragma unroll
         for (int u = 0; u < DM_U; ++u) {
             const int pp = min(pstep(r, u), KP - 1);
-            R.w[u] = __builtin_nontemporal_load(wcol + (int64_t)(2 * pp + dc) * 32);
+            if constexpr (ZF == WMMA_W4_FUSED)
+                R.w[u] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4*>(fw + (int64_t)pp * 1024 + 16 * lane));
+            else
+                R.w[u] = __builtin_nontemporal_load(wcol + (int64_t)(2 * pp + dc) * 32);
         }
     };
 
@@ -750,7 +897,9 @@ w4a16_decode_mfma_kernel(W4Args p) {
         uint32_t rs = R.s, rz = R.z;
         asm volatile("" : "+v"(rs), "+v"(rz));  // no work on them hoisted up to their load
         uint32_t z;
-        if constexpr (ZF != WMMA_ZEROS_U8)
+        if constexpr (ZF == WMMA_W4_FUSED)
+            z = (rz >> (4 * (col & 1))) & 0xFu;
+        else if constexpr (ZF != WMMA_ZEROS_U8)
             z = (rz >> (4 * (n & 7))) & 0xFu;
         else
             z = rz & 0xFu;
@@ -1568,6 +1717,33 @@ hipError_t launch_int4_params_slice(const void* scales, const void* zeros, int z
     return hipGetLastError();
 }
 
+hipError_t launch_int4_prepack_fused(const int32_t* qweight, const void* scales, const void* zeros,
+                                     int zeros_format, int K, int N, int G, int32_t* fused,
+                                     hipStream_t stream) {
+    const int64_t total = (int64_t)(N / 16) * (fused_slice_bytes(K) / 16);
+    const auto* s = static_cast<const uint16_t*>(scales);
+    if (zeros_format == WMMA_ZEROS_PACKED)
+        hipLaunchKernelGGL(int4_prepack_fused_kernel<WMMA_ZEROS_PACKED>, dim3(grid_for(total, 256)),
+                           dim3(256), 0, stream, qweight, s, zeros, K, N, G, fused);
+    else
+        hipLaunchKernelGGL(int4_prepack_fused_kernel<WMMA_ZEROS_U8>, dim3(grid_for(total, 256)),
+                           dim3(256), 0, stream, qweight, s, zeros, K, N, G, fused);
+    return hipGetLastError();
+}
+
+hipError_t launch_int4_unprepack_fused(const int32_t* fused, int K, int N, int G, int32_t* qweight,
+                                       void* scales, int32_t* zeros, hipStream_t stream) {
+    const int64_t total = (int64_t)(N / 16) * (K / 128) * 64 + (int64_t)(K / G) * (N / 16);
+    hipLaunchKernelGGL(int4_unprepack_fused_kernel, dim3(grid_for(total, 256)), dim3(256), 0,
+                       stream, fused, K, N, G, qweight, static_cast<uint16_t*>(scales), zeros);
+    return hipGetLastError();
+}
+
+bool w4a16_fused_decode_ok(int M, int K) {
+    return M >= 0 && M <= DM_MAXM && K % 128 == 0 &&
+           decode_mfma_lds_bytes(std::max(M, 1), K) <= kDecodeLdsMax;
+}
+
 // Host-only: choose the kernel and K split.
 //   decode-mfma  M <= 4, G = 128 * 2^j, K % 128 == 0, the staged activations fit LDS and
 //                the 16-column slices give at least half a workgroup per CU.
@@ -1786,6 +1962,18 @@ hipError_t launch_w4a16(const W4A16Launch& w, hipStream_t stream) {
     while (w.G >= 128 && (128 << (a.pp_shift + 1)) <= w.G) ++a.pp_shift;
     a.g_shift = 0;
     while ((2 << a.g_shift) <= w.G) ++a.g_shift;
+    if (w.zeros_format == WMMA_W4_FUSED) {
+        // The fused layout is read by the matrix-pipe decode kernel only (the planner gives
+        // it every shape the C-ABI accepts in this layout).
+        if (w.plan.kind != W4_DECODE_MFMA) return hipErrorInvalidValue;
+        const size_t lds = decode_mfma_lds_bytes(w.M, w.K);
+        const dim3 grid(w.N / 16), block(DM_NW * kWave);
+        if (decode_mfma_one(w.K))
+            launch_decode_mfma<WMMA_W4_FUSED, true>(a, w.M, grid, block, lds, stream);
+        else
+            launch_decode_mfma<WMMA_W4_FUSED, false>(a, w.M, grid, block, lds, stream);
+        return hipGetLastError();
+    }
     if (w.zeros_format == WMMA_ZEROS_PACKED) return launch_w4a16_zf<WMMA_ZEROS_PACKED>(a, w, stream);
     if (w.zeros_format == WMMA_ZEROS_SLICED) return launch_w4a16_zf<WMMA_ZEROS_SLICED>(a, w, stream);
     return launch_w4a16_zf<WMMA_ZEROS_U8>(a, w, stream);
