@@ -363,11 +363,7 @@ gemm_mfma_kernel(GemmArgs p) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int row = row0 + i * 32 + 8 * (r >> 2) + (r & 3);
-#ifdef WMMA_GEMM_NT_STORE
-                    __builtin_nontemporal_store(alpha * acc[i][j][r], &out[(int64_t)row * ldo + col0 + j * 32]);
-#else
                     out[(int64_t)row * ldo + col0 + j * 32] = alpha * acc[i][j][r];
-#endif
                 }
     } else if (full_tile) {
         // beta * C_in on a full tile: the C_in reads of 32x32 block b+1 are issued before
