@@ -124,9 +124,15 @@ int wmma_gemm_f16f32(const void* A, int64_t lda, const void* B, int64_t ldb,
  * ends), so the call performs no allocation of any kind.  A shape whose plan needs more
  * partial-sum space than that is rejected with WMMA_ERR_WORKSPACE (wmma_gemm_workspace_size
  * gives the need).  Every call on one GPU shares that GPU's array and nothing in it has to
- * start at zero (each split writes its whole partial tile before the reduction reads it);
- * calls that overlap on one GPU (other streams, other threads) race on it and must be
- * serialised by the caller.  Operands whose rows break 16-byte vectors are read in place
+ * start at zero (each split writes its whole partial tile before the reduction reads it).
+ * Calls outside stream capture are ordered by the library: a call on another stream than
+ * the previous split-K call on the GPU first waits (hipStreamWaitEvent) for an event
+ * recorded after that call's launches (the event is created by the first such call; host
+ * threads are serialised around wait + launch + record).  Under stream capture nothing is
+ * waited on or recorded: replays of a captured graph use the same array, so the caller
+ * must not let them overlap each other or other calls on the GPU.  The first call on a GPU
+ * (which looks up the array's address) may itself be made under capture.
+ * Operands whose rows break 16-byte vectors are read in place
  * by the element-wise kernels (no repacked copy).  No counterpart in the reference: for
  * callers that cannot allocate (code under stream capture, tight serving loops, harnesses
  * that forbid it).

@@ -132,3 +132,114 @@ def test_noalloc_ragged_shapes(first, second):
                 assert torch.equal(out_na, out_ref), (M, N, K)
             else:
                 assert og.max_rel_err(out_na, out_ref) <= 1e-6
+
+
+def _noalloc(lib, A, B, C, out, M, N, K, alpha, beta, stream):
+    return lib.wmma_gemm_f16f32_noalloc(A.data_ptr(), K, B.data_ptr(), N,
+                                        C.data_ptr() if C is not None else None, N,
+                                        out.data_ptr(), N, M, N, K, alpha, beta, -1, stream)
+
+
+def _workspace_ref(lib, A, B, C, M, N, K, alpha, beta):
+    need = lib.wmma_gemm_workspace_size(M, N, K, -1)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+    out = torch.empty(M, N, device="cuda")
+    rc = lib.wmma_gemm_f16f32(A.data_ptr(), K, B.data_ptr(), N,
+                              C.data_ptr() if C is not None else None, N, out.data_ptr(), N, M, N, K,
+                              alpha, beta, -1, ws.data_ptr(), need,
+                              torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.wmma_last_error()
+    torch.cuda.synchronize()
+    return out
+
+
+def _inputs(M, N, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    return ((torch.randn(M, K, generator=g)).half().cuda(),
+            (torch.randn(K, N, generator=g) * 0.05).half().cuda(),
+            torch.randn(M, N, generator=g).cuda())
+
+
+# Calls on two streams with no host synchronisation between them: the library orders them
+# (the second stream waits for the event recorded after the first call), so each output is
+# bit-identical to the workspace entry point's.  Several rounds alternate the streams and
+# the shapes (both split-K plans, the second smaller).
+def test_noalloc_two_streams_ordered():
+    lib = _lib()
+    shapes = [(128, 14336, 4096), (16, 4096, 4096), (64, 4096, 4096), (1, 4096, 4096)]
+    ins = [_inputs(M, N, K, 7 + i) for i, (M, N, K) in enumerate(shapes)]
+    refs = [_workspace_ref(lib, A, B, C, M, N, K, 2.0, 0.5) for (A, B, C), (M, N, K) in zip(ins, shapes)]
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    for rnd in range(3):
+        outs = []
+        for i, ((A, B, C), (M, N, K)) in enumerate(zip(ins, shapes)):
+            st = s1 if (i + rnd) % 2 == 0 else s2
+            out = torch.empty(M, N, device="cuda")
+            report("noalloc_streams", round=rnd, M=M, N=N, K=K)
+            assert _noalloc(lib, A, B, C, out, M, N, K, 2.0, 0.5, st.cuda_stream) == 0, lib.wmma_last_error()
+            outs.append(out)
+        torch.cuda.synchronize()
+        for out, ref in zip(outs, refs):
+            assert torch.equal(out, ref)
+
+
+# Free device memory is the same before and after a warmed-up call: the call allocates
+# nothing (hipMemGetInfo through torch.cuda.mem_get_info).
+def test_noalloc_allocates_nothing():
+    lib = _lib()
+    M, N, K = 128, 14336, 4096
+    A, B, C = _inputs(M, N, K, 11)
+    out = torch.empty(M, N, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    assert _noalloc(lib, A, B, C, out, M, N, K, 1.0, 0.0, st) == 0
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for _ in range(3):
+        assert _noalloc(lib, A, B, C, out, M, N, K, 1.0, 0.0, st) == 0
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+
+
+_CAPTURE_SCRIPT = r"""
+import ctypes, os, sys
+import torch
+sys.path.insert(0, {root!r})
+from tests.test_zz_no_alloc import _lib, _inputs, _workspace_ref, _noalloc
+lib = _lib()
+M, N, K = 128, 4096, 14336          # tiled split-K: partial sums in the scratch array
+A, B, C = _inputs(M, N, K, 5)
+out = torch.empty(M, N, device="cuda")
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):            # the process's first noalloc call happens under capture
+    rc = _noalloc(lib, A, B, C, out, M, N, K, 2.0, 0.5, torch.cuda.current_stream().cuda_stream)
+assert rc == 0, lib.wmma_last_error()
+ref = _workspace_ref(lib, A, B, C, M, N, K, 2.0, 0.5)
+M2, N2, K2 = 16, 4096, 4096         # eager noalloc work between replays (skinny split-K)
+A2, B2, C2 = _inputs(M2, N2, K2, 6)
+ref2 = _workspace_ref(lib, A2, B2, C2, M2, N2, K2, 1.0, 0.0)
+for rep in range(4):
+    out.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), rep
+    o2 = torch.empty(M2, N2, device="cuda")
+    assert _noalloc(lib, A2, B2, C2, o2, M2, N2, K2, 1.0, 0.0, torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(o2, ref2), rep
+print("CAPTURE_OK", flush=True)
+"""
+
+
+# A split-K noalloc GEMM captured into a graph, in a fresh process whose first noalloc call
+# is the captured one (the scratch address is looked up under capture), replayed four times
+# with eager noalloc calls in between; every replay equals the workspace entry point.
+def test_noalloc_first_call_under_graph_capture():
+    import subprocess
+    import sys
+
+    report("noalloc_capture", M=128, N=4096, K=14336)
+    r = subprocess.run([sys.executable, "-c", _CAPTURE_SCRIPT.format(root=ROOT)], cwd=ROOT,
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=110)
+    assert r.returncode == 0 and "CAPTURE_OK" in r.stdout, r.stdout[-3000:]

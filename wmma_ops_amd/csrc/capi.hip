@@ -83,9 +83,19 @@ namespace {
 void* g_scratch_ptr[kMaxDevices];
 hipError_t g_scratch_rc[kMaxDevices];
 std::once_flag g_scratch_once[kMaxDevices];
+// Cross-stream ordering of the calls that use a device's scratch array: each such call
+// (outside stream capture) first makes its stream wait for the event the previous call
+// recorded after its own launches, when that call ran on another stream.  The event is
+// created by the first such call on the device made outside capture; later calls create
+// nothing.  g_scratch_mu serialises host threads around wait + launch + record.
+hipEvent_t g_scratch_ev[kMaxDevices];
+bool g_scratch_ev_made[kMaxDevices];
+hipStream_t g_scratch_last[kMaxDevices];
+bool g_scratch_recorded[kMaxDevices];
+std::mutex g_scratch_mu[kMaxDevices];
 
 // Device address of `scratch` on the current device (once per device, with it current).
-int scratch_for_current_device(void** out) {
+int scratch_for_current_device(void** out, int* dev_out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_status(e, "hipGetDevice");
@@ -97,6 +107,37 @@ int scratch_for_current_device(void** out) {
     });
     if (g_scratch_rc[dev] != hipSuccess) return hip_status(g_scratch_rc[dev], "hipGetSymbolAddress(scratch)");
     *out = g_scratch_ptr[dev];
+    *dev_out = dev;
+    return WMMA_OK;
+}
+
+// Before a call's launches on `st` (with g_scratch_mu[dev] held): wait for the previous
+// scratch user when it ran on another stream.  *ordered is false under stream capture,
+// where no event is waited on or recorded (a captured graph is ordered by whoever
+// launches it).
+int scratch_order_before(int dev, hipStream_t st, bool* ordered) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(st, &cs);
+    if (e != hipSuccess) return hip_status(e, "hipStreamIsCapturing");
+    *ordered = cs == hipStreamCaptureStatusNone;
+    if (*ordered && !g_scratch_ev_made[dev]) {
+        e = hipEventCreateWithFlags(&g_scratch_ev[dev], hipEventDisableTiming);
+        if (e != hipSuccess) return hip_status(e, "hipEventCreate(scratch)");
+        g_scratch_ev_made[dev] = true;
+    }
+    if (*ordered && g_scratch_recorded[dev] && g_scratch_last[dev] != st) {
+        e = hipStreamWaitEvent(st, g_scratch_ev[dev], 0);
+        if (e != hipSuccess) return hip_status(e, "hipStreamWaitEvent(scratch)");
+    }
+    return WMMA_OK;
+}
+
+// After the launches: the next scratch user on another stream waits for this point.
+int scratch_order_after(int dev, hipStream_t st) {
+    hipError_t e = hipEventRecord(g_scratch_ev[dev], st);
+    if (e != hipSuccess) return hip_status(e, "hipEventRecord(scratch)");
+    g_scratch_last[dev] = st;
+    g_scratch_recorded[dev] = true;
     return WMMA_OK;
 }
 }  // namespace
@@ -190,14 +231,21 @@ static int gemm_run(const void* A, int64_t lda, const void* B, int64_t ldb, cons
         int rc = make_plan(M, N, K, tile_cfg, current_cus(), &plan);
         if (rc != WMMA_OK) return fail(rc, "planner rejected the shape");
     }
+    int scratch_dev = -1;
+    bool scratch_ordered = false;
+    std::unique_lock<std::mutex> scratch_lock;
     if (use_scratch && plan.workspace_bytes > 0) {
         if (plan.workspace_bytes > kScratchBytes)
             return fail(WMMA_ERR_WORKSPACE,
                         "split-K needs %zu bytes of scratch; the allocation-free entry point "
                         "holds at most %zu (use wmma_gemm_f16f32 with a workspace)",
                         plan.workspace_bytes, kScratchBytes);
-        if (int rc = scratch_for_current_device(&workspace)) return rc;
+        if (int rc = scratch_for_current_device(&workspace, &scratch_dev)) return rc;
         workspace_bytes = kScratchBytes;
+        scratch_lock = std::unique_lock<std::mutex>(g_scratch_mu[scratch_dev]);
+        if (int rc = scratch_order_before(scratch_dev, static_cast<hipStream_t>(stream),
+                                          &scratch_ordered))
+            return rc;
     }
     if (plan.workspace_bytes > 0) {
         if (!workspace)
@@ -270,20 +318,28 @@ static int gemm_run(const void* A, int64_t lda, const void* B, int64_t ldb, cons
         g.plan = pl;
         return hip_status(launch_gemm(g, static_cast<hipStream_t>(stream)), "gemm launch");
     };
-    if (plan.edge_dim == WMMA_EDGE_NONE) return launch_part(plan, 0, 0, M, N);
-    // Two parts, one after the other on the stream (the edge's split-K partial sums reuse
-    // the workspace): the bulk on whole waves of 256x256 tiles, then the edge with the plan
-    // the planner gives its own shape.  Column offsets keep 16-byte alignment (edge_at is a
-    // multiple of 256) and 4-byte alignment of B for the skinny kernel.
-    const bool rows = plan.edge_dim == WMMA_EDGE_ROWS;
-    const int at = plan.edge_at;
-    wmma_gemm_plan edge{};
-    if (make_plan(rows ? M - at : M, rows ? N : N - at, K, WMMA_TILE_AUTO, current_cus(), &edge) !=
-            WMMA_OK ||
-        edge.edge_dim != WMMA_EDGE_NONE || edge.workspace_bytes > plan.workspace_bytes)
-        return fail(WMMA_ERR_INVALID_ARG, "inconsistent two-part plan");
-    if (int rc = launch_part(plan, 0, 0, rows ? at : M, rows ? N : at)) return rc;
-    return rows ? launch_part(edge, at, 0, M - at, N) : launch_part(edge, 0, at, M, N - at);
+    auto launch_all = [&]() -> int {
+        if (plan.edge_dim == WMMA_EDGE_NONE) return launch_part(plan, 0, 0, M, N);
+        // Two parts, one after the other on the stream (the edge's split-K partial sums
+        // reuse the workspace): the bulk on whole waves of 256x256 tiles, then the edge with
+        // the plan the planner gives its own shape.  Column offsets keep 16-byte alignment
+        // (edge_at is a multiple of 256) and 4-byte alignment of B for the skinny kernel.
+        const bool rows = plan.edge_dim == WMMA_EDGE_ROWS;
+        const int at = plan.edge_at;
+        wmma_gemm_plan edge{};
+        if (make_plan(rows ? M - at : M, rows ? N : N - at, K, WMMA_TILE_AUTO, current_cus(),
+                      &edge) != WMMA_OK ||
+            edge.edge_dim != WMMA_EDGE_NONE || edge.workspace_bytes > plan.workspace_bytes)
+            return fail(WMMA_ERR_INVALID_ARG, "inconsistent two-part plan");
+        if (int rc = launch_part(plan, 0, 0, rows ? at : M, rows ? N : at)) return rc;
+        return rows ? launch_part(edge, at, 0, M - at, N) : launch_part(edge, 0, at, M, N - at);
+    };
+    const int rc = launch_all();
+    if (scratch_dev >= 0 && scratch_ordered) {
+        const int rc2 = scratch_order_after(scratch_dev, static_cast<hipStream_t>(stream));
+        if (rc == WMMA_OK) return rc2;
+    }
+    return rc;
 }
 
 int wmma_gemm_f16f32(const void* A, int64_t lda, const void* B, int64_t ldb, const float* C_in,
