@@ -178,6 +178,76 @@ def line(**kw):
     print(json.dumps(kw), flush=True)
 
 
+class ClockSampler:
+    """Samples the GPU's current gfx clock (MHz) and socket power (W) from the SMU's metrics
+    table (amdsmi, `current_gfxclk` / `current_socket_power`) every ~5 ms on a host thread
+    while the block runs.  `summary()` gives the medians over the samples, or None when
+    amdsmi is not available (the field is then null in the JSON)."""
+
+    def __init__(self, device_index=0):
+        self.samples = []
+        self._stop = False
+        self._h = None
+        try:
+            import amdsmi
+
+            amdsmi.amdsmi_init()
+            self._smi = amdsmi
+            self._h = amdsmi.amdsmi_get_processor_handles()[device_index]
+        except Exception:  # noqa: BLE001 - optional instrumentation
+            self._h = None
+
+    def _run(self):
+        while not self._stop:
+            try:
+                m = self._smi.amdsmi_get_gpu_metrics_info(self._h)
+                clk, pw = m.get("current_gfxclk"), m.get("current_socket_power")
+                if isinstance(clk, (int, float)):
+                    self.samples.append((float(clk), float(pw) if isinstance(pw, (int, float)) else None))
+            except Exception:  # noqa: BLE001
+                pass
+            time.sleep(0.005)
+
+    def __enter__(self):
+        import threading
+
+        if self._h is not None:
+            self._t = threading.Thread(target=self._run, daemon=True)
+            self._t.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop = True
+        if self._h is not None:
+            self._t.join()
+        return False
+
+    def summary(self):
+        if not self.samples:
+            return None
+        clk = statistics.median(c for c, _ in self.samples)
+        pw = [p for _, p in self.samples if p is not None]
+        return {"sclk_MHz": clk, "socket_power_W": statistics.median(pw) if pw else None,
+                "samples": len(self.samples)}
+
+
+def sustained_clock(fn, seconds=0.6):
+    """The gfx clock and socket power a sustained run of fn(i) holds: fn back to back for
+    `seconds` after the settle phase, sampled by ClockSampler (medians)."""
+    import torch
+
+    settle(fn)
+    with ClockSampler() as cs:
+        t_end = time.perf_counter() + seconds
+        i = 0
+        while time.perf_counter() < t_end:
+            for _ in range(32):
+                fn(i)
+                i += 1
+            torch.cuda.synchronize()
+    return cs.summary()
+
+
 def roofline(nbytes, flops, ms):
     """The binding roofline of a case: the larger of its HBM time (bytes / 8 TB/s) and its
     matrix-pipe time (FLOPs / 2.5 PFLOP/s), as a fraction of the measured time, with each
@@ -886,6 +956,21 @@ FAMILIES = {"gemm": fam_gemm, "epilogue": fam_epilogue, "skinny": fam_skinny, "r
 
 
 # ------------------------------------------------------------------------ headline --
+def gemm_clock_and_batches(wo):
+    """The headline GEMM's sustained clock / power (ClockSampler) and its median of 5
+    event-timed batches of 200 back-to-back calls (BASELINE.md's timing convention)."""
+    import torch
+
+    g = torch.Generator().manual_seed(42 + 1)
+    A = torch.randn(M, K, generator=g).half().cuda()
+    B = torch.randn(K, N, generator=g).half().cuda()
+    fn = lambda i: wo.matmul(A, B)
+    clock = sustained_clock(fn)
+    ms = time_batches(fn, 200)
+    return clock, {"us_per_call": round(ms * 1e3, 2),
+                   "TFLOPS": round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 1)}
+
+
 def gemm_bench(wo, steps, warmup):
     import torch
 
@@ -1032,6 +1117,10 @@ def headline(wo, args):
             traffic = json.load(f).get("hbm_bytes_per_launch")
     plan = wo.gemm_plan(M, N, K)
     ceiling, _ = mfma_ceiling(calls=100)
+    clock, batches = gemm_clock_and_batches(wo)
+    sclk = clock["sclk_MHz"] * 1e6 if clock else None
+    # dense FP16 MFMA peak at the measured clock: 256 CUs x 4096 FLOP per clock per CU
+    peak_sclk = 256 * 4096 * sclk if sclk else None
     out = {
         "metric": METRIC,
         "value": round(tflops, 2),
@@ -1061,7 +1150,16 @@ def headline(wo, args):
                                  "frac": round(achieved * 1e12 / ceiling, 4),
                                  "what": "v_mfma_f32_32x32x16_f16 back to back, 512 workgroups "
                                          "x 4 waves x 8 accumulators, random fp16 register "
-                                         "operands (bench.py --workload mfma_ceiling)"}},
+                                         "operands (bench.py --workload mfma_ceiling)"},
+                     # the gfx clock this GEMM holds under sustained load (SMU metrics via
+                     # amdsmi, median over ~0.6 s of back-to-back launches) and the dense
+                     # FP16 peak at that clock (256 CUs x 4096 FLOP/clk)
+                     "sclk_GHz": round(sclk / 1e9, 3) if sclk else None,
+                     "peak_at_sclk": round(peak_sclk / 1e12, 1) if peak_sclk else None,
+                     "frac_at_sclk": round(achieved * 1e12 / peak_sclk, 4) if peak_sclk else None,
+                     "socket_power_W": clock["socket_power_W"] if clock else None},
+        # BASELINE.md's convention: median of 5 event-timed batches of back-to-back calls
+        "median_of_5_batches": batches,
     }
     if not args.no_w4a16:
         out["w4a16_m1"] = [w4a16_case(wo, 1, n) for n in (4096, 14336)]

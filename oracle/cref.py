@@ -8,7 +8,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB = os.path.join(_HERE, "liboracle.so")
+# WMMA_ORACLE_LIBRARY: another build of the same sources (the host-sanitized one of
+# `python -m wmma_ops_amd.build --sanitize`)
+LIB = os.environ.get("WMMA_ORACLE_LIBRARY") or os.path.join(_HERE, "liboracle.so")
 _lib = None
 
 

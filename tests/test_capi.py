@@ -16,7 +16,9 @@ import torch
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "wmma_ops_amd.h")
-LIB = os.path.join(ROOT, "wmma_ops_amd", "libwmma_ops_amd.so")
+# WMMA_OPS_AMD_LIBRARY: another build of the same library (the host-sanitized one of
+# `python -m wmma_ops_amd.build --sanitize`)
+LIB = os.environ.get("WMMA_OPS_AMD_LIBRARY") or os.path.join(ROOT, "wmma_ops_amd", "libwmma_ops_amd.so")
 
 OK, INVALID, UNSUPPORTED, MISALIGNED, WORKSPACE = 0, 1, 2, 3, 4
 

@@ -134,6 +134,78 @@ def build(verbose: bool = False) -> None:
     build_calib(verbose)
 
 
+# ------------------------------------------------------------- host sanitizer build --
+# AddressSanitizer + UndefinedBehaviorSanitizer on the CPU side only: the C-ABI's argument
+# validation and host code (capi.hip and the host halves of the kernel files), the planner
+# (plan.cpp) and the plain-C oracle.  Device code is built exactly as in the product
+# (every -fsanitize= applies to the host pass only).  Outputs go to _build/sanitize/; the
+# product library is untouched.
+SAN_DIR = os.path.join(BUILD, "sanitize")
+LLVM_BIN = os.path.join(ROCM, "lib", "llvm", "bin")
+SAN_HOST = ["-fsanitize=address", "-fsanitize=undefined", "-fno-sanitize-recover=undefined",
+            "-fno-omit-frame-pointer"]
+
+
+def _asan_runtime() -> str:
+    out = subprocess.run([os.path.join(LLVM_BIN, "clang"), "-print-file-name=libclang_rt.asan-x86_64.so"],
+                         stdout=subprocess.PIPE, text=True, check=True).stdout.strip()
+    if not os.path.isfile(out):  # older layouts keep it under lib/linux
+        import glob
+        hits = glob.glob(os.path.join(ROCM, "lib", "llvm", "lib", "clang", "*", "lib", "linux",
+                                      "libclang_rt.asan-x86_64.so"))
+        out = hits[0] if hits else out
+    return out
+
+
+def build_sanitized(verbose: bool = False) -> dict:
+    """Host-sanitized copies of the C-ABI library and the C oracle (clang for every host
+    pass, so one ASan runtime serves both)."""
+    os.makedirs(SAN_DIR, exist_ok=True)
+    host_flags = [x for f in SAN_HOST for x in ("-Xarch_host", f)]
+    objs, jobs = [], []
+    for src in HIP_SOURCES:
+        obj = os.path.join(SAN_DIR, src + ".o")
+        objs.append(obj)
+        jobs.append([HIPCC, *HIP_FLAGS, *host_flags, "-g", "-c", os.path.join(CSRC, src), "-o", obj])
+    for src in HOST_SOURCES:
+        obj = os.path.join(SAN_DIR, src + ".o")
+        objs.append(obj)
+        jobs.append([os.path.join(LLVM_BIN, "clang++"), "-O1", "-g", "-std=c++17", "-fPIC", "-Wall",
+                     *SAN_HOST, "-c", os.path.join(CSRC, src), "-o", obj])
+    with ThreadPoolExecutor(max_workers=min(len(jobs), 8)) as ex:
+        list(ex.map(lambda c: _run(c, verbose), jobs))
+    lib = os.path.join(SAN_DIR, LIB_NAME)
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-shared-libsan", *host_flags,
+          "-o", lib, *objs], verbose)
+    odir = os.path.join(ROOT, "oracle")
+    olib = os.path.join(SAN_DIR, "liboracle.so")
+    _run([os.path.join(LLVM_BIN, "clang"), "-O1", "-g", "-fPIC", "-std=c11", "-Wall",
+          "-ffp-contract=off", *SAN_HOST, "-shared-libsan", "-shared", "-o", olib,
+          os.path.join(odir, "gemm_ref.c"), os.path.join(odir, "int4_ref.c"), "-lm"], verbose)
+    return {"library": lib, "oracle": olib, "runtime": _asan_runtime()}
+
+
+def run_sanitized_tests(verbose: bool = False) -> int:
+    """The CPU suites that drive the sanitized code -- tests/test_capi.py (every C-ABI
+    validation path, the planner) and tests/test_oracle.py (the C oracle) -- with the
+    sanitized libraries in place of the product ones and the ASan runtime preloaded.  Any
+    ASan or UBSan report aborts the process (halt_on_error), so a clean exit means none."""
+    paths = build_sanitized(verbose)
+    env = dict(os.environ)
+    env.update({
+        "LD_PRELOAD": paths["runtime"],
+        "ASAN_OPTIONS": "detect_leaks=0:halt_on_error=1:abort_on_error=1",
+        "UBSAN_OPTIONS": "halt_on_error=1:print_stacktrace=1",
+        "WMMA_OPS_AMD_LIBRARY": paths["library"],
+        "WMMA_ORACLE_LIBRARY": paths["oracle"],
+    })
+    cmd = [sys.executable, "-m", "pytest", "-q", "-x", "-m", "not gpu", "-p", "no:cacheprovider",
+           os.path.join(ROOT, "tests", "test_capi.py"), os.path.join(ROOT, "tests", "test_oracle.py")]
+    return subprocess.run(cmd, cwd=ROOT, env=env).returncode
+
+
 if __name__ == "__main__":
+    if "--sanitize" in sys.argv:
+        sys.exit(run_sanitized_tests(verbose="-v" in sys.argv))
     build(verbose="-v" in sys.argv)
     print("built", os.path.join(PKG, LIB_NAME), os.path.join(PKG, EXT_NAME))
