@@ -719,6 +719,29 @@ def fam_vendor(wo):
                      us=round(ms2 * 1e3, 2), TFLOPS=round(fl / (ms2 * 1e-3) / 1e12, 1),
                      frac_mfma_peak=round(fl / (ms2 * 1e-3) / PEAK_FP16_FLOPS, 4))
         del Ad, Bd
+    # Microsecond shapes, both libraries captured in a HIP graph and replayed (launch gaps
+    # out of the figure): the small squares of configs[0..1] with the inputs resident, and
+    # the few-row shapes of configs[2] with the inputs rotated over > 512 MB as in `skinny`.
+    small = [(512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048)] + \
+            [(m, 4096, 4096) for m in (1, 16, 32, 64, 128)] + [(128, 14336, 4096)]
+    for (m, n, k) in small:
+        g = torch.Generator().manual_seed(42 + 2)
+        A = torch.randn(m, k, generator=g).half()
+        B = (torch.randn(k, n, generator=g) * 0.02).half()
+        nbytes = 2 * m * k + 2 * k * n + 4 * m * n
+        cp = copies_for(nbytes) if m <= 128 and m < n else 2
+        As = [A.cuda() for _ in range(cp)]
+        Bs = [B.cuda() for _ in range(cp)]
+        fl = 2.0 * m * n * k
+        for lib, fn in (("torch.mm (hipBLASLt/rocBLAS)",
+                         lambda i: torch.mm(As[i % cp], Bs[i % cp], out_dtype=torch.float32)),
+                        ("wmma_ops_amd.matmul", lambda i: wo.matmul(As[i % cp], Bs[i % cp]))):
+            ms, _ = time_graph(fn, cp if cp > 2 else 20)
+            line(family="vendor_gemm_small", M=m, N=n, K=k, out="f32", library=lib,
+                 us=round(ms * 1e3, 2), TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
+                 GBps=round(nbytes / (ms * 1e-3) / 1e9, 1), rotation_copies=cp,
+                 timing="graph replay")
+        del As, Bs
     # 4096^3 fp32-output on all-ones operands (the operand bits never switch, so the board's
     # power limit holds the clock less): both kernels' pipelines without the data's energy.
     Ad = torch.ones(4096, 4096, dtype=torch.float16, device="cuda")
