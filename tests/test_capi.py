@@ -563,3 +563,82 @@ def test_w4a16_offset_limits(lib):
     rc = lib.wmma_w4a16_gemm(FAKE, K, FAKE, FAKE, FAKE, 0, 4, 64, K, 128, FAKE, 64, None, 0, None)
     assert rc == UNSUPPORTED
     assert b"weight offsets" in lib.wmma_last_error()
+
+
+# --------------------------------------------------- fused decode layout validation --
+def test_fused_layout_validation_codes(lib):
+    """wmma_int4_fused_bytes against the oracle's layout arithmetic, and every argument
+    check of the fused prepack / unprepack / W4A16 entry points (none reaches the GPU)."""
+    from oracle import int4 as oi
+    vp, i32, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    lib.wmma_int4_fused_bytes.argtypes = [i32, i32]
+    lib.wmma_int4_fused_bytes.restype = sz
+    for K, N in ((4096, 4096), (4096, 14336), (640, 32), (128, 64), (1152, 96)):
+        assert lib.wmma_int4_fused_bytes(K, N) == (N // 16) * oi.fused_slice_bytes(K), (K, N)
+    for K, N in ((192, 64), (4096, 48), (0, 64), (4096, -32)):
+        assert lib.wmma_int4_fused_bytes(K, N) == 0, (K, N)
+    lib.wmma_int4_prepack_fused.argtypes = [vp, vp, vp, i32, i32, i32, i32, vp, vp]
+    pf = lambda q=FAKE, s=FAKE, z=FAKE, zf=0, K=4096, N=4096, G=128, out=FAKE: \
+        lib.wmma_int4_prepack_fused(q, s, z, zf, K, N, G, out, None)
+    assert pf(K=192) == UNSUPPORTED            # K % 128
+    assert pf(N=48) == UNSUPPORTED             # N % 32
+    assert pf(K=0) == INVALID
+    for G in (64, 384, 96, 8192):              # not 128 * 2^j dividing K
+        assert pf(G=G) == UNSUPPORTED, G
+    assert pf(zf=2) == INVALID                 # slice-major parameters cannot be fused
+    assert pf(zf=7) == INVALID
+    assert pf(q=None) == INVALID and pf(s=None) == INVALID and pf(z=None) == INVALID
+    assert pf(out=None) == INVALID
+    assert pf(out=FAKE + 4) == MISALIGNED
+    assert pf(q=FAKE + 2) == MISALIGNED
+    assert pf(s=FAKE + 1) == MISALIGNED
+    assert pf(z=FAKE + 2) == MISALIGNED        # packed zeros: 4-byte aligned
+    lib.wmma_int4_unprepack_fused.argtypes = [vp, i32, i32, i32, vp, vp, vp, vp]
+    uf = lambda f=FAKE, K=4096, N=4096, G=128, q=FAKE, s=FAKE, z=FAKE: \
+        lib.wmma_int4_unprepack_fused(f, K, N, G, q, s, z, None)
+    assert uf(K=192) == UNSUPPORTED and uf(G=64) == UNSUPPORTED and uf(N=16) == UNSUPPORTED
+    assert uf(f=None) == INVALID and uf(q=None) == INVALID
+    assert uf(f=FAKE + 8) == MISALIGNED and uf(z=FAKE + 2) == MISALIGNED and uf(s=FAKE + 1) == MISALIGNED
+    # the W4A16 entry point with the fused layout: decode shapes only, G = 128 * 2^j
+    w = lambda M=1, K=4096, G=128, A=FAKE: lib.wmma_w4a16_gemm(A, K, FAKE, None, None, 3, M, 4096, K,
+                                                              G, FAKE, 4096, None, 0, None)
+    assert w(M=5) == UNSUPPORTED
+    assert b"decode kernel only" in lib.wmma_last_error()
+    assert w(G=64) == UNSUPPORTED
+    assert w(K=4160, G=64) == UNSUPPORTED      # K % 128 != 0
+    assert w(M=0) == OK                        # empty output: scales and zeros are not read
+    assert w(A=FAKE + 2) == MISALIGNED
+    assert w(A=None) == INVALID
+
+
+# ------------------------------------------------- allocation-free GEMM validation --
+def test_noalloc_validation_codes(lib):
+    """wmma_gemm_f16f32_noalloc rejects bad arguments exactly like wmma_gemm_f16f32 (before
+    touching a device: the scratch address is looked up only after these checks), and every
+    plan the planner makes fits its scratch array: over a sweep of shapes and every tile
+    choice, the split-K partial sums need at most 16 MiB of the 32 MiB (the entry point's
+    WMMA_ERR_WORKSPACE rejection is a guard that no planner plan reaches)."""
+    vp, i64, i32, f32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    lib.wmma_gemm_f16f32_noalloc.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32,
+                                             f32, f32, i32, vp]
+    lib.wmma_gemm_noalloc_scratch_bytes.restype = sz
+    cap = lib.wmma_gemm_noalloc_scratch_bytes()
+    assert cap == 32 << 20
+    na = lambda M=64, N=64, K=64, lda=64, ldb=64, ldc=64, C=FAKE, A=FAKE, cfg=-1: \
+        lib.wmma_gemm_f16f32_noalloc(A, lda, FAKE, ldb, None, 0, C, ldc, M, N, K, 1.0, 0.0, cfg, None)
+    assert na(M=-1) == INVALID
+    assert na(cfg=9) == INVALID
+    assert na(C=None) == INVALID
+    assert na(ldc=32) == INVALID
+    assert na(lda=32) == INVALID
+    assert na(A=None) == INVALID
+    assert na(M=0) == OK and na(N=0) == OK     # empty output
+    p = Plan()
+    largest = 0
+    for cfg in range(-1, 6):
+        for M in (1, 16, 32, 64, 128, 256, 1024, 4100):
+            for N in (520, 4096, 16384, 65536):
+                for K in (520, 4096, 65536, 262144):
+                    assert lib.wmma_gemm_plan_make(M, N, K, cfg, 256, ctypes.byref(p)) == OK
+                    largest = max(largest, p.workspace_bytes)
+    assert largest == 16 << 20 and largest <= cap
