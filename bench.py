@@ -263,6 +263,24 @@ def copies_for(nbytes):
     return max(2, math.ceil(ROTATE_BYTES / max(nbytes, 1)))
 
 
+ALLCLOSE_RTOL = 1e-3      # elementwise check beside the max-relative bar:
+ALLCLOSE_ATOL_REL = 1e-4  # |Y - ref| <= 1e-3 |ref| + 1e-4 max|ref| for every element
+
+
+def parity(Y, ref):
+    """The error metrics of a parity spot check against the fp32 oracle: max|Y-ref| /
+    max|ref| (the bar, 1e-3), the relative L2 error and an elementwise allclose."""
+    import torch
+
+    from oracle import gemm as og
+
+    Y, ref = Y.detach().float().cpu(), ref.detach().float().cpu()
+    m = float(ref.abs().max()) if ref.numel() else 0.0
+    return {"max_rel_err": float(f"{og.max_rel_err(Y, ref):.3e}"),
+            "rel_l2": float(f"{og.rel_l2_err(Y, ref):.3e}"),
+            "allclose": bool(torch.allclose(Y, ref, rtol=ALLCLOSE_RTOL, atol=ALLCLOSE_ATOL_REL * m))}
+
+
 # ------------------------------------------------------------------------ families --
 def fam_gemm(wo):
     import torch
@@ -277,12 +295,11 @@ def fam_gemm(wo):
         Ad, Bd = A.cuda(), B.cuda()
         calls = 200 if m <= 1024 else 50
         ms = time_batches(lambda i: wo.matmul(Ad, Bd), calls)
-        err = og.max_rel_err(wo.matmul(Ad[:256], Bd), og.gemm_ref(A[:256], B))
+        par = parity(wo.matmul(Ad[:256], Bd), og.gemm_ref(A[:256], B))
         fl = 2.0 * m * n * k
         line(family="gemm", M=m, N=n, K=k, plan=wo.gemm_plan(m, n, k), us=round(ms * 1e3, 2),
              TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
-             frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4),
-             max_rel_err=float(f"{err:.3e}"))
+             frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4), **par)
 
 
 def fam_epilogue(wo):
@@ -336,12 +353,12 @@ def fam_skinny(wo):
         C0 = wo.matmul(As[0], Bs[0])
         ms, outs = time_graph(lambda i: wo.matmul(As[i % cp], Bs[i % cp]), cp)
         assert torch.equal(outs[0], C0), "graph replay differs from eager"
-        err = og.max_rel_err(C0, og.gemm_ref(A, B))
+        par = parity(C0, og.gemm_ref(A, B))
         line(family="skinny", M=m, N=n, K=k, plan=wo.gemm_plan(m, n, k), us=round(ms * 1e3, 2),
              bytes=nbytes, GBps=round(nbytes / (ms * 1e-3) / 1e9, 1),
              TFLOPS=round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 2),
              **roofline(nbytes, 2.0 * m * n * k, ms), rotation_copies=cp, timing="graph replay",
-             max_rel_err=float(f"{err:.3e}"))
+             **par)
         del As, Bs, outs
 
 
@@ -459,7 +476,7 @@ def w4a16_case(wo, m, n, use_graph=True, layout=None):
         zds = [zd.clone() for _ in range(cp)]
         Y0 = wo.matmul_int4(Ad, pk0, sd, zd, G)
         fn = lambda i: wo.matmul_int4(Ad, pks[i % cp], sds[i % cp], zds[i % cp], G)
-    err = og.max_rel_err(Y0, oi.w4a16_ref(A, q, s, z, G))
+    par = parity(Y0, oi.w4a16_ref(A, q, s, z, G))
     if use_graph:
         ms, outs = time_graph(fn, cp)
         assert torch.equal(outs[0], Y0), "graph replay differs from eager"
@@ -470,8 +487,7 @@ def w4a16_case(wo, m, n, use_graph=True, layout=None):
             "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "TFLOPS": round(fl / (ms * 1e-3) / 1e12, 2), **roofline(nbytes, fl, ms),
             "rotation_copies": cp, "layout": layout,
-            "timing": "graph replay" if use_graph else "stream launches",
-            "max_rel_err": float(f"{err:.3e}")}
+            "timing": "graph replay" if use_graph else "stream launches", **par}
 
 
 def fam_w4a16(wo):
@@ -499,12 +515,11 @@ def fam_flash(wo):
             ms = time_batches(lambda i: wo.flash_attention(Qd, Kd, Vd, causal, 1.0 / math.sqrt(D)), 10)
             O = wo.flash_attention(Qd, Kd, Vd, causal, 1.0 / math.sqrt(D))
             ref = oatt.sdpa_ref(Q[0:1, 0:g], Kt[0:1, 0:1], V[0:1, 0:1], causal)
-            err = og.max_rel_err(O[0:1, 0:g].float(), ref)
+            par = parity(O[0:1, 0:g], ref)
             fl = 4.0 * B * H * S * S * D if not causal else 4.0 * B * H * D * S * (S + 1) / 2
             line(family="flash", B=B, H=H, Hkv=Hkv, S=S, D=D, causal=causal, us=round(ms * 1e3, 1),
                  TFLOPS=round(fl / (ms * 1e-3) / 1e12, 1),
-                 frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4),
-                 max_rel_err=float(f"{err:.3e}"))
+                 frac_mfma_peak=round(fl / (ms * 1e-3) / PEAK_FP16_FLOPS, 4), **par)
             # backward pass (dQ, dK, dV from dO): FLOPs counted as 2.5x the forward's (the five
             # matrix products of the gradient; the kernels also recompute S and dP once more)
             sc = 1.0 / math.sqrt(D)
@@ -1019,8 +1034,8 @@ def gemm_bench(wo, steps, warmup):
     # parity spot check of the benchmarked output (a 256-row slab against the fp32 CPU oracle)
     from oracle import gemm as og
 
-    err = og.max_rel_err(C[:256], og.gemm_ref(A[:256].cpu(), B.cpu()))
-    return ms_step, ms_kernel, err
+    par = parity(C[:256], og.gemm_ref(A[:256].cpu(), B.cpu()))
+    return ms_step, ms_kernel, par
 
 
 def cpu_model() -> str:
@@ -1130,7 +1145,7 @@ def cpu_baseline(seconds):
 
 
 def headline(wo, args):
-    ms_step, ms_kernel, err = gemm_bench(wo, args.steps, args.warmup)
+    ms_step, ms_kernel, par = gemm_bench(wo, args.steps, args.warmup)
     flops = 2.0 * M * N * K
     tflops = flops / (ms_step * 1e-3) / 1e12
     achieved = flops / (ms_kernel * 1e-3) / 1e12
@@ -1161,7 +1176,7 @@ def headline(wo, args):
                                "(configs[1], wmma_ops_amd.matmul)",
                    "M": M, "N": N, "K": K, "plan": plan},
         "pct_mfma_peak": round(100.0 * tflops * 1e12 / PEAK_FP16_FLOPS, 2),
-        "max_rel_err": float(f"{err:.3e}"),
+        **par,  # max_rel_err (the 1e-3 bar), rel_l2, allclose on a 256-row slab
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_FP16_FLOPS / 1e12, "unit": "TFLOP/s",
                      "frac": round(achieved * 1e12 / PEAK_FP16_FLOPS, 4), "traffic": traffic,
