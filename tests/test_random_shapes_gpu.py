@@ -1,4 +1,4 @@
-"""Randomised shape sweep: GEMM, W4A16 and flash attention (forward and backward) on shapes
+"""Randomised shape sweep: GEMM, W4A16 (both layouts) and flash attention (forward and backward) on shapes
 drawn from a fixed seed, each against the fp32 CPU oracle.
 
 The hand-picked cases of the other GPU test files pin the boundaries the kernels were
@@ -161,3 +161,42 @@ def test_random_flash_backward(wo, case):
         assert torch.isfinite(got).all(), name
         err = og.max_rel_err(got.float(), want)
         assert err <= 1e-3, f"{name}: max rel err {err:.3e}"
+
+
+# The fused decode layout on its own seeded draw (so the cases above keep their shapes):
+# K a multiple of 128 up to 8192 (single-round and multi-round decode), M = 1..4 (1..2 past
+# K = 4096, the layout's domain), N a multiple of 32, G = 128 * 2^j dividing K, fp32 or fp16
+# output.  Each case also checks the layout's exact inverse.
+_FRNG = np.random.Generator(np.random.PCG64(20261203))
+
+
+def _fused_cases(n):
+    out = []
+    for _ in range(n):
+        G = int(_FRNG.choice([128, 256, 512]))
+        K = G * int(_FRNG.integers(1, 8192 // G + 1))
+        m = int(_FRNG.integers(1, 5))
+        out.append((m if K <= 4096 else 1 + (m - 1) % 2, 32 * int(_FRNG.integers(1, 65)), K, G,
+                    bool(_FRNG.random() < 0.3)))
+    return out
+
+
+FUSED_CASES = _fused_cases(16)
+
+
+@pytest.mark.parametrize("case", range(len(FUSED_CASES)))
+def test_random_w4a16_fused(wo, case):
+    M, N, K, G, f16out = FUSED_CASES[case]
+    report("random_w4a16_fused", case=case, M=M, N=N, K=K, G=G, f16out=f16out)
+    A, q, s, z = oi.make_inputs(M, K, N, G, seed=5000 + case)
+    qd = torch.from_numpy(oi.pack_gptq(q)).cuda()
+    sd, zp = torch.from_numpy(s).cuda(), torch.from_numpy(oi.pack_zeros(z)).cuda()
+    f = wo.prepack_int4_fused(qd, sd, zp, G)
+    kw = {"out_dtype": torch.float16} if f16out else {}
+    Y = wo.matmul_int4_fused(A.cuda(), f, G, **kw)
+    assert Y.dtype == (torch.float16 if f16out else torch.float32)
+    assert torch.isfinite(Y).all()
+    err = og.max_rel_err(Y.float(), oi.w4a16_ref(A, q, s, z, G))
+    assert err <= 1e-3, f"max rel err {err:.3e}"
+    q2, s2, z2 = wo.unprepack_int4_fused(f, G)
+    assert torch.equal(q2, qd) and torch.equal(s2, sd) and torch.equal(z2, zp)
