@@ -206,9 +206,8 @@ int wmma_int4_prepack_params(const void* scales, const void* zeros, int zeros_fo
  * With G = 128 and K % 4096 == 0 these are exactly the bytes of the prepacked weights plus
  * the scales and packed zeros; a larger G repeats a group's parameters in each of its K
  * steps.  Requirements: K % 128 == 0, N % 32 == 0, G % 128 == 0 with G / 128 a power of two.
- * wmma_w4a16_gemm reads this layout for M <= 4 up to K = 4096 and M <= 2 above (decode
- * shapes: the kernel this layout is for, whose staged activations must fit 48 KB of LDS);
- * other M return WMMA_ERR_UNSUPPORTED.  No reference counterpart.
+ * wmma_w4a16_gemm reads this layout for M <= 4 (decode shapes: the kernel this layout is
+ * for); other M return WMMA_ERR_UNSUPPORTED.  No reference counterpart.
  */
 #define WMMA_W4_FUSED 3
 size_t wmma_int4_fused_bytes(int K, int N);

@@ -604,8 +604,7 @@ def test_fused_layout_validation_codes(lib):
                                                               G, FAKE, 4096, None, 0, None)
     assert w(M=5) == UNSUPPORTED
     assert b"decode kernel only" in lib.wmma_last_error()
-    assert w(M=3, K=4224) == UNSUPPORTED       # past one round (K > 4096): M <= 2
-    assert w(M=2, K=4224, A=None) == INVALID   # ... which M = 2 passes (then the NULL A)
+    assert w(M=4, K=14336, A=None) == INVALID  # M = 4 past one round is in the domain (NULL A)
     assert w(G=64) == UNSUPPORTED
     assert w(K=4160, G=64) == UNSUPPORTED      # K % 128 != 0
     assert w(M=0) == OK                        # empty output: scales and zeros are not read

@@ -164,9 +164,9 @@ def test_random_flash_backward(wo, case):
 
 
 # The fused decode layout on its own seeded draw (so the cases above keep their shapes):
-# K a multiple of 128 up to 8192 (single-round and multi-round decode), M = 1..4 (1..2 past
-# K = 4096, the layout's domain), N a multiple of 32, G = 128 * 2^j dividing K, fp32 or fp16
-# output.  Each case also checks the layout's exact inverse.
+# M = 1..4, K a multiple of 128 up to 8192 (single-round and multi-round decode), N a
+# multiple of 32, G = 128 * 2^j dividing K, fp32 or fp16 output.  Each case also checks the
+# layout's exact inverse.
 _FRNG = np.random.Generator(np.random.PCG64(20261203))
 
 
@@ -175,8 +175,7 @@ def _fused_cases(n):
     for _ in range(n):
         G = int(_FRNG.choice([128, 256, 512]))
         K = G * int(_FRNG.integers(1, 8192 // G + 1))
-        m = int(_FRNG.integers(1, 5))
-        out.append((m if K <= 4096 else 1 + (m - 1) % 2, 32 * int(_FRNG.integers(1, 65)), K, G,
+        out.append((int(_FRNG.integers(1, 5)), 32 * int(_FRNG.integers(1, 65)), K, G,
                     bool(_FRNG.random() < 0.3)))
     return out
 

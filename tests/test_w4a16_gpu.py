@@ -220,7 +220,8 @@ def test_prepack_fused_bit_exact(wo, K, N, G):
 @pytest.mark.parametrize("M,K,N,G", [(1, 4096, 4096, 128), (1, 4096, 14336, 128),
                                      (2, 4096, 4096, 128), (3, 4096, 1024, 128),
                                      (4, 4096, 14336, 128), (1, 8192, 1024, 128),
-                                     (2, 4224, 2048, 128), (1, 2048, 4096, 256), (4, 640, 4096, 128)])
+                                     (2, 4224, 2048, 128), (1, 2048, 4096, 256), (4, 640, 4096, 128),
+                                     (3, 8192, 1024, 128), (4, 14336, 2048, 128)])
 def test_w4a16_fused_decode(wo, M, K, N, G):
     report("w4a16_fused", M=M, K=K, N=N, G=G)
     A, q, s, z = oi.make_inputs(M, K, N, G, seed=42 + 3 if K == 4096 and G == 128 else M + K + N)

@@ -660,8 +660,8 @@ std::vector<torch::Tensor> unprepack_int4_fused(torch::Tensor fused, int64_t gro
 }
 
 // matmul_int4_fused(A [M,K] fp16, fused (from prepack_int4_fused), group_size=128,
-//   out_dtype=None, perm=None) -> [M, N]: the W4A16 product for decode shapes (M <= 4;
-//   M <= 2 past K = 4096) with the weights and group parameters read from the fused layout.
+//   out_dtype=None, perm=None) -> [M, N]: the W4A16 product for decode shapes (M <= 4)
+//   with the weights and group parameters read from the fused layout.
 torch::Tensor matmul_int4_fused(torch::Tensor A, torch::Tensor fused, int64_t group_size,
                                 c10::optional<at::ScalarType> out_dtype,
                                 c10::optional<torch::Tensor> perm) {
@@ -852,7 +852,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "Inverse of prepack_int4_fused: (qweight, scales, packed zeros)", py::arg("fused"),
           py::arg("group_size") = 128);
     m.def("matmul_int4_fused", &matmul_int4_fused,
-          "W4A16 for decode shapes (M <= 4; M <= 2 past K = 4096) from the fused layout", py::arg("A"), py::arg("fused"),
+          "W4A16 for decode shapes (M <= 4) from the fused layout", py::arg("A"), py::arg("fused"),
           py::arg("group_size") = 128, py::arg("out_dtype") = py::none(),
           py::arg("perm") = py::none());
     m.def("matmul_int4", &matmul_int4,

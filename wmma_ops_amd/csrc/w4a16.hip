@@ -992,14 +992,25 @@ w4a16_decode_mfma_kernel(W4Args p) {
     }
 }
 
+template <int ZF, bool ONE, int MM>
+void launch_decode_mfma_m(const W4Args& a, dim3 grid, dim3 block, size_t lds, hipStream_t stream) {
+    // Above 64 KB of dynamic LDS (the fused layout's M = 3, 4 past one round) the kernel's
+    // launch limit is raised first; the planner keeps the other layouts at or below 48 KB.
+    if (lds > 64 * 1024 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a16_decode_mfma_kernel<ZF, ONE, MM>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+        return;  // the error stays for the caller's hipGetLastError
+    hipLaunchKernelGGL((w4a16_decode_mfma_kernel<ZF, ONE, MM>), grid, block, lds, stream, a);
+}
+
 template <int ZF, bool ONE>
 void launch_decode_mfma(const W4Args& a, int M, dim3 grid, dim3 block, size_t lds,
                         hipStream_t stream) {
     switch (M) {
-        case 1: hipLaunchKernelGGL((w4a16_decode_mfma_kernel<ZF, ONE, 1>), grid, block, lds, stream, a); break;
-        case 2: hipLaunchKernelGGL((w4a16_decode_mfma_kernel<ZF, ONE, 2>), grid, block, lds, stream, a); break;
-        case 3: hipLaunchKernelGGL((w4a16_decode_mfma_kernel<ZF, ONE, 3>), grid, block, lds, stream, a); break;
-        default: hipLaunchKernelGGL((w4a16_decode_mfma_kernel<ZF, ONE, 4>), grid, block, lds, stream, a); break;
+        case 1: launch_decode_mfma_m<ZF, ONE, 1>(a, grid, block, lds, stream); break;
+        case 2: launch_decode_mfma_m<ZF, ONE, 2>(a, grid, block, lds, stream); break;
+        case 3: launch_decode_mfma_m<ZF, ONE, 3>(a, grid, block, lds, stream); break;
+        default: launch_decode_mfma_m<ZF, ONE, 4>(a, grid, block, lds, stream); break;
     }
 }
 
@@ -1739,9 +1750,13 @@ hipError_t launch_int4_unprepack_fused(const int32_t* fused, int K, int N, int G
     return hipGetLastError();
 }
 
+// The fused layout has no other kernel to fall back to, so its decode may take up to 96 KB
+// of dynamic LDS (M = 3, 4 past one round: 49.9 / 66.6 KB, two workgroups per CU).
+constexpr size_t kFusedDecodeLdsMax = 96 * 1024;
+
 bool w4a16_fused_decode_ok(int M, int K) {
     return M >= 0 && M <= DM_MAXM && K % 128 == 0 &&
-           decode_mfma_lds_bytes(std::max(M, 1), K) <= kDecodeLdsMax;
+           decode_mfma_lds_bytes(std::max(M, 1), K) <= kFusedDecodeLdsMax;
 }
 
 // Host-only: choose the kernel and K split.
