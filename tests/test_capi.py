@@ -256,6 +256,8 @@ def test_w4a16_plan_make(lib):
 
     assert plan(1, 14336, 4096)[:2] == (0, 1)          # decode on the matrix pipe
     assert plan(4, 4096, 4096)[:2] == (0, 1)
+    assert plan(3, 4096, 14336)[:2] == (0, 1)          # ... also past one round (49.9 KB LDS)
+    assert plan(4, 4096, 8192)[:2] == (0, 1)           # (66.6 KB)
     assert plan(16, 14336, 4096) == (4, 1, 4096, 0)    # skinny, 448 tiles: no split
     assert plan(16, 4096, 4096) == (4, 1, 4096, 0)     # skinny, 256 16-column workgroups
     assert plan(16, 2048, 4096) == (4, 1, 4096, 0)     # 128 of them: half the CUs, no split

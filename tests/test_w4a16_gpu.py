@@ -238,6 +238,24 @@ def test_w4a16_fused_decode(wo, M, K, N, G):
     assert torch.equal(Yh, Y.half())
 
 
+# Decode shapes past one round (K > 4096) at every M <= 4: the matrix-pipe decode kernel in
+# both layouts (M = 3, 4 stage up to 66.6 KB of activations in LDS), within the oracle's bar
+# and bit-equal between the layouts (the same kernel on the same values).
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("K,N", [(8192, 4096), (14336, 4096)])
+def test_w4a16_decode_long_k(wo, M, K, N):
+    G = 128
+    report("w4a16_decode_long_k", M=M, K=K, N=N, plan=wo.w4a16_plan(M, N, K, G))
+    assert wo.w4a16_plan(M, N, K, G)[0] == 0
+    A, q, s, z = oi.make_inputs(M, K, N, G, seed=M + K)
+    qd, sd = torch.from_numpy(oi.pack_gptq(q)).cuda(), torch.from_numpy(s).cuda()
+    zd = torch.from_numpy(oi.pack_zeros(z)).cuda()
+    Ad = A.cuda()
+    Y = wo.matmul_int4(Ad, wo.prepack_int4(qd), sd, zd, G)
+    assert og.max_rel_err(Y, oi.w4a16_ref(A, q, s, z, G)) <= 1e-3
+    assert torch.equal(wo.matmul_int4_fused(Ad, wo.prepack_int4_fused(qd, sd, zd, G), G), Y)
+
+
 def test_w4a16_fused_errors(wo):
     A, q, s, z = oi.make_inputs(5, 512, 64, 128, seed=3)
     qd, sd = torch.from_numpy(oi.pack_gptq(q)).cuda(), torch.from_numpy(s).cuda()

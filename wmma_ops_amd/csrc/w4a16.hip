@@ -994,8 +994,8 @@ w4a16_decode_mfma_kernel(W4Args p) {
 
 template <int ZF, bool ONE, int MM>
 void launch_decode_mfma_m(const W4Args& a, dim3 grid, dim3 block, size_t lds, hipStream_t stream) {
-    // Above 64 KB of dynamic LDS (the fused layout's M = 3, 4 past one round) the kernel's
-    // launch limit is raised first; the planner keeps the other layouts at or below 48 KB.
+    // Above 64 KB of dynamic LDS (M = 4 past one round) the kernel's launch limit is raised
+    // first.
     if (lds > 64 * 1024 &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a16_decode_mfma_kernel<ZF, ONE, MM>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
@@ -1750,13 +1750,15 @@ hipError_t launch_int4_unprepack_fused(const int32_t* fused, int K, int N, int G
     return hipGetLastError();
 }
 
-// The fused layout has no other kernel to fall back to, so its decode may take up to 96 KB
-// of dynamic LDS (M = 3, 4 past one round: 49.9 / 66.6 KB, two workgroups per CU).
-constexpr size_t kFusedDecodeLdsMax = 96 * 1024;
+// Dynamic LDS the matrix-pipe decode may take: M = 3, 4 past one round stage 49.9 / 66.6 KB
+// (two workgroups per CU).  Measured at N = 4096, K = 8192 / 14336: this kernel 7.0 / 10.0
+// (M = 3) and 7.0 / 10.7 us (M = 4) against 16.2 / 26.6 and 18.0 / 29.4 us for the split
+// GEMV the planner took under a 48 KB limit.
+constexpr size_t kDecodeMfmaLdsMax = 96 * 1024;
 
 bool w4a16_fused_decode_ok(int M, int K) {
     return M >= 0 && M <= DM_MAXM && K % 128 == 0 &&
-           decode_mfma_lds_bytes(std::max(M, 1), K) <= kFusedDecodeLdsMax;
+           decode_mfma_lds_bytes(std::max(M, 1), K) <= kDecodeMfmaLdsMax;
 }
 
 // Host-only: choose the kernel and K split.
@@ -1778,7 +1780,7 @@ W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
     const bool slices_ok = N / 16 >= num_cus / 2 && K % 128 == 0;
     (void)aligned;
     if (M >= 1 && M <= DM_MAXM && slices_ok && G % 128 == 0 && ((G / 128) & (G / 128 - 1)) == 0 &&
-        decode_mfma_lds_bytes(M, K) <= kDecodeLdsMax) {
+        decode_mfma_lds_bytes(M, K) <= kDecodeMfmaLdsMax) {
         pl.kind = W4_DECODE_MFMA;
         return pl;
     }
