@@ -258,6 +258,18 @@ def test_w4a16_plan_make(lib):
     assert plan(4, 4096, 4096)[:2] == (0, 1)
     assert plan(3, 4096, 14336)[:2] == (0, 1)          # ... also past one round (49.9 KB LDS)
     assert plan(4, 4096, 8192)[:2] == (0, 1)           # (66.6 KB)
+    assert plan(1, 1024, 4096)[:2] == (0, 1)           # ... at narrow N (64 slices) too
+    assert plan(4, 256, 4096)[:2] == (0, 1)
+    assert plan(4, 1536, 14336)[:2] == (0, 1)
+    assert plan(2, 1024, 14336)[:2] == (0, 1)
+    assert plan(2, 256, 8192)[:2] == (0, 1)
+    assert plan(1, 256, 14336)[:2] == (0, 1)
+    assert plan(3, 256, 8192)[0] == 4                  # narrow N, long K: skinny, K split
+    assert plan(2, 512, 11008)[0] == 4
+    assert plan(4, 1024, 14336)[0] == 4
+    assert plan(3, 1024, 11008)[0] == 4
+    assert plan(4, 1024, 8192)[:2] == (0, 1)           # (K under 10240 at N = 1024)
+    assert plan(3, 512, 6144)[:2] == (0, 1)
     assert plan(16, 14336, 4096) == (4, 1, 4096, 0)    # skinny, 448 tiles: no split
     assert plan(16, 4096, 4096) == (4, 1, 4096, 0)     # skinny, 256 16-column workgroups
     assert plan(16, 2048, 4096) == (4, 1, 4096, 0)     # 128 of them: half the CUs, no split

@@ -256,6 +256,33 @@ def test_w4a16_decode_long_k(wo, M, K, N):
     assert torch.equal(wo.matmul_int4_fused(Ad, wo.prepack_int4_fused(qd, sd, zd, G), G), Y)
 
 
+# Narrow N at M <= 4 (under half a 16-column slice per CU): the planner's matrix-pipe decode,
+# or, at long K with enough rows, the skinny kernel with a K split (K = 14336, N = 512:
+# M >= 2; K = 11008, N = 1024: M >= 3; K = 8192, N = 256: M >= 3).  Within the oracle's bar;
+# where the decode runs, bit-equal to the fused layout (same kernel, same values).
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("K,N", [(4096, 256), (1024, 1536), (8192, 256), (11008, 1024),
+                                 (14336, 512)])
+def test_w4a16_narrow_n(wo, M, K, N):
+    G = 128
+    plan = wo.w4a16_plan(M, N, K, G)
+    report("w4a16_narrow_n", M=M, K=K, N=N, plan=plan)
+    skinny = (K, N) == (14336, 512) and M >= 2 or K in (8192, 11008) and M >= 3 and N <= 1024
+    assert plan[0] == (4 if skinny else 0)
+    A, q, s, z = oi.make_inputs(M, K, N, G, seed=5 * M + K + N)
+    qd, sd = torch.from_numpy(oi.pack_gptq(q)).cuda(), torch.from_numpy(s).cuda()
+    zd = torch.from_numpy(oi.pack_zeros(z)).cuda()
+    Ad = A.cuda()
+    Y = wo.matmul_int4(Ad, wo.prepack_int4(qd), sd, zd, G)
+    assert torch.isfinite(Y).all()
+    assert og.max_rel_err(Y, oi.w4a16_ref(A, q, s, z, G)) <= 1e-3
+    Yf = wo.matmul_int4_fused(Ad, wo.prepack_int4_fused(qd, sd, zd, G), G)
+    if skinny:
+        assert og.max_rel_err(Yf, oi.w4a16_ref(A, q, s, z, G)) <= 1e-3
+    else:
+        assert torch.equal(Yf, Y)
+
+
 def test_w4a16_fused_errors(wo):
     A, q, s, z = oi.make_inputs(5, 512, 64, 128, seed=3)
     qd, sd = torch.from_numpy(oi.pack_gptq(q)).cuda(), torch.from_numpy(s).cuda()
@@ -385,9 +412,23 @@ def test_int4_from_gptq_v1_q_equals_z_is_zero(wo):
     qw, zo, _ = wo.int4_from_gptq(torch.from_numpy(oi.pack_gptq(q)).cuda(),
                                   torch.from_numpy(oi.pack_gptq_v1_zeros(z)).cuda())
     pk = wo.prepack_int4(qw)
+    # the same zeros read as v2 (no +1): every column is off by s * sum(a) per group
+    qw2, zo2, _ = wo.int4_from_gptq(torch.from_numpy(oi.pack_gptq(q)).cuda(),
+                                    torch.from_numpy(oi.pack_gptq_v1_zeros(z)).cuda(),
+                                    zero_format="v2")
     for M in (1, 5, 40):
         A = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).half().cuda()
-        assert torch.count_nonzero(wo.matmul_int4(A, pk, torch.from_numpy(s).cuda(), zo, G)) == 0
+        Y = wo.matmul_int4(A, pk, torch.from_numpy(s).cuda(), zo, G)
+        if M <= 2 and wo.w4a16_plan(M, N, K, G)[0] == 0:
+            # the M <= 2 decode subtracts the zero point through fp32 sums of the activations:
+            # a difference of two sums of the same terms, zero up to their rounding (a few
+            # fp32 ulps of the offset term 1024 s sum|a| per group)
+            bound = 1e-6 * 1024 * float(s.max()) * A.float().abs().sum(dim=1, keepdim=True)
+            assert (Y.abs() <= bound).all()
+            Yw = wo.matmul_int4(A, wo.prepack_int4(qw2), torch.from_numpy(s).cuda(), zo2, G)
+            assert (Yw.abs() > 10 * bound).any()
+        else:
+            assert torch.count_nonzero(Y) == 0
 
 
 @pytest.mark.parametrize("M", [1, 16, 128])

@@ -1761,14 +1761,37 @@ bool w4a16_fused_decode_ok(int M, int K) {
            decode_mfma_lds_bytes(std::max(M, 1), K) <= kDecodeMfmaLdsMax;
 }
 
+// M <= 4 rows against few columns and a long K: the decode gives one workgroup per
+// 16-column slice, each walking all of K, so with under num_cus / 4 slices a K-split skinny
+// launch finishes first.  Measured on MI355X (256 CUs), decode against skinny, us:
+//   K = 8192,  N = 128 / 256: M = 3 5.1 / 5.3 vs 4.6 / 4.7; M = 2 4.4 / 4.6 vs 4.6 / 4.6;
+//   K = 11008, N = 512: M = 2 5.7 vs 5.3, M = 4 7.1 vs 5.6; N = 1024: M = 2 6.0 vs 6.7,
+//              M = 3 7.1 vs 6.7;
+//   K = 14336, N = 256: M = 4 7.6 vs 5.5; N = 1024: M = 4 7.9 vs 7.3; N = 1536: M = 4 8.1
+//              vs 9.0;
+//   K <= 6144 the decode at every N <= 1024, M <= 4 (N = 1024, M = 4: 4.8 vs 6.7).
+bool w4a16_narrow_skinny(int M, int N, int K, int num_cus) {
+    const int slices = N / 16;
+    int min_m = DM_MAXM + 1;
+    if (8 * slices <= num_cus)
+        min_m = K >= 10240 ? 2 : (K >= 8192 ? 3 : DM_MAXM + 1);
+    else if (4 * slices <= num_cus)
+        min_m = K >= 10240 ? 3 : DM_MAXM + 1;
+    return M >= min_m && M <= DM_MAXM;
+}
+
 // Host-only: choose the kernel and K split.
-//   decode-mfma  M <= 4, G = 128 * 2^j, K % 128 == 0, the staged activations fit LDS and
-//                the 16-column slices give at least half a workgroup per CU.
-//   decode       M <= 4 with the same slice condition, other group sizes.
+//   decode-mfma  M <= 4, G = 128 * 2^j, K % 128 == 0 and the staged activations fit LDS, at
+//                any N (narrow N included: at N = 256..1536, K = 1024..14336 it runs
+//                1.2-2.5x faster than the split GEMV), except the narrow, long-K shapes
+//                above, which take the skinny kernel.
+//   decode       M <= 4 where the 16-column slices give at least half a workgroup per CU,
+//                other group sizes.
 //   gemv-split   other M <= 4 shapes: one workgroup per 32 columns, K split (plus a reduce
 //                pass) only when fewer than 2*CUs workgroups would exist.
-//   skinny       4 < M <= 32 with G = 128 * 2^j: 32 or 64 columns per workgroup, K split (plus
-//                a reduce pass) only when the tiles alone give under half a workgroup per CU.
+//   skinny       4 < M <= 32 (and the narrow, long-K M <= 4 shapes) with G = 128 * 2^j: 16,
+//                32 or 64 columns per workgroup, K split (plus a reduce pass) only when the
+//                tiles alone give under half a workgroup per CU.
 //   gemm         M > 32 with G a power of two: LDS-DMA MFMA GEMM (tile below), K split
 //                (plus a reduce pass) only when the tiles cannot fill the chip.
 //   mfma         everything else (the shapes the kernels above do not take).
@@ -1777,18 +1800,19 @@ W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
     W4A16Plan pl{};
     pl.split = 1;
     pl.k_per_split = K;
-    const bool slices_ok = N / 16 >= num_cus / 2 && K % 128 == 0;
     (void)aligned;
-    if (M >= 1 && M <= DM_MAXM && slices_ok && G % 128 == 0 && ((G / 128) & (G / 128 - 1)) == 0 &&
+    const bool g_ok = G % 128 == 0 && ((G / 128) & (G / 128 - 1)) == 0;
+    const bool narrow_skinny = K % 128 == 0 && g_ok && w4a16_narrow_skinny(M, N, K, num_cus);
+    if (M >= 1 && M <= DM_MAXM && K % 128 == 0 && g_ok && !narrow_skinny &&
         decode_mfma_lds_bytes(M, K) <= kDecodeMfmaLdsMax) {
         pl.kind = W4_DECODE_MFMA;
         return pl;
     }
-    if (w4a16_use_decode(M, N, K, num_cus)) {
+    if (!narrow_skinny && w4a16_use_decode(M, N, K, num_cus)) {
         pl.kind = W4_DECODE;
         return pl;
     }
-    if (M > DM_MAXM && M <= 32 && K % 128 == 0 && G % 128 == 0 && ((G / 128) & (G / 128 - 1)) == 0) {
+    if ((M > DM_MAXM || narrow_skinny) && M <= 32 && K % 128 == 0 && g_ok) {
         // Two tiles per workgroup when the pairs alone still give half a workgroup per CU
         // (M <= 16) or 3/4 of one (M > 16, where each workgroup carries twice the MFMA work).
         // Measured at K = 4096: M = 16 11.8 -> 10.2-10.7 us at N = 14336 and 11.6 -> 10.0 at
