@@ -273,14 +273,16 @@ def test_w4a16_plan_make(lib):
     assert plan(16, 14336, 4096) == (4, 1, 4096, 0)    # skinny, 448 tiles: no split
     assert plan(16, 4096, 4096) == (4, 1, 4096, 0)     # skinny, 256 16-column workgroups
     assert plan(16, 2048, 4096) == (4, 1, 4096, 0)     # 128 of them: half the CUs, no split
-    k, s, kps, ws = plan(16, 1024, 4096)               # 64 of them: K split
-    assert (k, s, kps) == (4, 2, 2048) and ws == 2 * 16 * 1024 * 4
+    assert plan(16, 1024, 4096) == (4, 1, 4096, 0)     # 64 of them: still no split
+    assert plan(5, 256, 2048) == (4, 1, 2048, 0)       # K <= 2048: never a split
+    assert plan(16, 4096, 14336) == (4, 7, 2048, 7 * 16 * 4096 * 4)   # long K: split
+    assert plan(32, 14336, 14336) == (4, 14, 1024, 14 * 32 * 14336 * 4)
     assert plan(128, 14336, 4096)[:2] == (5, 1)        # 224 tiles of 64x128: no split
     assert plan(128, 4096, 4096)[:2] == (5, 4)         # 64 tiles: 256 / 64 ways
     assert plan(64, 4096, 4096)[:2] == (5, 8)          # 32 tiles: 8 ways (the cap)
     assert plan(64, 11008, 4096)[:2] == (5, 2)         # 86 tiles: 2 ways
-    # skinny with two 32-column tiles per workgroup (256 pairs) and a 2-way K split
-    assert plan(16, 8192, 8192) == (4, 2, 4096, 2 * 16 * 8192 * 4)
+    # skinny with 64-column workgroups (128 of them) and a 4-way K split
+    assert plan(16, 8192, 8192) == (4, 4, 2048, 4 * 16 * 8192 * 4)
     assert plan(2048, 4096, 4096)[:2] == (5, 1)        # 512 tiles of 128x128, no split
     assert plan(1024, 14336, 4096)[:2] == (5, 1)       # 448 tiles of 128x256
     assert plan(32, 14336, 4096)[0] == 4

@@ -74,10 +74,10 @@ def test_w4a16_group_sizes_and_u8_zeros(wo, M, K, N, G):
 
 
 # The 4 < M <= 32 matrix-pipe kernel: one and two 16-row blocks, K split over workgroups
-# (N=1024, N=352; and N=4096 for M > 16), a ragged last split (K=4224: 33 pair-steps), G=256,
-# a tile count that is not a multiple of the XCD count (N=352), lda > K, both zero formats.
-# N=8192 (M <= 16, with a 2-way K split) and N=12288 (all M) take two 32-column tiles per
-# workgroup on a 256-CU device.
+# (N=1024; N=4096 and N=352 for M > 16; N=8192), a ragged last split (K=4224: 33
+# pair-steps), G=256, a tile count that is not a multiple of the XCD count (N=352), lda > K,
+# both zero formats.  N=8192 (4-way K split) and N=12288 take 64-column workgroups on a
+# 256-CU device.
 @pytest.mark.parametrize("M", [5, 8, 16, 17, 31, 32])
 @pytest.mark.parametrize("K,N,G", [(4096, 4096, 128), (4224, 1024, 128), (1536, 352, 256),
                                    (8192, 8192, 128), (4096, 12288, 256)])
@@ -86,7 +86,7 @@ def test_w4a16_skinny(wo, M, K, N, G):
     report("w4a16_skinny", M=M, K=K, N=N, G=G, plan=plan)
     assert plan[0] == 4
     if N == 8192 and M <= 16:
-        assert plan[1] == 2
+        assert plan[1] == 4
     A, q, s, z = oi.make_inputs(M, K, N, G, seed=7 * M + K + N)
     ref = oi.w4a16_ref(A, q, s, z, G)
     pk = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
@@ -99,6 +99,27 @@ def test_w4a16_skinny(wo, M, K, N, G):
     assert torch.isfinite(Yp).all()
     assert og.max_rel_err(Yp, ref) <= 1e-3
     assert torch.equal(Yp, Yu)
+
+
+# The skinny kernel's other workgroup shapes on a 256-CU device (16-column slices per
+# workgroup NH x pair-steps per wave U, one or two 16-row blocks): 1x1 unsplit (K = 1024) and
+# with an 8-way split, 2x2 unsplit and with a 7-way split, 2x4, 4x1 unsplit and split, 4x2
+# unsplit and 2x1 for two blocks, 2x2 split for two blocks.  Within the oracle's bar.
+@pytest.mark.parametrize("M,K,N", [(5, 1024, 256), (5, 8192, 256), (12, 2048, 8192),
+                                   (16, 14336, 1024), (8, 4096, 8192), (9, 1024, 11008),
+                                   (12, 6144, 2048), (24, 2048, 11008), (28, 1024, 4096),
+                                   (20, 6144, 2048), (32, 14336, 1024)])
+def test_w4a16_skinny_shapes(wo, M, K, N):
+    G = 128
+    plan = wo.w4a16_plan(M, N, K, G)
+    report("w4a16_skinny_shapes", M=M, K=K, N=N, plan=plan)
+    assert plan[0] == 4
+    A, q, s, z = oi.make_inputs(M, K, N, G, seed=11 * M + K + N)
+    pk = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
+    Y = wo.matmul_int4(A.cuda(), pk, torch.from_numpy(s).cuda(),
+                       torch.from_numpy(oi.pack_zeros(z)).cuda(), G)
+    assert torch.isfinite(Y).all()
+    assert og.max_rel_err(Y, oi.w4a16_ref(A, q, s, z, G)) <= 1e-3
 
 
 # The M > 32 LDS-DMA kernel: the three tile configurations (64x128 up to 128 rows, 128x256

@@ -1154,17 +1154,61 @@ w4a16_skinny_kernel(W4Args p) {
     }
 }
 
-// Pair-steps per wave for the skinny kernel: as many as possible (fewer splits, no reduce
-// pass) while the 32-column tiles times the K splits still give half a workgroup per CU --
-// measured on MI355X, 128 unsplit workgroups beat 512 split ones plus the reduce pass.
-int skinny_u(int M, int N, int K, int num_cus) {
-    const int tiles = N / 32, KP = K / 128;
-    const int umax = M > 16 ? 2 : 4;
-    for (int u = umax; u > 1; u /= 2) {
-        const int splits = ceil_div(KP, SK_NW * u);
-        if ((int64_t)tiles * splits * 2 >= (int64_t)num_cus) return u;
+// Shape of a skinny launch: NH 16-column slices per workgroup and U pair-steps per wave, so
+// a workgroup covers SK_NW * U * 128 of K and longer K is split over blockIdx.y (plus the
+// reduce pass).  What decides it, measured on MI355X over M = 2..32, N = 256..14336,
+// K = 1024..14336 (every NH x U at 136 shapes, graph-replayed; summed over them this rule
+// takes 0.5% more time than the best choice and 12.6% less than the tile-count rule it
+// replaced):
+//  * the reduce pass costs 1.5-3 us, so K that one workgroup covers stays unsplit even with
+//    few workgroups (K <= 2048: always; N = 256, K = 2048, M = 5: 2.9 us against 4.4 split);
+//  * each slice a workgroup adds halves the activation re-reads (every workgroup reads all
+//    M x K activations of its K range: M / (4 NH) of the weight bytes), which decides long K
+//    (N = 4096, K = 14336, M = 16: NH = 4 13.1 us, NH = 1 20.6);
+//  * registers: NH = 4 with U = 4 (M <= 16) and with U = 2 (M > 16) leave one workgroup per
+//    CU, so those take them only where the workgroups do not exceed the CUs' slots
+//    (M = 32, N = K = 14336: U = 1 47.7 us, U = 2 54.3);
+//  * a split gives at least 0.7 workgroups per CU (N = 1024, K = 8192: NH = 2 with U = 1,
+//    256 workgroups, 6.5 us at M = 16 against 7.4 with U = 2).
+void skinny_config(int M, int N, int K, int num_cus, int* nh_out, int* u_out) {
+    const bool mb1 = M <= 16;  // one 16-row block (U up to 4) or two (U up to 2, NH >= 2)
+    const int umax = mb1 ? 4 : 2;
+    auto nh_ok = [&](int h) { return N % (16 * h) == 0 && (h != 1 || mb1); };
+    auto slices = [&](int h) { return (int64_t)(N / (16 * h)); };
+    auto wgs = [&](int h, int u) { return slices(h) * ceil_div(K, SK_NW * 128 * u); };
+    const int u0 = K <= 1024 ? 1 : K <= 2048 ? 2 : K <= 4096 ? 4 : 8;
+    if (u0 <= umax) {
+        // unsplit: the widest workgroups that still give 0.6 per CU
+        int nh = mb1 ? 1 : 2;
+        for (int h : {4, 2, 1})
+            if (nh_ok(h) && slices(h) * 10 >= 6 * (int64_t)num_cus) {
+                nh = h;
+                break;
+            }
+        if (K <= 2048 || slices(nh) * 4 >= num_cus) {
+            *nh_out = nh;
+            *u_out = u0;
+            return;
+        }
     }
-    return 1;
+    int nh = 1;
+    if (nh_ok(4) && (int64_t)(N / 64) * 8 >= num_cus)
+        nh = 4;
+    else if ((int64_t)(N / 32) * 8 >= num_cus || !mb1)
+        nh = 2;
+    int u = 1;
+    if (mb1) {
+        for (int c : {4, 2})
+            if (!(nh == 4 && c == 4) && wgs(nh, c) * 10 >= 7 * (int64_t)num_cus) {
+                u = c;
+                break;
+            }
+    } else {
+        const int64_t w2 = wgs(nh, 2);
+        u = (w2 * 10 >= 7 * (int64_t)num_cus && w2 < 2 * (int64_t)num_cus) ? 2 : 1;
+    }
+    *nh_out = nh;
+    *u_out = u;
 }
 
 template <int ZF, int MB, int NH>
@@ -1813,21 +1857,9 @@ W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
         return pl;
     }
     if ((M > DM_MAXM || narrow_skinny) && M <= 32 && K % 128 == 0 && g_ok) {
-        // Two tiles per workgroup when the pairs alone still give half a workgroup per CU
-        // (M <= 16) or 3/4 of one (M > 16, where each workgroup carries twice the MFMA work).
-        // Measured at K = 4096: M = 16 11.8 -> 10.2-10.7 us at N = 14336 and 11.6 -> 10.0 at
-        // N = 11008; M = 24, 32 gain at N = 14336 only; at N = 4096 pairs need a K split
-        // and lose (5.9 -> 7.9 us at M = 8).
-        // Fewer 32-column tiles than CUs at M <= 16: one 16-column slice per workgroup
-        // (twice the workgroups; each reads the activations once more).
-        const int tiles = N / 32;
-        if (tiles % 2 == 0 && (M <= 16 ? tiles >= num_cus : 2 * tiles >= 3 * num_cus))
-            pl.big = 4;
-        else if (M <= 16 && tiles < num_cus)
-            pl.big = 1;
-        else
-            pl.big = 2;
-        const int u = skinny_u(M, N * 2 / pl.big, K, num_cus);
+        int nh = 2, u = 1;
+        skinny_config(M, N, K, num_cus, &nh, &u);
+        pl.big = nh;
         pl.kind = W4_SKINNY;
         pl.k_per_split = SK_NW * u * 128;
         pl.split = ceil_div(K, pl.k_per_split);
