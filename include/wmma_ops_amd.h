@@ -88,6 +88,14 @@ int wmma_device_cu_count(int device);
  * split_k::compute_config (wmma_xor_swizzle.hpp:293-332). */
 int wmma_gemm_plan_make(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* out);
 
+/* The same planner's choice among the plans whose split-K partial sums fit
+ * max_workspace_bytes (a plan without a K split needs none, so one always exists): for
+ * callers with a fixed workspace budget; wmma_gemm_f16f32_noalloc plans this way within
+ * its scratch array.  No counterpart in the reference (its split-K wrapper allocates its
+ * own workspace, wmma_xor_swizzle.hpp:1208-1215). */
+int wmma_gemm_plan_make_within(int M, int N, int K, int tile_cfg, int num_cus,
+                               size_t max_workspace_bytes, wmma_gemm_plan* out);
+
 /* Workspace bytes wmma_gemm_f16f32 uses for this shape on the current device, for
  * contiguous 16-byte-aligned operands (lda = K, ldb = N): the split-K partial sums
  * (plan.workspace_bytes) plus, when K or N is not a multiple of 8, room for zero-padded
@@ -118,12 +126,13 @@ int wmma_gemm_f16f32(const void* A, int64_t lda, const void* B, int64_t ldb,
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Allocation-free variant of wmma_gemm_f16f32: the same computation, kernels and plan, but
- * no workspace argument -- the split-K partial sums go to a device array inside this
- * library (wmma_gemm_noalloc_scratch_bytes() = 32 MiB per GPU, held until the process
- * ends), so the call performs no allocation of any kind.  A shape whose plan needs more
- * partial-sum space than that is rejected with WMMA_ERR_WORKSPACE (wmma_gemm_workspace_size
- * gives the need).  Every call on one GPU shares that GPU's array and nothing in it has to
+ * Allocation-free variant of wmma_gemm_f16f32: the same computation and kernels, but no
+ * workspace argument -- the split-K partial sums go to a device array inside this library
+ * (wmma_gemm_noalloc_scratch_bytes() = 32 MiB per GPU, held until the process ends), so the
+ * call performs no allocation of any kind.  Its plan is wmma_gemm_plan_make_within(...,
+ * wmma_gemm_noalloc_scratch_bytes(), ...): the same as wmma_gemm_f16f32's wherever that
+ * plan's partial sums fit the array, else the planner's next choice that fits (a smaller
+ * K split, so a bit-different fp32 sum order).  Every call on one GPU shares that GPU's array and nothing in it has to
  * start at zero (each split writes its whole partial tile before the reduction reads it).
  * Calls outside stream capture are ordered by the library: a call on another stream than
  * the previous split-K call on the GPU first waits (hipStreamWaitEvent) for an event

@@ -170,17 +170,57 @@ def test_plan_make(lib):
         assert (p.tile_m, p.tile_n, p.split_k) == (bm, bn, 1)
     assert lib.wmma_gemm_plan_make(10, 10, 10, 9, 256, ctypes.byref(p)) == INVALID
     assert lib.wmma_gemm_plan_make(10, 10, 10, -1, 256, None) == INVALID
-    # 16 < M <= 32: the skinny kernel with two 16-row blocks, the largest K split whose
-    # workgroups fit one wave of the CUs (measured fastest of splits 1-8)
-    for (M, N, K), split in {(32, 4096, 4096): 8, (17, 11008, 4096): 2, (32, 14336, 4096): 2,
-                             (32, 4096, 14336): 8, (24, 32768, 4096): 1}.items():
+    # M <= 16 with K > 1024: the streaming kernel with its own split rule
+    for (M, N, K), split in {(1, 4096, 4096): 8, (16, 4096, 4096): 8, (16, 14336, 4096): 2,
+                             (16, 4096, 14336): 8}.items():
         assert lib.wmma_gemm_plan_make(M, N, K, -1, 256, ctypes.byref(p)) == OK
-        assert (p.kernel, p.tile_m, p.tile_n, p.split_k) == (1, 32, 128, split), (M, N, K)
-    # M = 33..128 keeps the tiled kernel; few tiles split K from K = 2048 on, never below
-    for (M, N, K), split in {(48, 4096, 4096): 4, (64, 1024, 4096): 4, (48, 1024, 2048): 4,
-                             (64, 1024, 1024): 1, (128, 4096, 512): 1}.items():
+        assert (p.kernel, p.tile_m, p.tile_n, p.split_k) == (1, 16, 128, split), (M, N, K)
+    # every other M <= 768: the fitted launch model's choice (kernel, tile, split), each the
+    # fastest plan measured at that shape in the sweep the model was fitted on, with the
+    # previous heuristics' time beside it: K <= 1024 never splits; few rows and long K split
+    # deep; the streaming kernel where it still wins
+    MODEL = {(8, 4096, 1024): (0, 0, 1),        # 9.1 us (skinny split 4: 10.7)
+             (24, 14336, 1024): (0, 0, 1),      # 10.5 (skinny split 2: 14.0)
+             (32, 4096, 4096): (0, 0, 4),       # 14.6 (skinny split 8: 15.0)
+             (32, 14336, 4096): (1, -1, 2),     # 29.1, unchanged
+             (64, 1024, 1024): (0, 0, 1), (128, 4096, 512): (0, 0, 1),
+             (48, 1024, 14336): (0, 0, 16),     # 14.4 (64x64 split 4: 27.2)
+             (128, 1024, 14336): (0, 1, 16),    # 17.7 (64x64 split 4: 27.2)
+             (96, 4096, 14336): (0, 3, 8),      # 37.2 (64x64 split 2: 49.0)
+             (256, 4096, 14336): (0, 3, 4),     # 53.8 (64x64 split 1: 83.5)
+             (768, 14336, 1024): (0, 5, 1)}     # 33.2 (128x128 split 1: 46.2)
+    for (M, N, K), want in MODEL.items():
         assert lib.wmma_gemm_plan_make(M, N, K, -1, 256, ctypes.byref(p)) == OK
-        assert (p.kernel, p.split_k) == (0, split), (M, N, K, p.split_k)
+        assert (p.kernel, p.tile_cfg, p.split_k) == want, (M, N, K)
+        assert p.edge_dim == 0
+    # a split only from K = 2048 on, at least 256 of K per part, within one wave of the CUs
+    for M in (1, 8, 24, 40, 96, 200, 768):
+        for N in (512, 4096, 14336):
+            for K in (512, 1024, 2048, 8192):
+                assert lib.wmma_gemm_plan_make(M, N, K, -1, 256, ctypes.byref(p)) == OK
+                if p.split_k > 1:
+                    assert K >= 2048 and K // p.split_k >= 192 and p.grid <= 3 * 256, (M, N, K)
+
+
+def test_plan_make_within(lib):
+    # the planner's choice among plans whose partial sums fit a budget: the same plan when it
+    # fits, else another that does; a budget of 0 leaves only unsplit plans
+    lib.wmma_gemm_plan_make_within.argtypes = [ctypes.c_int] * 5 + [ctypes.c_size_t,
+                                                                    ctypes.POINTER(Plan)]
+    p, q = Plan(), Plan()
+    for (M, N, K) in [(512, 4096, 14336), (256, 4096, 14336), (64, 4096, 4096), (1, 4096, 4096),
+                      (4100, 4096, 4096), (128, 4096, 14336), (16, 14336, 4096), (2048, 1024, 8192)]:
+        assert lib.wmma_gemm_plan_make(M, N, K, -1, 256, ctypes.byref(p)) == OK
+        for cap in (0, 1 << 20, 16 << 20, 32 << 20, 1 << 40):
+            assert lib.wmma_gemm_plan_make_within(M, N, K, -1, 256, cap, ctypes.byref(q)) == OK
+            assert q.workspace_bytes <= cap, (M, N, K, cap)
+            if p.workspace_bytes <= cap:
+                assert (q.kernel, q.tile_cfg, q.split_k, q.edge_dim, q.edge_at) == \
+                    (p.kernel, p.tile_cfg, p.split_k, p.edge_dim, p.edge_at), (M, N, K, cap)
+    assert lib.wmma_gemm_plan_make_within(512, 4096, 14336, -1, 256, 0, ctypes.byref(q)) == OK
+    assert q.split_k == 1 and q.workspace_bytes == 0
+    assert lib.wmma_gemm_plan_make_within(10, 10, 10, -1, 256, 0, None) == INVALID
+    assert lib.wmma_gemm_plan_make_within(-1, 10, 10, -1, 256, 0, ctypes.byref(q)) == INVALID
 
 
 class W4Plan(ctypes.Structure):
@@ -632,9 +672,10 @@ def test_fused_layout_validation_codes(lib):
 def test_noalloc_validation_codes(lib):
     """wmma_gemm_f16f32_noalloc rejects bad arguments exactly like wmma_gemm_f16f32 (before
     touching a device: the scratch address is looked up only after these checks), and every
-    plan the planner makes fits its scratch array: over a sweep of shapes and every tile
-    choice, the split-K partial sums need at most 16 MiB of the 32 MiB (the entry point's
-    WMMA_ERR_WORKSPACE rejection is a guard that no planner plan reaches)."""
+    plan it makes fits its scratch array: it plans with wmma_gemm_plan_make_within(scratch
+    size), which over a sweep of shapes and every tile choice stays within the 32 MiB where
+    the unconstrained planner's plan would not (the entry point's WMMA_ERR_WORKSPACE
+    rejection is a guard that no such plan reaches)."""
     vp, i64, i32, f32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
     lib.wmma_gemm_f16f32_noalloc.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32,
                                              f32, f32, i32, vp]
@@ -651,11 +692,16 @@ def test_noalloc_validation_codes(lib):
     assert na(A=None) == INVALID
     assert na(M=0) == OK and na(N=0) == OK     # empty output
     p = Plan()
-    largest = 0
+    lib.wmma_gemm_plan_make_within.argtypes = [ctypes.c_int] * 5 + [ctypes.c_size_t,
+                                                                    ctypes.POINTER(Plan)]
+    largest = over = 0
     for cfg in range(-1, 6):
-        for M in (1, 16, 32, 64, 128, 256, 1024, 4100):
+        for M in (1, 16, 32, 64, 128, 256, 512, 1024, 4100):
             for N in (520, 4096, 16384, 65536):
-                for K in (520, 4096, 65536, 262144):
+                for K in (520, 4096, 14336, 65536, 262144):
                     assert lib.wmma_gemm_plan_make(M, N, K, cfg, 256, ctypes.byref(p)) == OK
+                    over += p.workspace_bytes > cap
+                    assert lib.wmma_gemm_plan_make_within(M, N, K, cfg, 256, cap,
+                                                          ctypes.byref(p)) == OK
                     largest = max(largest, p.workspace_bytes)
-    assert largest == 16 << 20 and largest <= cap
+    assert over > 0 and largest <= cap

@@ -163,7 +163,7 @@ def test_gemm_strided_c(wo, M, N, K, tile):
 # (fixed summation order), within tolerance of the oracle, and so must the in-place
 # epilogue through the same workspace.
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (16, 14336, 4096), (5, 1024, 14336),
-                                   (3, 4096, 520)])
+                                   (3, 4096, 2056)])
 def test_skinny_split_k_any_workspace(wo, M, N, K):
     report("skinny_ws", M=M, N=N, K=K, plan=wo.gemm_plan(M, N, K))
     lib = _capi()
@@ -341,9 +341,9 @@ def test_ragged_repack_matches_inplace(wo, M, N, K, case):
 # operands with B moved 2 bytes off a dword and only the split-K workspace take the
 # element-wise kernel: the products match it bit for bit and the oracle to the 1e-3 bar.
 @pytest.mark.parametrize("M,N,K,ldb_pad", [
-    (1, 4100, 4096, 0), (16, 4100, 4096, 0), (1, 4101, 4096, 0), (7, 1027, 300, 0),
-    (3, 4096, 520, 3), (16, 32001, 256, 0), (1, 9, 64, 0), (2, 5, 16, 0), (9, 130, 1000, 1),
-    (17, 4100, 4096, 0), (32, 1027, 300, 1), (25, 4101, 520, 3)])
+    (1, 4100, 4096, 0), (16, 4100, 4096, 0), (1, 4101, 4096, 0), (7, 1027, 1100, 0),
+    (3, 4096, 1096, 3), (16, 32001, 1280, 0), (1, 9, 1088, 0), (2, 5, 1040, 0), (9, 130, 1064, 1),
+    (17, 4100, 4096, 0), (32, 4101, 4100, 1), (25, 4101, 2056, 3)])
 def test_skinny_unaligned_b_in_place(wo, M, N, K, ldb_pad):
     plan = wo.gemm_plan(M, N, K)
     report("skinny_unaligned_b", M=M, N=N, K=K, ldb=N + ldb_pad, plan=plan)
@@ -387,7 +387,7 @@ def test_skinny_unaligned_b_in_place(wo, M, N, K, ldb_pad):
 # strip; with B repacked (N off a multiple of 8); through matmul, gemm out of place and in
 # place (bitwise equal), the C-ABI with row strides of C_in / C_out above N (padding left
 # alone) and wmma_gemm_f16f32_plan with the planner's own two-part plan (bitwise equal).
-@pytest.mark.parametrize("M,N,K,dim", [(4100, 4096, 512, 1), (4103, 4096, 520, 1),
+@pytest.mark.parametrize("M,N,K,dim", [(4100, 4096, 2048, 1), (4103, 4096, 520, 1),
                                        (4352, 4096, 256, 1), (8200, 2048, 512, 1),
                                        (4100, 4100, 1000, 1), (4096, 4101, 1024, 2),
                                        (4096, 4200, 1024, 2)])

@@ -51,7 +51,7 @@ def _replays_match(fn, replays=3):
 
 # (M, N, K): tiled 64x64 split 4, tiled 256x256, skinny split 8, skinny two-block split,
 # tiled 128x64 split 4, a two-part plan (bulk 256x256 + edge GEMM)
-GEMM_SHAPES = [(64, 4096, 4096), (1024, 1024, 2048), (1, 4096, 4096), (32, 4096, 4096),
+GEMM_SHAPES = [(64, 4096, 4096), (1024, 1024, 2048), (1, 4096, 4096), (32, 14336, 4096),
                (128, 4096, 4096), (4100, 1024, 512)]
 
 

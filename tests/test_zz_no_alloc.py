@@ -36,13 +36,15 @@ def _lib():
 
 # (first, second): the second call is smaller.  Plans: tiled 128x128 split 2 (14 MiB of
 # partial sums) then skinny split 8; the tuned tiled split 8 (16 MiB) then skinny split 8;
-# tiled 64x64 split 4 then a ragged skinny split; a shape without a split (no scratch); a
-# two-part plan whose edge is a skinny split 4 then a tiled split 4.
+# tiled 64x64 split 4 then a skinny split whose last part is shorter (K = 4104); shapes
+# without a split (no scratch); a two-part plan whose edge is a skinny split 8 then a tiled
+# split 4; tiled 64x64 split 8 on a narrow N.
 PAIRS = [((128, 14336, 4096), (16, 4096, 4096)),
          ((128, 4096, 14336), (1, 4096, 4096)),
-         ((64, 4096, 4096), (3, 1024, 520)),
+         ((64, 4096, 4096), (3, 1024, 4104)),
          ((1024, 1024, 1024), (300, 264, 640)),
-         ((4100, 4096, 1024), (64, 4096, 4096))]
+         ((4100, 4096, 4096), (64, 4096, 4096)),
+         ((300, 264, 4096), (40, 512, 2048))]
 
 
 @pytest.mark.parametrize("first,second", PAIRS)
@@ -91,7 +93,7 @@ def test_noalloc_scratch_covers_baseline_shapes():
 
 # Ragged shapes (N or K off a multiple of 8): the allocation-free entry point makes no
 # padded copies, so its operands go to the element-wise kernels (split-K partials in the
-# scratch array) or, at M <= 32, the skinny kernel's in-place B modes, while
+# scratch array) or, on the skinny kernel (1 x 4101 x 4096), its in-place B modes, while
 # wmma_gemm_f16f32 with its full workspace repacks them for the vector kernels.  Both are
 # held to the oracle's 1e-3 bar and to each other (products bit-equal: the same MFMA
 # inputs in the same order; the alpha/beta epilogue to rounding).  Two calls in a row, the
@@ -132,6 +134,50 @@ def test_noalloc_ragged_shapes(first, second):
                 assert torch.equal(out_na, out_ref), (M, N, K)
             else:
                 assert og.max_rel_err(out_na, out_ref) <= 1e-6
+
+
+class Plan(ctypes.Structure):
+    _fields_ = [("kernel", ctypes.c_int), ("tile_cfg", ctypes.c_int), ("tile_m", ctypes.c_int),
+                ("tile_n", ctypes.c_int), ("split_k", ctypes.c_int), ("k_per_split", ctypes.c_int),
+                ("grid", ctypes.c_int), ("workspace_bytes", ctypes.c_size_t),
+                ("edge_dim", ctypes.c_int), ("edge_at", ctypes.c_int)]
+
+
+# A shape whose planner plan needs more partial-sum space than the scratch array holds
+# (512 x 4096 x 14336: 256x256 split 8, 64 MiB): the allocation-free entry point runs
+# wmma_gemm_plan_make_within's plan for its array instead (128x128 split 2, 16 MiB),
+# bit-equal to wmma_gemm_f16f32_plan with that plan and within the oracle's bar; then a
+# smaller call, whose plan fits and is the planner's own.
+def test_noalloc_plans_within_scratch():
+    lib = _lib()
+    vp, i64, i32, f32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    lib.wmma_gemm_plan_make.argtypes = [i32] * 5 + [ctypes.POINTER(Plan)]
+    lib.wmma_gemm_plan_make_within.argtypes = [i32] * 5 + [sz, ctypes.POINTER(Plan)]
+    lib.wmma_gemm_f16f32_plan.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32,
+                                          f32, f32, ctypes.POINTER(Plan), vp, sz, vp]
+    cap = lib.wmma_gemm_noalloc_scratch_bytes()
+    st = torch.cuda.current_stream().cuda_stream
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    for i, (M, N, K) in enumerate([(512, 4096, 14336), (64, 4096, 4096)]):
+        report("noalloc_within", M=M, N=N, K=K)
+        full, within = Plan(), Plan()
+        assert lib.wmma_gemm_plan_make(M, N, K, -1, cus, ctypes.byref(full)) == 0
+        assert lib.wmma_gemm_plan_make_within(M, N, K, -1, cus, cap, ctypes.byref(within)) == 0
+        assert 0 < within.workspace_bytes <= cap
+        if i == 0 and cus == 256:
+            assert full.workspace_bytes > cap
+        A, B, C = _inputs(M, N, K, 21 + i)
+        out_na = torch.empty(M, N, device="cuda")
+        out_p = torch.empty(M, N, device="cuda")
+        assert _noalloc(lib, A, B, C, out_na, M, N, K, 1.0, 0.0, st) == 0, lib.wmma_last_error()
+        ws = torch.empty(within.workspace_bytes, dtype=torch.uint8, device="cuda")
+        rc = lib.wmma_gemm_f16f32_plan(A.data_ptr(), K, B.data_ptr(), N, None, 0, out_p.data_ptr(), N,
+                                       M, N, K, 1.0, 0.0, ctypes.byref(within), ws.data_ptr(),
+                                       within.workspace_bytes, st)
+        assert rc == 0, lib.wmma_last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(out_na, out_p), (M, N, K)
+        assert og.max_rel_err(out_na, og.gemm_ref(A.cpu(), B.cpu(), 1.0, 0.0, None)) <= 1e-3
 
 
 def _noalloc(lib, A, B, C, out, M, N, K, alpha, beta, stream):

@@ -171,6 +171,18 @@ int wmma_gemm_plan_make(int M, int N, int K, int tile_cfg, int num_cus, wmma_gem
     return rc == WMMA_OK ? ok() : fail(rc, "planner rejected the shape");
 }
 
+int wmma_gemm_plan_make_within(int M, int N, int K, int tile_cfg, int num_cus,
+                               size_t max_workspace_bytes, wmma_gemm_plan* out) {
+    if (!out) return fail(WMMA_ERR_INVALID_ARG, "plan output pointer is NULL");
+    if (M < 0 || N < 0 || K < 0) return fail(WMMA_ERR_INVALID_ARG, "negative GEMM dimension");
+    if (tile_cfg < WMMA_TILE_AUTO || tile_cfg >= WMMA_TILE_COUNT)
+        return fail(WMMA_ERR_INVALID_ARG,
+                    "Invalid tile_config: 0=64x64, 1=128x64, 2=256x64, 3=128x128, 4=256x128, "
+                    "5=256x256");
+    int rc = make_plan_within(M, N, K, tile_cfg, num_cus, max_workspace_bytes, out);
+    return rc == WMMA_OK ? ok() : fail(rc, "planner rejected the shape");
+}
+
 size_t wmma_gemm_workspace_size(int M, int N, int K, int tile_cfg) {
     wmma_gemm_plan p{};
     if (make_plan(M, N, K, tile_cfg, current_cus(), &p) != WMMA_OK) return 0;
@@ -210,6 +222,8 @@ static int gemm_run(const void* A, int64_t lda, const void* B, int64_t ldb, cons
             (int64_t)kSkinnyMaxMWide * (lda + 7) * 2 > kMaxOffset)
             return fail(WMMA_ERR_UNSUPPORTED, "leading dimension too large for 32-bit offsets");
     }
+    // The allocation-free entry point plans within its scratch array.
+    const size_t plan_cap = use_scratch ? kScratchBytes : SIZE_MAX;
     wmma_gemm_plan plan{};
     if (explicit_plan) {
         // Rebuild the plan from its choices for this shape: a plan made for another shape,
@@ -228,7 +242,7 @@ static int gemm_run(const void* A, int64_t lda, const void* B, int64_t ldb, cons
             return fail(WMMA_ERR_INVALID_ARG, "plan does not describe this shape (make it with "
                                               "wmma_gemm_plan_custom or wmma_gemm_plan_make)");
     } else {
-        int rc = make_plan(M, N, K, tile_cfg, current_cus(), &plan);
+        int rc = make_plan_within(M, N, K, tile_cfg, current_cus(), plan_cap, &plan);
         if (rc != WMMA_OK) return fail(rc, "planner rejected the shape");
     }
     int scratch_dev = -1;
@@ -327,8 +341,8 @@ static int gemm_run(const void* A, int64_t lda, const void* B, int64_t ldb, cons
         const bool rows = plan.edge_dim == WMMA_EDGE_ROWS;
         const int at = plan.edge_at;
         wmma_gemm_plan edge{};
-        if (make_plan(rows ? M - at : M, rows ? N : N - at, K, WMMA_TILE_AUTO, current_cus(),
-                      &edge) != WMMA_OK ||
+        if (make_plan_within(rows ? M - at : M, rows ? N : N - at, K, WMMA_TILE_AUTO,
+                             current_cus(), plan_cap, &edge) != WMMA_OK ||
             edge.edge_dim != WMMA_EDGE_NONE || edge.workspace_bytes > plan.workspace_bytes)
             return fail(WMMA_ERR_INVALID_ARG, "inconsistent two-part plan");
         if (int rc = launch_part(plan, 0, 0, rows ? at : M, rows ? N : at)) return rc;

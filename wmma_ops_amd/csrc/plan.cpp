@@ -4,12 +4,16 @@
 // wmma_tile_selection.hpp:30-66) and has an unreachable split-K config
 // (compute_config, wmma_xor_swizzle.hpp:293-332: target tiles = 4 x CUs, split capped at
 // 32 and at K/256, k_per_split = ceil(K/split)).  Here the choice is made against a
-// 256-CU device: fill the chip with whole waves of workgroups, prefer the tile that
-// reuses the most bytes per LDS byte, and split K only when too few output tiles exist
-// to occupy the CUs.  The result never depends on the plan beyond fp32 summation order.
+// 256-CU device, in four tiers: exact shapes from the autotuned table; M <= 16 with
+// K > 1024 on the streaming kernel with its split rule; every other M <= 768 by a launch
+// model fitted to measured times of every plan (model_plan); larger M by whole waves of
+// workgroups, the tile that reuses the most bytes per LDS byte, a K split only when too
+// few output tiles exist to occupy the CUs, and bulk + edge plans.  The result never
+// depends on the plan beyond fp32 summation order.
 #include "plan.hpp"
 
 #include <algorithm>
+#include <cstdint>
 
 namespace wmma_amd {
 
@@ -23,6 +27,13 @@ static void finish_split(int M, int N, int K, int tiles, int split, wmma_gemm_pl
     p->k_per_split = split > 1 ? kps : std::max(K, 0);
     p->grid = tiles * split;
     p->workspace_bytes = split > 1 ? (size_t)split * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+// Lower the split of p until its partial sums fit max_ws (a plan without a split needs none).
+static void fit_split(int M, int N, int K, size_t max_ws, wmma_gemm_plan* p) {
+    const int tiles = p->grid / std::max(p->split_k, 1);
+    for (int split = p->split_k - 1; p->workspace_bytes > max_ws && split >= 1; --split)
+        finish_split(M, N, K, tiles, split, p);
 }
 
 double plan_time_us(const wmma_gemm_plan& p, int M, int N, int K, int num_cus) {
@@ -41,6 +52,72 @@ double plan_time_us(const wmma_gemm_plan& p, int M, int N, int K, int num_cus) {
     }
     if (split > 1) t += (split + 1) * 4.0 * M * N / kHbmBytesPerUs + kReduceUs;
     return t + kLaunchUs;
+}
+
+double model_time_us(const wmma_gemm_plan& p, int M, int N, int K, int num_cus) {
+    if (num_cus <= 0) num_cus = 256;
+    const int split = std::max(p.split_k, 1);
+    const double kk = split > 1 ? p.k_per_split : K;
+    double t;
+    if (p.kernel == WMMA_KERNEL_SKINNY) {
+        const int mb = M <= 16 ? 16 : 32;
+        const int64_t wgs = (int64_t)ceil_div(N, kSkinnyBlockN) * split;
+        const double kb = (kSkinnyBlockN + mb) * kk * 2.0 / 1000.0;
+        t = (double)ceil_div64(wgs, num_cus) * (kSkinnyWgFixedUs + kb / kSkinnyKbPerUs);
+    } else {
+        const TileShape& ts = kTiles[p.tile_cfg];
+        const int64_t wgs = (int64_t)ceil_div(M, ts.bm) * ceil_div(N, ts.bn) * split;
+        const double kb = (std::min(M, ts.bm) + ts.bn) * kk * 2.0 / 1000.0;
+        const double mflop = 2.0 * ts.bm * ts.bn * kk / 1e6;
+        const TileRate& r = kTileRate[p.tile_cfg];
+        t = (double)ceil_div64(wgs, num_cus) *
+            (kWgFixedUs + std::max(kb / r.kb_per_us, mflop / r.mflop_per_us));
+    }
+    const double mb_io = (2.0 * M * K + 2.0 * K * N + 4.0 * M * N) / 1e6;
+    t = std::max(t, mb_io / kModelHbmMBPerUs);
+    if (split > 1) t += kSplitFixedUs + kPartialUsPerMB * (split + 1) * 4.0 * M * N / 1e6;
+    return t;
+}
+
+// The plan with the shortest modelled time: every tile with K splits 1, 2, 4, 8, 16 (a
+// split only from K = 2048, at least 256 of K per part, and only while the workgroups fit
+// one wave of the CUs), and for M <= 32 the streaming kernel with splits up to K / 256.
+// Over the fitted shapes the choice costs 0.65% more time than the fastest plan of each
+// shape (the previous heuristics: 14%), and 0.8% on a second sweep of 63 shapes.
+static wmma_gemm_plan model_plan(int M, int N, int K, int num_cus, size_t max_ws) {
+    wmma_gemm_plan best{};
+    double best_t = 1e300;
+    for (int cfg = 0; cfg < WMMA_TILE_COUNT; ++cfg) {
+        const TileShape& ts = kTiles[cfg];
+        const int64_t tiles = (int64_t)ceil_div(M, ts.bm) * ceil_div(N, ts.bn);
+        for (int sp : {1, 2, 4, 8, 16}) {
+            if (sp > 1 && (K / sp < 256 || K < 2048 || tiles * sp > num_cus)) break;
+            wmma_gemm_plan c{};
+            if (make_custom_plan(M, N, K, WMMA_KERNEL_TILED, cfg, sp, &c) != WMMA_OK ||
+                c.workspace_bytes > max_ws)
+                continue;
+            const double t = model_time_us(c, M, N, K, num_cus);
+            if (t < best_t * 0.999) {
+                best_t = t;
+                best = c;
+            }
+        }
+    }
+    if (M <= 32) {
+        for (int sp : {1, 2, 3, 4, 5, 6, 8, 12, 16, 24, 32}) {
+            if (sp > std::max(1, K / 256)) break;
+            wmma_gemm_plan c{};
+            if (make_custom_plan(M, N, K, WMMA_KERNEL_SKINNY, -1, sp, &c) != WMMA_OK ||
+                c.workspace_bytes > max_ws)
+                continue;
+            const double t = model_time_us(c, M, N, K, num_cus);
+            if (t < best_t * 0.999) {
+                best_t = t;
+                best = c;
+            }
+        }
+    }
+    return best;
 }
 
 // The autotuned table: exact shapes measured on a 256-CU MI355X.
@@ -87,7 +164,7 @@ int make_custom_plan(int M, int N, int K, int kernel, int tile_cfg, int split,
 // tile or a K split and spread over the chip).  Measured on MI355X (N = K = 4096): M = 4352
 // one launch of 128x128 tiles 193 us, 4096 + 256 rows 148 us; M = 5000: 209 vs 171 us;
 // M = 9192: 347 vs 295 us.  Taken when plan_time_us says it gains more than 7%.
-static void two_part(int M, int N, int K, int num_cus, wmma_gemm_plan* p) {
+static void two_part(int M, int N, int K, int num_cus, size_t max_ws, wmma_gemm_plan* p) {
     const int64_t tm = ceil_div(M, 256), tn = ceil_div(N, 256);
     const int64_t whole = tm * tn / num_cus * num_cus;  // 256x256 tiles in whole waves
     if (whole == 0) return;
@@ -101,7 +178,7 @@ static void two_part(int M, int N, int K, int num_cus, wmma_gemm_plan* p) {
         const int em = dim == WMMA_EDGE_ROWS ? M - at : M, en = dim == WMMA_EDGE_ROWS ? N : N - at;
         wmma_gemm_plan bulk{}, edge{};
         if (make_custom_plan(bm, bn, K, WMMA_KERNEL_TILED, WMMA_TILE_256x256, 1, &bulk) != WMMA_OK ||
-            make_plan(em, en, K, WMMA_TILE_AUTO, num_cus, &edge) != WMMA_OK ||
+            make_plan_within(em, en, K, WMMA_TILE_AUTO, num_cus, max_ws, &edge) != WMMA_OK ||
             edge.edge_dim != WMMA_EDGE_NONE)
             continue;
         const double t = plan_time_us(bulk, bm, bn, K, num_cus) + plan_time_us(edge, em, en, K, num_cus);
@@ -116,6 +193,11 @@ static void two_part(int M, int N, int K, int num_cus, wmma_gemm_plan* p) {
 }
 
 int make_plan(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* out) {
+    return make_plan_within(M, N, K, tile_cfg, num_cus, SIZE_MAX, out);
+}
+
+int make_plan_within(int M, int N, int K, int tile_cfg, int num_cus, size_t max_ws,
+                     wmma_gemm_plan* out) {
     if (!out || M < 0 || N < 0 || K < 0) return WMMA_ERR_INVALID_ARG;
     if (tile_cfg < WMMA_TILE_AUTO || tile_cfg >= WMMA_TILE_COUNT) return WMMA_ERR_INVALID_ARG;
     if (num_cus <= 0) num_cus = 256;
@@ -123,8 +205,12 @@ int make_plan(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* ou
 
     if (tile_cfg == WMMA_TILE_AUTO && num_cus == 256) {
         for (const TunedPlan& e : kTunedPlans)
-            if (e.M == M && e.N == N && e.K == K)
-                return make_custom_plan(M, N, K, e.kernel, e.tile_cfg, e.split, out);
+            if (e.M == M && e.N == N && e.K == K &&
+                make_custom_plan(M, N, K, e.kernel, e.tile_cfg, e.split, &p) == WMMA_OK &&
+                p.workspace_bytes <= max_ws) {
+                *out = p;
+                return WMMA_OK;
+            }
     }
 
     if (tile_cfg != WMMA_TILE_AUTO) {
@@ -140,84 +226,41 @@ int make_plan(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* ou
         return WMMA_OK;
     }
 
-    if (M <= kSkinnyAutoMaxM && M > 0 && N > 0 && K > 0) {
-        // Streaming kernel: each workgroup owns kSkinnyBlockN columns and one K range.
+    if (M <= kSkinnyAutoMaxM && M > 0 && N > 0 && K > 1024) {
+        // Streaming kernel (M <= 16 with K > 1024; the launch model takes shorter K, where
+        // an unsplit 64x64 tile measured 10-30% faster): each workgroup owns
+        // kSkinnyBlockN columns and one K range.
         // The launch lasts as long as the busiest CU, which streams ceil(W / CUs) of the
         // W = tiles x split workgroups, each 1/W of the bytes.  M <= 16: pick the split
         // that minimises ceil(W / CUs) / W over W <= 3 x CUs (measured on MI355X: a split
         // that leaves some CUs one workgroup more than the rest costs 10-25%, and beyond
         // three workgroups per CU the extra partial sums cost more than the balance gains),
-        // the smaller split on a tie (fewer partial sums to write and reduce).  16 < M <= 32
-        // (two 16-row blocks, twice the partial sums): the largest split that keeps W
-        // within one wave of the CUs -- the fastest of splits 1-8 in every case measured
-        // (M = 17, 32; N = 4096, 11008, 14336; K = 4096, 14336), e.g. M = 32, N = 11008:
-        // split 2 25.9 us against 27.2-31.6 for 3-8, 27.1 for the tiled kernel.
+        // the smaller split on a tie (fewer partial sums to write and reduce).
         p.kernel = WMMA_KERNEL_SKINNY;
         p.tile_cfg = -1;
-        p.tile_m = M <= 16 ? 16 : 32;
+        p.tile_m = 16;
         p.tile_n = kSkinnyBlockN;
         const int tiles = ceil_div(N, kSkinnyBlockN);
         const int smax = std::min(std::max(1, K / 256), kMaxSplitK);
         int split = 1;
-        if (M > 16) {
-            split = (int)std::max<int64_t>(1, std::min<int64_t>(smax, num_cus / tiles));
-        } else {
-            double best = 1e300;
-            for (int sp = 1; sp <= smax; ++sp) {
-                const int64_t w = (int64_t)tiles * sp;
-                if (sp > 1 && w > 3 * (int64_t)num_cus) break;
-                const double cost = (double)ceil_div64(w, num_cus) / (double)w;
-                if (cost < best * 0.99) {
-                    best = cost;
-                    split = sp;
-                }
+        double best = 1e300;
+        for (int sp = 1; sp <= smax; ++sp) {
+            const int64_t w = (int64_t)tiles * sp;
+            if (sp > 1 && w > 3 * (int64_t)num_cus) break;
+            const double cost = (double)ceil_div64(w, num_cus) / (double)w;
+            if (cost < best * 0.99) {
+                best = cost;
+                split = sp;
             }
         }
         finish_split(M, N, K, tiles, split, &p);
+        fit_split(M, N, K, max_ws, &p);
         *out = p;
         return WMMA_OK;
     }
 
-    if (M <= 128 && K >= 512) {
-        // Few rows: the GEMM streams B, and the chip is filled by choosing the tile and the
-        // K split together.  Estimated time = (workgroups on the busiest CU) x tile area /
-        // (split x tile efficiency x the fraction of the tile's rows that exist), with 15%
-        // per extra split for the partial sums.  Measured on MI355X at M = 64, 128 and
-        // N = 4096..14336, K = 4096, 14336: this picks the fastest of the 64x64, 128x64 and
-        // 128x128 tiles with splits 1, 2, 4 in every case (up to 22% over choosing the tile
-        // first and splitting only an under-filled chip; with a 10% split term it chose
-        // split 4 for M = 64, N = 11008, measured 17% slower than no split).
-        const int cands[] = {WMMA_TILE_64x64, WMMA_TILE_128x64, WMMA_TILE_128x128};
-        int best_cfg = WMMA_TILE_64x64, best_split = 1;
-        double best_cost = 1e300;
-        for (int cfg : cands) {
-            const TileShape& t = kTiles[cfg];
-            const int64_t tiles = (int64_t)ceil_div(M, t.bm) * ceil_div(N, t.bn);
-            const double eff = kTileEff[cfg] * std::min(1.0, (double)M / t.bm);
-            for (int sp : {1, 2, 4}) {
-                // a split needs K >= 256 per part and K >= 2048 for the partial-sum pass
-                // to pay for itself: measured on MI355X, every shape with K >= 2048 split
-                // faster (48 x 1024 x 2048: 15.2 -> 11.2 us; 64 x 1024 x 4096: 25.5 ->
-                // 12.7; 48 x 4096 x 4096: 26.8 -> 15.0), every one with K <= 1024 slower
-                // (64 x 1024 x 1024: 9.4 -> 11.7; 128 x 4096 x 512: 7.9 -> 11.0)
-                if (sp > 1 && (K / sp < 256 || K < 2048)) break;
-                const int64_t w = tiles * sp;
-                const double cost = (double)ceil_div64(w, num_cus) * t.bm * t.bn / (sp * eff) *
-                                    (1.0 + 0.15 * (sp - 1));
-                if (cost < best_cost * 0.999) {
-                    best_cost = cost;
-                    best_cfg = cfg;
-                    best_split = sp;
-                }
-            }
-        }
-        const TileShape& t = kTiles[best_cfg];
-        p.kernel = WMMA_KERNEL_TILED;
-        p.tile_cfg = best_cfg;
-        p.tile_m = t.bm;
-        p.tile_n = t.bn;
-        finish_split(M, N, K, ceil_div(M, t.bm) * ceil_div(N, t.bn), best_split, &p);
-        *out = p;
+    if (M > 0 && N > 0 && K > 0 && M <= kModelMaxM) {
+        *out = model_plan(M, N, K, num_cus, max_ws);
         return WMMA_OK;
     }
 
@@ -253,7 +296,8 @@ int make_plan(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* ou
         split = std::max(split, 1);
     }
     finish_split(M, N, K, tiles, split, &p);
-    if (tile_cfg == WMMA_TILE_AUTO && split == 1) two_part(M, N, K, num_cus, &p);
+    fit_split(M, N, K, max_ws, &p);
+    if (tile_cfg == WMMA_TILE_AUTO && p.split_k == 1) two_part(M, N, K, num_cus, max_ws, &p);
     *out = p;
     return WMMA_OK;
 }

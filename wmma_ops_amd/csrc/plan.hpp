@@ -27,7 +27,8 @@ constexpr TileShape kTiles[WMMA_TILE_COUNT] = {
 };
 
 constexpr int kBlockK = 64;        // K depth of one LDS stage (fp16: 128-byte rows)
-constexpr int kSkinnyAutoMaxM = 32; // M at or below this: the planner picks the streaming kernel
+constexpr int kSkinnyAutoMaxM = 16; // M at or below this (K > 1024): the streaming kernel's own rule
+constexpr int kModelMaxM = 768;     // M at or below this: the measured launch model picks the plan
 constexpr int kSkinnyMaxMWide = 64; // the streaming kernel's limit (four 16-row blocks)
 constexpr int kSkinnyBlockN = 128; // columns per skinny workgroup
 constexpr int kMaxSplitK = 32;     // cap from the reference's split-K config (wmma_xor_swizzle.hpp:318)
@@ -35,10 +36,28 @@ constexpr int kMaxSplitK = 32;     // cap from the reference's split-K config (w
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 inline int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Relative per-CU throughput of each tile in the few-rows branch (M <= 128, B streamed),
-// where it ranks tile / split pairs together with the fraction of the tile's rows that
-// exist (calibrated on M = 64, 128, N = 4096..14336, K = 4096, 14336).
-constexpr double kTileEff[WMMA_TILE_COUNT] = {0.40, 0.55, 0.65, 0.75, 0.88, 1.0};
+// Launch model for M <= kModelMaxM, fitted on MI355X (256 CUs) to the autotuner's timings
+// of every plan (6 tiles x splits 1-16, the streaming kernel with splits 1-32) at 819
+// shapes, M = 1-768, N = 512-14336, K = 512-14336.  A workgroup streams its operand bytes
+// (the rows of A that exist plus the tile's columns of B, over its K range) at a per-CU
+// rate, or is held by its MFMA work, whichever is longer, plus a fixed cost; the launch
+// takes as many such times as it has waves of workgroups (one per CU), at least the HBM
+// time of its operands, plus, with a K split, a fixed cost and the partial sums' bytes.
+struct TileRate {
+    double kb_per_us;     // operand bytes a workgroup streams per microsecond (KB)
+    double mflop_per_us;  // its MFMA rate (MFLOP per microsecond, full tile rows)
+};
+constexpr TileRate kTileRate[WMMA_TILE_COUNT] = {
+    {40, 2}, {40, 4}, {10, 4}, {40, 4}, {30, 3}, {35, 5}};
+constexpr double kWgFixedUs = 2.0;         // per workgroup: prologue, epilogue
+constexpr double kSkinnyKbPerUs = 50;      // the streaming kernel's per-workgroup rate
+constexpr double kSkinnyWgFixedUs = 3.0;
+constexpr double kSplitFixedUs = 2.0;      // a K split: the reduction launch
+constexpr double kPartialUsPerMB = 0.5;    // and (split + 1) x M x N x 4 bytes of partial sums
+constexpr double kModelHbmMBPerUs = 8.0;   // operand bytes per microsecond at most
+
+// Modelled duration (microseconds) of a one-launch plan for M <= kModelMaxM.
+double model_time_us(const wmma_gemm_plan& p, int M, int N, int K, int num_cus);
 
 // Time model of the tiled kernel on full waves of workgroups (one workgroup per CU),
 // fitted on MI355X to full-wave launches of every tile (4096^3, 8192 x 8192 x 4096,
@@ -67,6 +86,12 @@ constexpr double kEdgeGain = 0.93;
 // (tuned_table.inc) takes the measured plan; every other shape the heuristics in
 // plan.cpp, which may split it into a bulk and an edge GEMM (out->edge_dim).
 int make_plan(int M, int N, int K, int tile_cfg, int num_cus, wmma_gemm_plan* out);
+
+// make_plan among the plans whose split-K partial sums fit max_ws bytes: a tuned-table
+// entry or a split that needs more is passed over for the next choice (a plan without a
+// split needs none, so there always is one).
+int make_plan_within(int M, int N, int K, int tile_cfg, int num_cus, size_t max_ws,
+                     wmma_gemm_plan* out);
 
 // A plan with an explicit kernel (WMMA_KERNEL_*), tile (WMMA_TILE_*; ignored by the skinny
 // kernel) and K split, completed as the planner completes its own (k_per_split a whole
