@@ -101,6 +101,43 @@ def test_w4a16_skinny(wo, M, K, N, G):
     assert torch.equal(Yp, Yu)
 
 
+# The LDS-DMA W4A16 GEMM with a K split, called repeatedly through the C-ABI on a workspace
+# filled with NaN each time: every call bit-identical and within the oracle's bar.  (Its
+# ring once let a stage's DMA overwrite LDS rows another wave was still reading, which
+# showed as wrong 8-row groups in a few calls out of several.)
+@pytest.mark.parametrize("M,N,K", [(64, 4096, 4096), (128, 4096, 4096), (33, 14336, 4096),
+                                   (256, 4096, 2048)])
+def test_w4a16_gemm_split_repeatable(wo, M, N, K):
+    import ctypes
+    G = 128
+    plan = wo.w4a16_plan(M, N, K, G)
+    report("w4a16_gemm_repeat", M=M, N=N, K=K, plan=plan)
+    assert plan[0] == 5 and plan[1] > 1
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                                   "wmma_ops_amd", "libwmma_ops_amd.so"))
+    vp, i64, i32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
+    lib.wmma_w4a16_gemm.argtypes = [vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, vp, i64, vp, sz, vp]
+    lib.wmma_last_error.restype = ctypes.c_char_p
+    A, q, s, z = oi.make_inputs(M, K, N, G, seed=M + N + K)
+    ref = oi.w4a16_ref(A, q, s, z, G)
+    pk = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
+    sd, zd = torch.from_numpy(s).cuda(), torch.from_numpy(oi.pack_zeros(z)).cuda()
+    Ad = A.cuda()
+    st = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for rep in range(8):
+        ws = torch.full((plan[3] // 4,), float("nan"), device="cuda")
+        Y = torch.full((M, N), float("nan"), device="cuda")
+        rc = lib.wmma_w4a16_gemm(Ad.data_ptr(), K, pk.data_ptr(), sd.data_ptr(), zd.data_ptr(), 0,
+                                 M, N, K, G, Y.data_ptr(), N, ws.data_ptr(), plan[3], st)
+        assert rc == 0, lib.wmma_last_error()
+        outs.append(Y)
+    torch.cuda.synchronize()
+    assert og.max_rel_err(outs[0], ref) <= 1e-3
+    for Y in outs[1:]:
+        assert torch.equal(Y, outs[0])
+
+
 # The skinny kernel's other workgroup shapes on a 256-CU device (16-column slices per
 # workgroup NH x pair-steps per wave U, one or two 16-row blocks): 1x1 unsplit (K = 1024) and
 # with an 8-way split, 2x2 unsplit and with a 7-way split, 2x4, 4x1 unsplit and split, 4x2

@@ -1452,6 +1452,12 @@ w4a16_gemm_kernel(W4Args p) {
 #pragma unroll
             for (int q = 0; q < NS; ++q) {
                 wait_vmcnt<(NS - 2) * C::PER>();
+                // lgkmcnt(0): this wave's LDS reads of the previous stage are done before
+                // the barrier, after which the stage's DMA overwrites that slot.  Without it
+                // the compiler left up to 6 reads in flight across the barrier, and a DMA
+                // that won the race fed stale rows to one wave's MFMAs (seen on MI355X with
+                // the 128 x 128 tile and a K split: 8-row groups of one wave's columns).
+                __builtin_amdgcn_s_waitcnt(0xC07F);
                 __builtin_amdgcn_s_barrier();
                 asm volatile("" ::: "memory");
                 const int tn_ = t0 + q + NS - 1;
@@ -1466,6 +1472,7 @@ w4a16_gemm_kernel(W4Args p) {
         for (int q = 0; q < NS - 1; ++q) {
             if (t1 + q < nk) {  // uniform
                 wait_vmcnt<(NS - 2) * C::PER>();
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), as in the loop above
                 __builtin_amdgcn_s_barrier();
                 asm volatile("" ::: "memory");
                 w4g_stage<C, ZF>(p, L, ra, rw, rs, rz, lds + q * C::A_BYTES,
