@@ -321,6 +321,8 @@ def test_w4a16_plan_make(lib):
     assert plan(128, 4096, 4096)[:2] == (5, 4)         # 64 tiles: 256 / 64 ways
     assert plan(64, 4096, 4096)[:2] == (5, 8)          # 32 tiles: 8 ways (the cap)
     assert plan(64, 11008, 4096)[:2] == (5, 2)         # 86 tiles: 2 ways
+    assert plan(128, 4096, 1024)[:2] == (5, 1)         # K <= 1024: never a split
+    assert plan(1024, 1024, 1024)[:2] == (5, 1)
     # skinny with 64-column workgroups (128 of them) and a 4-way K split
     assert plan(16, 8192, 8192) == (4, 4, 2048, 4 * 16 * 8192 * 4)
     assert plan(2048, 4096, 4096)[:2] == (5, 1)        # 512 tiles of 128x128, no split

@@ -1900,9 +1900,13 @@ W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
         // sums cost a second pass over M x N fp32 per split), at most 8 (measured with
         // 64 x 128 tiles at N = 4096: M = 48, 64 best with 8 ways; M = 96, 128 with 4; at
         // N = 11008, 14336: M = 64 with 2, M = 128 unsplit).
+        // No split at K <= 1024: the partial sums and their reduction launch cost more
+        // than the idle CUs (measured: 128 x 4096 x 1024 11.5 -> 8.5 us unsplit, 256 x
+        // 4096 x 1024 12.4 -> 8.7, 1024 x 1024 x 1024 12.3 -> 8.7, 64 x 14336 x 1024
+        // 12.5 -> 9.0).
         int s = 1;
         const int max_split = 8;
-        if (tiles < num_cus)
+        if (tiles < num_cus && K > 1024)
             s = (int)std::min<int64_t>(std::max<int64_t>(num_cus / tiles, 1), max_split);
         s = std::max(1, std::min(s, KC / 4));
         const int kcps = ceil_div(KC, s);
