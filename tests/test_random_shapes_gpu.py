@@ -11,6 +11,9 @@ id.
 
 Bars: GEMM max rel err <= 1e-4 (fp32 accumulation of exact fp16 products; the documented
 bar is 1e-3); W4A16, flash forward and each flash gradient 1e-3, the documented bar.
+Every path is deterministic, so each case also repeats its call (with other work and fresh
+allocations in between) and requires bit-identical results: a race that corrupts a call
+now and then shows there, not only as an error above the bar.
 """
 import numpy as np
 import pytest
@@ -101,7 +104,11 @@ def test_random_gemm(wo, case):
     assert torch.isfinite(Y).all()
     err = og.max_rel_err(Y, ref)
     assert err <= 1e-4, f"max rel err {err:.3e}"
-    assert og.max_rel_err(wo.matmul(A.cuda(), B.cuda()), og.gemm_ref(A, B)) <= 1e-4
+    P = wo.matmul(A.cuda(), B.cuda())
+    assert og.max_rel_err(P, og.gemm_ref(A, B)) <= 1e-4
+    for _ in range(2):
+        assert torch.equal(wo.gemm(A.cuda(), B.cuda(), alpha, beta, C.cuda() if beta != 0.0 else None), Y)
+        assert torch.equal(wo.matmul(A.cuda(), B.cuda()), P)
 
 
 @pytest.mark.parametrize("case", range(len(W4_CASES)))
@@ -126,6 +133,8 @@ def test_random_w4a16(wo, case):
     assert torch.isfinite(Y).all()
     err = og.max_rel_err(Y.float(), ref)
     assert err <= 1e-3, f"max rel err {err:.3e}"
+    for _ in range(3):
+        assert torch.equal(wo.matmul_int4(A.cuda(), pk, *args, G, **kw), Y)
 
 
 @pytest.mark.parametrize("case", range(len(FLASH_CASES)))
@@ -139,6 +148,8 @@ def test_random_flash_forward(wo, case):
     assert torch.isfinite(O).all()
     err = og.max_rel_err(O.float(), ref)
     assert err <= 1e-3, f"max rel err {err:.3e}"
+    for _ in range(2):
+        assert torch.equal(wo.flash_attention(Q.cuda(), K.cuda(), V.cuda(), causal=causal), O)
 
 
 @pytest.mark.parametrize("case", range(len(FLASH_BWD_CASES)))
@@ -161,6 +172,10 @@ def test_random_flash_backward(wo, case):
         assert torch.isfinite(got).all(), name
         err = og.max_rel_err(got.float(), want)
         assert err <= 1e-3, f"{name}: max rel err {err:.3e}"
+    Q2, K2, V2 = (t.cuda().requires_grad_(True) for t in (Q, K, V))
+    wo.flash_attention(Q2, K2, V2, causal=causal).backward(dO.cuda())
+    for got, again in ((Qd.grad, Q2.grad), (Kd.grad, K2.grad), (Vd.grad, V2.grad)):
+        assert torch.equal(got, again)
 
 
 # The fused decode layout on its own seeded draw (so the cases above keep their shapes):
