@@ -9,6 +9,11 @@ classes this library must never contain:
 * writes through the scalar data cache (scalar stores and atomics, and that cache's
   write-back / discard): all GPU writes here are vector stores.
 
+and for one ordering pattern: a workgroup barrier crossed with this wave's LDS reads still
+in flight and followed by an LDS DMA (buffer_load ... lds) before they are waited for.
+Ring kernels reuse, right after such a barrier, the LDS slot the previous stage read, so
+a DMA landing early would overwrite rows another wave has not read yet.
+
 This file names those instructions, so it is listed in .gpurunignore (it never runs on
 the GPU box).
 """
@@ -77,3 +82,56 @@ def test_library_has_gfx950_kernels(disassembly):
 def test_no_forbidden_instructions(disassembly):
     bad = sorted({m.group(0) for m in FORBIDDEN.finditer(disassembly)})
     assert not bad, f"forbidden instructions in device code: {bad}"
+
+
+_FUNC = re.compile(r"^[0-9a-f]+ <(\S+)>:$")
+_LGKM = re.compile(r"lgkmcnt\((\d+)\)")
+
+
+def lds_reads_pending_at_dma_barriers(text):
+    """Kernels with a barrier that some path reaches with LDS reads in flight (counted from
+    ds_* issues since the last lgkmcnt(0), capped by later lgkmcnt(N) waits; a straight
+    scan of the listing) and after which an LDS DMA issues before lgkmcnt(0)."""
+    found = {}
+    func, pending, armed = None, 0, False
+    for line in text.splitlines():
+        m = _FUNC.match(line)
+        if m:
+            func, pending, armed = m.group(1), 0, False
+            continue
+        ins = line.strip().split("//")[0].strip()
+        if not ins or func is None:
+            continue
+        op = ins.split()[0]
+        if op.startswith("ds_"):
+            pending += 1
+        elif op == "s_waitcnt":
+            w = _LGKM.search(ins)
+            if w:
+                pending = min(pending, int(w.group(1)))
+                if pending == 0:
+                    armed = False
+        elif op == "s_barrier":
+            armed = pending > 0
+        elif armed and op.startswith(("buffer_load", "global_load")) and " lds" in ins:
+            found[func] = found.get(func, 0) + 1
+            armed = False
+    return found
+
+
+def test_no_lds_reads_in_flight_across_a_dma_barrier(disassembly):
+    found = lds_reads_pending_at_dma_barriers(disassembly)
+    assert not found, f"LDS reads in flight at a barrier followed by an LDS DMA: {sorted(found)}"
+
+
+def test_race_scan_finds_the_pattern():
+    # the scan itself, on a listing with the pattern and on the same listing with the wait
+    bad = """0000000000001000 <kern>:
+	ds_read_b128 v[0:3], v4
+	s_waitcnt vmcnt(14)
+	s_barrier
+	buffer_load_dwordx4 v5, s[8:11], 0 offen lds
+"""
+    good = bad.replace("\ts_barrier", "\ts_waitcnt lgkmcnt(0)\n\ts_barrier")
+    assert lds_reads_pending_at_dma_barriers(bad) == {"kern": 1}
+    assert lds_reads_pending_at_dma_barriers(good) == {}
