@@ -106,7 +106,7 @@ def test_w4a16_skinny(wo, M, K, N, G):
 # ring once let a stage's DMA overwrite LDS rows another wave was still reading, which
 # showed as wrong 8-row groups in a few calls out of several.)
 @pytest.mark.parametrize("M,N,K", [(64, 4096, 4096), (128, 4096, 4096), (33, 14336, 4096),
-                                   (256, 4096, 2048)])
+                                   (192, 4096, 8192), (128, 11008, 14336)])
 def test_w4a16_gemm_split_repeatable(wo, M, N, K):
     import ctypes
     G = 128

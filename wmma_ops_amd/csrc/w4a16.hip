@@ -1833,6 +1833,46 @@ bool w4a16_fused_decode_ok(int M, int K) {
            decode_mfma_lds_bytes(std::max(M, 1), K) <= kDecodeMfmaLdsMax;
 }
 
+// Launch model of the W4A16 GEMM for 32 < M <= kW4gModelMaxM: a workgroup streams its
+// activation rows (those that exist) and its tile's int4 columns over its K range at a
+// per-CU rate, or is held by its MFMA work, plus 1 us; the launch takes that per wave of
+// workgroups, plus 2 us and 0.5 us per MB of partial sums with a K split.  Constants set
+// by coordinate search on the planning loss over every tile x split 1-8 timed at 128
+// shapes (M = 33-1024, N = 1024-14336, K = 2048-14336, graph-replayed): fitted on half the
+// K values it takes 1.3% / 0.5% more time than the fastest plan per shape on the other
+// half, against 2.5% / 1.4% for the tile-count rule it replaced (up to 1.22x faster:
+// 64 x 14336 x 2048 16.1 -> 13.2 us unsplit; 128 x 11008 x 14336 67.3 -> 59.7 us with
+// 128 x 256 tiles split 4).
+constexpr int kW4gModelMaxM = 1024;
+constexpr double kW4gKbPerUs[3] = {40, 35, 35};      // per tile config (W4G_TILE_*)
+constexpr double kW4gMflopPerUs[3] = {4, 4, 3};
+
+void w4g_model_plan(int M, int N, int K, int num_cus, int* cfg_out, int* split_out) {
+    const int KC = K / 64;
+    double best_t = 1e300;
+    *cfg_out = W4G_TILE_SHORT;
+    *split_out = 1;
+    for (int cfg : {W4G_TILE_SHORT, W4G_TILE_MID, W4G_TILE_WIDE}) {
+        const int bm = kW4gTileM[cfg], bn = kW4gTileN[cfg];
+        for (int sp : {1, 2, 4, 8}) {
+            if (sp > 1 && (K <= 1024 || KC < 4 * sp)) continue;
+            const int kcps = ceil_div(KC, sp), s = ceil_div(KC, kcps);
+            const double kk = kcps * 64.0;
+            const int64_t wgs = (int64_t)ceil_div(M, bm) * ceil_div(N, bn) * s;
+            const double kb = (std::min(M, bm) * 2.0 + bn / 2.0) * kk / 1000.0;
+            const double mflop = 2.0 * bm * bn * kk / 1e6;
+            double t = (double)((wgs + num_cus - 1) / num_cus) *
+                       (1.0 + std::max(kb / kW4gKbPerUs[cfg], mflop / kW4gMflopPerUs[cfg]));
+            if (s > 1) t += 2.0 + 0.5 * (s + 1) * 4.0 * M * N / 1e6;
+            if (t < best_t * 0.999) {
+                best_t = t;
+                *cfg_out = cfg;
+                *split_out = sp;
+            }
+        }
+    }
+}
+
 // M <= 4 rows against few columns and a long K: the decode gives one workgroup per
 // 16-column slice, each walking all of K, so with under num_cus / 4 slices a K-split skinny
 // launch finishes first.  Measured on MI355X (256 CUs), decode against skinny, us:
@@ -1895,41 +1935,32 @@ W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
     }
     const int KC = K / 64;
     if (M > 32 && (G & (G - 1)) == 0) {
-        // LDS-DMA W4A16 GEMM.  Tile (measured on MI355X at K = 4096, N in {4096, 11008,
-        // 14336}):
-        //   64 x 128 for M <= 128 (2-20% faster than 128 x 128 at M = 48..128), and above
-        //     while its tiles fit one wave of the CUs (N = 4096: M = 160 / 192 / 256 / 384 /
-        //     512 19.0 / 19.2 / 21.2 / 22.8 / 25.1 us against 20.4 / 22.3 / 22.4 / 25.9 /
-        //     30.1 for 128 x 128 with its best split; where they take more than a wave,
-        //     M = 768 or N = 14336, 128 x 128 is the faster);
-        //   128 x 256 when those tiles give at least one per CU, in whole multiples of the
-        //     CU count or 1.7 of them (M = 2048: 5-26% faster than 128 x 128; M = 1024,
-        //     N = 11008, 1.34 tiles per CU: 4% slower);
-        //   else 128 x 128.
-        // K split only to fill the chip.
-        const int64_t wide_tiles = (int64_t)ceil_div(M, 128) * ceil_div(N, 256);
-        const int64_t short_tiles = (int64_t)ceil_div(M, 64) * ceil_div(N, 128);
-        int cfg = W4G_TILE_MID;
-        if (M <= 128 || short_tiles <= num_cus)
-            cfg = W4G_TILE_SHORT;
-        else if (wide_tiles >= num_cus &&
-                 (wide_tiles % num_cus == 0 || 10 * wide_tiles >= 17 * (int64_t)num_cus))
-            cfg = W4G_TILE_WIDE;
-        const int64_t tiles = (int64_t)ceil_div(M, kW4gTileM[cfg]) * ceil_div(N, kW4gTileN[cfg]);
+        // LDS-DMA W4A16 GEMM.  M <= 1024: the tile (64 x 128, 128 x 128, 128 x 256) and the
+        // K split (1, 2, 4, 8) with the shortest modelled time (w4g_model_plan).  Larger M
+        // (measured at K = 4096, N in {4096, 11008, 14336}): 64 x 128 while its tiles fit
+        // one wave of the CUs; 128 x 256 when those tiles give at least one per CU, in whole
+        // multiples of the CU count or 1.7 of them (M = 2048: 5-26% faster than 128 x 128;
+        // M = 1024, N = 11008, 1.34 tiles per CU: 4% slower); else 128 x 128.
+        int cfg, s = 1;
+        if (M <= kW4gModelMaxM) {
+            w4g_model_plan(M, N, K, num_cus, &cfg, &s);
+        } else {
+            const int64_t wide_tiles = (int64_t)ceil_div(M, 128) * ceil_div(N, 256);
+            const int64_t short_tiles = (int64_t)ceil_div(M, 64) * ceil_div(N, 128);
+            cfg = W4G_TILE_MID;
+            if (short_tiles <= num_cus)
+                cfg = W4G_TILE_SHORT;
+            else if (wide_tiles >= num_cus &&
+                     (wide_tiles % num_cus == 0 || 10 * wide_tiles >= 17 * (int64_t)num_cus))
+                cfg = W4G_TILE_WIDE;
+            // Split while the tiles do not give one per CU: num_cus / tiles ways, at most 8,
+            // never at K <= 1024.
+            const int64_t tiles = (int64_t)ceil_div(M, kW4gTileM[cfg]) * ceil_div(N, kW4gTileN[cfg]);
+            if (tiles < num_cus && K > 1024)
+                s = (int)std::min<int64_t>(std::max<int64_t>(num_cus / tiles, 1), 8);
+            s = std::max(1, std::min(s, KC / 4));
+        }
         pl.big = cfg;
-        // Split while the tiles do not give one per CU: num_cus / tiles ways (the partial
-        // sums cost a second pass over M x N fp32 per split), at most 8 (measured with
-        // 64 x 128 tiles at N = 4096: M = 48, 64 best with 8 ways; M = 96, 128 with 4; at
-        // N = 11008, 14336: M = 64 with 2, M = 128 unsplit).
-        // No split at K <= 1024: the partial sums and their reduction launch cost more
-        // than the idle CUs (measured: 128 x 4096 x 1024 11.5 -> 8.5 us unsplit, 256 x
-        // 4096 x 1024 12.4 -> 8.7, 1024 x 1024 x 1024 12.3 -> 8.7, 64 x 14336 x 1024
-        // 12.5 -> 9.0).
-        int s = 1;
-        const int max_split = 8;
-        if (tiles < num_cus && K > 1024)
-            s = (int)std::min<int64_t>(std::max<int64_t>(num_cus / tiles, 1), max_split);
-        s = std::max(1, std::min(s, KC / 4));
         const int kcps = ceil_div(KC, s);
         pl.kind = W4_GEMM;
         pl.split = ceil_div(KC, kcps);
