@@ -239,6 +239,8 @@ size_t wmma_w4a16_workspace_size(int M, int N, int K, int group_size);
 #define WMMA_W4_KERNEL_MFMA 3         /* other shapes: tiled MFMA kernel                     */
 #define WMMA_W4_KERNEL_SKINNY 4       /* 4 < M <= 32: 32/64 columns per workgroup, matrix pipe */
 #define WMMA_W4_KERNEL_GEMM 5         /* M > 32: LDS-DMA MFMA GEMM                           */
+#define WMMA_W4_KERNEL_ROWS 6         /* M > 32, short K: 16/32 rows x 32/64 columns per
+                                         workgroup over all of K, no LDS ring, no split    */
 
 typedef struct wmma_w4a16_plan {
     int kernel;             /* WMMA_W4_KERNEL_*                                           */
@@ -259,7 +261,7 @@ int wmma_w4a16_plan_make(int M, int N, int K, int group_size, int num_cus, wmma_
  * zeros_format.  G = group_size, G % 32 == 0, K % G == 0.  With WMMA_W4_FUSED, packed is
  * the output of wmma_int4_prepack_fused and scales / zeros are not read (may be NULL).
  * Arithmetic by path (wmma_w4a16_plan_make reports the path of a shape).  The tiled
- * kernels (WMMA_W4_KERNEL_SKINNY, _GEMM, _MFMA, _GEMV_SPLIT) and the decode kernel at
+ * kernels (WMMA_W4_KERNEL_SKINNY, _GEMM, _ROWS, _MFMA, _GEMV_SPLIT) and the decode kernel at
  * M = 3, 4 form each weight exactly as written above before its fp32-accumulated product.
  * Two decode paths form no per-weight fp16 value: WMMA_W4_KERNEL_DECODE_MFMA at M <= 2
  * and WMMA_W4_KERNEL_DECODE (M <= 4).  For each 128-deep (resp. 32-deep) K run inside a

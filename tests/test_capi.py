@@ -318,11 +318,20 @@ def test_w4a16_plan_make(lib):
     assert plan(16, 4096, 14336) == (4, 7, 2048, 7 * 16 * 4096 * 4)   # long K: split
     assert plan(32, 14336, 14336) == (4, 14, 1024, 14 * 32 * 14336 * 4)
     assert plan(128, 14336, 4096)[:2] == (5, 1)        # 224 tiles of 64x128: no split
-    assert plan(128, 4096, 4096)[:2] == (5, 4)         # 64 tiles: 256 / 64 ways
-    assert plan(64, 4096, 4096)[:2] == (5, 8)          # 32 tiles: 8 ways (the cap)
+    assert plan(96, 4096, 4096)[:2] == (5, 4)          # 64 tiles: 4 ways
+    assert plan(64, 4096, 8192)[:2] == (5, 8)          # 32 tiles: 8 ways (the cap)
     assert plan(64, 11008, 4096)[:2] == (5, 2)         # 86 tiles: 2 ways
-    assert plan(128, 4096, 1024)[:2] == (5, 1)         # K <= 1024: never a split
-    assert plan(1024, 1024, 1024)[:2] == (5, 1)
+    assert plan(1024, 1024, 1024)[:2] == (5, 1)        # K <= 1024: never a split
+    # the rows kernel: short K, few columns, no split
+    assert plan(128, 4096, 4096) == (6, 1, 4096, 0)
+    assert plan(64, 4096, 4096) == (6, 1, 4096, 0)
+    assert plan(128, 4096, 1024) == (6, 1, 1024, 0)
+    assert plan(512, 1024, 2048) == (6, 1, 2048, 0)
+    assert plan(33, 1024, 4096) == (6, 1, 4096, 0)
+    assert plan(64, 1024, 4096, 512) == (6, 1, 4096, 0)
+    assert plan(64, 1024, 4096, 64)[0] == 5            # ... for G = 128 * 2^j only
+    assert plan(128, 4096, 8192)[:2] == (5, 4)         # longer K: LDS-DMA tiles again
+    assert plan(2048, 1024, 1024)[:2] == (5, 1)        # M > 1024: the tile rules
     # skinny with 64-column workgroups (128 of them) and a 4-way K split
     assert plan(16, 8192, 8192) == (4, 4, 2048, 4 * 16 * 8192 * 4)
     assert plan(2048, 4096, 4096)[:2] == (5, 1)        # 512 tiles of 128x128, no split

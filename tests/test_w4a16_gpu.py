@@ -105,7 +105,7 @@ def test_w4a16_skinny(wo, M, K, N, G):
 # filled with NaN each time: every call bit-identical and within the oracle's bar.  (Its
 # ring once let a stage's DMA overwrite LDS rows another wave was still reading, which
 # showed as wrong 8-row groups in a few calls out of several.)
-@pytest.mark.parametrize("M,N,K", [(64, 4096, 4096), (128, 4096, 4096), (33, 14336, 4096),
+@pytest.mark.parametrize("M,N,K", [(64, 4096, 8192), (96, 4096, 4096), (33, 14336, 4096),
                                    (192, 4096, 8192), (128, 11008, 14336)])
 def test_w4a16_gemm_split_repeatable(wo, M, N, K):
     import ctypes
@@ -162,10 +162,10 @@ def test_w4a16_skinny_shapes(wo, M, K, N):
 # The M > 32 LDS-DMA kernel: the three tile configurations (64x128 up to 128 rows, 128x256
 # for grids of many such tiles -- M=4000, N=4128: 544, partial in M and N -- else 128x128),
 # partial M and N tiles, K shorter than the stage ring (K=192), K split (M=64, N=1024: few
-# tiles), G=32 (the two K halves of a chunk in different groups), lda > K, both zero
-# formats.
-@pytest.mark.parametrize("M,K,N,G", [(33, 1024, 4096, 128), (64, 2048, 1024, 64), (200, 192, 288, 32),
-                                     (512, 1024, 2048, 128), (600, 512, 288, 256),
+# tiles; M=33, N=14336), G=32 (the two K halves of a chunk in different groups), lda > K,
+# both zero formats.
+@pytest.mark.parametrize("M,K,N,G", [(33, 4096, 14336, 128), (64, 2048, 1024, 64), (200, 192, 288, 32),
+                                     (512, 1024, 2048, 128), (1100, 512, 288, 256),
                                      (1030, 2048, 1056, 128), (100, 768, 4128, 64),
                                      (4000, 512, 4128, 128)])
 def test_w4a16_gemm_tiles(wo, M, K, N, G):
@@ -184,6 +184,62 @@ def test_w4a16_gemm_tiles(wo, M, K, N, G):
     assert torch.isfinite(Yp).all()
     assert og.max_rel_err(Yp, ref) <= 1e-3
     assert torch.equal(Yp, Yu)
+
+
+def _w4a16_capi(lib, Ad, lda, pk, S, Z, zfmt, M, N, K, G, Y, half=False):
+    import ctypes
+    vp, i64, i32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
+    fn = lib.wmma_w4a16_gemm_f16out if half else lib.wmma_w4a16_gemm
+    fn.argtypes = [vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, vp, i64, vp, sz, vp]
+    lib.wmma_last_error.restype = ctypes.c_char_p
+    rc = fn(Ad.data_ptr(), lda, pk.data_ptr(), S.data_ptr(), Z.data_ptr(), zfmt, M, N, K, G,
+            Y.data_ptr(), N, None, 0, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.wmma_last_error()
+    return Y
+
+
+def _capi_lib():
+    import ctypes
+    return ctypes.CDLL(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                                    "wmma_ops_amd", "libwmma_ops_amd.so"))
+
+
+# The rows kernel (M > 32, short K, few columns) through the C-ABI: each of its workgroup
+# shapes -- 16 rows x 32 columns (M=40, 77, 50, 600), 16 x 64 (M=37), 32 x 64 (M=200,
+# 333) -- with the last row group partial, N a multiple of 32 but not 64 (N=288),
+# G = 128, 256, 512 (a pair-step's group found by a shift), lda > K, packed and byte zeros
+# and the slice-major parameters (identical bits), fp16 output (the fp32 result rounded
+# once), and repeated calls bit-identical.
+@pytest.mark.parametrize("M,K,N,G", [(40, 1024, 512, 128), (77, 2048, 1024, 128), (37, 2048, 4096, 128),
+                                     (200, 2048, 2048, 256), (333, 1024, 1024, 128),
+                                     (50, 4096, 2048, 512), (600, 512, 288, 256)])
+def test_w4a16_rows(wo, M, K, N, G):
+    plan = wo.w4a16_plan(M, N, K, G)
+    report("w4a16_rows", M=M, K=K, N=N, G=G, plan=plan)
+    assert plan[0] == 6 and plan[1] == 1 and plan[3] == 0
+    lib = _capi_lib()
+    A, q, s, z = oi.make_inputs(M, K, N, G, seed=5 * M + K + N + G)
+    ref = oi.w4a16_ref(A, q, s, z, G)
+    pk = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
+    sd = torch.from_numpy(s).cuda()
+    zp = torch.from_numpy(oi.pack_zeros(z)).cuda()
+    zu = torch.from_numpy(z).cuda()
+    ss, zs = wo.prepack_int4_params(sd, zp)
+    lda = K + 64
+    Abig = torch.zeros(M, lda, dtype=torch.half)
+    Abig[:, :K] = A
+    Ad = Abig.cuda()
+    outs = [_w4a16_capi(lib, Ad, lda, pk, S, Z, f, M, N, K, G, torch.full((M, N), float("nan"), device="cuda"))
+            for S, Z, f in ((sd, zp, 0), (sd, zu, 1), (ss, zs, 2), (sd, zp, 0))]
+    Yh = _w4a16_capi(lib, Ad, lda, pk, sd, zp, 0, M, N, K, G,
+                     torch.full((M, N), float("nan"), dtype=torch.half, device="cuda"), half=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(outs[0]).all()
+    assert og.max_rel_err(outs[0], ref) <= 1e-3
+    for Y in outs[1:]:
+        assert torch.equal(Y, outs[0])
+    assert torch.equal(Yh, outs[0].half())
+    assert torch.equal(wo.matmul_int4(A.cuda(), pk, sd, zp, G), outs[0])
 
 
 # The M <= 2 decode kernel applies s and z to each 128-deep partial sum: the MFMA sees the

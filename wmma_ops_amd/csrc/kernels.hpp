@@ -80,13 +80,15 @@ enum W4A16Kind {
     W4_MFMA = 3,         // larger M: tiled MFMA kernel, K split + reduce when few tiles
     W4_SKINNY = 4,       // 4 < M <= 32: 32 columns per workgroup, K split + reduce when few tiles
     W4_GEMM = 5,         // M > 32: LDS-DMA MFMA GEMM, K split + reduce when few tiles
+    W4_ROWS = 6,         // M > 32: row groups x column groups, register-staged, no LDS ring
 };
 
 struct W4A16Plan {
     int kind;         // W4A16Kind
     int split;        // K partitions (1: no workspace)
     int k_per_split;  // multiple of 64 (and of G when split > 1)
-    int big = 0;      // W4_GEMM: tile (W4G_TILE_*); W4_SKINNY: 16-column slices per workgroup
+    int big = 0;      // W4_GEMM: tile (W4G_TILE_*); W4_SKINNY, W4_ROWS: 16-column slices per workgroup
+    int mb = 0;       // W4_ROWS: 16-row blocks per workgroup
 };
 
 struct W4A16Launch {

@@ -1222,6 +1222,179 @@ void launch_skinny_mb(const W4Args& a, int U, dim3 grid, hipStream_t stream) {
         hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, 1, NH>), grid, block, 0, stream, a);
 }
 
+// ------------------------------------------ rows (M > 32) on the matrix pipe, no LDS ring --
+// The skinny kernel's structure extended to any M: a workgroup covers 16*MB rows (row
+// group blockIdx.z) by 16*NH columns over its whole K range (or one split of it), eight
+// waves taking interleaved 128-deep pair-steps (wave w: pair-steps kb + w + 8r).  Each wave
+// loads its activations straight from L2 into registers in the MFMA A-operand layout and
+// its weights, scales and zeros into registers, one round (one pair-step) ahead of the
+// round it computes, so no barrier sits anywhere before the final cross-wave sum and no
+// wave waits for another's loads.  A workgroup reads 32*MB + 8*NH bytes of activations and
+// weights per K value; the weights of a column group are shared through L2 by the row
+// groups (blockIdx.x is the column group, so with a grid width divisible by eight every
+// row group of a column group runs on one XCD).
+// Loads of rounds past the wave's last go to an out-of-range buffer offset and return
+// zeros without a memory request, so the loop body stays straight-line.
+// B operand: the skinny kernel's W = fp16((q - z) s), one rounding.  D layout per block b,
+// slice sc: lane l holds column 16*NH*wg + 16*sc + l%16, rows 16*MB*z + 16*b + 4*(l/16) + r.
+constexpr int RW_NW = 8;
+
+template <int MB, int NH>
+struct RowsRound {
+    u32x4 a[MB][4];
+    u32x4 w[NH];
+    uint32_t s[NH], z[NH];
+};
+
+template <int ZF, int MB, int NH>
+__global__ void __launch_bounds__(RW_NW * kWave)
+w4a16_rows_kernel(W4Args p) {
+    constexpr int NC = 16 * NH, MR = 16 * MB;
+    __shared__ float red[RW_NW][MR][NC + 1];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wg = xcd_remap(blockIdx.x, gridDim.x);
+    const int n0 = NC * wg, m0 = MR * blockIdx.z;
+    const int col = lane & 15, sub = lane >> 4, dc = sub >> 1, h = sub & 1;
+    const int M = p.M, KC = p.K / 64, KP = KC / 2;
+    const int kpps = p.kc_per_split >> 1;
+    const int kb = blockIdx.y * kpps, ke = min(KP, kb + kpps);
+    const int rounds = max(0, (ke - kb - wave + RW_NW - 1) / RW_NW);
+
+    // The activation resource starts at the workgroup's first row; its 16*MB rows span under
+    // 2 GB because the C-ABI rejects min(M, 256) * lda * 2 bytes above that, and M > 32 here.
+    // Rows past M read row M-1 and are never stored.
+    const __amdgpu_buffer_rsrc_t ar = make_rsrc(p.A + (int64_t)m0 * p.lda), wr = make_rsrc(p.W),
+                                 sr = make_rsrc(p.S), zr = make_rsrc(p.Z);
+    uint32_t aoff[MB];
+#pragma unroll
+    for (int b = 0; b < MB; ++b)
+        aoff[b] = (uint32_t)(((int64_t)(min(m0 + 16 * b + col, M - 1) - m0) * p.lda + 32 * sub) * 2);
+    const uint32_t woff = (uint32_t)(pk_index(n0 + col, 0, h, KC) * 16) + 512u * dc;
+    // Byte offsets of this lane's scale and zero element: lane part + sc * (slice step) +
+    // g * (group step), per zeros format.
+    uint32_t s_lane, s_sc, s_g, z_lane, z_sc, z_g;
+    if constexpr (ZF == WMMA_ZEROS_SLICED) {
+        s_lane = (uint32_t)(((int64_t)(n0 >> 4) * p.kg * 16 + col) * 2);
+        s_sc = (uint32_t)p.kg * 32u;
+        s_g = 32u;
+        z_lane = (uint32_t)(((int64_t)(n0 >> 4) * p.kg * 2 + ((col >> 3) & 1)) * 4);
+        z_sc = (uint32_t)p.kg * 8u;
+        z_g = 8u;
+    } else {
+        s_lane = (uint32_t)(n0 + col) * 2u;
+        s_sc = 32u;
+        s_g = (uint32_t)p.N * 2u;
+        if constexpr (ZF == WMMA_ZEROS_PACKED) {
+            z_lane = (uint32_t)((n0 + col) >> 3) * 4u;
+            z_sc = 8u;
+            z_g = (uint32_t)p.N / 2u;
+        } else {
+            z_lane = (uint32_t)(n0 + col);
+            z_sc = 16u;
+            z_g = (uint32_t)p.N;
+        }
+    }
+    auto load = [&](int r, RowsRound<MB, NH>& R) {
+        const int pp = kb + wave + RW_NW * r;
+        const uint32_t oob = r < rounds ? 0u : kOobOffset;
+        const uint32_t g = (uint32_t)(min(pp, KP - 1) >> p.pp_shift);  // G = 128 << pp_shift
+#pragma unroll
+        for (int sc = 0; sc < NH; ++sc) {
+            R.s[sc] = buf_load2(sr, (s_lane + sc * s_sc + g * s_g) | oob);
+            if constexpr (ZF != WMMA_ZEROS_U8)
+                R.z[sc] = buf_load4(zr, (z_lane + sc * z_sc + g * z_g) | oob);
+            else
+                R.z[sc] = buf_load1(zr, (z_lane + sc * z_sc + g * z_g) | oob);
+        }
+#pragma unroll
+        for (int b = 0; b < MB; ++b)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                R.a[b][q] = buf_load16(ar, (aoff[b] + 256u * pp + 16u * q) | oob);
+#pragma unroll
+        for (int sc = 0; sc < NH; ++sc)
+            R.w[sc] = buf_load16_nt(wr, (woff + (uint32_t)sc * KC * 512u + 1024u * pp) | oob);
+    };
+
+    uint32_t magic = 0x64006400u, magic_hi = 0x54005400u;
+    asm volatile("" : "+v"(magic), "+v"(magic_hi));
+    f32x4 d[MB][NH];
+#pragma unroll
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int sc = 0; sc < NH; ++sc) d[b][sc] = f32x4{};
+    auto compute = [&](const RowsRound<MB, NH>& R) {
+#pragma unroll
+        for (int sc = 0; sc < NH; ++sc) {
+            uint32_t z;
+            if constexpr (ZF != WMMA_ZEROS_U8)
+                z = (R.z[sc] >> (4 * ((n0 + 16 * sc + col) & 7))) & 0xFu;
+            else
+                z = R.z[sc] & 0xFu;
+            const uint32_t s = R.s[sc];
+            const uint32_t z1 = 0x6400u | z, zhi = 0x5400u | (z << 4);
+            const f16x2 zs1 = as_h2(z1 | (z1 << 16)), zshi = as_h2(zhi | (zhi << 16));
+            const f16x2 ss = as_h2(s | (s << 16));
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t x = R.w[sc][q], x8 = x >> 8;
+                u32x4 bv;
+                bv[0] = as_u32((as_h2((x & 0x000F000Fu) | magic) - zs1) * ss);
+                bv[1] = as_u32((as_h2((x & 0x00F000F0u) | magic_hi) - zshi) * ss);
+                bv[2] = as_u32((as_h2((x8 & 0x000F000Fu) | magic) - zs1) * ss);
+                bv[3] = as_u32((as_h2((x8 & 0x00F000F0u) | magic_hi) - zshi) * ss);
+#pragma unroll
+                for (int b = 0; b < MB; ++b) d[b][sc] = mfma16(as_f16x8(R.a[b][q]), as_f16x8(bv), d[b][sc]);
+            }
+        }
+    };
+
+    RowsRound<MB, NH> R0, R1;
+    load(0, R0);
+    __builtin_amdgcn_sched_barrier(0);
+    load(1, R1);
+    __builtin_amdgcn_sched_barrier(0);
+    // A round past the last (odd round counts) computes on zeros and adds nothing.  The
+    // scheduling barriers keep each round's loads where they are written: issued right
+    // after the round that frees their registers, a full round ahead of their use.
+    for (int r = 0; r < rounds; r += 2) {
+        compute(R0);
+        __builtin_amdgcn_sched_barrier(0);
+        load(r + 2, R0);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(R1);
+        __builtin_amdgcn_sched_barrier(0);
+        load(r + 3, R1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int sc = 0; sc < NH; ++sc)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[wave][16 * b + 4 * sub + r][16 * sc + col] = d[b][sc][r];
+    __syncthreads();
+    const bool partial = gridDim.y > 1;
+    const int mrows = min(MR, M - m0);
+    for (int i = tid; i < mrows * NC; i += RW_NW * kWave) {
+        const int m = i / NC, c = i % NC;
+        float acc = red[0][m][c];
+#pragma unroll
+        for (int w = 1; w < RW_NW; ++w) acc += red[w][m][c];
+        const int n = n0 + c;
+        if (partial)
+            p.ws[((int64_t)blockIdx.y * M + m0 + m) * p.N + n] = acc;
+        else
+            store_y(p, (int64_t)(m0 + m) * p.ldy + n, acc);
+    }
+}
+
+template <int ZF, int MB, int NH>
+void launch_rows(const W4Args& a, dim3 grid, hipStream_t stream) {
+    hipLaunchKernelGGL((w4a16_rows_kernel<ZF, MB, NH>), grid, dim3(RW_NW * kWave), 0, stream, a);
+}
+
 // ------------------------------------------------------ W4A16 GEMM (M > 32), LDS-DMA --
 // Output tile BM x BN per workgroup, WM x WN waves, wave tile TM x TN = FM x FN MFMA
 // 32x32x16 tiles.  K advances in 64-deep stages (one prepacked block row):
@@ -1846,12 +2019,35 @@ bool w4a16_fused_decode_ok(int M, int K) {
 constexpr int kW4gModelMaxM = 1024;
 constexpr double kW4gKbPerUs[3] = {40, 35, 35};      // per tile config (W4G_TILE_*)
 constexpr double kW4gMflopPerUs[3] = {4, 4, 3};
+// The rows kernel (W4_ROWS) in the same model: a workgroup of 16*mb rows x 16*nh columns
+// reads its activation rows and int4 columns over all of K at kRowsKbPerUs, plus a fixed
+// cost per configuration (the final cross-wave sum grows with the tile), per wave of
+// workgroups; no split.  Fitted the same way, on 208 shapes (M = 33-1024, N = 512-14336,
+// K = 1024-8192; each configuration below and the LDS-DMA plan timed in one process): the
+// model's choices take 0.2% more time than the fastest of them per shape, against 9.5% for
+// the LDS-DMA plans alone; each K value held out in turn, the constants fitted on the
+// others choose within 0-2.5% of the fastest on it.  It takes the rows kernel at short K
+// and few columns (K = 2048, N = 1024, M = 33-256: 4.9-6.5 us against 8.0-10.4) and the
+// LDS-DMA tiles elsewhere.
+constexpr double kRowsKbPerUs = 40;
+constexpr int kRowsCfg[3][2] = {{1, 2}, {1, 4}, {2, 4}};  // {mb, nh}
+constexpr double kRowsWgFixedUs[3] = {0.75, 1.5, 3.0};
 
-void w4g_model_plan(int M, int N, int K, int num_cus, int* cfg_out, int* split_out) {
+// Shapes the rows kernel takes: whole 128-deep pair-steps inside one group, and weights
+// addressable with 32-bit byte offsets.
+bool rows_shape_ok(int N, int K, int G) {
+    return K % 128 == 0 && G % 128 == 0 && ((G / 128) & (G / 128 - 1)) == 0 &&
+           (int64_t)N * K < ((int64_t)1 << 32);
+}
+
+// Tile config and split of the LDS-DMA GEMM, or (rows_mb > 0) the rows kernel's shape.
+void w4g_model_plan(int M, int N, int K, int G, int num_cus, int* cfg_out, int* split_out,
+                    int* rows_mb, int* rows_nh) {
     const int KC = K / 64;
     double best_t = 1e300;
     *cfg_out = W4G_TILE_SHORT;
     *split_out = 1;
+    *rows_mb = *rows_nh = 0;
     for (int cfg : {W4G_TILE_SHORT, W4G_TILE_MID, W4G_TILE_WIDE}) {
         const int bm = kW4gTileM[cfg], bn = kW4gTileN[cfg];
         for (int sp : {1, 2, 4, 8}) {
@@ -1869,6 +2065,20 @@ void w4g_model_plan(int M, int N, int K, int num_cus, int* cfg_out, int* split_o
                 *cfg_out = cfg;
                 *split_out = sp;
             }
+        }
+    }
+    if (!rows_shape_ok(N, K, G)) return;
+    for (int c = 0; c < 3; ++c) {
+        const int mb = kRowsCfg[c][0], nh = kRowsCfg[c][1];
+        if (N % (16 * nh) != 0) continue;
+        const int64_t wgs = (int64_t)(N / (16 * nh)) * ceil_div(M, 16 * mb);
+        const double kb = (std::min(M, 16 * mb) * 2.0 + 8.0 * nh) * K / 1000.0;
+        const double t =
+            (double)((wgs + num_cus - 1) / num_cus) * (kRowsWgFixedUs[c] + kb / kRowsKbPerUs);
+        if (t < best_t * 0.999) {
+            best_t = t;
+            *rows_mb = mb;
+            *rows_nh = nh;
         }
     }
 }
@@ -1906,6 +2116,8 @@ bool w4a16_narrow_skinny(int M, int N, int K, int num_cus) {
 //                tiles alone give under half a workgroup per CU.
 //   gemm         M > 32 with G a power of two: LDS-DMA MFMA GEMM (tile below), K split
 //                (plus a reduce pass) only when the tiles cannot fill the chip.
+//   rows         32 < M <= 1024 with G = 128 * 2^j where the launch model prefers it to
+//                every LDS-DMA plan (short K, few columns): no ring, no split.
 //   mfma         everything else (the shapes the kernels above do not take).
 W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
     if (num_cus <= 0) num_cus = 256;
@@ -1943,7 +2155,15 @@ W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
         // M = 1024, N = 11008, 1.34 tiles per CU: 4% slower); else 128 x 128.
         int cfg, s = 1;
         if (M <= kW4gModelMaxM) {
-            w4g_model_plan(M, N, K, num_cus, &cfg, &s);
+            int mb, nh;
+            w4g_model_plan(M, N, K, G, num_cus, &cfg, &s, &mb, &nh);
+            if (mb > 0) {
+                pl.kind = W4_ROWS;
+                pl.mb = mb;
+                pl.big = nh;
+                pl.k_per_split = K;
+                return pl;
+            }
         } else {
             const int64_t wide_tiles = (int64_t)ceil_div(M, 128) * ceil_div(N, 256);
             const int64_t short_tiles = (int64_t)ceil_div(M, 64) * ceil_div(N, 128);
@@ -2028,6 +2248,14 @@ hipError_t launch_w4a16_zf(const W4Args& a, const W4A16Launch& w, hipStream_t st
         const int bm = kW4gTileM[pl.big], bn = kW4gTileN[pl.big];
         const dim3 grid(ceil_div(w.M, bm) * ceil_div(w.N, bn), pl.split);
         launch_w4g<ZF>(a, pl.big, grid, stream);
+    } else if (pl.kind == W4_ROWS) {
+        const dim3 grid(w.N / (16 * pl.big), 1, ceil_div(w.M, 16 * pl.mb));
+        if (pl.mb == 1 && pl.big == 2)
+            launch_rows<ZF, 1, 2>(a, grid, stream);
+        else if (pl.mb == 1)
+            launch_rows<ZF, 1, 4>(a, grid, stream);
+        else
+            launch_rows<ZF, 2, 4>(a, grid, stream);
     } else if (pl.kind == W4_SKINNY) {
         const int U = pl.k_per_split / (SK_NW * 128);
         const dim3 grid(w.N / (16 * pl.big), pl.split);
