@@ -42,20 +42,30 @@ def test_prepack_unpack_bit_exact(wo, K, N):
     assert torch.equal(wo.unprepack_int4(pk), qd)
 
 
-# M in {1,16,128,2048}, K=4096, N in {4096, 14336}, G=128, seed 42 + 3
+# M in {1,16,128,2048}, K=4096, N in {4096, 14336}, G=128, seed 42 + 3; also in
+# the layout bench.py times there (M <= 4: the fused decode layout; otherwise the
+# slice-major parameters, bit-identical to the standard ones)
 @pytest.mark.parametrize("N", [4096, 14336])
 @pytest.mark.parametrize("M", [1, 16, 128, 2048])
 def test_w4a16_baseline(wo, M, N):
     K, G = 4096, 128
-    report("w4a16", M=M, N=N, K=K, G=G)
+    report("w4a16", M=M, N=N, K=K, G=G, plan=wo.w4a16_plan(M, N, K, G))
     A, q, s, z = oi.make_inputs(M, K, N, G, seed=42 + 3)
     ref = oi.w4a16_ref(A, q, s, z, G)
-    pk = wo.prepack_int4(torch.from_numpy(oi.pack_gptq(q)).cuda())
-    Y = wo.matmul_int4(A.cuda(), pk, torch.from_numpy(s).cuda(),
-                       torch.from_numpy(oi.pack_zeros(z)).cuda(), G)
+    qd = torch.from_numpy(oi.pack_gptq(q)).cuda()
+    pk = wo.prepack_int4(qd)
+    sd, zd, Ad = torch.from_numpy(s).cuda(), torch.from_numpy(oi.pack_zeros(z)).cuda(), A.cuda()
+    Y = wo.matmul_int4(Ad, pk, sd, zd, G)
     assert torch.isfinite(Y).all()
     err = og.max_rel_err(Y, ref)
     assert err <= 1e-3, err
+    if M <= 4:
+        Yb = wo.matmul_int4_fused(Ad, wo.prepack_int4_fused(qd, sd, zd, G), G)
+        assert torch.isfinite(Yb).all()
+        assert og.max_rel_err(Yb, ref) <= 1e-3
+    else:
+        Yb = wo.matmul_int4(Ad, pk, *wo.prepack_int4_params(sd, zd), G)
+        assert torch.equal(Yb, Y)
 
 
 @pytest.mark.parametrize("M,K,N,G", [(1, 256, 64, 32), (3, 512, 96, 64), (5, 1024, 128, 256),
