@@ -318,8 +318,8 @@ def test_w4a16_plan_make(lib):
     assert plan(16, 4096, 14336) == (4, 7, 2048, 7 * 16 * 4096 * 4)   # long K: split
     assert plan(32, 14336, 14336) == (4, 14, 1024, 14 * 32 * 14336 * 4)
     assert plan(128, 14336, 4096)[:2] == (5, 1)        # 224 tiles of 64x128: no split
-    assert plan(96, 4096, 4096)[:2] == (5, 4)          # 64 tiles: 4 ways
-    assert plan(64, 4096, 8192)[:2] == (5, 8)          # 32 tiles: 8 ways (the cap)
+    assert plan(256, 4096, 4096)[:2] == (5, 2)         # 128 tiles: 2 ways
+    assert plan(48, 4096, 8192)[:2] == (5, 8)          # 32 tiles: 8 ways (the cap)
     assert plan(64, 11008, 4096)[:2] == (5, 2)         # 86 tiles: 2 ways
     assert plan(1024, 1024, 1024)[:2] == (5, 1)        # K <= 1024: never a split
     # the rows kernel: short K, few columns, no split

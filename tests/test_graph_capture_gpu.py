@@ -74,9 +74,10 @@ def test_graph_gemm_epilogue(wo, M, N, K):
     _replays_match(lambda: wo.gemm(A, B, 2.0, 0.5, C))
 
 
-# W4A16 at configs[3] K: decode (M = 1, 2), skinny (16), tiled with a K split (96 at
-# N = 4096; 300 at N = 1024), the rows kernel (128 at N = 4096)
-@pytest.mark.parametrize("M,N", [(1, 4096), (2, 1024), (16, 4096), (96, 4096), (128, 4096), (300, 1024)])
+# W4A16 at configs[3] K: decode (M = 1, 2), skinny (16), tiled with a K split (256 at
+# N = 4096), without (300), the rows kernel (128 at N = 4096, 300 at N = 1024)
+@pytest.mark.parametrize("M,N", [(1, 4096), (2, 1024), (16, 4096), (256, 4096), (300, 4096), (128, 4096),
+                                 (300, 1024)])
 def test_graph_matmul_int4(wo, M, N):
     K, G = 4096, 128
     report("graph_w4a16", M=M, N=N, K=K, plan=wo.w4a16_plan(M, N, K, G))

@@ -115,7 +115,7 @@ def test_w4a16_skinny(wo, M, K, N, G):
 # filled with NaN each time: every call bit-identical and within the oracle's bar.  (Its
 # ring once let a stage's DMA overwrite LDS rows another wave was still reading, which
 # showed as wrong 8-row groups in a few calls out of several.)
-@pytest.mark.parametrize("M,N,K", [(64, 4096, 8192), (96, 4096, 4096), (33, 14336, 4096),
+@pytest.mark.parametrize("M,N,K", [(48, 4096, 8192), (256, 4096, 4096), (33, 14336, 4096),
                                    (192, 4096, 8192), (128, 11008, 14336)])
 def test_w4a16_gemm_split_repeatable(wo, M, N, K):
     import ctypes

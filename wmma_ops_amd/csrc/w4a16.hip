@@ -1226,10 +1226,15 @@ void launch_skinny_mb(const W4Args& a, int U, dim3 grid, hipStream_t stream) {
 // The skinny kernel's structure extended to any M: a workgroup covers 16*MB rows (row
 // group blockIdx.z) by 16*NH columns over its whole K range (or one split of it), eight
 // waves taking interleaved 128-deep pair-steps (wave w: pair-steps kb + w + 8r).  Each wave
-// loads its activations straight from L2 into registers in the MFMA A-operand layout and
-// its weights, scales and zeros into registers, one round (one pair-step) ahead of the
-// round it computes, so no barrier sits anywhere before the final cross-wave sum and no
-// wave waits for another's loads.  A workgroup reads 32*MB + 8*NH bytes of activations and
+// loads its activations straight from L2 into registers in the MFMA A-operand layout, and
+// its weights, scales and zeros into registers: the weights (from HBM) one round (one
+// pair-step) ahead of the round that uses them, the activations, scales and zeros at the
+// start of their own round.  No barrier sits anywhere before the final cross-wave sum and
+// no wave waits for another's loads.  Fewer bytes in flight per CU run faster here: measured
+// on MI355X over 54 shape x configuration cases (M = 33-128, N = 1024 / 4096, K = 2048-8192),
+// this schedule took 10% less time than loading the whole next round ahead, which took 16%
+// less than loading two rounds ahead; the weights go through the cache (streaming them
+// past it was 3% slower).  A workgroup reads 32*MB + 8*NH bytes of activations and
 // weights per K value; the weights of a column group are shared through L2 by the row
 // groups (blockIdx.x is the column group, so with a grid width divisible by eight every
 // row group of a column group runs on one XCD).
@@ -1295,7 +1300,8 @@ w4a16_rows_kernel(W4Args p) {
             z_g = (uint32_t)p.N;
         }
     }
-    auto load = [&](int r, RowsRound<MB, NH>& R) {
+    // Round r's scales, zeros and activations, and (load_w) its weights.
+    auto load_ap = [&](int r, RowsRound<MB, NH>& R) {
         const int pp = kb + wave + RW_NW * r;
         const uint32_t oob = r < rounds ? 0u : kOobOffset;
         const uint32_t g = (uint32_t)(min(pp, KP - 1) >> p.pp_shift);  // G = 128 << pp_shift
@@ -1312,9 +1318,13 @@ w4a16_rows_kernel(W4Args p) {
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 R.a[b][q] = buf_load16(ar, (aoff[b] + 256u * pp + 16u * q) | oob);
+    };
+    auto load_w = [&](int r, RowsRound<MB, NH>& R) {
+        const int pp = kb + wave + RW_NW * r;
+        const uint32_t oob = r < rounds ? 0u : kOobOffset;
 #pragma unroll
         for (int sc = 0; sc < NH; ++sc)
-            R.w[sc] = buf_load16_nt(wr, (woff + (uint32_t)sc * KC * 512u + 1024u * pp) | oob);
+            R.w[sc] = buf_load16(wr, (woff + (uint32_t)sc * KC * 512u + 1024u * pp) | oob);
     };
 
     uint32_t magic = 0x64006400u, magic_hi = 0x54005400u;
@@ -1350,22 +1360,25 @@ w4a16_rows_kernel(W4Args p) {
         }
     };
 
-    RowsRound<MB, NH> R0, R1;
-    load(0, R0);
+    // Two register sets, rounds alternating between them.  A round past the last (odd round
+    // counts) computes on zeros and adds nothing.  The scheduling barriers keep each load
+    // where it is written (without them the compiler sinks loads behind the MFMAs that
+    // follow).
+    RowsRound<MB, NH> RA, RB;
+    load_w(0, RA);
     __builtin_amdgcn_sched_barrier(0);
-    load(1, R1);
-    __builtin_amdgcn_sched_barrier(0);
-    // A round past the last (odd round counts) computes on zeros and adds nothing.  The
-    // scheduling barriers keep each round's loads where they are written: issued right
-    // after the round that frees their registers, a full round ahead of their use.
     for (int r = 0; r < rounds; r += 2) {
-        compute(R0);
+        load_ap(r, RA);
         __builtin_amdgcn_sched_barrier(0);
-        load(r + 2, R0);
+        load_w(r + 1, RB);
         __builtin_amdgcn_sched_barrier(0);
-        compute(R1);
+        compute(RA);
         __builtin_amdgcn_sched_barrier(0);
-        load(r + 3, R1);
+        load_ap(r + 1, RB);
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(r + 2, RA);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(RB);
         __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
@@ -2022,16 +2035,16 @@ constexpr double kW4gMflopPerUs[3] = {4, 4, 3};
 // The rows kernel (W4_ROWS) in the same model: a workgroup of 16*mb rows x 16*nh columns
 // reads its activation rows and int4 columns over all of K at kRowsKbPerUs, plus a fixed
 // cost per configuration (the final cross-wave sum grows with the tile), per wave of
-// workgroups; no split.  Fitted the same way, on 208 shapes (M = 33-1024, N = 512-14336,
+// workgroups; no split.  Fitted the same way, on 189 shapes (M = 33-1024, N = 512-14336,
 // K = 1024-8192; each configuration below and the LDS-DMA plan timed in one process): the
-// model's choices take 0.2% more time than the fastest of them per shape, against 9.5% for
+// model's choices take 0.1% more time than the fastest of them per shape, against 13.3% for
 // the LDS-DMA plans alone; each K value held out in turn, the constants fitted on the
-// others choose within 0-2.5% of the fastest on it.  It takes the rows kernel at short K
-// and few columns (K = 2048, N = 1024, M = 33-256: 4.9-6.5 us against 8.0-10.4) and the
+// others choose within 0-4% of the fastest on it.  It takes the rows kernel at short K and
+// few columns (K = 2048, N = 1024, M = 33-256: 4.6-5.6 us against 7.9-10.4) and the
 // LDS-DMA tiles elsewhere.
-constexpr double kRowsKbPerUs = 40;
+constexpr double kRowsKbPerUs = 45;
 constexpr int kRowsCfg[3][2] = {{1, 2}, {1, 4}, {2, 4}};  // {mb, nh}
-constexpr double kRowsWgFixedUs[3] = {0.75, 1.5, 3.0};
+constexpr double kRowsWgFixedUs[3] = {0.75, 1.0, 2.0};
 
 // Shapes the rows kernel takes: whole 128-deep pair-steps inside one group, and weights
 // addressable with 32-bit byte offsets.
