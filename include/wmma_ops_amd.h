@@ -239,8 +239,9 @@ size_t wmma_w4a16_workspace_size(int M, int N, int K, int group_size);
 #define WMMA_W4_KERNEL_MFMA 3         /* other shapes: tiled MFMA kernel                     */
 #define WMMA_W4_KERNEL_SKINNY 4       /* 4 < M <= 32: 32/64 columns per workgroup, matrix pipe */
 #define WMMA_W4_KERNEL_GEMM 5         /* M > 32: LDS-DMA MFMA GEMM                           */
-#define WMMA_W4_KERNEL_ROWS 6         /* M > 32, short K: 16/32 rows x 32/64 columns per
-                                         workgroup over all of K, no LDS ring, no split    */
+#define WMMA_W4_KERNEL_ROWS 6         /* M > 4, short K or wide N: 16/32 rows x 16-64
+                                         columns per workgroup over all of K, no LDS ring,
+                                         no split                                          */
 
 typedef struct wmma_w4a16_plan {
     int kernel;             /* WMMA_W4_KERNEL_*                                           */

@@ -316,7 +316,9 @@ def test_w4a16_plan_make(lib):
     assert plan(16, 1024, 4096) == (4, 1, 4096, 0)     # 64 of them: still no split
     assert plan(5, 256, 2048) == (4, 1, 2048, 0)       # K <= 2048: never a split
     assert plan(16, 4096, 14336) == (4, 7, 2048, 7 * 16 * 4096 * 4)   # long K: split
-    assert plan(32, 14336, 14336) == (4, 14, 1024, 14 * 32 * 14336 * 4)
+    assert plan(32, 4096, 14336) == (4, 7, 2048, 7 * 32 * 4096 * 4)
+    assert plan(32, 1024, 2048) == (6, 1, 2048, 0)     # the rows kernel beats it at short K
+    assert plan(17, 14336, 8192) == (6, 1, 8192, 0)    # ... and at wide N
     assert plan(128, 14336, 4096)[:2] == (5, 1)        # 224 tiles of 64x128: no split
     assert plan(256, 4096, 4096)[:2] == (5, 2)         # 128 tiles: 2 ways
     assert plan(48, 4096, 8192)[:2] == (5, 8)          # 32 tiles: 8 ways (the cap)
@@ -336,7 +338,7 @@ def test_w4a16_plan_make(lib):
     assert plan(16, 8192, 8192) == (4, 4, 2048, 4 * 16 * 8192 * 4)
     assert plan(2048, 4096, 4096)[:2] == (5, 1)        # 512 tiles of 128x128, no split
     assert plan(1024, 14336, 4096)[:2] == (5, 1)       # 448 tiles of 128x256
-    assert plan(32, 14336, 4096)[0] == 4
+    assert plan(32, 14336, 2048)[0] == 4
     assert plan(33, 14336, 4096)[0] == 5               # LDS-DMA GEMM beyond 32 rows ...
     assert plan(64, 4096, 4608, 384)[0] == 3           # ... for group sizes 2^j only
     assert plan(2048, 14336, 4096)[:2] == (5, 1)

@@ -94,8 +94,8 @@ def test_w4a16_group_sizes_and_u8_zeros(wo, M, K, N, G):
 def test_w4a16_skinny(wo, M, K, N, G):
     plan = wo.w4a16_plan(M, N, K, G)
     report("w4a16_skinny", M=M, K=K, N=N, G=G, plan=plan)
-    assert plan[0] == 4
-    if N == 8192 and M <= 16:
+    assert plan[0] in (4, 6)  # the skinny kernel, or the rows kernel where the model prefers it
+    if N == 8192 and M <= 16 and plan[0] == 4:
         assert plan[1] == 4
     A, q, s, z = oi.make_inputs(M, K, N, G, seed=7 * M + K + N)
     ref = oi.w4a16_ref(A, q, s, z, G)

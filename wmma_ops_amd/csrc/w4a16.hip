@@ -1222,7 +1222,7 @@ void launch_skinny_mb(const W4Args& a, int U, dim3 grid, hipStream_t stream) {
         hipLaunchKernelGGL((w4a16_skinny_kernel<ZF, MB, 1, NH>), grid, block, 0, stream, a);
 }
 
-// ------------------------------------------ rows (M > 32) on the matrix pipe, no LDS ring --
+// --------------------------------------------- rows (M > 4) on the matrix pipe, no LDS ring --
 // The skinny kernel's structure extended to any M: a workgroup covers 16*MB rows (row
 // group blockIdx.z) by 16*NH columns over its whole K range (or one split of it), eight
 // waves taking interleaved 128-deep pair-steps (wave w: pair-steps kb + w + 8r).  Each wave
@@ -1266,9 +1266,9 @@ w4a16_rows_kernel(W4Args p) {
     const int kb = blockIdx.y * kpps, ke = min(KP, kb + kpps);
     const int rounds = max(0, (ke - kb - wave + RW_NW - 1) / RW_NW);
 
-    // The activation resource starts at the workgroup's first row; its 16*MB rows span under
-    // 2 GB because the C-ABI rejects min(M, 256) * lda * 2 bytes above that, and M > 32 here.
-    // Rows past M read row M-1 and are never stored.
+    // The activation resource starts at the workgroup's first row; the rows it reads span at
+    // most min(M, 16*MB) * lda * 2 bytes, which the C-ABI keeps under 2 GB (it rejects
+    // min(M, 256) * lda * 2 bytes above that).  Rows past M read row M-1 and are never stored.
     const __amdgpu_buffer_rsrc_t ar = make_rsrc(p.A + (int64_t)m0 * p.lda), wr = make_rsrc(p.W),
                                  sr = make_rsrc(p.S), zr = make_rsrc(p.Z);
     uint32_t aoff[MB];
@@ -2096,6 +2096,47 @@ void w4g_model_plan(int M, int N, int K, int G, int num_cus, int* cfg_out, int* 
     }
 }
 
+// 4 < M <= 32: the skinny kernel's plan (skinny_config) against the rows kernel, both in
+// the units of the model above.  The skinny launch: slices x K splits workgroups, each
+// reading its rows' activations and its columns' int4 weights over its K range at
+// kW4SkKbPerUs plus kW4SkWgFixedUs, per wave of workgroups, plus kW4SkSplitUs and
+// kW4SkPartialUsPerMB per MB of partial sums with a split.  The rows kernel here also has
+// a 16 x 16 configuration.  Fitted on 120 shapes (M = 5-32, N = 1024-14336,
+// K = 2048-14336; the skinny plan and four rows configurations timed in one process): the
+// model's choices take 0.4% more time than the fastest per shape, against 6.3% for the
+// skinny plans alone (M = 32, K = 2048, N = 1024-2048: 4.4 us against 6.3-6.4; M = 32,
+// N = K = 4096: 7.3 against 9.4; M = 5-16 keep the skinny kernel except at long K and wide
+// N).
+constexpr double kW4SkKbPerUs = 60, kW4SkWgFixedUs = 0.25, kW4SkSplitUs = 3.0,
+                 kW4SkPartialUsPerMB = 0.5, kRowsSmallFixedUs = 0.5;
+
+bool rows_beats_skinny(int M, int N, int K, int G, int num_cus, int nh, int u, int* mb_out,
+                       int* nh_out) {
+    if (!rows_shape_ok(N, K, G)) return false;
+    const int kps = SK_NW * u * 128, sp = ceil_div(K, kps);
+    const int skmb = M <= 16 ? 1 : 2;
+    const int64_t sk_wgs = (int64_t)(N / (16 * nh)) * sp;
+    const double sk_kb = (std::min(M, 16 * skmb) * 2.0 + 8.0 * nh) * std::min(K, kps) / 1000.0;
+    double best = (double)((sk_wgs + num_cus - 1) / num_cus) * (kW4SkWgFixedUs + sk_kb / kW4SkKbPerUs);
+    if (sp > 1) best += kW4SkSplitUs + kW4SkPartialUsPerMB * (sp + 1) * 4.0 * M * N / 1e6;
+    bool rows = false;
+    for (int c = -1; c < 3; ++c) {
+        const int mb = c < 0 ? 1 : kRowsCfg[c][0], rnh = c < 0 ? 1 : kRowsCfg[c][1];
+        const double fixed = c < 0 ? kRowsSmallFixedUs : kRowsWgFixedUs[c];
+        if (N % (16 * rnh) != 0) continue;
+        const int64_t wgs = (int64_t)(N / (16 * rnh)) * ceil_div(M, 16 * mb);
+        const double kb = (std::min(M, 16 * mb) * 2.0 + 8.0 * rnh) * K / 1000.0;
+        const double t = (double)((wgs + num_cus - 1) / num_cus) * (fixed + kb / kRowsKbPerUs);
+        if (t < best * 0.999) {
+            best = t;
+            rows = true;
+            *mb_out = mb;
+            *nh_out = rnh;
+        }
+    }
+    return rows;
+}
+
 // M <= 4 rows against few columns and a long K: the decode gives one workgroup per
 // 16-column slice, each walking all of K, so with under num_cus / 4 slices a K-split skinny
 // launch finishes first.  Measured on MI355X (256 CUs), decode against skinny, us:
@@ -2129,8 +2170,9 @@ bool w4a16_narrow_skinny(int M, int N, int K, int num_cus) {
 //                tiles alone give under half a workgroup per CU.
 //   gemm         M > 32 with G a power of two: LDS-DMA MFMA GEMM (tile below), K split
 //                (plus a reduce pass) only when the tiles cannot fill the chip.
-//   rows         32 < M <= 1024 with G = 128 * 2^j where the launch model prefers it to
-//                every LDS-DMA plan (short K, few columns): no ring, no split.
+//   rows         4 < M <= 1024 with G = 128 * 2^j where the launch model prefers it to
+//                the skinny plan (M <= 32) or to every LDS-DMA plan (short K, few
+//                columns): no ring, no split.
 //   mfma         everything else (the shapes the kernels above do not take).
 W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
     if (num_cus <= 0) num_cus = 256;
@@ -2152,6 +2194,14 @@ W4A16Plan w4a16_plan(int M, int N, int K, int G, int num_cus, bool aligned) {
     if ((M > DM_MAXM || narrow_skinny) && M <= 32 && K % 128 == 0 && g_ok) {
         int nh = 2, u = 1;
         skinny_config(M, N, K, num_cus, &nh, &u);
+        int mb, rnh;
+        if (M > DM_MAXM && rows_beats_skinny(M, N, K, G, num_cus, nh, u, &mb, &rnh)) {
+            pl.kind = W4_ROWS;
+            pl.mb = mb;
+            pl.big = rnh;
+            pl.k_per_split = K;
+            return pl;
+        }
         pl.big = nh;
         pl.kind = W4_SKINNY;
         pl.k_per_split = SK_NW * u * 128;
@@ -2263,7 +2313,9 @@ hipError_t launch_w4a16_zf(const W4Args& a, const W4A16Launch& w, hipStream_t st
         launch_w4g<ZF>(a, pl.big, grid, stream);
     } else if (pl.kind == W4_ROWS) {
         const dim3 grid(w.N / (16 * pl.big), 1, ceil_div(w.M, 16 * pl.mb));
-        if (pl.mb == 1 && pl.big == 2)
+        if (pl.mb == 1 && pl.big == 1)
+            launch_rows<ZF, 1, 1>(a, grid, stream);
+        else if (pl.mb == 1 && pl.big == 2)
             launch_rows<ZF, 1, 2>(a, grid, stream);
         else if (pl.mb == 1)
             launch_rows<ZF, 1, 4>(a, grid, stream);
