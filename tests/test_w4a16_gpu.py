@@ -214,15 +214,17 @@ def _capi_lib():
                                     "wmma_ops_amd", "libwmma_ops_amd.so"))
 
 
-# The rows kernel (M > 32, short K, few columns) through the C-ABI: each of its workgroup
-# shapes -- 16 rows x 32 columns (M=40, 77, 50, 600), 16 x 64 (M=37), 32 x 64 (M=200,
-# 333) -- with the last row group partial, N a multiple of 32 but not 64 (N=288),
-# G = 128, 256, 512 (a pair-step's group found by a shift), lda > K, packed and byte zeros
-# and the slice-major parameters (identical bits), fp16 output (the fp32 result rounded
-# once), and repeated calls bit-identical.
+# The rows kernel through the C-ABI: each of its workgroup shapes -- 16 rows x 32 columns
+# (M=40, 77, 50, 600; M=17), 16 x 64 (M=37; M=17), 32 x 64 (M=200, 333; M=17) above and
+# below 33 rows, and 16 x 16 (M=5, below 33 rows only) -- with the last row group partial,
+# N a multiple of 32 but not 64 (N=288), G = 128, 256, 512 (a pair-step's group found by a
+# shift), lda > K, packed and byte zeros and the slice-major parameters (identical bits),
+# fp16 output (the fp32 result rounded once), and repeated calls bit-identical.
 @pytest.mark.parametrize("M,K,N,G", [(40, 1024, 512, 128), (77, 2048, 1024, 128), (37, 2048, 4096, 128),
                                      (200, 2048, 2048, 256), (333, 1024, 1024, 128),
-                                     (50, 4096, 2048, 512), (600, 512, 288, 256)])
+                                     (50, 4096, 2048, 512), (600, 512, 288, 256),
+                                     (5, 3072, 256, 128), (17, 3072, 4096, 128), (17, 3072, 8192, 128),
+                                     (17, 3072, 14336, 128)])
 def test_w4a16_rows(wo, M, K, N, G):
     plan = wo.w4a16_plan(M, N, K, G)
     report("w4a16_rows", M=M, K=K, N=N, G=G, plan=plan)
